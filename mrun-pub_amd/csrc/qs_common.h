@@ -1,0 +1,110 @@
+// Shared device/host helpers for the QStore gfx950 kernels.
+//
+// Everything here is CDNA4 (gfx950) specific: wave64, MFMA operand layouts of the
+// 16x16 families, hardware RNE fp32->bf16 conversion (v_cvt_pk_bf16_f32).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/qstore_hip.h"
+
+namespace qs {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------------
+// host-side error plumbing: every entry point returns a qs_status and records a
+// human-readable message retrievable with qs_last_error().
+// ---------------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+int fail(int status, const char* fmt, ...);
+int hip_check(hipError_t e, const char* what);
+
+inline bool aligned(const void* p, int bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(bytes)) == 0;
+}
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------------
+
+// int8 code (byte b of a dword) -> exact fp32. Compiles to v_cvt_f32_i32_sdwa sext.
+__device__ __forceinline__ float byte_f32(int d, int b) {
+  return static_cast<float>(static_cast<signed char>(d >> (8 * b)));
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
+  __bf16 b = static_cast<__bf16>(v);  // hardware RNE
+  return __builtin_bit_cast(uint16_t, b);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+  _Float16 h = static_cast<_Float16>(v);  // RNE
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t bits) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+}
+
+// Dequantize 16 int8 codes held in one 128-bit register group with one fp32 row
+// scale, rounding each fp32 product to bf16 (the W8A16 weight contract
+// bf16(float(code) * scale)).  Element e of the 16 lands in lo[e] / hi[e-8].
+__device__ __forceinline__ void deq16_bf16(i32x4 w, float s, bf16x8& lo, bf16x8& hi) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      lo[4 * j + b] = static_cast<__bf16>(byte_f32(w[j], b) * s);
+      hi[4 * j + b] = static_cast<__bf16>(byte_f32(w[j + 2], b) * s);
+    }
+  }
+}
+
+__device__ __forceinline__ void deq16_f16(i32x4 w, float s, f16x8& lo, f16x8& hi) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      lo[4 * j + b] = static_cast<_Float16>(byte_f32(w[j], b) * s);
+      hi[4 * j + b] = static_cast<_Float16>(byte_f32(w[j + 2], b) * s);
+    }
+  }
+}
+
+// Full-wave sum with a fixed butterfly order (deterministic, identical for every
+// call with the same operand).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Non-contracted fp32 product / sum (keeps the reference's separate roundings).
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+
+}  // namespace qs

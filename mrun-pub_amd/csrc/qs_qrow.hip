@@ -1,0 +1,640 @@
+// int8 row-scaled ("qrow") QStore linears on gfx950.
+//
+// Kernels
+//   k_dequant16 / k_dequant_any : W = float(code) * scale -> f32 / bf16 / f16.
+//   k_w8a16<...>                : y = x @ W^T for bf16/f16 activations.  Weights stream
+//                                 straight from HBM into VGPRs with 128-bit loads, are
+//                                 dequantized in registers (bf16(float(code)*scale), the
+//                                 W8A16 contract) and fed to v_mfma_f32_16x16x32_{bf16,f16}
+//                                 with the activations as the A operand (M <= 32 rows
+//                                 padded to 16-row tiles).  MFMA replaces the per-element
+//                                 multiply-add, so the VALU only pays for the dequant
+//                                 (cvt_sdwa + mul + half a cvt_pk per weight byte).
+//                                 K is split across the waves of a workgroup and reduced
+//                                 through LDS in a fixed order.
+//   k_f32_gemv<...>             : fp32 activations (QStore fp32 compute contract): VALU
+//                                 dequant + fma, fixed-order wave butterfly reduction.
+//   k_generic                   : any shape / alignment, one wave per output row.
+//
+// MFMA operand mapping (16x16x32, wave64): lane l supplies row (l & 15) of A and
+// column (l & 15) of B, holding 8 consecutive k of the k-block (l >> 4).  The k order
+// inside the block is irrelevant as long as A and B agree, so lane l simply loads the
+// 16 contiguous bytes at k = 64*c + 16*(l>>4) of weight row (l & 15) and the matching
+// 16 activations; elements 0..7 feed one MFMA and 8..15 the next.  The accumulator of
+// lane l holds D[4*(l>>4) + q][l & 15], q = 0..3.
+#include "qs_common.h"
+
+namespace qs {
+
+struct QrowLin {
+  const int8_t* codes;
+  const float* scales;
+  void* y;
+  int64_t ldy;
+  int N;
+  int tile_begin;  // first workgroup index of this linear
+};
+
+struct QrowParams {
+  const void* x;
+  int64_t ldx;
+  int M;
+  int K;
+  int n_lin;
+  QrowLin lin[4];
+};
+
+// ----------------------------------------------------------------------------------
+// dequant
+// ----------------------------------------------------------------------------------
+template <int OUT>
+__global__ __launch_bounds__(256) void k_dequant16(const int8_t* __restrict__ codes,
+                                                   const float* __restrict__ scales,
+                                                   void* __restrict__ out, int64_t N,
+                                                   int64_t K, int64_t ld_out) {
+  const int64_t per_row = K / 16;
+  const int64_t total = N * per_row;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = i / per_row;
+    const int64_t c = i - n * per_row;
+    const i32x4 w = *reinterpret_cast<const i32x4*>(codes + n * K + c * 16);
+    const float s = scales[n];
+    if (OUT == QS_F32) {
+      f32x4* o = reinterpret_cast<f32x4*>(static_cast<float*>(out) + n * ld_out + c * 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f32x4 v;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) v[b] = byte_f32(w[j], b) * s;
+        o[j] = v;
+      }
+    } else if (OUT == QS_BF16) {
+      bf16x8 lo, hi;
+      deq16_bf16(w, s, lo, hi);
+      bf16x8* o = reinterpret_cast<bf16x8*>(static_cast<uint16_t*>(out) + n * ld_out + c * 16);
+      o[0] = lo;
+      o[1] = hi;
+    } else {
+      f16x8 lo, hi;
+      deq16_f16(w, s, lo, hi);
+      f16x8* o = reinterpret_cast<f16x8*>(static_cast<uint16_t*>(out) + n * ld_out + c * 16);
+      o[0] = lo;
+      o[1] = hi;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_dequant_any(const int8_t* __restrict__ codes,
+                                                     const float* __restrict__ scales,
+                                                     void* __restrict__ out, int out_dtype,
+                                                     int64_t N, int64_t K, int64_t ld_out) {
+  const int64_t total = N * K;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = i / K;
+    const int64_t k = i - n * K;
+    const float v = static_cast<float>(codes[i]) * scales[n];
+    if (out_dtype == QS_F32)
+      static_cast<float*>(out)[n * ld_out + k] = v;
+    else if (out_dtype == QS_BF16)
+      static_cast<uint16_t*>(out)[n * ld_out + k] = f32_to_bf16_bits(v);
+    else
+      static_cast<uint16_t*>(out)[n * ld_out + k] = f32_to_f16_bits(v);
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// W8A16 MFMA kernel
+// ----------------------------------------------------------------------------------
+template <bool F16>
+struct HalfOps;
+
+template <>
+struct HalfOps<false> {
+  typedef bf16x8 vec;
+  static __device__ __forceinline__ void deq(i32x4 w, float s, vec& lo, vec& hi) {
+    deq16_bf16(w, s, lo, hi);
+  }
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t out(float v) { return f32_to_bf16_bits(v); }
+};
+
+template <>
+struct HalfOps<true> {
+  typedef f16x8 vec;
+  static __device__ __forceinline__ void deq(i32x4 w, float s, vec& lo, vec& hi) {
+    deq16_f16(w, s, lo, hi);
+  }
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t out(float v) { return f32_to_f16_bits(v); }
+};
+
+__device__ __forceinline__ float silu_f32(float g) { return g * (1.0f / (1.0f + expf(-g))); }
+
+// R    : 16-row weight tiles per workgroup (SWIGLU: R == 2, gate and up of one tile)
+// MT   : 16-row activation tiles (M <= 16 * MT)
+// WAVES: waves splitting K; U: chunks (64 k each) in flight per wave
+template <int R, int MT, int WAVES, int U, bool SWIGLU, bool F16>
+__global__ __launch_bounds__(WAVES * 64) void k_w8a16(QrowParams p) {
+  typedef HalfOps<F16> H;
+  typedef typename H::vec hvec;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+
+  int li = 0;
+  if (!SWIGLU) {
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      if (j < p.n_lin && (int)blockIdx.x >= p.lin[j].tile_begin) li = j;
+  }
+  const int tile = (int)blockIdx.x - p.lin[li].tile_begin;
+  const int N = p.lin[li].N;
+  const int K = p.K;
+  const int M = p.M;
+  const int n0 = tile * 16 * (SWIGLU ? 1 : R);
+
+  const int8_t* wrow[R];
+  float sc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const QrowLin& L = SWIGLU ? p.lin[r] : p.lin[li];
+    int n = SWIGLU ? n0 + col : n0 + 16 * r + col;
+    n = n < N ? n : N - 1;  // clamp: the lane's outputs are not stored
+    wrow[r] = L.codes + (int64_t)n * K + 16 * grp;
+    sc[r] = L.scales[n];
+  }
+  const uint16_t* xrow[MT];
+  bool mval[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = 16 * t + col;
+    mval[t] = m < M;
+    xrow[t] = static_cast<const uint16_t*>(p.x) + (int64_t)(mval[t] ? m : 0) * p.ldx + 16 * grp;
+  }
+
+  f32x4 acc[R][MT];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int C = K / 64;
+  int c = wave;
+  // main loop: U chunks per wave in flight
+  for (; c + (U - 1) * WAVES < C; c += U * WAVES) {
+    i32x4 wv[U][R];
+    hvec xv[U][MT][2];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t off = (int64_t)(c + u * WAVES) * 64;
+#pragma unroll
+      for (int r = 0; r < R; ++r) wv[u][r] = *reinterpret_cast<const i32x4*>(wrow[r] + off);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        if (mval[t]) {
+          xv[u][t][0] = *reinterpret_cast<const hvec*>(xrow[t] + off);
+          xv[u][t][1] = *reinterpret_cast<const hvec*>(xrow[t] + off + 8);
+        } else {
+          xv[u][t][0] = hvec{};
+          xv[u][t][1] = hvec{};
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        hvec b0, b1;
+        H::deq(wv[u][r], sc[r], b0, b1);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acc[r][t] = H::mma(xv[u][t][0], b0, acc[r][t]);
+          acc[r][t] = H::mma(xv[u][t][1], b1, acc[r][t]);
+        }
+      }
+    }
+  }
+  // remainder chunks, one at a time
+  for (; c < C; c += WAVES) {
+    const int64_t off = (int64_t)c * 64;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const i32x4 w = *reinterpret_cast<const i32x4*>(wrow[r] + off);
+      hvec b0, b1;
+      H::deq(w, sc[r], b0, b1);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        hvec a0{}, a1{};
+        if (mval[t]) {
+          a0 = *reinterpret_cast<const hvec*>(xrow[t] + off);
+          a1 = *reinterpret_cast<const hvec*>(xrow[t] + off + 8);
+        }
+        acc[r][t] = H::mma(a0, b0, acc[r][t]);
+        acc[r][t] = H::mma(a1, b1, acc[r][t]);
+      }
+    }
+  }
+
+  // cross-wave reduction in fixed wave order
+  if (WAVES > 1) {
+    __shared__ f32x4 red[WAVES][R * MT][64];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) red[wave][r * MT + t][lane] = acc[r][t];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        f32x4 s = red[0][r * MT + t][lane];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) s += red[w][r * MT + t][lane];
+        acc[r][t] = s;
+      }
+  }
+
+  // store: lane holds D[m = 16t + 4*grp + q][n = col]
+  if (SWIGLU) {
+    const int n = n0 + col;
+    if (n >= N) return;
+    uint16_t* y = static_cast<uint16_t*>(p.lin[0].y);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = 16 * t + 4 * grp + q;
+        if (m < M) {
+          const float gt = bf16_bits_to_f32(f32_to_bf16_bits(acc[0][t][q]));
+          const float ut = bf16_bits_to_f32(f32_to_bf16_bits(acc[1][t][q]));
+          const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f32(gt)));
+          y[(int64_t)m * p.lin[0].ldy + n] = f32_to_bf16_bits(sl * ut);
+        }
+      }
+  } else {
+    uint16_t* y = static_cast<uint16_t*>(p.lin[li].y);
+    const int64_t ldy = p.lin[li].ldy;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = n0 + 16 * r + col;
+      if (n < N) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int m = 16 * t + 4 * grp + q;
+            if (m < M) y[(int64_t)m * ldy + n] = H::out(acc[r][t][q]);
+          }
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// fp32-activation GEMV (VALU)
+// ----------------------------------------------------------------------------------
+// Each wave owns R consecutive output rows over the whole K; lane l handles the 16-byte
+// chunks l, l+64, ... of every row.  M rows of x are processed MB at a time.
+template <int R, int MB, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void k_f32_gemv(QrowParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int li = 0;
+#pragma unroll
+  for (int j = 1; j < 4; ++j)
+    if (j < p.n_lin && (int)blockIdx.x >= p.lin[j].tile_begin) li = j;
+  const QrowLin& L = p.lin[li];
+  const int N = L.N;
+  const int K = p.K;
+  const int nb = (((int)blockIdx.x - L.tile_begin) * WAVES + wave) * R;
+  if (nb >= N) return;
+  const float* x = static_cast<const float*>(p.x);
+  float* y = static_cast<float*>(L.y);
+
+  const int8_t* wrow[R];
+  float sc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = nb + r < N ? nb + r : N - 1;
+    wrow[r] = L.codes + (int64_t)n * K;
+    sc[r] = L.scales[n];
+  }
+  const int C = K / 16;
+  for (int m0 = 0; m0 < p.M; m0 += MB) {
+    float acc[MB][R];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[i][r] = 0.f;
+    for (int c = lane; c < C; c += 64) {
+      i32x4 wv[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) wv[r] = *reinterpret_cast<const i32x4*>(wrow[r] + c * 16);
+      f32x4 xv[MB][4];
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const int m = m0 + i < p.M ? m0 + i : p.M - 1;
+        const f32x4* xp = reinterpret_cast<const f32x4*>(x + (int64_t)m * p.ldx + c * 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[i][j] = xp[j];
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const float w = byte_f32(wv[r][j], b) * sc[r];
+#pragma unroll
+            for (int i = 0; i < MB; ++i) acc[i][r] = fmaf(xv[i][j][b], w, acc[i][r]);
+          }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float s = wave_sum(acc[i][r]);
+        if (lane == 0 && m0 + i < p.M && nb + r < N) y[(int64_t)(m0 + i) * L.ldy + nb + r] = s;
+      }
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// generic fallback: any K, any alignment.  One wave per (linear, row).
+// ----------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_generic(QrowParams p, int x_dtype) {
+  const int lane = threadIdx.x & 63;
+  const int gw = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+  int li = 0;
+#pragma unroll
+  for (int j = 1; j < 4; ++j)
+    if (j < p.n_lin && gw >= p.lin[j].tile_begin) li = j;
+  const QrowLin& L = p.lin[li];
+  const int n = gw - L.tile_begin;
+  if (n >= L.N) return;
+  const int8_t* w = L.codes + (int64_t)n * p.K;
+  const float s = L.scales[n];
+  for (int m = 0; m < p.M; ++m) {
+    float acc = 0.f;
+    for (int k = lane; k < p.K; k += 64) {
+      float wf = static_cast<float>(w[k]) * s;
+      float xf;
+      const int64_t xi = (int64_t)m * p.ldx + k;
+      if (x_dtype == QS_F32) {
+        xf = static_cast<const float*>(p.x)[xi];
+      } else if (x_dtype == QS_BF16) {
+        wf = bf16_bits_to_f32(f32_to_bf16_bits(wf));
+        xf = bf16_bits_to_f32(static_cast<const uint16_t*>(p.x)[xi]);
+      } else {
+        wf = f16_bits_to_f32(f32_to_f16_bits(wf));
+        xf = f16_bits_to_f32(static_cast<const uint16_t*>(p.x)[xi]);
+      }
+      acc = fmaf(xf, wf, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) {
+      const int64_t yi = (int64_t)m * L.ldy + n;
+      if (x_dtype == QS_F32)
+        static_cast<float*>(L.y)[yi] = acc;
+      else if (x_dtype == QS_BF16)
+        static_cast<uint16_t*>(L.y)[yi] = f32_to_bf16_bits(acc);
+      else
+        static_cast<uint16_t*>(L.y)[yi] = f32_to_f16_bits(acc);
+    }
+  }
+}
+
+// generic SwiGLU fallback (bf16): one wave per output column n.
+__global__ __launch_bounds__(256) void k_generic_swiglu(QrowParams p) {
+  const int lane = threadIdx.x & 63;
+  const int n = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (n >= p.lin[0].N) return;
+  const int8_t* wg = p.lin[0].codes + (int64_t)n * p.K;
+  const int8_t* wu = p.lin[1].codes + (int64_t)n * p.K;
+  const float sg = p.lin[0].scales[n], su = p.lin[1].scales[n];
+  const uint16_t* x = static_cast<const uint16_t*>(p.x);
+  for (int m = 0; m < p.M; ++m) {
+    float ag = 0.f, au = 0.f;
+    for (int k = lane; k < p.K; k += 64) {
+      const float xf = bf16_bits_to_f32(x[(int64_t)m * p.ldx + k]);
+      ag = fmaf(xf, bf16_bits_to_f32(f32_to_bf16_bits(static_cast<float>(wg[k]) * sg)), ag);
+      au = fmaf(xf, bf16_bits_to_f32(f32_to_bf16_bits(static_cast<float>(wu[k]) * su)), au);
+    }
+    ag = wave_sum(ag);
+    au = wave_sum(au);
+    if (lane == 0) {
+      const float gt = bf16_bits_to_f32(f32_to_bf16_bits(ag));
+      const float ut = bf16_bits_to_f32(f32_to_bf16_bits(au));
+      const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f32(gt)));
+      static_cast<uint16_t*>(p.lin[0].y)[(int64_t)m * p.lin[0].ldy + n] =
+          f32_to_bf16_bits(sl * ut);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// host launchers
+// ----------------------------------------------------------------------------------
+namespace {
+
+constexpr int kMfmaWaves = 4;
+
+template <int R, int MT, bool SWIGLU, bool F16>
+void launch_w8a16(const QrowParams& p, int blocks, hipStream_t s) {
+  constexpr int U = (MT == 1) ? 4 : 2;
+  hipLaunchKernelGGL((k_w8a16<R, MT, kMfmaWaves, U, SWIGLU, F16>), dim3(blocks),
+                     dim3(kMfmaWaves * 64), 0, s, p);
+}
+
+bool mfma_eligible(const QrowParams& p, int x_dtype) {
+  if (x_dtype != QS_BF16 && x_dtype != QS_F16) return false;
+  if (p.K % 64 != 0 || p.ldx % 8 != 0 || !aligned(p.x, 16)) return false;
+  for (int i = 0; i < p.n_lin; ++i)
+    if (!aligned(p.lin[i].codes, 16)) return false;
+  return true;
+}
+
+int validate_common(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K) {
+  if (!x) return fail(QS_ERR_INVALID, "activation pointer is null");
+  if (x_dtype != QS_F32 && x_dtype != QS_BF16 && x_dtype != QS_F16)
+    return fail(QS_ERR_INVALID, "activation dtype must be F32, BF16 or F16");
+  if (M < 0 || K <= 0) return fail(QS_ERR_INVALID, "invalid M=%lld K=%lld", (long long)M, (long long)K);
+  if (ldx < K) return fail(QS_ERR_INVALID, "ldx (%lld) < K (%lld)", (long long)ldx, (long long)K);
+  if (K > (int64_t)1 << 30 || M > (int64_t)1 << 30)
+    return fail(QS_ERR_LIMIT, "dimension exceeds 2^30");
+  return QS_OK;
+}
+
+// Runs one set of linears sharing x, M <= 32 rows at a time for the MFMA path.
+int run_linears(QrowParams p, int x_dtype, int64_t M, hipStream_t s) {
+  if (M == 0) return QS_OK;
+  const int esz = x_dtype == QS_F32 ? 4 : 2;
+  if (mfma_eligible(p, x_dtype)) {
+    for (int64_t m0 = 0; m0 < M; m0 += 32) {
+      QrowParams q = p;
+      const int mm = (int)((M - m0) < 32 ? (M - m0) : 32);
+      q.M = mm;
+      q.x = static_cast<const char*>(p.x) + m0 * p.ldx * esz;
+      const int R = mm <= 4 ? 1 : 2;
+      int blocks = 0;
+      for (int i = 0; i < q.n_lin; ++i) {
+        q.lin[i].y = static_cast<char*>(p.lin[i].y) + m0 * p.lin[i].ldy * 2;
+        q.lin[i].tile_begin = blocks;
+        blocks += (int)cdiv(q.lin[i].N, 16 * R);
+      }
+      const bool f16 = x_dtype == QS_F16;
+      if (mm <= 16) {
+        if (R == 1) f16 ? launch_w8a16<1, 1, false, true>(q, blocks, s) : launch_w8a16<1, 1, false, false>(q, blocks, s);
+        else f16 ? launch_w8a16<2, 1, false, true>(q, blocks, s) : launch_w8a16<2, 1, false, false>(q, blocks, s);
+      } else {
+        f16 ? launch_w8a16<2, 2, false, true>(q, blocks, s) : launch_w8a16<2, 2, false, false>(q, blocks, s);
+      }
+    }
+    return hip_check(hipGetLastError(), "k_w8a16 launch");
+  }
+  bool f32_fast = x_dtype == QS_F32 && p.K % 16 == 0 && p.ldx % 4 == 0 && aligned(p.x, 16);
+  for (int i = 0; i < p.n_lin; ++i) f32_fast = f32_fast && aligned(p.lin[i].codes, 16);
+  if (f32_fast) {
+    constexpr int R = 4, WAVES = 4;
+    int blocks = 0;
+    for (int i = 0; i < p.n_lin; ++i) {
+      p.lin[i].tile_begin = blocks;
+      blocks += (int)cdiv(p.lin[i].N, R * WAVES);
+    }
+    p.M = (int)M;
+    if (M == 1)
+      hipLaunchKernelGGL((k_f32_gemv<R, 1, WAVES>), dim3(blocks), dim3(WAVES * 64), 0, s, p);
+    else
+      hipLaunchKernelGGL((k_f32_gemv<R, 4, WAVES>), dim3(blocks), dim3(WAVES * 64), 0, s, p);
+    return hip_check(hipGetLastError(), "k_f32_gemv launch");
+  }
+  int waves = 0;
+  for (int i = 0; i < p.n_lin; ++i) {
+    p.lin[i].tile_begin = waves;
+    waves += p.lin[i].N;
+  }
+  p.M = (int)M;
+  hipLaunchKernelGGL(k_generic, dim3((unsigned)cdiv(waves, 4)), dim3(256), 0, s, p, x_dtype);
+  return hip_check(hipGetLastError(), "k_generic launch");
+}
+
+}  // namespace
+}  // namespace qs
+
+using namespace qs;
+
+extern "C" int qs_qrow_dequant(const int8_t* codes, const float* scales, void* out, int out_dtype,
+                               int64_t N, int64_t K, int64_t ld_out, void* stream) {
+  if (!codes || !scales || !out) return fail(QS_ERR_INVALID, "dequant: null pointer");
+  if (N < 0 || K <= 0 || ld_out < K) return fail(QS_ERR_INVALID, "dequant: bad shape");
+  if (out_dtype != QS_F32 && out_dtype != QS_BF16 && out_dtype != QS_F16)
+    return fail(QS_ERR_INVALID, "dequant: out dtype must be F32, BF16 or F16");
+  if (N == 0) return QS_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int osz = out_dtype == QS_F32 ? 4 : 2;
+  const bool fast = K % 16 == 0 && aligned(codes, 16) && aligned(out, 16) &&
+                    (ld_out * osz) % 16 == 0;
+  if (fast) {
+    const int64_t work = N * (K / 16);
+    const unsigned blocks = (unsigned)(cdiv(work, 256) < 65536 ? cdiv(work, 256) : 65536);
+    if (out_dtype == QS_F32)
+      hipLaunchKernelGGL(k_dequant16<QS_F32>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
+    else if (out_dtype == QS_BF16)
+      hipLaunchKernelGGL(k_dequant16<QS_BF16>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
+    else
+      hipLaunchKernelGGL(k_dequant16<QS_F16>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
+  } else {
+    const int64_t work = N * K;
+    const unsigned blocks = (unsigned)(cdiv(work, 256) < 65536 ? cdiv(work, 256) : 65536);
+    hipLaunchKernelGGL(k_dequant_any, dim3(blocks), dim3(256), 0, s, codes, scales, out, out_dtype, N, K, ld_out);
+  }
+  return hip_check(hipGetLastError(), "dequant launch");
+}
+
+extern "C" int qs_qrow_matmul(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
+                              const float* scales, void* y, int64_t ldy, int64_t M, int64_t N,
+                              int64_t K, void* stream) {
+  int st = validate_common(x, x_dtype, ldx, M, K);
+  if (st) return st;
+  if (!codes || !scales || !y) return fail(QS_ERR_INVALID, "matmul: null pointer");
+  if (N <= 0 || N > (int64_t)1 << 30) return fail(QS_ERR_INVALID, "matmul: bad N=%lld", (long long)N);
+  if (ldy < N) return fail(QS_ERR_INVALID, "matmul: ldy < N");
+  QrowParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.M = (int)M;
+  p.K = (int)K;
+  p.n_lin = 1;
+  p.lin[0] = QrowLin{codes, scales, y, ldy, (int)N, 0};
+  return run_linears(p, x_dtype, M, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qs_qrow_matmul_multi(const void* x, int x_dtype, int64_t ldx, int n_linear,
+                                    const int8_t* const* codes, const float* const* scales,
+                                    void* const* y, const int64_t* ldy, const int64_t* N,
+                                    int64_t M, int64_t K, void* stream) {
+  int st = validate_common(x, x_dtype, ldx, M, K);
+  if (st) return st;
+  if (n_linear < 1 || n_linear > 4) return fail(QS_ERR_LIMIT, "matmul_multi: 1..4 linears");
+  if (!codes || !scales || !y || !ldy || !N) return fail(QS_ERR_INVALID, "matmul_multi: null array");
+  QrowParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.M = (int)M;
+  p.K = (int)K;
+  p.n_lin = n_linear;
+  for (int i = 0; i < n_linear; ++i) {
+    if (!codes[i] || !scales[i] || !y[i]) return fail(QS_ERR_INVALID, "matmul_multi: null pointer in linear %d", i);
+    if (N[i] <= 0 || N[i] > (int64_t)1 << 30 || ldy[i] < N[i])
+      return fail(QS_ERR_INVALID, "matmul_multi: bad N/ldy for linear %d", i);
+    p.lin[i] = QrowLin{codes[i], scales[i], y[i], ldy[i], (int)N[i], 0};
+  }
+  return run_linears(p, x_dtype, M, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qs_qrow_swiglu(const void* x, int64_t ldx, const int8_t* gate_codes,
+                              const float* gate_scales, const int8_t* up_codes,
+                              const float* up_scales, void* y, int64_t ldy, int64_t M, int64_t N,
+                              int64_t K, void* stream) {
+  int st = validate_common(x, QS_BF16, ldx, M, K);
+  if (st) return st;
+  if (!gate_codes || !gate_scales || !up_codes || !up_scales || !y)
+    return fail(QS_ERR_INVALID, "swiglu: null pointer");
+  if (N <= 0 || N > (int64_t)1 << 30 || ldy < N) return fail(QS_ERR_INVALID, "swiglu: bad N/ldy");
+  if (M == 0) return QS_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  QrowParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.K = (int)K;
+  p.n_lin = 2;
+  p.lin[0] = QrowLin{gate_codes, gate_scales, y, ldy, (int)N, 0};
+  p.lin[1] = QrowLin{up_codes, up_scales, nullptr, 0, (int)N, 0};
+  if (mfma_eligible(p, QS_BF16)) {
+    for (int64_t m0 = 0; m0 < M; m0 += 32) {
+      QrowParams q = p;
+      const int mm = (int)((M - m0) < 32 ? (M - m0) : 32);
+      q.M = mm;
+      q.x = static_cast<const uint16_t*>(x) + m0 * ldx;
+      q.lin[0].y = static_cast<uint16_t*>(y) + m0 * ldy;
+      const int blocks = (int)cdiv(N, 16);
+      if (mm <= 16)
+        launch_w8a16<2, 1, true, false>(q, blocks, s);
+      else
+        launch_w8a16<2, 2, true, false>(q, blocks, s);
+    }
+    return hip_check(hipGetLastError(), "k_w8a16 swiglu launch");
+  }
+  p.M = (int)M;
+  hipLaunchKernelGGL(k_generic_swiglu, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, s, p);
+  return hip_check(hipGetLastError(), "k_generic_swiglu launch");
+}

@@ -1,0 +1,256 @@
+"""int8 row-scaled (qrow) linears on gfx950: the fused dequant+matmul operator surface.
+
+Mirrors the reference kernel-level API
+(src/mrun/engine/kernels/dense_qstore_cuda.py:78-101, 1003-1153) with the HIP kernels of
+``csrc/qs_qrow.hip`` underneath:
+
+* ``CompactQRowPage``        -- device-resident ``(codes int8[rows, K], scales f32[rows])``.
+* ``fused_qrow_matmul``       -- ``y = x @ (bf16|fp16|fp32)(codes * scales)^T``.
+* ``fused_qrow_swiglu``       -- paired gate/up projections with the BF16 SwiGLU epilogue.
+* ``qrow_dequant``            -- the materialized weight (``_dequant_qrow``, qstore.py:385).
+
+There is no CPU or "reference-materialized" branch: CPU tensors raise ``ValueError`` and a
+missing native library raises ``RuntimeError`` (the reference's ``require_triton`` fail-closed
+behaviour, dense_qstore_cuda.py:1125-1128, is therefore always in force).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _native as nat
+
+IMPL_W8A16 = "hip-gfx950-w8a16-qrow-v1"
+IMPL_FP32 = "hip-gfx950-qrow-fp32-v1"
+IMPL_SWIGLU = "hip-gfx950-paired-w8a16-swiglu-bf16-v1"
+
+_ACT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _tensor_bytes(tensor: torch.Tensor) -> int:
+    return int(tensor.numel() * tensor.element_size())
+
+
+@dataclass(frozen=True)
+class CompactQRowPage:
+    """Row range ``[start_row, end_row)`` of one qrow block, codes and scales in HBM.
+
+    Same fields and byte accounting as the reference ``CompactQRowPage``
+    (dense_qstore_cuda.py:78-101).
+    """
+
+    name: str
+    start_row: int
+    end_row: int
+    in_features: int
+    codes: torch.Tensor
+    scales: torch.Tensor
+
+    @property
+    def out_features(self) -> int:
+        return self.end_row - self.start_row
+
+    @property
+    def compact_bytes(self) -> int:
+        return _tensor_bytes(self.codes) + _tensor_bytes(self.scales)
+
+    @property
+    def expanded_fp32_bytes(self) -> int:
+        return self.out_features * self.in_features * 4
+
+    def expanded_compute_bytes(self, dtype: torch.dtype) -> int:
+        return self.out_features * self.in_features * torch.empty((), dtype=dtype).element_size()
+
+
+def _check_codes(codes: torch.Tensor, scales: torch.Tensor) -> tuple[int, int]:
+    if codes.dtype != torch.int8 or codes.ndim != 2:
+        raise ValueError("qrow codes must be int8 [out, in]")
+    if scales.dtype != torch.float32 or scales.ndim != 1 or scales.numel() != codes.shape[0]:
+        raise ValueError("qrow scales must be float32 [out]")
+    if not codes.is_contiguous() or not scales.is_contiguous():
+        raise ValueError("qrow codes and scales must be contiguous")
+    return int(codes.shape[0]), int(codes.shape[1])
+
+
+@torch.inference_mode()
+def qrow_dequant(
+    codes: torch.Tensor, scales: torch.Tensor, dtype: torch.dtype = torch.float32
+) -> torch.Tensor:
+    """``dtype(float32(codes) * scales[:, None])`` on the device (bit-exact widen+scale)."""
+    n, k = _check_codes(codes, scales)
+    device = nat.require_device(codes, scales)
+    out = torch.empty((n, k), dtype=dtype, device=device)
+    nat.call(
+        "qs_qrow_dequant",
+        nat.ptr(codes),
+        nat.ptr(scales),
+        nat.ptr(out),
+        nat.dtype_code(dtype),
+        n,
+        k,
+        k,
+        nat.stream_of(device),
+    )
+    return out
+
+
+@torch.inference_mode()
+def qrow_matmul(codes: torch.Tensor, scales: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """``x[..., K] @ W^T`` with the dtype contract of ``qs_qrow_matmul``.
+
+    fp32 activations: fp32 weights and output (QStore compute contract, qstore.py:1082-1092).
+    bf16 / fp16 activations: weights rounded per element to the activation dtype, fp32
+    accumulation, output in the activation dtype (W8A16, dense_qstore_cuda.py:467-512).
+    """
+    n, k = _check_codes(codes, scales)
+    if x.dtype not in _ACT_DTYPES:
+        raise ValueError(f"activation dtype {x.dtype} not supported")
+    if x.ndim < 1 or int(x.shape[-1]) != k:
+        raise ValueError("activation width does not match compact qrow page")
+    device = nat.require_device(codes, scales, x)
+    flat = x.reshape(-1, k)
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    m = int(flat.shape[0])
+    y = torch.empty((m, n), dtype=x.dtype, device=device)
+    if m:
+        nat.call(
+            "qs_qrow_matmul",
+            nat.ptr(flat),
+            nat.dtype_code(x.dtype),
+            k,
+            nat.ptr(codes),
+            nat.ptr(scales),
+            nat.ptr(y),
+            n,
+            m,
+            n,
+            k,
+            nat.stream_of(device),
+        )
+    return y.reshape(*x.shape[:-1], n)
+
+
+@torch.inference_mode()
+def qrow_matmul_multi(
+    pages: list[tuple[torch.Tensor, torch.Tensor]], x: torch.Tensor
+) -> list[torch.Tensor]:
+    """Several linears over one activation in a single launch (q/k/v)."""
+    if not 1 <= len(pages) <= 4:
+        raise ValueError("qrow_matmul_multi takes 1..4 linears")
+    k = int(x.shape[-1])
+    shapes = [_check_codes(c, s) for c, s in pages]
+    if any(kk != k for _, kk in shapes):
+        raise ValueError("all linears must share the activation width")
+    if x.dtype not in _ACT_DTYPES:
+        raise ValueError(f"activation dtype {x.dtype} not supported")
+    device = nat.require_device(x, *[t for p in pages for t in p])
+    flat = x.reshape(-1, k).contiguous()
+    m = int(flat.shape[0])
+    outs = [torch.empty((m, n), dtype=x.dtype, device=device) for n, _ in shapes]
+    if m:
+        nat.call(
+            "qs_qrow_matmul_multi",
+            nat.ptr(flat),
+            nat.dtype_code(x.dtype),
+            k,
+            len(pages),
+            nat.pointer_array([nat.ptr(c) for c, _ in pages]),
+            nat.pointer_array([nat.ptr(s) for _, s in pages]),
+            nat.pointer_array([nat.ptr(o) for o in outs]),
+            nat.int64_array([n for n, _ in shapes]),
+            nat.int64_array([n for n, _ in shapes]),
+            m,
+            k,
+            nat.stream_of(device),
+        )
+    return [o.reshape(*x.shape[:-1], o.shape[1]) for o in outs]
+
+
+def _validate_block_m(block_m: int) -> None:
+    # Same accepted values as the reference; the HIP kernels choose their own tiles.
+    if block_m not in {16, 32, 64}:
+        raise ValueError("block_m must be one of 16, 32, or 64")
+
+
+@torch.inference_mode()
+def fused_qrow_matmul(
+    page: CompactQRowPage,
+    activations: torch.Tensor,
+    *,
+    require_triton: bool = False,
+    block_m: int = 16,
+) -> tuple[torch.Tensor, str]:
+    """Drop-in for ``fused_qrow_matmul`` (dense_qstore_cuda.py:1105-1153).
+
+    Returns ``(y, implementation_tag)``.  ``require_triton`` is accepted for signature
+    compatibility; the native path is the only path.
+    """
+    del require_triton
+    if activations.shape[-1] != page.in_features:
+        raise ValueError("activation width does not match compact qrow page")
+    if page.codes.device != activations.device or page.scales.device != activations.device:
+        raise ValueError("compact qrow page and activations must use one device")
+    _validate_block_m(block_m)
+    y = qrow_matmul(page.codes, page.scales, activations)
+    return y, (IMPL_FP32 if activations.dtype == torch.float32 else IMPL_W8A16)
+
+
+def _validate_paired_qrow_pages(
+    gate_page: CompactQRowPage, up_page: CompactQRowPage, activations: torch.Tensor
+) -> None:
+    """Same checks and messages as dense_qstore_cuda.py:1016-1034."""
+    if activations.ndim < 2 or activations.dtype is not torch.bfloat16:
+        raise ValueError("paired SwiGLU requires BF16 activation rows")
+    if gate_page.in_features != activations.shape[-1]:
+        raise ValueError("activation width does not match paired compact qrow pages")
+    if (
+        gate_page.in_features != up_page.in_features
+        or gate_page.out_features != up_page.out_features
+        or gate_page.start_row != up_page.start_row
+        or gate_page.end_row != up_page.end_row
+    ):
+        raise ValueError("gate/up compact qrow pages must have identical geometry")
+    tensors = (gate_page.codes, gate_page.scales, up_page.codes, up_page.scales)
+    if any(tensor.device != activations.device for tensor in tensors):
+        raise ValueError("paired compact qrow pages and activations must use one device")
+
+
+@torch.inference_mode()
+def fused_qrow_swiglu(
+    gate_page: CompactQRowPage,
+    up_page: CompactQRowPage,
+    activations: torch.Tensor,
+    *,
+    require_triton: bool = False,
+    block_m: int = 16,
+) -> tuple[torch.Tensor, str]:
+    """Drop-in for ``fused_qrow_swiglu`` (dense_qstore_cuda.py:1053-1102)."""
+    del require_triton
+    _validate_paired_qrow_pages(gate_page, up_page, activations)
+    _validate_block_m(block_m)
+    n, k = _check_codes(gate_page.codes, gate_page.scales)
+    _check_codes(up_page.codes, up_page.scales)
+    device = nat.require_device(activations, gate_page.codes)
+    flat = activations.reshape(-1, k).contiguous()
+    m = int(flat.shape[0])
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    if m:
+        nat.call(
+            "qs_qrow_swiglu",
+            nat.ptr(flat),
+            k,
+            nat.ptr(gate_page.codes),
+            nat.ptr(gate_page.scales),
+            nat.ptr(up_page.codes),
+            nat.ptr(up_page.scales),
+            nat.ptr(y),
+            n,
+            m,
+            n,
+            k,
+            nat.stream_of(device),
+        )
+    return y.reshape(*activations.shape[:-1], n), IMPL_SWIGLU

@@ -1,0 +1,57 @@
+"""CPU checks of the C ABI: the built library loads and exports every declared entry point."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def _declared() -> list[str]:
+    names: list[str] = []
+    for h in HEADERS:
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(qs_\w+)\s*\(", text, re.M):
+            names.append(m.group(1))
+    return sorted(set(names))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "qs_qrow_matmul" in names and "qs_last_error" in names
+    assert len(names) >= 6
+
+
+def test_library_exports_every_declared_symbol():
+    import mrun_pub_amd._native as nat
+
+    if not nat.LIB_PATH.exists():
+        pytest.skip("library not built (run __graft_entry__.build())")
+    import torch  # noqa: F401  (HIP runtime first, as in production)
+
+    lib = ctypes.CDLL(str(nat.LIB_PATH))
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    # every declared symbol has a ctypes signature in the binding and vice versa
+    assert set(_declared()) == set(nat.SIGNATURES)
+
+
+def test_version_and_error_string_without_gpu():
+    import mrun_pub_amd._native as nat
+
+    if not nat.LIB_PATH.exists():
+        pytest.skip("library not built")
+    lib = nat.load()
+    assert lib.qs_version() >= 100
+    # a validation failure is reported without touching the device
+    st = lib.qs_qrow_matmul(None, 1, 16, None, None, None, 16, 1, 16, 16, None)
+    assert st == nat.QS_ERR_INVALID
+    assert b"null" in lib.qs_last_error()
+    with pytest.raises(ValueError):
+        nat.check(st, "qs_qrow_matmul")

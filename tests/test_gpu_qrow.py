@@ -1,0 +1,148 @@
+"""GPU parity of the int8 qrow kernels against the CPU oracle (through the C ABI)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import qrow as oq
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-3  # rel-L2, bf16 outputs
+F32_TOL = 1e-5  # rel-L2, fp32 outputs
+
+
+def _qrow():
+    from mrun_pub_amd import qrow
+
+    return qrow
+
+
+def _case(n, k, seed=0):
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    scales = (rng.uniform(0.5, 1.5, size=n) / 127).astype(np.float32)
+    return rng, codes, scales
+
+
+def _dev(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+@pytest.mark.parametrize("n,k", [(64, 128), (300, 1024), (17, 48), (5, 7)])
+@pytest.mark.parametrize("dtype", ["fp32", "bf16", "fp16"])
+def test_dequant_bit_exact(dev, n, k, dtype):
+    _, codes, scales = _case(n, k, seed=n + k)
+    tdt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[dtype]
+    got = _qrow().qrow_dequant(_dev(codes, dev), _dev(scales, dev), tdt).float().cpu().numpy()
+    ref = oq.qrow_weight(codes, scales, dtype)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_reference_kat_fp32_exact(dev):
+    # reference tests/test_dense_qstore_cuda.py:72-96 (generic kernel: K=4)
+    codes = np.array([[1, -2, 3, 4], [-1, 2, 0, 3], [4, 1, -3, 2]], dtype=np.int8)
+    scales = np.array([0.5, 0.25, 0.125], dtype=np.float32)
+    x = np.array([[1.0, 2.0, -1.0, 0.5], [0.5, -1.0, 2.0, 3.0]], dtype=np.float32)
+    from mrun_pub_amd.qrow import CompactQRowPage, fused_qrow_matmul
+
+    page = CompactQRowPage("toy", 0, 3, 4, _dev(codes, dev), _dev(scales, dev))
+    y, tag = fused_qrow_matmul(page, _dev(x, dev))
+    assert tag.startswith("hip-gfx950")
+    np.testing.assert_array_equal(y.cpu().numpy(), oq.qrow_matmul_f32(codes, scales, x))
+
+
+@pytest.mark.parametrize("m", [1, 2, 5])
+@pytest.mark.parametrize("n,k", [(4096, 1024), (256, 1536), (33, 80), (7, 13)])
+def test_matmul_fp32(dev, m, n, k):
+    rng, codes, scales = _case(n, k, seed=m * 7 + n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = _qrow().qrow_matmul(_dev(codes, dev), _dev(scales, dev), _dev(x, dev))
+    assert y.dtype == torch.float32 and y.shape == (m, n)
+    err = oq.rel_l2(y.cpu().numpy(), oq.qrow_matmul_f32(codes, scales, x))
+    assert err <= F32_TOL, err
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 32, 37])
+@pytest.mark.parametrize("n,k", [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (100, 192), (24, 40)])
+def test_matmul_bf16_w8a16(dev, m, n, k):
+    rng, codes, scales = _case(n, k, seed=m * 31 + n + k)
+    x = oq.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    y = _qrow().qrow_matmul(_dev(codes, dev), _dev(scales, dev), _dev(x, dev, torch.bfloat16))
+    assert y.dtype == torch.bfloat16 and y.shape == (m, n)
+    err = oq.rel_l2(y.float().cpu().numpy(), oq.qrow_matmul_w8a16(codes, scales, x))
+    assert err <= BF16_TOL, err
+
+
+@pytest.mark.parametrize("m", [1, 16])
+def test_matmul_fp16(dev, m):
+    rng, codes, scales = _case(512, 1024, seed=m)
+    x = oq.round_f16(rng.standard_normal((m, 1024)).astype(np.float32))
+    y = _qrow().qrow_matmul(_dev(codes, dev), _dev(scales, dev), _dev(x, dev, torch.float16))
+    assert y.dtype == torch.float16
+    err = oq.rel_l2(y.float().cpu().numpy(), oq.qrow_matmul_w8a16(codes, scales, x, "fp16"))
+    assert err <= BF16_TOL, err
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_batch_invariance(dev, dtype):
+    """Row m of a batched call is bit-identical to a B=1 call (QStore.matmul_row_stable)."""
+    rng, codes, scales = _case(1536, 1536, seed=11)
+    x = torch.from_numpy(rng.standard_normal((32, 1536)).astype(np.float32)).to(dev).to(dtype)
+    c, s = _dev(codes, dev), _dev(scales, dev)
+    full = _qrow().qrow_matmul(c, s, x)
+    for m in (0, 5, 17, 31):
+        one = _qrow().qrow_matmul(c, s, x[m : m + 1])
+        assert torch.equal(one[0], full[m])
+
+
+def test_multi_linear_equals_individual(dev):
+    rng = np.random.default_rng(12)
+    k = 1536
+    pages = []
+    for n in (1536, 256, 256):
+        c = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+        s = (rng.uniform(0.5, 1.5, size=n) / 127).astype(np.float32)
+        pages.append((_dev(c, dev), _dev(s, dev)))
+    x = torch.from_numpy(rng.standard_normal((4, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    outs = _qrow().qrow_matmul_multi(pages, x)
+    for (c, s), o in zip(pages, outs):
+        assert torch.equal(o, _qrow().qrow_matmul(c, s, x))
+
+
+@pytest.mark.parametrize("m", [1, 4, 32])
+@pytest.mark.parametrize("n,k", [(8960, 1536), (96, 64), (5, 4)])
+def test_swiglu(dev, m, n, k):
+    rng = np.random.default_rng(m + n)
+    gq = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    uq = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    gs = (rng.uniform(0.5, 1.5, size=n) / 127).astype(np.float32)
+    us = (rng.uniform(0.5, 1.5, size=n) / 127).astype(np.float32)
+    x = oq.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    from mrun_pub_amd.qrow import CompactQRowPage, fused_qrow_swiglu
+
+    gp = CompactQRowPage("gate", 0, n, k, _dev(gq, dev), _dev(gs, dev))
+    up = CompactQRowPage("up", 0, n, k, _dev(uq, dev), _dev(us, dev))
+    y, tag = fused_qrow_swiglu(gp, up, _dev(x, dev, torch.bfloat16))
+    assert y.dtype == torch.bfloat16 and tag.startswith("hip-gfx950")
+    err = oq.rel_l2(y.float().cpu().numpy(), oq.qrow_swiglu(gq, gs, uq, us, x))
+    assert err <= BF16_TOL, err
+
+
+def test_errors_are_reference_exceptions(dev):
+    from mrun_pub_amd.qrow import CompactQRowPage, fused_qrow_matmul, fused_qrow_swiglu
+
+    codes = torch.zeros((8, 16), dtype=torch.int8, device=dev)
+    scales = torch.ones(8, dtype=torch.float32, device=dev)
+    page = CompactQRowPage("p", 0, 8, 16, codes, scales)
+    with pytest.raises(ValueError, match="activation width"):
+        fused_qrow_matmul(page, torch.zeros((1, 15), device=dev))
+    with pytest.raises(ValueError, match="one device"):
+        fused_qrow_matmul(page, torch.zeros((1, 16)))
+    with pytest.raises(ValueError, match="block_m"):
+        fused_qrow_matmul(page, torch.zeros((1, 16), device=dev), block_m=8)
+    with pytest.raises(ValueError, match="BF16"):
+        fused_qrow_swiglu(page, page, torch.zeros((1, 16), device=dev))
