@@ -19,8 +19,8 @@
 // MFMA operand mapping (16x16x32, wave64): lane l supplies row (l & 15) of A and
 // column (l & 15) of B, holding 8 consecutive k of the k-block (l >> 4).  The k order
 // inside the block is irrelevant as long as A and B agree, so lane l simply loads the
-// 16 contiguous bytes at k = 64*c + 16*(l>>4) of weight row (l & 15) and the matching
-// 16 activations; elements 0..7 feed one MFMA and 8..15 the next.  The accumulator of
+// 32 contiguous bytes at k = 128*c + 32*(l>>4) of weight row (l & 15) and the matching
+// 32 activations; each 8 of them feed one MFMA (4 per 128-k chunk).  The accumulator of
 // lane l holds D[4*(l>>4) + q][l & 15], q = 0..3.
 #include "qs_common.h"
 
@@ -136,136 +136,135 @@ struct HalfOps<true> {
 
 __device__ __forceinline__ float silu_f32(float g) { return g * (1.0f / (1.0f + expf(-g))); }
 
-// R    : 16-row weight tiles per workgroup (SWIGLU: R == 2, gate and up of one tile)
-// MT   : 16-row activation tiles (M <= 16 * MT)
-// WAVES: waves splitting K; U: chunks (64 k each) in flight per wave
-template <int R, int MT, int WAVES, int U, bool SWIGLU, bool F16>
-__global__ __launch_bounds__(WAVES * 64) void k_w8a16(QrowParams p) {
+// One round of the K loop for one wave.  A chunk is 128 k of 16 weight rows: lane l
+// reads the 32 contiguous bytes at k = 128*c + 32*(l>>4) of row (l & 15) with two
+// back-to-back 128-bit loads, so the wave's two instructions cover whole 128-byte lines
+// of all 16 rows (no line is shared with another wave).  Order of requests: the
+// activations of U chunks (L2-resident, they return first), the U weight chunks
+// (nontemporal HBM loads), then -- on the first round -- the row scale; only then
+// dequantize and feed 4 MFMAs per chunk, so one round costs one memory latency.
+template <int MT, int U, int KW, bool F16>
+__device__ __forceinline__ void w8a16_round(int c0, int C, const int8_t* wrow,
+                                            const float* srow, float& sc, bool first,
+                                            const uint16_t* const (&xrow)[MT],
+                                            const bool (&mval)[MT], f32x4 (&acc)[MT]) {
   typedef HalfOps<F16> H;
   typedef typename H::vec hvec;
+  hvec xa[U][MT][4];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int cc = c0 + u * KW;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        xa[u][t][j] = (cc < C && mval[t])
+                          ? *reinterpret_cast<const hvec*>(xrow[t] + (int64_t)cc * 128 + 8 * j)
+                          : hvec{};
+    }
+  }
+  i32x4 wv[U][2];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int cc = c0 + u * KW;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      wv[u][h] = cc < C ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
+                              wrow + (int64_t)cc * 128 + 16 * h))
+                        : i32x4{0, 0, 0, 0};
+  }
+  if (first) sc = *srow;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (c0 + u * KW < C) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        hvec b0, b1;
+        H::deq(wv[u][h], sc, b0, b1);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acc[t] = H::mma(xa[u][t][2 * h], b0, acc[t]);
+          acc[t] = H::mma(xa[u][t][2 * h + 1], b1, acc[t]);
+        }
+      }
+    }
+  }
+}
+
+// One workgroup = one 16-row weight tile of P planes (P = 1: a plain linear; P = 2: the
+// gate and up projections of one SwiGLU tile).  Its P*KW waves split the work as
+// plane = wave % P, K slice = wave / P; each wave owns chunks ks, ks+KW, ks+2*KW, ...
+// The per-row accumulation order depends only on (K, KW) -- chosen from (N, K), never
+// from M -- so batched rows are bit-identical to B = 1 rows.
+// MT: 16-row activation tiles (M <= 16 * MT).  U: chunks in flight per wave per round.
+template <int P, int MT, int KW, int U, bool F16>
+__global__ __launch_bounds__(P * KW * 64) void k_w8a16(QrowParams p) {
+  typedef HalfOps<F16> H;
+  constexpr int WAVES = P * KW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int plane = wave % P;
+  const int ks = wave / P;
   const int col = lane & 15;
   const int grp = lane >> 4;
 
   int li = 0;
-  if (!SWIGLU) {
+  if (P == 1) {
 #pragma unroll
     for (int j = 1; j < 4; ++j)
       if (j < p.n_lin && (int)blockIdx.x >= p.lin[j].tile_begin) li = j;
   }
   const int tile = (int)blockIdx.x - p.lin[li].tile_begin;
+  const QrowLin& L = p.lin[P == 2 ? plane : li];
   const int N = p.lin[li].N;
   const int K = p.K;
   const int M = p.M;
-  const int n0 = tile * 16 * (SWIGLU ? 1 : R);
+  const int n0 = tile * 16;
+  int n = n0 + col;
+  n = n < N ? n : N - 1;  // clamp: the lane's outputs are not stored
+  const int8_t* wrow = L.codes + (int64_t)n * K + 32 * grp;
+  const float* srow = L.scales + n;
 
-  const int8_t* wrow[R];
-  float sc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const QrowLin& L = SWIGLU ? p.lin[r] : p.lin[li];
-    int n = SWIGLU ? n0 + col : n0 + 16 * r + col;
-    n = n < N ? n : N - 1;  // clamp: the lane's outputs are not stored
-    wrow[r] = L.codes + (int64_t)n * K + 16 * grp;
-    sc[r] = L.scales[n];
-  }
   const uint16_t* xrow[MT];
   bool mval[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
     const int m = 16 * t + col;
     mval[t] = m < M;
-    xrow[t] = static_cast<const uint16_t*>(p.x) + (int64_t)(mval[t] ? m : 0) * p.ldx + 16 * grp;
+    xrow[t] = static_cast<const uint16_t*>(p.x) + (int64_t)(mval[t] ? m : 0) * p.ldx + 32 * grp;
   }
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  f32x4 acc[R][MT];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int C = K / 128;
+  float sc = 0.f;
+  // first round peeled so that the scale load trails the first weight loads
+  w8a16_round<MT, U, KW, F16>(ks, C, wrow, srow, sc, true, xrow, mval, acc);
+  for (int c0 = ks + U * KW; c0 < C; c0 += U * KW)
+    w8a16_round<MT, U, KW, F16>(c0, C, wrow, srow, sc, false, xrow, mval, acc);
 
-  const int C = K / 64;
-  int c = wave;
-  // main loop: U chunks per wave in flight
-  for (; c + (U - 1) * WAVES < C; c += U * WAVES) {
-    i32x4 wv[U][R];
-    hvec xv[U][MT][2];
+  // cross-wave reduction: per plane, K slices summed in fixed order
+  __shared__ f32x4 red[WAVES][MT][64];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t off = (int64_t)(c + u * WAVES) * 64;
+  for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 out[P][MT];
 #pragma unroll
-      for (int r = 0; r < R; ++r) wv[u][r] = *reinterpret_cast<const i32x4*>(wrow[r] + off);
+  for (int pl = 0; pl < P; ++pl)
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        if (mval[t]) {
-          xv[u][t][0] = *reinterpret_cast<const hvec*>(xrow[t] + off);
-          xv[u][t][1] = *reinterpret_cast<const hvec*>(xrow[t] + off + 8);
-        } else {
-          xv[u][t][0] = hvec{};
-          xv[u][t][1] = hvec{};
-        }
-      }
+    for (int t = 0; t < MT; ++t) {
+      f32x4 s = red[pl][t][lane];
+#pragma unroll
+      for (int k2 = 1; k2 < KW; ++k2) s += red[k2 * P + pl][t][lane];
+      out[pl][t] = s;
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        hvec b0, b1;
-        H::deq(wv[u][r], sc[r], b0, b1);
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          acc[r][t] = H::mma(xv[u][t][0], b0, acc[r][t]);
-          acc[r][t] = H::mma(xv[u][t][1], b1, acc[r][t]);
-        }
-      }
-    }
-  }
-  // remainder chunks, one at a time
-  for (; c < C; c += WAVES) {
-    const int64_t off = (int64_t)c * 64;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const i32x4 w = *reinterpret_cast<const i32x4*>(wrow[r] + off);
-      hvec b0, b1;
-      H::deq(w, sc[r], b0, b1);
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        hvec a0{}, a1{};
-        if (mval[t]) {
-          a0 = *reinterpret_cast<const hvec*>(xrow[t] + off);
-          a1 = *reinterpret_cast<const hvec*>(xrow[t] + off + 8);
-        }
-        acc[r][t] = H::mma(a0, b0, acc[r][t]);
-        acc[r][t] = H::mma(a1, b1, acc[r][t]);
-      }
-    }
-  }
 
-  // cross-wave reduction in fixed wave order
-  if (WAVES > 1) {
-    __shared__ f32x4 red[WAVES][R * MT][64];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int t = 0; t < MT; ++t) red[wave][r * MT + t][lane] = acc[r][t];
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        f32x4 s = red[0][r * MT + t][lane];
-#pragma unroll
-        for (int w = 1; w < WAVES; ++w) s += red[w][r * MT + t][lane];
-        acc[r][t] = s;
-      }
-  }
-
-  // store: lane holds D[m = 16t + 4*grp + q][n = col]
-  if (SWIGLU) {
-    const int n = n0 + col;
-    if (n >= N) return;
+  // store: lane holds D[m = 16t + 4*grp + q][n = n0 + col]
+  const int no = n0 + col;
+  if (no >= N) return;
+  if (P == 2) {
     uint16_t* y = static_cast<uint16_t*>(p.lin[0].y);
 #pragma unroll
     for (int t = 0; t < MT; ++t)
@@ -273,28 +272,22 @@ __global__ __launch_bounds__(WAVES * 64) void k_w8a16(QrowParams p) {
       for (int q = 0; q < 4; ++q) {
         const int m = 16 * t + 4 * grp + q;
         if (m < M) {
-          const float gt = bf16_bits_to_f32(f32_to_bf16_bits(acc[0][t][q]));
-          const float ut = bf16_bits_to_f32(f32_to_bf16_bits(acc[1][t][q]));
+          const float gt = bf16_bits_to_f32(f32_to_bf16_bits(out[0][t][q]));
+          const float ut = bf16_bits_to_f32(f32_to_bf16_bits(out[P - 1][t][q]));
           const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f32(gt)));
-          y[(int64_t)m * p.lin[0].ldy + n] = f32_to_bf16_bits(sl * ut);
+          y[(int64_t)m * p.lin[0].ldy + no] = f32_to_bf16_bits(sl * ut);
         }
       }
   } else {
     uint16_t* y = static_cast<uint16_t*>(p.lin[li].y);
     const int64_t ldy = p.lin[li].ldy;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int n = n0 + 16 * r + col;
-      if (n < N) {
+    for (int t = 0; t < MT; ++t)
 #pragma unroll
-        for (int t = 0; t < MT; ++t)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int m = 16 * t + 4 * grp + q;
-            if (m < M) y[(int64_t)m * ldy + n] = H::out(acc[r][t][q]);
-          }
+      for (int q = 0; q < 4; ++q) {
+        const int m = 16 * t + 4 * grp + q;
+        if (m < M) y[(int64_t)m * ldy + no] = H::out(out[0][t][q]);
       }
-    }
   }
 }
 
@@ -446,18 +439,48 @@ __global__ __launch_bounds__(256) void k_generic_swiglu(QrowParams p) {
 // ----------------------------------------------------------------------------------
 namespace {
 
-constexpr int kMfmaWaves = 4;
+// K-split (waves per plane) chosen from (N, K) only -- never from M -- so the
+// accumulation order of a row does not depend on the batch.  Aim for ~16 waves per CU
+// over 256 CUs and at most 8 chunks per wave per round.
+int pick_kw(int64_t N, int64_t K) {
+  const int64_t tiles = cdiv(N, 16);
+  const int64_t chunks = K / 128;
+  int w = 4;
+  while (w < 16 && (tiles * w < 4096 || chunks > (int64_t)w * 4)) w *= 2;
+  return w;
+}
 
-template <int R, int MT, bool SWIGLU, bool F16>
-void launch_w8a16(const QrowParams& p, int blocks, hipStream_t s) {
-  constexpr int U = (MT == 1) ? 4 : 2;
-  hipLaunchKernelGGL((k_w8a16<R, MT, kMfmaWaves, U, SWIGLU, F16>), dim3(blocks),
-                     dim3(kMfmaWaves * 64), 0, s, p);
+template <int P, int MT, int KW, bool F16>
+void launch_w8a16_kw(const QrowParams& p, int blocks, hipStream_t s) {
+  const int u = (int)cdiv(p.K / 128, KW);
+  // two activation tiles double the live activation registers: keep U at 2
+  if constexpr (MT == 2) {
+    hipLaunchKernelGGL((k_w8a16<P, MT, KW, 2, F16>), dim3(blocks), dim3(P * KW * 64), 0, s, p);
+  } else {
+    if (u <= 2)
+      hipLaunchKernelGGL((k_w8a16<P, MT, KW, 2, F16>), dim3(blocks), dim3(P * KW * 64), 0, s, p);
+    else
+      hipLaunchKernelGGL((k_w8a16<P, MT, KW, 4, F16>), dim3(blocks), dim3(P * KW * 64), 0, s, p);
+  }
+}
+
+template <int P, int MT, bool F16>
+void launch_w8a16(const QrowParams& p, int blocks, int kw, hipStream_t s) {
+  if (kw == 4) {
+    launch_w8a16_kw<P, MT, 4, F16>(p, blocks, s);
+  } else if (kw == 8) {
+    launch_w8a16_kw<P, MT, 8, F16>(p, blocks, s);
+  } else {
+    if constexpr (P == 1)
+      launch_w8a16_kw<P, MT, 16, F16>(p, blocks, s);
+    else
+      launch_w8a16_kw<P, MT, 8, F16>(p, blocks, s);  // 2 planes x 8 = 1024 threads
+  }
 }
 
 bool mfma_eligible(const QrowParams& p, int x_dtype) {
   if (x_dtype != QS_BF16 && x_dtype != QS_F16) return false;
-  if (p.K % 64 != 0 || p.ldx % 8 != 0 || !aligned(p.x, 16)) return false;
+  if (p.K % 128 != 0 || p.ldx % 8 != 0 || !aligned(p.x, 16)) return false;
   for (int i = 0; i < p.n_lin; ++i)
     if (!aligned(p.lin[i].codes, 16)) return false;
   return true;
@@ -484,20 +507,20 @@ int run_linears(QrowParams p, int x_dtype, int64_t M, hipStream_t s) {
       const int mm = (int)((M - m0) < 32 ? (M - m0) : 32);
       q.M = mm;
       q.x = static_cast<const char*>(p.x) + m0 * p.ldx * esz;
-      const int R = mm <= 4 ? 1 : 2;
       int blocks = 0;
+      int64_t nmax = 0;
       for (int i = 0; i < q.n_lin; ++i) {
         q.lin[i].y = static_cast<char*>(p.lin[i].y) + m0 * p.lin[i].ldy * 2;
         q.lin[i].tile_begin = blocks;
-        blocks += (int)cdiv(q.lin[i].N, 16 * R);
+        blocks += (int)cdiv(q.lin[i].N, 16);
+        nmax = q.lin[i].N > nmax ? q.lin[i].N : nmax;
       }
+      const int kw = pick_kw(nmax, q.K);
       const bool f16 = x_dtype == QS_F16;
-      if (mm <= 16) {
-        if (R == 1) f16 ? launch_w8a16<1, 1, false, true>(q, blocks, s) : launch_w8a16<1, 1, false, false>(q, blocks, s);
-        else f16 ? launch_w8a16<2, 1, false, true>(q, blocks, s) : launch_w8a16<2, 1, false, false>(q, blocks, s);
-      } else {
-        f16 ? launch_w8a16<2, 2, false, true>(q, blocks, s) : launch_w8a16<2, 2, false, false>(q, blocks, s);
-      }
+      if (mm <= 16)
+        f16 ? launch_w8a16<1, 1, true>(q, blocks, kw, s) : launch_w8a16<1, 1, false>(q, blocks, kw, s);
+      else
+        f16 ? launch_w8a16<1, 2, true>(q, blocks, kw, s) : launch_w8a16<1, 2, false>(q, blocks, kw, s);
     }
     return hip_check(hipGetLastError(), "k_w8a16 launch");
   }
@@ -627,10 +650,11 @@ extern "C" int qs_qrow_swiglu(const void* x, int64_t ldx, const int8_t* gate_cod
       q.x = static_cast<const uint16_t*>(x) + m0 * ldx;
       q.lin[0].y = static_cast<uint16_t*>(y) + m0 * ldy;
       const int blocks = (int)cdiv(N, 16);
+      const int kw = pick_kw(N, K);
       if (mm <= 16)
-        launch_w8a16<2, 1, true, false>(q, blocks, s);
+        launch_w8a16<2, 1, false>(q, blocks, kw, s);
       else
-        launch_w8a16<2, 2, true, false>(q, blocks, s);
+        launch_w8a16<2, 2, false>(q, blocks, kw, s);
     }
     return hip_check(hipGetLastError(), "k_w8a16 swiglu launch");
   }
