@@ -55,11 +55,18 @@ int qs_qrow_dequant(const int8_t* codes, const float* scales, void* out, int out
  *   x_dtype F32 : W in fp32, fp32 accumulate, y F32 (QStore fp32 compute contract).
  *   x_dtype BF16: W rounded to bf16 per element, fp32 accumulate, y BF16 (W8A16).
  *   x_dtype F16 : W rounded to fp16 per element, fp32 accumulate, y F16.
- * Every output row is computed with the same reduction order whatever M is, so the
- * result is batch invariant (QStore.matmul_row_stable, qstore.py:49-76, 1094-1097). */
+ * M <= 2 (decode) and fp32 use a VALU kernel, larger M an MFMA kernel; results agree
+ * within the fp32-accumulation tolerance but are not bitwise batch invariant. */
 int qs_qrow_matmul(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
                    const float* scales, void* y, int64_t ldy, int64_t M, int64_t N,
                    int64_t K, void* stream);
+
+/* Replaces QStore.matmul_row_stable / _row_stable_loaded_matmul (qstore.py:49-76,
+ * 1094-1097): same contract as qs_qrow_matmul, and every output row is reduced in one
+ * fixed order whatever M is, so row b equals the M = 1 result for x[b] bit for bit. */
+int qs_qrow_matmul_row_stable(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
+                              const float* scales, void* y, int64_t ldy, int64_t M, int64_t N,
+                              int64_t K, void* stream);
 
 /* Several qrow linears sharing one activation x (e.g. q/k/v projections,
  * src/mrun/engine/kernels/paged_forward.py:481-490) in one launch; same contract as

@@ -11,9 +11,12 @@
 //                                 multiply-add, so the VALU only pays for the dequant
 //                                 (cvt_sdwa + mul + half a cvt_pk per weight byte).
 //                                 K is split across the waves of a workgroup and reduced
-//                                 through LDS in a fixed order.
-//   k_f32_gemv<...>             : fp32 activations (QStore fp32 compute contract): VALU
-//                                 dequant + fma, fixed-order wave butterfly reduction.
+//                                 through LDS in a fixed order.  Used for 3 <= M.
+//   k_gemv_valu<...>            : M <= 2 decode rows (any activation dtype) and every
+//                                 fp32-activation call: one wave per weight row(s), 1 KiB
+//                                 contiguous row segments per instruction, activations in
+//                                 LDS, VALU dequant + fma / v_dot2, fixed-order wave
+//                                 butterfly.  Also the row-stable (batch invariant) lane.
 //   k_generic                   : any shape / alignment, one wave per output row.
 //
 // MFMA operand mapping (16x16x32, wave64): lane l supplies row (l & 15) of A and
@@ -292,72 +295,139 @@ __global__ __launch_bounds__(P * KW * 64) void k_w8a16(QrowParams p) {
 }
 
 // ----------------------------------------------------------------------------------
-// fp32-activation GEMV (VALU)
+// VALU GEMV for small M (and every fp32-activation call)
 // ----------------------------------------------------------------------------------
-// Each wave owns R consecutive output rows over the whole K; lane l handles the 16-byte
-// chunks l, l+64, ... of every row.  M rows of x are processed MB at a time.
-template <int R, int MB, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void k_f32_gemv(QrowParams p) {
+// One wave per weight row: lane l reads the 16 contiguous codes at k = 1024*c + 16*l
+// (one wave instruction = one 1 KiB contiguous row segment) and the whole row is in
+// flight at once.  The M <= MB activation rows are staged in LDS per workgroup while
+// the codes are in flight.
+//   fp32 x : w = float(code)*scale, fma per element        (QStore fp32 contract)
+//   bf16 x : w = bf16(float(code)*scale), v_dot2_f32_bf16   (W8A16 contract)
+//   fp16 x : w = fp16(float(code)*scale), v_dot2_f32_f16
+// Each row's sum is lane-local in chunk/element order, then a fixed butterfly across
+// the wave: the result of a row never depends on M or on the other rows.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <int XT>
+struct XElem {
+  static constexpr int size = XT == QS_F32 ? 4 : 2;
+};
+
+// tile_begin of linear i holds its first global row (one wave per row).
+template <int XT, int MB, int U>
+__global__ __launch_bounds__(256) void k_gemv_valu(QrowParams p, int rows) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+  constexpr int ES = XElem<XT>::size;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int r = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int K = p.K;
+  const int M = p.M;  // <= MB
+  const bool live = r < rows;
+  const int rr = live ? r : rows - 1;
   int li = 0;
 #pragma unroll
   for (int j = 1; j < 4; ++j)
-    if (j < p.n_lin && (int)blockIdx.x >= p.lin[j].tile_begin) li = j;
+    if (j < p.n_lin && rr >= p.lin[j].tile_begin) li = j;
   const QrowLin& L = p.lin[li];
-  const int N = L.N;
-  const int K = p.K;
-  const int nb = (((int)blockIdx.x - L.tile_begin) * WAVES + wave) * R;
-  if (nb >= N) return;
-  const float* x = static_cast<const float*>(p.x);
-  float* y = static_cast<float*>(L.y);
+  const int n = rr - L.tile_begin;
+  const int8_t* wrow = L.codes + (int64_t)n * K + 16 * lane;
 
-  const int8_t* wrow[R];
-  float sc[R];
+  // 1) the row's codes (all of K in flight at once), 2) its scale
+  i32x4 wv[U];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int n = nb + r < N ? nb + r : N - 1;
-    wrow[r] = L.codes + (int64_t)n * K;
-    sc[r] = L.scales[n];
+  for (int u = 0; u < U; ++u)
+    wv[u] = (u * 1024 + 16 * lane < K)
+                ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wrow + u * 1024))
+                : i32x4{0, 0, 0, 0};
+  const float sc = L.scales[n];
+  // 3) stage the activations (M rows x K) in LDS while the codes are in flight
+  const int row16 = K * ES / 16;
+  for (int i = threadIdx.x; i < M * row16; i += 256) {
+    const int m = i / row16;
+    const int c = i - m * row16;
+    reinterpret_cast<i32x4*>(xs)[i] = *reinterpret_cast<const i32x4*>(
+        static_cast<const uint8_t*>(p.x) + ((int64_t)m * p.ldx * ES + (int64_t)c * 16));
   }
-  const int C = K / 16;
-  for (int m0 = 0; m0 < p.M; m0 += MB) {
-    float acc[MB][R];
+  __syncthreads();
+  if (!live) return;
+
+  float acc[MB];
 #pragma unroll
-    for (int i = 0; i < MB; ++i)
+  for (int m = 0; m < MB; ++m) acc[m] = 0.f;
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[i][r] = 0.f;
-    for (int c = lane; c < C; c += 64) {
-      i32x4 wv[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) wv[r] = *reinterpret_cast<const i32x4*>(wrow[r] + c * 16);
-      f32x4 xv[MB][4];
-#pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        const int m = m0 + i < p.M ? m0 + i : p.M - 1;
-        const f32x4* xp = reinterpret_cast<const f32x4*>(x + (int64_t)m * p.ldx + c * 16);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) xv[i][j] = xp[j];
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
+  for (int u = 0; u < U; ++u) {
+    const int k = u * 1024 + 16 * lane;
+    if (k < K) {
+      if constexpr (XT == QS_F32) {
+        float w[16];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const float w = byte_f32(wv[r][j], b) * sc[r];
+          for (int e = 0; e < 4; ++e) w[4 * j + e] = byte_f32(wv[u][j], e) * sc;
 #pragma unroll
-            for (int i = 0; i < MB; ++i) acc[i][r] = fmaf(xv[i][j][b], w, acc[i][r]);
+        for (int m = 0; m < MB; ++m) {
+          if (m < M) {
+            const f32x4* xp = reinterpret_cast<const f32x4*>(xs + ((int64_t)m * K + k) * ES);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const f32x4 xv = xp[j];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[m] = fmaf(xv[e], w[4 * j + e], acc[m]);
+            }
           }
+        }
+      } else if constexpr (XT == QS_BF16) {
+        bf16x8 w0, w1;
+        deq16_bf16(wv[u], sc, w0, w1);
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+          if (m < M) {
+            const bf16x8* xp = reinterpret_cast<const bf16x8*>(xs + ((int64_t)m * K + k) * ES);
+            const bf16x8 x0 = xp[0], x1 = xp[1];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[m] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w0[2 * j], w0[2 * j + 1]},
+                                                       bf16x2{x0[2 * j], x0[2 * j + 1]}, acc[m], false);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[m] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w1[2 * j], w1[2 * j + 1]},
+                                                       bf16x2{x1[2 * j], x1[2 * j + 1]}, acc[m], false);
+          }
+        }
+      } else {
+        f16x8 w0, w1;
+        deq16_f16(wv[u], sc, w0, w1);
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+          if (m < M) {
+            const f16x8* xp = reinterpret_cast<const f16x8*>(xs + ((int64_t)m * K + k) * ES);
+            const f16x8 x0 = xp[0], x1 = xp[1];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[m] = __builtin_amdgcn_fdot2(f16x2{w0[2 * j], w0[2 * j + 1]},
+                                              f16x2{x0[2 * j], x0[2 * j + 1]}, acc[m], false);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[m] = __builtin_amdgcn_fdot2(f16x2{w1[2 * j], w1[2 * j + 1]},
+                                              f16x2{x1[2 * j], x1[2 * j + 1]}, acc[m], false);
+          }
+        }
       }
     }
+  }
 #pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float s = wave_sum(acc[i][r]);
-        if (lane == 0 && m0 + i < p.M && nb + r < N) y[(int64_t)(m0 + i) * L.ldy + nb + r] = s;
-      }
+  for (int m = 0; m < MB; ++m) {
+    const float v = wave_sum(acc[m]);
+    if (lane == 0 && m < M) {
+      const int64_t yi = (int64_t)m * L.ldy + n;
+      if constexpr (XT == QS_F32)
+        static_cast<float*>(L.y)[yi] = v;
+      else if constexpr (XT == QS_BF16)
+        static_cast<uint16_t*>(L.y)[yi] = f32_to_bf16_bits(v);
+      else
+        static_cast<uint16_t*>(L.y)[yi] = f32_to_f16_bits(v);
+    }
   }
 }
 
@@ -497,11 +567,80 @@ int validate_common(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
   return QS_OK;
 }
 
+constexpr int kLdsBudget = 64 * 1024;
+
+// Activation rows per VALU launch: the largest of 4/2/1 whose LDS copy fits.
+int valu_mb(int x_dtype, int64_t K, int64_t M) {
+  const int es = x_dtype == QS_F32 ? 4 : 2;
+  const int cap = x_dtype == QS_F32 ? 4 : 2;
+  for (int mb = cap; mb >= 1; mb /= 2)
+    if ((int64_t)mb * K * es <= kLdsBudget && (mb <= M || mb == 1)) return mb;
+  return 0;
+}
+
+bool valu_eligible(const QrowParams& p, int x_dtype) {
+  const int es = x_dtype == QS_F32 ? 4 : 2;
+  if (p.K % 16 != 0 || (p.ldx * es) % 16 != 0 || !aligned(p.x, 16)) return false;
+  if ((int64_t)p.K * es > kLdsBudget || p.K > 12 * 1024) return false;
+  for (int i = 0; i < p.n_lin; ++i)
+    if (!aligned(p.lin[i].codes, 16)) return false;
+  return true;
+}
+
+template <int XT, int MB>
+void launch_valu_mb(const QrowParams& q, int rows, int blocks, size_t lds, hipStream_t s) {
+  const int chunks = (q.K + 1023) / 1024;
+  if (chunks <= 2)
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 2>), dim3(blocks), dim3(256), lds, s, q, rows);
+  else if (chunks <= 4)
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 4>), dim3(blocks), dim3(256), lds, s, q, rows);
+  else if (chunks <= 8)
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 8>), dim3(blocks), dim3(256), lds, s, q, rows);
+  else
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 12>), dim3(blocks), dim3(256), lds, s, q, rows);
+}
+
+// VALU path: rows of x in batches of MB (each batch one launch).  Every row is reduced
+// in the same order whatever M is.
+int run_valu(QrowParams p, int x_dtype, int64_t M, hipStream_t s) {
+  const int es = x_dtype == QS_F32 ? 4 : 2;
+  const int mb = valu_mb(x_dtype, p.K, M);
+  int rows = 0;
+  for (int i = 0; i < p.n_lin; ++i) {
+    p.lin[i].tile_begin = rows;
+    rows += p.lin[i].N;
+  }
+  const int blocks = (rows + 3) / 4;
+  for (int64_t m0 = 0; m0 < M; m0 += mb) {
+    QrowParams q = p;
+    q.M = (int)((M - m0) < mb ? (M - m0) : mb);
+    q.x = static_cast<const char*>(p.x) + m0 * p.ldx * es;
+    for (int i = 0; i < q.n_lin; ++i)
+      q.lin[i].y = static_cast<char*>(p.lin[i].y) + m0 * p.lin[i].ldy * es;
+    const size_t lds = (size_t)q.M * q.K * es;
+    if (x_dtype == QS_F32) {
+      if (mb == 4) launch_valu_mb<QS_F32, 4>(q, rows, blocks, lds, s);
+      else if (mb == 2) launch_valu_mb<QS_F32, 2>(q, rows, blocks, lds, s);
+      else launch_valu_mb<QS_F32, 1>(q, rows, blocks, lds, s);
+    } else if (x_dtype == QS_BF16) {
+      if (mb == 2) launch_valu_mb<QS_BF16, 2>(q, rows, blocks, lds, s);
+      else launch_valu_mb<QS_BF16, 1>(q, rows, blocks, lds, s);
+    } else {
+      if (mb == 2) launch_valu_mb<QS_F16, 2>(q, rows, blocks, lds, s);
+      else launch_valu_mb<QS_F16, 1>(q, rows, blocks, lds, s);
+    }
+  }
+  return hip_check(hipGetLastError(), "k_gemv_valu launch");
+}
+
 // Runs one set of linears sharing x, M <= 32 rows at a time for the MFMA path.
-int run_linears(QrowParams p, int x_dtype, int64_t M, hipStream_t s) {
+int run_linears(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool row_stable) {
   if (M == 0) return QS_OK;
   const int esz = x_dtype == QS_F32 ? 4 : 2;
-  if (mfma_eligible(p, x_dtype)) {
+  // decode-sized batches (and the row-stable contract) take the VALU path
+  if ((row_stable || M <= 2 || x_dtype == QS_F32) && valu_eligible(p, x_dtype))
+    return run_valu(p, x_dtype, M, s);
+  if (!row_stable && mfma_eligible(p, x_dtype)) {
     for (int64_t m0 = 0; m0 < M; m0 += 32) {
       QrowParams q = p;
       const int mm = (int)((M - m0) < 32 ? (M - m0) : 32);
@@ -524,22 +663,7 @@ int run_linears(QrowParams p, int x_dtype, int64_t M, hipStream_t s) {
     }
     return hip_check(hipGetLastError(), "k_w8a16 launch");
   }
-  bool f32_fast = x_dtype == QS_F32 && p.K % 16 == 0 && p.ldx % 4 == 0 && aligned(p.x, 16);
-  for (int i = 0; i < p.n_lin; ++i) f32_fast = f32_fast && aligned(p.lin[i].codes, 16);
-  if (f32_fast) {
-    constexpr int R = 4, WAVES = 4;
-    int blocks = 0;
-    for (int i = 0; i < p.n_lin; ++i) {
-      p.lin[i].tile_begin = blocks;
-      blocks += (int)cdiv(p.lin[i].N, R * WAVES);
-    }
-    p.M = (int)M;
-    if (M == 1)
-      hipLaunchKernelGGL((k_f32_gemv<R, 1, WAVES>), dim3(blocks), dim3(WAVES * 64), 0, s, p);
-    else
-      hipLaunchKernelGGL((k_f32_gemv<R, 4, WAVES>), dim3(blocks), dim3(WAVES * 64), 0, s, p);
-    return hip_check(hipGetLastError(), "k_f32_gemv launch");
-  }
+  if (valu_eligible(p, x_dtype)) return run_valu(p, x_dtype, M, s);
   int waves = 0;
   for (int i = 0; i < p.n_lin; ++i) {
     p.lin[i].tile_begin = waves;
@@ -598,7 +722,26 @@ extern "C" int qs_qrow_matmul(const void* x, int x_dtype, int64_t ldx, const int
   p.K = (int)K;
   p.n_lin = 1;
   p.lin[0] = QrowLin{codes, scales, y, ldy, (int)N, 0};
-  return run_linears(p, x_dtype, M, static_cast<hipStream_t>(stream));
+  return run_linears(p, x_dtype, M, static_cast<hipStream_t>(stream), false);
+}
+
+extern "C" int qs_qrow_matmul_row_stable(const void* x, int x_dtype, int64_t ldx,
+                                         const int8_t* codes, const float* scales, void* y,
+                                         int64_t ldy, int64_t M, int64_t N, int64_t K,
+                                         void* stream) {
+  int st = validate_common(x, x_dtype, ldx, M, K);
+  if (st) return st;
+  if (!codes || !scales || !y) return fail(QS_ERR_INVALID, "matmul_row_stable: null pointer");
+  if (N <= 0 || N > (int64_t)1 << 30) return fail(QS_ERR_INVALID, "matmul_row_stable: bad N");
+  if (ldy < N) return fail(QS_ERR_INVALID, "matmul_row_stable: ldy < N");
+  QrowParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.M = (int)M;
+  p.K = (int)K;
+  p.n_lin = 1;
+  p.lin[0] = QrowLin{codes, scales, y, ldy, (int)N, 0};
+  return run_linears(p, x_dtype, M, static_cast<hipStream_t>(stream), true);
 }
 
 extern "C" int qs_qrow_matmul_multi(const void* x, int x_dtype, int64_t ldx, int n_linear,
@@ -621,7 +764,7 @@ extern "C" int qs_qrow_matmul_multi(const void* x, int x_dtype, int64_t ldx, int
       return fail(QS_ERR_INVALID, "matmul_multi: bad N/ldy for linear %d", i);
     p.lin[i] = QrowLin{codes[i], scales[i], y[i], ldy[i], (int)N[i], 0};
   }
-  return run_linears(p, x_dtype, M, static_cast<hipStream_t>(stream));
+  return run_linears(p, x_dtype, M, static_cast<hipStream_t>(stream), false);
 }
 
 extern "C" int qs_qrow_swiglu(const void* x, int64_t ldx, const int8_t* gate_codes,

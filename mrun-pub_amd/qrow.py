@@ -97,12 +97,16 @@ def qrow_dequant(
 
 
 @torch.inference_mode()
-def qrow_matmul(codes: torch.Tensor, scales: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+def qrow_matmul(
+    codes: torch.Tensor, scales: torch.Tensor, x: torch.Tensor, *, row_stable: bool = False
+) -> torch.Tensor:
     """``x[..., K] @ W^T`` with the dtype contract of ``qs_qrow_matmul``.
 
     fp32 activations: fp32 weights and output (QStore compute contract, qstore.py:1082-1092).
     bf16 / fp16 activations: weights rounded per element to the activation dtype, fp32
     accumulation, output in the activation dtype (W8A16, dense_qstore_cuda.py:467-512).
+    ``row_stable=True`` selects the batch-invariant lane (``matmul_row_stable``,
+    qstore.py:49-76): every row equals its own ``M = 1`` result bit for bit.
     """
     n, k = _check_codes(codes, scales)
     if x.dtype not in _ACT_DTYPES:
@@ -117,7 +121,7 @@ def qrow_matmul(codes: torch.Tensor, scales: torch.Tensor, x: torch.Tensor) -> t
     y = torch.empty((m, n), dtype=x.dtype, device=device)
     if m:
         nat.call(
-            "qs_qrow_matmul",
+            "qs_qrow_matmul_row_stable" if row_stable else "qs_qrow_matmul",
             nat.ptr(flat),
             nat.dtype_code(x.dtype),
             k,

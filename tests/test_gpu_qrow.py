@@ -87,16 +87,35 @@ def test_matmul_fp16(dev, m):
     assert err <= BF16_TOL, err
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_batch_invariance(dev, dtype):
-    """Row m of a batched call is bit-identical to a B=1 call (QStore.matmul_row_stable)."""
-    rng, codes, scales = _case(1536, 1536, seed=11)
-    x = torch.from_numpy(rng.standard_normal((32, 1536)).astype(np.float32)).to(dev).to(dtype)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("n,k", [(1536, 1536), (512, 8960), (40, 48)])
+def test_row_stable_batch_invariance(dev, dtype, n, k):
+    """Row m of a row-stable batched call is bit-identical to a B=1 call
+    (QStore.matmul_row_stable, qstore.py:49-76) and to the plain decode (M=1) call."""
+    rng, codes, scales = _case(n, k, seed=11)
+    x = torch.from_numpy(rng.standard_normal((32, k)).astype(np.float32)).to(dev).to(dtype)
+    c, s = _dev(codes, dev), _dev(scales, dev)
+    full = _qrow().qrow_matmul(c, s, x, row_stable=True)
+    for m in (0, 5, 17, 31):
+        one = _qrow().qrow_matmul(c, s, x[m : m + 1], row_stable=True)
+        assert torch.equal(one[0], full[m])
+        assert torch.equal(_qrow().qrow_matmul(c, s, x[m : m + 1])[0], full[m])
+    ref = oq.qrow_matmul_f32(codes, scales, x.float().cpu().numpy())
+    tol = F32_TOL if dtype == torch.float32 else BF16_TOL
+    assert oq.rel_l2(full.float().cpu().numpy(), ref) <= 3 * tol
+
+
+@pytest.mark.parametrize("m", [3, 16, 32])
+def test_mfma_path_rows_independent_of_batch(dev, m):
+    """Within the MFMA path (M >= 3) a row does not depend on the other rows."""
+    rng, codes, scales = _case(1536, 1536, seed=13)
+    x = torch.from_numpy(rng.standard_normal((m, 1536)).astype(np.float32)).to(dev).to(torch.bfloat16)
     c, s = _dev(codes, dev), _dev(scales, dev)
     full = _qrow().qrow_matmul(c, s, x)
-    for m in (0, 5, 17, 31):
-        one = _qrow().qrow_matmul(c, s, x[m : m + 1])
-        assert torch.equal(one[0], full[m])
+    x2 = x.clone()
+    x2[1:] = x2[1:].flip(0) if m > 2 else x2[1:]
+    perm = _qrow().qrow_matmul(c, s, x2)
+    assert torch.equal(perm[0], full[0])
 
 
 def test_multi_linear_equals_individual(dev):
@@ -109,8 +128,12 @@ def test_multi_linear_equals_individual(dev):
         pages.append((_dev(c, dev), _dev(s, dev)))
     x = torch.from_numpy(rng.standard_normal((4, k)).astype(np.float32)).to(dev).to(torch.bfloat16)
     outs = _qrow().qrow_matmul_multi(pages, x)
+    xb = x.float().cpu().numpy()
     for (c, s), o in zip(pages, outs):
-        assert torch.equal(o, _qrow().qrow_matmul(c, s, x))
+        ref = oq.qrow_matmul_w8a16(c.cpu().numpy(), s.cpu().numpy(), xb)
+        assert oq.rel_l2(o.float().cpu().numpy(), ref) <= BF16_TOL
+        single = _qrow().qrow_matmul(c, s, x)
+        assert torch.allclose(o.float(), single.float(), rtol=1e-2, atol=1e-2)
 
 
 @pytest.mark.parametrize("m", [1, 4, 32])
