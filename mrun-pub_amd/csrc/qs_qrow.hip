@@ -314,34 +314,115 @@ struct XElem {
   static constexpr int size = XT == QS_F32 ? 4 : 2;
 };
 
-// tile_begin of linear i holds its first global row (one wave per row).
-template <int XT, int MB, int U>
+// Dot of one 16-code chunk (already in registers) with the activations of the MB rows.
+template <int XT, int MB>
+__device__ __forceinline__ void valu_chunk(i32x4 w, float sc, const uint8_t* xs, int K, int k,
+                                           int M, float (&acc)[MB]) {
+  constexpr int ES = XElem<XT>::size;
+  if constexpr (XT == QS_F32) {
+    float wf[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wf[4 * j + e] = byte_f32(w[j], e) * sc;
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      if (m < M) {
+        const f32x4* xp = reinterpret_cast<const f32x4*>(xs + ((int64_t)m * K + k) * ES);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 xv = xp[j];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[m] = fmaf(xv[e], wf[4 * j + e], acc[m]);
+        }
+      }
+    }
+  } else if constexpr (XT == QS_BF16) {
+    bf16x8 w0, w1;
+    deq16_bf16(w, sc, w0, w1);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      if (m < M) {
+        const bf16x8* xp = reinterpret_cast<const bf16x8*>(xs + ((int64_t)m * K + k) * ES);
+        const bf16x8 x0 = xp[0], x1 = xp[1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[m] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w0[2 * j], w0[2 * j + 1]},
+                                                   bf16x2{x0[2 * j], x0[2 * j + 1]}, acc[m], false);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[m] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w1[2 * j], w1[2 * j + 1]},
+                                                   bf16x2{x1[2 * j], x1[2 * j + 1]}, acc[m], false);
+      }
+    }
+  } else {
+    f16x8 w0, w1;
+    deq16_f16(w, sc, w0, w1);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      if (m < M) {
+        const f16x8* xp = reinterpret_cast<const f16x8*>(xs + ((int64_t)m * K + k) * ES);
+        const f16x8 x0 = xp[0], x1 = xp[1];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[m] = __builtin_amdgcn_fdot2(f16x2{w0[2 * j], w0[2 * j + 1]},
+                                          f16x2{x0[2 * j], x0[2 * j + 1]}, acc[m], false);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[m] = __builtin_amdgcn_fdot2(f16x2{w1[2 * j], w1[2 * j + 1]},
+                                          f16x2{x1[2 * j], x1[2 * j + 1]}, acc[m], false);
+      }
+    }
+  }
+}
+
+// One wave owns R consecutive rows (SWI: gate row n and up row n, R = 1) and requests
+// all of their codes up front, row after row; rows are then consumed in the same order,
+// so the dequant/dot work of row 0 runs while the later rows are still arriving.  The
+// activations are staged in LDS per workgroup while the codes are in flight.
+// For plain linears tile_begin of linear i holds its first global row; all rows of a
+// wave belong to one linear (each linear's rows are padded to a multiple of R).
+template <int XT, int MB, int U, int R, bool SWI>
 __global__ __launch_bounds__(256) void k_gemv_valu(QrowParams p, int rows) {
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
   constexpr int ES = XElem<XT>::size;
+  constexpr int P = SWI ? 2 : R;
   const int lane = threadIdx.x & 63;
-  const int r = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int K = p.K;
   const int M = p.M;  // <= MB
-  const bool live = r < rows;
-  const int rr = live ? r : rows - 1;
+  const int r0 = ((int)blockIdx.x * 4 + (threadIdx.x >> 6)) * (SWI ? 1 : R);
+  const bool live = r0 < rows;
+  const int rr = live ? r0 : 0;
   int li = 0;
+  if (!SWI) {
 #pragma unroll
-  for (int j = 1; j < 4; ++j)
-    if (j < p.n_lin && rr >= p.lin[j].tile_begin) li = j;
-  const QrowLin& L = p.lin[li];
-  const int n = rr - L.tile_begin;
-  const int8_t* wrow = L.codes + (int64_t)n * K + 16 * lane;
+    for (int j = 1; j < 4; ++j)
+      if (j < p.n_lin && rr >= p.lin[j].tile_begin) li = j;
+  }
+  const int n0 = rr - p.lin[li].tile_begin;
+  const int N = p.lin[li].N;
 
-  // 1) the row's codes (all of K in flight at once), 2) its scale
-  i32x4 wv[U];
+  i32x4 wv[P][U];
+  float sc[P];
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    wv[u] = (u * 1024 + 16 * lane < K)
-                ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wrow + u * 1024))
-                : i32x4{0, 0, 0, 0};
-  const float sc = L.scales[n];
-  // 3) stage the activations (M rows x K) in LDS while the codes are in flight
+  for (int pl = 0; pl < P; ++pl) {
+    const QrowLin& L = p.lin[SWI ? pl : li];
+    int n = SWI ? n0 : n0 + pl;
+    n = n < N ? n : N - 1;
+    const int8_t* wrow = L.codes + (int64_t)n * K + 16 * lane;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      wv[pl][u] = (u * 1024 + 16 * lane < K)
+                      ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wrow + u * 1024))
+                      : i32x4{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) {
+    int n = SWI ? n0 : n0 + pl;
+    n = n < N ? n : N - 1;
+    sc[pl] = p.lin[SWI ? pl : li].scales[n];
+  }
+  // stage the activations (M rows x K) in LDS while the codes are in flight
   const int row16 = K * ES / 16;
   for (int i = threadIdx.x; i < M * row16; i += 256) {
     const int m = i / row16;
@@ -352,81 +433,44 @@ __global__ __launch_bounds__(256) void k_gemv_valu(QrowParams p, int rows) {
   __syncthreads();
   if (!live) return;
 
-  float acc[MB];
+  const QrowLin& L = p.lin[li];
+  float acc_g[MB];
 #pragma unroll
-  for (int m = 0; m < MB; ++m) acc[m] = 0.f;
+  for (int pl = 0; pl < P; ++pl) {
+    float acc[MB];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int k = u * 1024 + 16 * lane;
-    if (k < K) {
-      if constexpr (XT == QS_F32) {
-        float w[16];
+    for (int m = 0; m < MB; ++m) acc[m] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+    for (int u = 0; u < U; ++u) {
+      const int k = u * 1024 + 16 * lane;
+      if (k < K) valu_chunk<XT, MB>(wv[pl][u], sc[pl], xs, K, k, M, acc);
+    }
+    if constexpr (SWI) {
+      if (pl == 0) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) w[4 * j + e] = byte_f32(wv[u][j], e) * sc;
-#pragma unroll
-        for (int m = 0; m < MB; ++m) {
-          if (m < M) {
-            const f32x4* xp = reinterpret_cast<const f32x4*>(xs + ((int64_t)m * K + k) * ES);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const f32x4 xv = xp[j];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) acc[m] = fmaf(xv[e], w[4 * j + e], acc[m]);
-            }
-          }
-        }
-      } else if constexpr (XT == QS_BF16) {
-        bf16x8 w0, w1;
-        deq16_bf16(wv[u], sc, w0, w1);
-#pragma unroll
-        for (int m = 0; m < MB; ++m) {
-          if (m < M) {
-            const bf16x8* xp = reinterpret_cast<const bf16x8*>(xs + ((int64_t)m * K + k) * ES);
-            const bf16x8 x0 = xp[0], x1 = xp[1];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[m] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w0[2 * j], w0[2 * j + 1]},
-                                                       bf16x2{x0[2 * j], x0[2 * j + 1]}, acc[m], false);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[m] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w1[2 * j], w1[2 * j + 1]},
-                                                       bf16x2{x1[2 * j], x1[2 * j + 1]}, acc[m], false);
-          }
-        }
-      } else {
-        f16x8 w0, w1;
-        deq16_f16(wv[u], sc, w0, w1);
-#pragma unroll
-        for (int m = 0; m < MB; ++m) {
-          if (m < M) {
-            const f16x8* xp = reinterpret_cast<const f16x8*>(xs + ((int64_t)m * K + k) * ES);
-            const f16x8 x0 = xp[0], x1 = xp[1];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[m] = __builtin_amdgcn_fdot2(f16x2{w0[2 * j], w0[2 * j + 1]},
-                                              f16x2{x0[2 * j], x0[2 * j + 1]}, acc[m], false);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[m] = __builtin_amdgcn_fdot2(f16x2{w1[2 * j], w1[2 * j + 1]},
-                                              f16x2{x1[2 * j], x1[2 * j + 1]}, acc[m], false);
-          }
-        }
+        for (int m = 0; m < MB; ++m) acc_g[m] = wave_sum(acc[m]);
+        continue;
       }
     }
-  }
+    const int n = n0 + (SWI ? 0 : pl);
 #pragma unroll
-  for (int m = 0; m < MB; ++m) {
-    const float v = wave_sum(acc[m]);
-    if (lane == 0 && m < M) {
-      const int64_t yi = (int64_t)m * L.ldy + n;
-      if constexpr (XT == QS_F32)
-        static_cast<float*>(L.y)[yi] = v;
-      else if constexpr (XT == QS_BF16)
-        static_cast<uint16_t*>(L.y)[yi] = f32_to_bf16_bits(v);
-      else
-        static_cast<uint16_t*>(L.y)[yi] = f32_to_f16_bits(v);
+    for (int m = 0; m < MB; ++m) {
+      const float v = wave_sum(acc[m]);
+      if (lane == 0 && m < M && n < N) {
+        const int64_t yi = (int64_t)m * L.ldy + n;
+        if constexpr (SWI) {
+          const float gt = bf16_bits_to_f32(f32_to_bf16_bits(acc_g[m]));
+          const float ut = bf16_bits_to_f32(f32_to_bf16_bits(v));
+          const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f32(gt)));
+          static_cast<uint16_t*>(L.y)[yi] = f32_to_bf16_bits(sl * ut);
+        } else if constexpr (XT == QS_F32) {
+          static_cast<float*>(L.y)[yi] = v;
+        } else if constexpr (XT == QS_BF16) {
+          static_cast<uint16_t*>(L.y)[yi] = f32_to_bf16_bits(v);
+        } else {
+          static_cast<uint16_t*>(L.y)[yi] = f32_to_f16_bits(v);
+        }
+      }
     }
   }
 }
@@ -587,47 +631,72 @@ bool valu_eligible(const QrowParams& p, int x_dtype) {
   return true;
 }
 
-template <int XT, int MB>
-void launch_valu_mb(const QrowParams& q, int rows, int blocks, size_t lds, hipStream_t s) {
+template <int XT, int MB, int R, bool SWI>
+void launch_valu_r(const QrowParams& q, int rows, int blocks, size_t lds, hipStream_t s) {
   const int chunks = (q.K + 1023) / 1024;
   if (chunks <= 2)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 2>), dim3(blocks), dim3(256), lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 2, R, SWI>), dim3(blocks), dim3(256), lds, s, q, rows);
   else if (chunks <= 4)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 4>), dim3(blocks), dim3(256), lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 4, R, SWI>), dim3(blocks), dim3(256), lds, s, q, rows);
   else if (chunks <= 8)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 8>), dim3(blocks), dim3(256), lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 8, R, SWI>), dim3(blocks), dim3(256), lds, s, q, rows);
   else
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 12>), dim3(blocks), dim3(256), lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 12, R, SWI>), dim3(blocks), dim3(256), lds, s, q, rows);
+}
+
+template <int XT, int MB, bool SWI>
+void launch_valu_mb(const QrowParams& q, int R, int rows, size_t lds, hipStream_t s) {
+  const int blocks = (int)cdiv(cdiv(rows, R), 4);
+  if constexpr (SWI) {
+    launch_valu_r<XT, MB, 1, true>(q, rows, blocks, lds, s);
+  } else {
+    if (R == 4) launch_valu_r<XT, MB, 4, false>(q, rows, blocks, lds, s);
+    else if (R == 2) launch_valu_r<XT, MB, 2, false>(q, rows, blocks, lds, s);
+    else launch_valu_r<XT, MB, 1, false>(q, rows, blocks, lds, s);
+  }
 }
 
 // VALU path: rows of x in batches of MB (each batch one launch).  Every row is reduced
-// in the same order whatever M is.
-int run_valu(QrowParams p, int x_dtype, int64_t M, hipStream_t s) {
+// in the same order whatever M is.  R rows per wave: more when there are rows to spare,
+// and only while the wave's codes stay within a modest register budget.
+int run_valu(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool swiglu) {
   const int es = x_dtype == QS_F32 ? 4 : 2;
   const int mb = valu_mb(x_dtype, p.K, M);
+  int64_t total = 0;
+  for (int i = 0; i < p.n_lin; ++i) total += p.lin[i].N;
+  const int chunks = (p.K + 1023) / 1024;
+  int R = 1;
+  (void)chunks;
+  (void)total;
   int rows = 0;
-  for (int i = 0; i < p.n_lin; ++i) {
-    p.lin[i].tile_begin = rows;
-    rows += p.lin[i].N;
+  if (swiglu) {
+    rows = p.lin[0].N;
+  } else {
+    for (int i = 0; i < p.n_lin; ++i) {
+      p.lin[i].tile_begin = rows;
+      rows += (int)cdiv(p.lin[i].N, R) * R;
+    }
   }
-  const int blocks = (rows + 3) / 4;
   for (int64_t m0 = 0; m0 < M; m0 += mb) {
     QrowParams q = p;
     q.M = (int)((M - m0) < mb ? (M - m0) : mb);
     q.x = static_cast<const char*>(p.x) + m0 * p.ldx * es;
     for (int i = 0; i < q.n_lin; ++i)
-      q.lin[i].y = static_cast<char*>(p.lin[i].y) + m0 * p.lin[i].ldy * es;
+      if (p.lin[i].y) q.lin[i].y = static_cast<char*>(p.lin[i].y) + m0 * p.lin[i].ldy * es;
     const size_t lds = (size_t)q.M * q.K * es;
-    if (x_dtype == QS_F32) {
-      if (mb == 4) launch_valu_mb<QS_F32, 4>(q, rows, blocks, lds, s);
-      else if (mb == 2) launch_valu_mb<QS_F32, 2>(q, rows, blocks, lds, s);
-      else launch_valu_mb<QS_F32, 1>(q, rows, blocks, lds, s);
+    if (swiglu) {
+      if (mb == 2) launch_valu_mb<QS_BF16, 2, true>(q, 1, rows, lds, s);
+      else launch_valu_mb<QS_BF16, 1, true>(q, 1, rows, lds, s);
+    } else if (x_dtype == QS_F32) {
+      if (mb == 4) launch_valu_mb<QS_F32, 4, false>(q, R, rows, lds, s);
+      else if (mb == 2) launch_valu_mb<QS_F32, 2, false>(q, R, rows, lds, s);
+      else launch_valu_mb<QS_F32, 1, false>(q, R, rows, lds, s);
     } else if (x_dtype == QS_BF16) {
-      if (mb == 2) launch_valu_mb<QS_BF16, 2>(q, rows, blocks, lds, s);
-      else launch_valu_mb<QS_BF16, 1>(q, rows, blocks, lds, s);
+      if (mb == 2) launch_valu_mb<QS_BF16, 2, false>(q, R, rows, lds, s);
+      else launch_valu_mb<QS_BF16, 1, false>(q, R, rows, lds, s);
     } else {
-      if (mb == 2) launch_valu_mb<QS_F16, 2>(q, rows, blocks, lds, s);
-      else launch_valu_mb<QS_F16, 1>(q, rows, blocks, lds, s);
+      if (mb == 2) launch_valu_mb<QS_F16, 2, false>(q, R, rows, lds, s);
+      else launch_valu_mb<QS_F16, 1, false>(q, R, rows, lds, s);
     }
   }
   return hip_check(hipGetLastError(), "k_gemv_valu launch");
@@ -639,7 +708,7 @@ int run_linears(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool row_st
   const int esz = x_dtype == QS_F32 ? 4 : 2;
   // decode-sized batches (and the row-stable contract) take the VALU path
   if ((row_stable || M <= 2 || x_dtype == QS_F32) && valu_eligible(p, x_dtype))
-    return run_valu(p, x_dtype, M, s);
+    return run_valu(p, x_dtype, M, s, false);
   if (!row_stable && mfma_eligible(p, x_dtype)) {
     for (int64_t m0 = 0; m0 < M; m0 += 32) {
       QrowParams q = p;
@@ -663,7 +732,7 @@ int run_linears(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool row_st
     }
     return hip_check(hipGetLastError(), "k_w8a16 launch");
   }
-  if (valu_eligible(p, x_dtype)) return run_valu(p, x_dtype, M, s);
+  if (valu_eligible(p, x_dtype)) return run_valu(p, x_dtype, M, s, false);
   int waves = 0;
   for (int i = 0; i < p.n_lin; ++i) {
     p.lin[i].tile_begin = waves;
@@ -785,6 +854,7 @@ extern "C" int qs_qrow_swiglu(const void* x, int64_t ldx, const int8_t* gate_cod
   p.n_lin = 2;
   p.lin[0] = QrowLin{gate_codes, gate_scales, y, ldy, (int)N, 0};
   p.lin[1] = QrowLin{up_codes, up_scales, nullptr, 0, (int)N, 0};
+  if (M <= 2 && valu_eligible(p, QS_BF16)) return run_valu(p, QS_BF16, M, s, true);
   if (mfma_eligible(p, QS_BF16)) {
     for (int64_t m0 = 0; m0 < M; m0 += 32) {
       QrowParams q = p;

@@ -1,0 +1,227 @@
+"""QStore v3 int8 on-disk format: manifest reader/validator and a writer.
+
+Format (reference src/mrun/engine/kernels/qstore_build.py:1-25, 556-713; reader
+src/mrun/engine/kernels/qstore.py:124-219, 326-373, 677-741):
+
+* ``manifest.json`` -- ``{"dtype": "int8", "config": {...}, "blocks": {name: desc}}``
+  where ``desc`` is ``{"kind": "qrow", "shape": [out, in], "w_off", "w_len", "s_off",
+  "s_len"}``, ``{"kind": "fp32", "shape": [...], "e_off", "e_len"}`` or
+  ``{"alias": other}``;
+* ``weights.i8`` -- int8 row-major codes of every qrow block, back to back;
+* ``scales.f32`` -- one fp32 scale per output row of every qrow block;
+* ``extras.f32`` -- fp32 tensors (norms, biases).
+
+Validation mirrors ``_validate_int8_layout`` (qstore.py:124-219): every qrow/fp32 range
+is checked against its shape, ranges of each file are contiguous, gap-free, in bounds
+and cover the whole file, aliases resolve without cycles.  Violations raise
+``RuntimeError`` (store corruption), unknown blocks ``KeyError``.  The content-addressed
+provenance digests of the reference (store_provenance.py) are not part of this path.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from collections.abc import Mapping
+from pathlib import Path
+from typing import Any
+
+import numpy as np
+
+QSTORE_FILES = ("weights.i8", "scales.f32", "extras.f32")
+
+
+def _req_int(block: Mapping[str, Any], key: str, *, positive: bool = False) -> int:
+    value = block.get(key)
+    if isinstance(value, bool) or not isinstance(value, int):
+        raise RuntimeError(f"QStore block field {key!r} must be an integer")
+    if value < (1 if positive else 0):
+        raise RuntimeError(f"QStore block field {key!r} must be {'positive' if positive else 'non-negative'}")
+    return value
+
+
+def _req_shape(block: Mapping[str, Any], dims: int | None = None) -> tuple[int, ...]:
+    raw = block.get("shape")
+    if not isinstance(raw, list) or not raw:
+        raise RuntimeError("QStore block shape must be a non-empty list")
+    if any(isinstance(v, bool) or not isinstance(v, int) or v <= 0 for v in raw):
+        raise RuntimeError("QStore block shape dimensions must be positive integers")
+    if dims is not None and len(raw) != dims:
+        raise RuntimeError(f"QStore block shape must have {dims} dimensions")
+    return tuple(raw)
+
+
+def validate_int8_layout(directory: Path, manifest: Mapping[str, Any]) -> None:
+    """Check every block mapping before any memory map is opened (qstore.py:124-219)."""
+    if manifest.get("dtype") != "int8":
+        raise RuntimeError("QStore must declare dtype='int8'")
+    blocks = manifest.get("blocks")
+    if not isinstance(manifest.get("config"), Mapping) or not isinstance(blocks, Mapping) or not blocks:
+        raise RuntimeError("QStore requires config and a non-empty block table")
+    intervals: dict[str, list[tuple[int, int, str]]] = {f: [] for f in QSTORE_FILES}
+    n_qrow = 0
+    for name, blk in blocks.items():
+        if not isinstance(name, str) or not name or not isinstance(blk, Mapping):
+            raise RuntimeError("QStore block names and descriptors must be non-empty mappings")
+        if "alias" in blk:
+            if not isinstance(blk.get("alias"), str) or not blk["alias"]:
+                raise RuntimeError(f"QStore alias {name!r} has an invalid target")
+            continue
+        kind = blk.get("kind")
+        if kind == "qrow":
+            out, inn = _req_shape(blk, 2)
+            w_off, w_len = _req_int(blk, "w_off"), _req_int(blk, "w_len", positive=True)
+            s_off, s_len = _req_int(blk, "s_off"), _req_int(blk, "s_len", positive=True)
+            if w_len != out * inn:
+                raise RuntimeError(f"QStore qrow {name!r} weight length does not match its shape")
+            if s_len != out * 4 or s_off % 4:
+                raise RuntimeError(f"QStore qrow {name!r} scale range does not match its shape")
+            intervals["weights.i8"].append((w_off, w_off + w_len, name))
+            intervals["scales.f32"].append((s_off, s_off + s_len, name))
+            n_qrow += 1
+        elif kind == "fp32":
+            shape = _req_shape(blk)
+            e_off, e_len = _req_int(blk, "e_off"), _req_int(blk, "e_len", positive=True)
+            if e_len != math.prod(shape) * 4 or e_off % 4:
+                raise RuntimeError(f"QStore fp32 {name!r} range does not match its shape")
+            intervals["extras.f32"].append((e_off, e_off + e_len, name))
+        else:
+            raise RuntimeError(f"QStore block {name!r} has unsupported kind {kind!r}")
+    if not n_qrow:
+        raise RuntimeError("QStore requires qrow blocks")
+    for name, blk in blocks.items():
+        if isinstance(blk, Mapping) and "alias" in blk:
+            seen = {name}
+            target = blk["alias"]
+            while True:
+                if target not in blocks:
+                    raise RuntimeError(f"QStore alias {name!r} targets missing block {target!r}")
+                if target in seen:
+                    raise RuntimeError(f"QStore alias cycle contains {target!r}")
+                seen.add(target)
+                nxt = blocks[target].get("alias") if isinstance(blocks[target], Mapping) else None
+                if nxt is None:
+                    break
+                target = nxt
+    for filename, ranges in intervals.items():
+        path = directory / filename
+        if not path.is_file():
+            raise RuntimeError(f"QStore derived file is missing: {filename}")
+        size = path.stat().st_size
+        if not ranges:
+            if size:
+                raise RuntimeError(f"QStore block table does not reference {filename}")
+            continue
+        prev = 0
+        for start, end, bname in sorted(ranges):
+            if end > size:
+                raise RuntimeError(f"QStore {filename} range for block {bname!r} exceeds file bounds")
+            if start < prev:
+                raise RuntimeError(f"QStore {filename} ranges overlap at block {bname!r}")
+            if start != prev:
+                raise RuntimeError(f"QStore {filename} has an unreferenced gap before block {bname!r}")
+            prev = end
+        if prev != size:
+            raise RuntimeError(f"QStore {filename} block ranges do not cover the complete file")
+
+
+class QStoreReader:
+    """Memory-mapped read-only view of an int8 QStore directory."""
+
+    def __init__(self, directory: str | Path):
+        d = Path(directory).resolve()
+        manifest = json.loads((d / "manifest.json").read_text(encoding="utf-8"))
+        if not isinstance(manifest, dict):
+            raise RuntimeError("QStore manifest must be a JSON object")
+        validate_int8_layout(d, manifest)
+        self.directory = d
+        self.man = manifest
+        self.blocks: dict[str, dict] = manifest["blocks"]
+        self.cfg = manifest["config"]
+        self.w = np.memmap(d / "weights.i8", dtype=np.int8, mode="r")
+        self.s = np.memmap(d / "scales.f32", dtype=np.float32, mode="r")
+        e = d / "extras.f32"
+        self.e = np.memmap(e, dtype=np.float32, mode="r") if e.stat().st_size else np.zeros(0, np.float32)
+
+    def _resolve(self, name: str) -> dict:
+        """Follow aliases (qstore.py:928-942)."""
+        key = str(name)
+        seen: set[str] = set()
+        while True:
+            if key in seen:
+                raise RuntimeError(f"cyclic QStore alias at {name!r}")
+            seen.add(key)
+            try:
+                block = self.blocks[key]
+            except KeyError as exc:
+                raise KeyError(f"QStore has no block {key!r}") from exc
+            alias = block.get("alias")
+            if alias is None:
+                return block
+            key = str(alias)
+
+    def has(self, name: str) -> bool:
+        return name in self.blocks
+
+    def qrow(self, name: str, start_row: int = 0, end_row: int | None = None) -> tuple[np.ndarray, np.ndarray]:
+        """``(codes int8[rows, in], scales f32[rows])`` views of a qrow block row range."""
+        b = self._resolve(name)
+        if b.get("kind") != "qrow":
+            raise ValueError(f"{name} is not a qrow block")
+        out, inn = (int(v) for v in b["shape"])
+        stop = out if end_row is None else int(end_row)
+        if start_row < 0 or stop <= start_row or stop > out:
+            raise ValueError(f"invalid row range [{start_row}, {stop}) for {name}")
+        w0 = int(b["w_off"]) + start_row * inn
+        codes = np.asarray(self.w[w0 : w0 + (stop - start_row) * inn]).reshape(stop - start_row, inn)
+        s0 = int(b["s_off"]) // 4 + start_row
+        scales = np.asarray(self.s[s0 : s0 + stop - start_row])
+        return codes, scales
+
+    def fp32(self, name: str) -> np.ndarray:
+        b = self._resolve(name)
+        if b.get("kind") != "fp32":
+            raise ValueError(f"{name} is not an fp32 block")
+        n = math.prod(b["shape"])
+        off = int(b["e_off"]) // 4
+        return np.array(self.e[off : off + n], dtype=np.float32).reshape(b["shape"])
+
+    def qrow_names(self) -> list[str]:
+        return [n for n, b in self.blocks.items() if b.get("kind") == "qrow"]
+
+
+def write_qstore(
+    directory: str | Path,
+    qrow: Mapping[str, tuple[np.ndarray, np.ndarray]],
+    fp32: Mapping[str, np.ndarray] | None = None,
+    *,
+    aliases: Mapping[str, str] | None = None,
+    config: Mapping[str, Any] | None = None,
+) -> Path:
+    """Write an int8 QStore (same layout as the reference builder, qstore_build.py:556-713)."""
+    d = Path(directory)
+    d.mkdir(parents=True, exist_ok=True)
+    blocks: dict[str, dict] = {}
+    w_off = s_off = e_off = 0
+    with open(d / "weights.i8", "wb") as wf, open(d / "scales.f32", "wb") as sf, open(d / "extras.f32", "wb") as ef:
+        for name, (codes, scales) in qrow.items():
+            codes = np.ascontiguousarray(codes, dtype=np.int8)
+            scales = np.ascontiguousarray(scales, dtype=np.float32)
+            if codes.ndim != 2 or scales.shape != (codes.shape[0],):
+                raise ValueError(f"{name}: codes [out,in] and scales [out] required")
+            wf.write(codes.tobytes())
+            sf.write(scales.tobytes())
+            blocks[name] = {"kind": "qrow", "shape": list(codes.shape), "w_off": w_off,
+                            "w_len": codes.nbytes, "s_off": s_off, "s_len": scales.nbytes}
+            w_off += codes.nbytes
+            s_off += scales.nbytes
+        for name, arr in (fp32 or {}).items():
+            arr = np.ascontiguousarray(arr, dtype=np.float32)
+            ef.write(arr.tobytes())
+            blocks[name] = {"kind": "fp32", "shape": list(arr.shape), "e_off": e_off, "e_len": arr.nbytes}
+            e_off += arr.nbytes
+    for name, target in (aliases or {}).items():
+        blocks[name] = {"alias": target}
+    manifest = {"dtype": "int8", "config": dict(config or {}), "blocks": blocks}
+    (d / "manifest.json").write_text(json.dumps(manifest, indent=1))
+    return d
