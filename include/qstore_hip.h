@@ -85,6 +85,39 @@ int qs_qrow_swiglu(const void* x, int64_t ldx, const int8_t* gate_codes,
                    const float* gate_scales, const int8_t* up_codes, const float* up_scales,
                    void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* ---- W8A8 (int8 weights x per-token int8 activations) ------------------------------ */
+
+/* Activation quantizer of w8a8_matmul (src/mrun/engine/kernels/w8a8.py:118-121):
+ * per row m, v = x*keep (keep nullable, fp32 [K]); s[m] = max|v|/127 (0 -> 1);
+ * q[m,k] = clamp(round_half_even(v/s[m]), -127, 127).  IEEE fp32 ops, bit-exact. */
+int qs_act_quant_i8(const void* x, int x_dtype, int64_t ldx, const float* keep, int8_t* q,
+                    float* scale, int64_t M, int64_t K, void* stream);
+
+/* Outlier column selection of w8a8_matmul (w8a8.py:98-102): colmax[k] = max_m |x[m,k]|,
+ * idx = the k largest (1 <= k <= 64, ties -> lower column), keep = 1 except 0 at idx.
+ * colmax is caller-provided workspace of K floats. */
+int qs_outlier_topk(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int k,
+                    float* colmax, int64_t* idx, float* keep, void* stream);
+
+/* Operands of the exact fp32 side path (w8a8.py:108-112): xp[m,p] = float(x[m, idx[p]]),
+ * wp[n,p] = float(qw[n, idx[p]]) * sw[n]; 1 <= P <= 64. */
+int qs_w8a8_side_gather(const void* x, int x_dtype, int64_t ldx, const int8_t* qw,
+                        const float* sw, const int64_t* idx, int P, int64_t M, int64_t N,
+                        int64_t K, float* xp, float* wp, void* stream);
+
+/* Replaces _int8_gemm / torch._int_mm (w8a8.py:33-64): acc[M,N] = qx[M,K] . qw[N,K]^T,
+ * exact int32 accumulation (v_mfma_i32_32x32x32_i8). */
+int qs_gemm_i8i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int64_t M, int64_t N,
+                     int64_t K, void* stream);
+
+/* GEMM + epilogue of w8a8_matmul (w8a8.py:123-125):
+ * y[m,n] = side[m,n] + (float(acc[m,n]) * act_scale[m]) * w_scale[n], with
+ * side[m,n] = sum_p side_x[m,p] * side_w[n,p] (P = 0: no side path, y is the bare
+ * product bit for bit); y_dtype F32 or BF16 (RNE of the fp32 value). */
+int qs_w8a8_gemm(const int8_t* qx, const float* act_scale, const int8_t* qw,
+                 const float* w_scale, const float* side_x, const float* side_w, int P, void* y,
+                 int y_dtype, int64_t M, int64_t N, int64_t K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,474 @@
+// W8A8: per-token int8 activation quantization + int8 x int8 -> int32 MFMA GEMM with a
+// fused dequant epilogue, and the fp32 outlier side path (LLM.int8 style).
+//
+// Kernels
+//   k_act_quant      : per row, s = max|x*keep| / 127 (0 -> 1), q = clamp(rint(x*keep / s))
+//                      -- one IEEE fp32 multiply/divide per element, round-half-even, the
+//                      exact recipe of the reference (bit-exact codes and scales).
+//   k_col_absmax     : max over rows of |x[:, k]| (outlier column detection).
+//   k_topk           : the k largest column maxima (ties -> lower column index).
+//   k_gather_side    : xp[m, p] = x[m, idx[p]], wp[n, p] = float(qw[n, idx[p]]) * sw[n].
+//   k_gemm_i8<...>   : C = A[M,K] . B[N,K]^T with v_mfma_i32_32x32x32_i8, 64-byte K
+//                      steps staged through padded, double-buffered LDS tiles, an XCD-aware
+//                      tile order, and one of three epilogues: raw int32, or
+//                      y = side + (float(acc) * a_scale[m]) * b_scale[n] in fp32 / bf16.
+//   k_gemm_i8_generic: any shape (one thread per output, exact int32).
+//
+// MFMA operand mapping (32x32x32 i8, wave64): lane l supplies row (l & 31) of A and
+// column (l & 31) of B with 16 int8 of the k half (l >> 5); A and B use the same
+// lane -> k assignment, so each lane just loads 16 contiguous bytes at k = 16*(l>>5) of
+// its row.  Accumulator register r of lane l holds
+// C[8*(r/4) + 4*(l>>5) + (r%4)][l & 31].
+#include "qs_common.h"
+
+namespace qs {
+
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+// ----------------------------------------------------------------------------------
+// activation quantization
+// ----------------------------------------------------------------------------------
+template <int XT>
+__device__ __forceinline__ float load_x(const void* x, int64_t i) {
+  if constexpr (XT == QS_F32) return static_cast<const float*>(x)[i];
+  else if constexpr (XT == QS_BF16) return bf16_bits_to_f32(static_cast<const uint16_t*>(x)[i]);
+  else return f16_bits_to_f32(static_cast<const uint16_t*>(x)[i]);
+}
+
+// One workgroup per row.  keep (nullable) multiplies x before everything (protected
+// outlier columns carry 0, the rest 1).
+template <int XT>
+__global__ __launch_bounds__(256) void k_act_quant(const void* __restrict__ x, int64_t ldx,
+                                                   const float* __restrict__ keep,
+                                                   int8_t* __restrict__ q, int64_t ldq,
+                                                   float* __restrict__ scale, int K) {
+  const int64_t row = blockIdx.x;
+  const void* xr = static_cast<const char*>(x) + row * ldx * (XT == QS_F32 ? 4 : 2);
+  float amax = 0.f;
+  for (int k = threadIdx.x; k < K; k += 256) {
+    float v = load_x<XT>(xr, k);
+    if (keep) v = mul_rn(v, keep[k]);
+    amax = fmaxf(amax, fabsf(v));
+  }
+  amax = wave_max(amax);
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float s = amax / 127.0f;  // IEEE division
+  if (s == 0.f) s = 1.f;
+  if (threadIdx.x == 0) scale[row] = s;
+  int8_t* qr = q + row * ldq;
+  for (int k = threadIdx.x; k < K; k += 256) {
+    float v = load_x<XT>(xr, k);
+    if (keep) v = mul_rn(v, keep[k]);
+    float r = rintf(v / s);  // IEEE division, round half to even
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    qr[k] = static_cast<int8_t>(r);
+  }
+}
+
+template <int XT>
+__global__ __launch_bounds__(256) void k_col_absmax(const void* __restrict__ x, int64_t ldx,
+                                                    int M, int K, float* __restrict__ out) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  if (k >= K) return;
+  float amax = 0.f;
+  for (int m = 0; m < M; ++m) amax = fmaxf(amax, fabsf(load_x<XT>(x, (int64_t)m * ldx + k)));
+  out[k] = amax;
+}
+
+// Single workgroup: kk rounds of a block-wide argmax over vals[0..K).  Selected entries
+// are excluded by index; ties go to the lower index.  Emits int64 indices (descending
+// value order) and the keep mask (1 everywhere, 0 at the selected columns).
+__global__ __launch_bounds__(1024) void k_topk(const float* __restrict__ vals, int K, int kk,
+                                               int64_t* __restrict__ idx, float* __restrict__ keep) {
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  __shared__ int chosen[64];
+  for (int k = threadIdx.x; k < K; k += 1024) keep[k] = 1.f;
+  for (int round = 0; round < kk; ++round) {
+    float best = -1.f;
+    int besti = 0x7fffffff;
+    for (int k = threadIdx.x; k < K; k += 1024) {
+      bool taken = false;
+      for (int j = 0; j < round; ++j) taken |= chosen[j] == k;
+      if (taken) continue;
+      const float v = vals[k];
+      if (v > best || (v == best && k < besti)) {
+        best = v;
+        besti = k;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(best, off, 64);
+      const int oi = __shfl_xor(besti, off, 64);
+      if (ov > best || (ov == best && oi < besti)) {
+        best = ov;
+        besti = oi;
+      }
+    }
+    if ((threadIdx.x & 63) == 0) {
+      bv[threadIdx.x >> 6] = best;
+      bi[threadIdx.x >> 6] = besti;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float b = bv[0];
+      int i = bi[0];
+      for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+        if (bv[w] > b || (bv[w] == b && bi[w] < i)) {
+          b = bv[w];
+          i = bi[w];
+        }
+      chosen[round] = i;
+      idx[round] = i;
+      keep[i] = 0.f;
+    }
+    __syncthreads();
+  }
+}
+
+template <int XT>
+__global__ __launch_bounds__(256) void k_gather_side(const void* __restrict__ x, int64_t ldx,
+                                                     const int8_t* __restrict__ qw, int64_t ldw,
+                                                     const float* __restrict__ sw,
+                                                     const int64_t* __restrict__ idx, int P,
+                                                     int M, int N, float* __restrict__ xp,
+                                                     float* __restrict__ wp) {
+  const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+  const int64_t nx = (int64_t)M * P;
+  if (i < nx) {
+    const int64_t m = i / P, pp = i - m * P;
+    xp[i] = load_x<XT>(x, m * ldx + idx[pp]);
+  } else if (i < nx + (int64_t)N * P) {
+    const int64_t j = i - nx;
+    const int64_t n = j / P, pp = j - n * P;
+    wp[j] = static_cast<float>(qw[n * ldw + idx[pp]]) * sw[n];
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// int8 MFMA GEMM
+// ----------------------------------------------------------------------------------
+struct GemmParams {
+  const int8_t* a;  // [M, K]
+  const int8_t* b;  // [N, K]
+  int64_t lda, ldb;
+  int M, N, K;
+  void* c;
+  int64_t ldc;
+  const float* as;  // [M]   (epilogue 1/2)
+  const float* bs;  // [N]
+  const float* xp;  // [M, P] side-path activations (nullable)
+  const float* wp;  // [N, P] side-path weights
+  int P;
+};
+
+enum { EPI_I32 = 0, EPI_F32 = 1, EPI_BF16 = 2 };
+
+constexpr int kBK = 64;        // k bytes per step
+constexpr int kLdsRow = 80;    // padded LDS row (64 data + 16): conflict-free 16B reads
+
+template <int BM, int BN, int WM, int WN, int EPI>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmParams p) {
+  constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
+  constexpr int NT = WAVES_M * WAVES_N * 64;
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int A_CH = BM * 4 / NT, B_CH = BN * 4 / NT;  // 16-byte chunks per thread
+  static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for the thread count");
+  __shared__ __attribute__((aligned(16))) int8_t lds[2][(BM + BN) * kLdsRow];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+
+  // XCD-aware tile order: consecutive workgroup ids are dealt round-robin to the 8 XCDs,
+  // so regroup them such that the workgroups of one XCD walk consecutive M tiles of the
+  // same N tile (its B tile is then served from that XCD's L2).
+  const int tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int G = tiles_m * tiles_n;
+  const int bid = blockIdx.x;
+  int lid = bid;
+  if ((G & 7) == 0) lid = (bid & 7) * (G >> 3) + (bid >> 3);
+  const int tm = lid % tiles_m, tn = lid / tiles_m;
+  const int bm = tm * BM, bn = tn * BN;
+
+  // global -> register staging
+  const int8_t* ga[A_CH];
+  const int8_t* gb[B_CH];
+  int la[A_CH], lb[B_CH];
+#pragma unroll
+  for (int i = 0; i < A_CH; ++i) {
+    const int c = tid + i * NT;
+    const int r = c >> 2, col = (c & 3) * 16;
+    const int gr = bm + r < p.M ? bm + r : p.M - 1;
+    ga[i] = p.a + (int64_t)gr * p.lda + col;
+    la[i] = r * kLdsRow + col;
+  }
+#pragma unroll
+  for (int i = 0; i < B_CH; ++i) {
+    const int c = tid + i * NT;
+    const int r = c >> 2, col = (c & 3) * 16;
+    const int gr = bn + r < p.N ? bn + r : p.N - 1;
+    gb[i] = p.b + (int64_t)gr * p.ldb + col;
+    lb[i] = (BM + r) * kLdsRow + col;
+  }
+  i32x4 ra[A_CH], rb[B_CH];
+  auto gload = [&](int kt) {
+    const int64_t ko = (int64_t)kt * kBK;
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const i32x4*>(ga[i] + ko);
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) rb[i] = *reinterpret_cast<const i32x4*>(gb[i] + ko);
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) *reinterpret_cast<i32x4*>(&lds[buf][la[i]]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) *reinterpret_cast<i32x4*>(&lds[buf][lb[i]]) = rb[i];
+  };
+
+  i32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int KT = p.K / kBK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int arow = wm * WM + (lane & 31);
+  const int brow = BM + wn * WN + (lane & 31);
+  const int kh = 16 * (lane >> 5);
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) gload(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      i32x4 fa[FM], fb[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        fa[i] = *reinterpret_cast<const i32x4*>(&lds[buf][(arow + 32 * i) * kLdsRow + 32 * ks + kh]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        fb[j] = *reinterpret_cast<const i32x4*>(&lds[buf][(brow + 32 * j) * kLdsRow + 32 * ks + kh]);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < KT) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = bn + wn * WN + 32 * j + (lane & 31);
+      if (col >= p.N) continue;
+      float bsc = 0.f;
+      if constexpr (EPI != EPI_I32) bsc = p.bs[col];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = bm + wm * WM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row >= p.M) continue;
+        if constexpr (EPI == EPI_I32) {
+          static_cast<int32_t*>(p.c)[(int64_t)row * p.ldc + col] = acc[i][j][r];
+        } else {
+          // reference order: (float(acc) * act_scale) * w_scale, added to the side path
+          float v = mul_rn(mul_rn(static_cast<float>(acc[i][j][r]), p.as[row]), bsc);
+          if (p.P > 0) {
+            float side = 0.f;
+            const float* xr = p.xp + (int64_t)row * p.P;
+            const float* wr = p.wp + (int64_t)col * p.P;
+            for (int q = 0; q < p.P; ++q) side = fmaf(xr[q], wr[q], side);
+            v = add_rn(side, v);
+          }
+          if constexpr (EPI == EPI_F32)
+            static_cast<float*>(p.c)[(int64_t)row * p.ldc + col] = v;
+          else
+            static_cast<uint16_t*>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16_bits(v);
+        }
+      }
+    }
+}
+
+// Any shape: one thread per output, exact int32 accumulation.
+__global__ __launch_bounds__(256) void k_gemm_i8_generic(GemmParams p, int epi) {
+  const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+  if (i >= (int64_t)p.M * p.N) return;
+  const int row = (int)(i / p.N), col = (int)(i % p.N);
+  const int8_t* a = p.a + (int64_t)row * p.lda;
+  const int8_t* b = p.b + (int64_t)col * p.ldb;
+  int acc = 0;
+  for (int k = 0; k < p.K; ++k) acc += (int)a[k] * (int)b[k];
+  if (epi == EPI_I32) {
+    static_cast<int32_t*>(p.c)[(int64_t)row * p.ldc + col] = acc;
+    return;
+  }
+  float v = mul_rn(mul_rn(static_cast<float>(acc), p.as[row]), p.bs[col]);
+  if (p.P > 0) {
+    float side = 0.f;
+    for (int q = 0; q < p.P; ++q) side = fmaf(p.xp[(int64_t)row * p.P + q], p.wp[(int64_t)col * p.P + q], side);
+    v = add_rn(side, v);
+  }
+  if (epi == EPI_F32)
+    static_cast<float*>(p.c)[(int64_t)row * p.ldc + col] = v;
+  else
+    static_cast<uint16_t*>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16_bits(v);
+}
+
+namespace {
+
+template <int EPI>
+void launch_gemm(const GemmParams& p, hipStream_t s) {
+  const bool big = (int64_t)p.M * p.N >= (int64_t)1024 * 8192;
+  if (big) {
+    constexpr int BM = 256, BN = 256;
+    const int G = (int)(cdiv(p.M, BM) * cdiv(p.N, BN));
+    hipLaunchKernelGGL((k_gemm_i8<BM, BN, 128, 64, EPI>), dim3(G), dim3(8 * 64), 0, s, p);
+  } else {
+    constexpr int BM = 128, BN = 128;
+    const int G = (int)(cdiv(p.M, BM) * cdiv(p.N, BN));
+    hipLaunchKernelGGL((k_gemm_i8<BM, BN, 64, 64, EPI>), dim3(G), dim3(4 * 64), 0, s, p);
+  }
+}
+
+int run_gemm(const GemmParams& p, int epi, hipStream_t s) {
+  if (p.M == 0 || p.N == 0) return QS_OK;
+  const bool fast = p.K % kBK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned(p.a, 16) &&
+                    aligned(p.b, 16);
+  if (fast) {
+    if (epi == EPI_I32) launch_gemm<EPI_I32>(p, s);
+    else if (epi == EPI_F32) launch_gemm<EPI_F32>(p, s);
+    else launch_gemm<EPI_BF16>(p, s);
+    return hip_check(hipGetLastError(), "k_gemm_i8 launch");
+  }
+  const int64_t outs = (int64_t)p.M * p.N;
+  hipLaunchKernelGGL(k_gemm_i8_generic, dim3((unsigned)cdiv(outs, 256)), dim3(256), 0, s, p, epi);
+  return hip_check(hipGetLastError(), "k_gemm_i8_generic launch");
+}
+
+int check_mnk(int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N <= 0 || K <= 0) return fail(QS_ERR_INVALID, "bad GEMM shape M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30)) return fail(QS_ERR_LIMIT, "GEMM dimension exceeds 2^30");
+  return QS_OK;
+}
+
+}  // namespace
+}  // namespace qs
+
+using namespace qs;
+
+extern "C" int qs_act_quant_i8(const void* x, int x_dtype, int64_t ldx, const float* keep,
+                               int8_t* q, float* scale, int64_t M, int64_t K, void* stream) {
+  if (!x || !q || !scale) return fail(QS_ERR_INVALID, "act_quant: null pointer");
+  if (M < 0 || K <= 0 || ldx < K) return fail(QS_ERR_INVALID, "act_quant: bad shape");
+  if (M > (1 << 30) || K > (1 << 30)) return fail(QS_ERR_LIMIT, "act_quant: dimension exceeds 2^30");
+  if (M == 0) return QS_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_dtype == QS_F32)
+    hipLaunchKernelGGL(k_act_quant<QS_F32>, dim3((unsigned)M), dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)K);
+  else if (x_dtype == QS_BF16)
+    hipLaunchKernelGGL(k_act_quant<QS_BF16>, dim3((unsigned)M), dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)K);
+  else if (x_dtype == QS_F16)
+    hipLaunchKernelGGL(k_act_quant<QS_F16>, dim3((unsigned)M), dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)K);
+  else
+    return fail(QS_ERR_INVALID, "act_quant: dtype must be F32, BF16 or F16");
+  return hip_check(hipGetLastError(), "k_act_quant launch");
+}
+
+extern "C" int qs_outlier_topk(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                               int k, float* colmax, int64_t* idx, float* keep, void* stream) {
+  if (!x || !colmax || !idx || !keep) return fail(QS_ERR_INVALID, "outlier_topk: null pointer");
+  if (M <= 0 || K <= 0 || ldx < K) return fail(QS_ERR_INVALID, "outlier_topk: bad shape");
+  if (k < 1 || k > 64 || k > K) return fail(QS_ERR_LIMIT, "outlier_topk: k must be in 1..min(64, K)");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned blocks = (unsigned)cdiv(K, 256);
+  if (x_dtype == QS_F32)
+    hipLaunchKernelGGL(k_col_absmax<QS_F32>, dim3(blocks), dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
+  else if (x_dtype == QS_BF16)
+    hipLaunchKernelGGL(k_col_absmax<QS_BF16>, dim3(blocks), dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
+  else if (x_dtype == QS_F16)
+    hipLaunchKernelGGL(k_col_absmax<QS_F16>, dim3(blocks), dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
+  else
+    return fail(QS_ERR_INVALID, "outlier_topk: dtype must be F32, BF16 or F16");
+  hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), 0, s, colmax, (int)K, k, idx, keep);
+  return hip_check(hipGetLastError(), "outlier_topk launch");
+}
+
+extern "C" int qs_w8a8_side_gather(const void* x, int x_dtype, int64_t ldx, const int8_t* qw,
+                                   const float* sw, const int64_t* idx, int P, int64_t M,
+                                   int64_t N, int64_t K, float* xp, float* wp, void* stream) {
+  if (!x || !qw || !sw || !idx || !xp || !wp) return fail(QS_ERR_INVALID, "side_gather: null pointer");
+  if (P < 1 || P > 64) return fail(QS_ERR_LIMIT, "side_gather: 1..64 protected columns");
+  if (M < 0 || N <= 0 || K <= 0 || ldx < K) return fail(QS_ERR_INVALID, "side_gather: bad shape");
+  const int64_t total = (M + N) * P;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned blocks = (unsigned)cdiv(total, 256);
+  if (x_dtype == QS_F32)
+    hipLaunchKernelGGL(k_gather_side<QS_F32>, dim3(blocks), dim3(256), 0, s, x, ldx, qw, K, sw, idx, P, (int)M, (int)N, xp, wp);
+  else if (x_dtype == QS_BF16)
+    hipLaunchKernelGGL(k_gather_side<QS_BF16>, dim3(blocks), dim3(256), 0, s, x, ldx, qw, K, sw, idx, P, (int)M, (int)N, xp, wp);
+  else if (x_dtype == QS_F16)
+    hipLaunchKernelGGL(k_gather_side<QS_F16>, dim3(blocks), dim3(256), 0, s, x, ldx, qw, K, sw, idx, P, (int)M, (int)N, xp, wp);
+  else
+    return fail(QS_ERR_INVALID, "side_gather: dtype must be F32, BF16 or F16");
+  return hip_check(hipGetLastError(), "k_gather_side launch");
+}
+
+extern "C" int qs_gemm_i8i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int64_t M,
+                                int64_t N, int64_t K, void* stream) {
+  if (!qx || !qw || !acc) return fail(QS_ERR_INVALID, "gemm_i8: null pointer");
+  int st = check_mnk(M, N, K);
+  if (st) return st;
+  GemmParams p{};
+  p.a = qx;
+  p.b = qw;
+  p.lda = K;
+  p.ldb = K;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.c = acc;
+  p.ldc = N;
+  return run_gemm(p, EPI_I32, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qs_w8a8_gemm(const int8_t* qx, const float* act_scale, const int8_t* qw,
+                            const float* w_scale, const float* side_x, const float* side_w,
+                            int P, void* y, int y_dtype, int64_t M, int64_t N, int64_t K,
+                            void* stream) {
+  if (!qx || !act_scale || !qw || !w_scale || !y) return fail(QS_ERR_INVALID, "w8a8_gemm: null pointer");
+  if (P < 0 || P > 64 || (P > 0 && (!side_x || !side_w)))
+    return fail(QS_ERR_INVALID, "w8a8_gemm: side path needs 1..64 columns and both operands");
+  if (y_dtype != QS_F32 && y_dtype != QS_BF16) return fail(QS_ERR_INVALID, "w8a8_gemm: y dtype must be F32 or BF16");
+  int st = check_mnk(M, N, K);
+  if (st) return st;
+  GemmParams p{};
+  p.a = qx;
+  p.b = qw;
+  p.lda = K;
+  p.ldb = K;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.c = y;
+  p.ldc = N;
+  p.as = act_scale;
+  p.bs = w_scale;
+  p.xp = side_x;
+  p.wp = side_w;
+  p.P = P;
+  return run_gemm(p, y_dtype == QS_F32 ? EPI_F32 : EPI_BF16, static_cast<hipStream_t>(stream));
+}

@@ -95,8 +95,8 @@ class DenseQStore:
 
     def _load_page(self, key: str) -> CompactQRowPage:
         codes, scales = self.reader.qrow(key)
-        c = torch.from_numpy(np.ascontiguousarray(codes)).to(self.device, non_blocking=False)
-        s = torch.from_numpy(np.ascontiguousarray(scales)).to(self.device, non_blocking=False)
+        c = torch.from_numpy(np.array(codes, copy=True)).to(self.device)
+        s = torch.from_numpy(np.array(scales, copy=True)).to(self.device)
         page = CompactQRowPage(key, 0, int(codes.shape[0]), int(codes.shape[1]), c, s)
         self.stats.page_loads += 1
         self.stats.compact_h2d_bytes += page.compact_bytes

@@ -1,0 +1,134 @@
+"""GPU parity of the W8A8 kernels against the CPU oracle (through the C ABI)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import qrow as oq
+from oracle import w8a8 as ow
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_TOL = 1e-3
+
+
+def _w():
+    from mrun_pub_amd import w8a8
+
+    return w8a8
+
+
+def _weights(out, inn, seed):
+    rng = np.random.default_rng(seed)
+    q_w = rng.integers(-127, 128, size=(out, inn), dtype=np.int8)
+    sc_w = (rng.uniform(0.5, 1.5, size=out) / 127).astype(np.float32)
+    return rng, q_w, sc_w
+
+
+@pytest.mark.parametrize("t,n,k", [(512, 1024, 4096), (96, 640, 384), (7, 33, 80), (5, 3, 4), (300, 256, 192)])
+def test_int8_gemm_int32_bit_exact(dev, t, n, k):
+    rng = np.random.default_rng(t + n + k)
+    qx = rng.integers(-128, 128, size=(t, k), dtype=np.int8)
+    qw = rng.integers(-128, 128, size=(n, k), dtype=np.int8)
+    acc = _w()._int8_gemm(torch.from_numpy(qx).to(dev), torch.from_numpy(qw).to(dev))
+    assert acc.dtype == torch.int32
+    assert np.array_equal(acc.cpu().numpy(), ow.int8_gemm(qx, qw))
+
+
+def test_int8_gemm_extreme_values(dev):
+    qx = np.full((64, 4096), 127, np.int8)
+    qw = np.full((128, 4096), -127, np.int8)
+    qw[1] = 127
+    acc = _w()._int8_gemm(torch.from_numpy(qx).to(dev), torch.from_numpy(qw).to(dev)).cpu().numpy()
+    assert (acc[:, 0] == -4096 * 127 * 127).all() and (acc[:, 1] == 4096 * 127 * 127).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_act_quant_bit_exact(dev, dtype):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((33, 4096)).astype(np.float32)
+    x[0] = 0.0
+    x[1, :4] = [1.5, 2.5, -0.5, 127.0]
+    x[5, 7] = 2000.0
+    xt = torch.from_numpy(x).to(dtype)
+    xs = xt.float().numpy()
+    keep = np.ones(4096, np.float32)
+    keep[[7, 99]] = 0.0
+    for kp in (None, keep):
+        q, s = _w().quantize_activation(xt.to(dev), None if kp is None else torch.from_numpy(kp).to(dev))
+        qr, sr = ow.act_quant(xs, kp)
+        assert np.array_equal(q.cpu().numpy(), qr)
+        assert np.array_equal(s.cpu().numpy().view(np.uint32), sr.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [1, 17, 512])
+def test_w8a8_no_protection_bit_exact(dev, t):
+    rng, q_w, sc_w = _weights(1536, 1024, t)
+    x = rng.standard_normal((t, 1024)).astype(np.float32)
+    y = _w().w8a8_matmul(torch.from_numpy(q_w).to(dev), torch.from_numpy(sc_w).to(dev), torch.from_numpy(x).to(dev))
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), ow.w8a8_matmul(q_w, sc_w, x).view(np.uint32))
+
+
+@pytest.mark.parametrize("protect_k", [4, 8])
+def test_w8a8_outlier_protection(dev, protect_k):
+    rng, q_w, sc_w = _weights(640, 4096, protect_k)
+    x = rng.standard_normal((64, 4096)).astype(np.float32)
+    x[:, rng.permutation(4096)[:4]] *= 20.0  # 0.1% outlier channels x20
+    y = _w().w8a8_matmul(
+        torch.from_numpy(q_w).to(dev), torch.from_numpy(sc_w).to(dev), torch.from_numpy(x).to(dev), protect_k=protect_k
+    )
+    ref = ow.w8a8_matmul(q_w, sc_w, x, protect_k=protect_k)
+    assert ow.protect_topk(x, protect_k).tolist()  # same columns chosen: checked via result
+    assert oq.rel_l2(y.cpu().numpy(), ref) <= F32_TOL
+
+
+def test_w8a8_static_list_matches_topk(dev):
+    rng, q_w, sc_w = _weights(256, 512, 9)
+    x = rng.standard_normal((8, 512)).astype(np.float32)
+    x[:, [3, 300, 301]] *= 300.0
+    dq, ds, dx = (torch.from_numpy(a).to(dev) for a in (q_w, sc_w, x))
+    idx = torch.from_numpy(ow.protect_topk(x, 4)).to(dev)
+    y_static = _w().w8a8_matmul(dq, ds, dx, protect_idx=idx)
+    y_topk = _w().w8a8_matmul(dq, ds, dx, protect_k=4)
+    assert torch.equal(y_static, y_topk)
+
+
+@pytest.mark.parametrize("m", [512, 2048])
+def test_w8a8_prefill_config3_bf16(dev, m):
+    """BASELINE config 3 shape: [M,4096] bf16 with 0.1% outliers x20, W [14336,4096]."""
+    rng, q_w, sc_w = _weights(14336, 4096, m)
+    x = rng.standard_normal((m, 4096)).astype(np.float32)
+    x[:, rng.permutation(4096)[:4]] *= 20.0
+    xb = oq.round_bf16(x)
+    dq, ds = torch.from_numpy(q_w).to(dev), torch.from_numpy(sc_w).to(dev)
+    dx = torch.from_numpy(xb).to(dev).to(torch.bfloat16)
+    # int32 accumulators bit-exact against the oracle on a row sample
+    q, s = _w().quantize_activation(dx)
+    qr, sr = ow.act_quant(xb)
+    assert np.array_equal(q.cpu().numpy(), qr) and np.array_equal(s.cpu().numpy(), sr)
+    acc = _w()._int8_gemm(q, dq).cpu().numpy()
+    rows = np.arange(0, m, 97)
+    assert np.array_equal(acc[rows], ow.int8_gemm(qr[rows], q_w))
+    y = _w().w8a8_matmul(dq, ds, dx, out_dtype=torch.bfloat16)
+    ref = oq.round_bf16((acc.astype(np.float32) * sr[:, None]).astype(np.float32) * sc_w[None, :])
+    assert np.array_equal(y.float().cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+def test_enable_w8a8_on_dense_store(dev, tmp_path):
+    from mrun_pub_amd.dense_store import DenseQStore
+    from mrun_pub_amd.store import write_qstore
+    from mrun_pub_amd.w8a8 import disable_w8a8, enable_w8a8
+
+    rng, q_w, sc_w = _weights(128, 256, 21)
+    d = write_qstore(tmp_path / "s", {"L0.q": (q_w, sc_w)}, {"L0.norm": np.ones(256, np.float32)})
+    store = DenseQStore(d, device=dev, compute_dtype="fp32")
+    x = rng.standard_normal((4, 256)).astype(np.float32)
+    base = store.matmul("L0.q", torch.from_numpy(x).to(dev))
+    enable_w8a8(store, protect_k=8)
+    yq = store.matmul("L0.q", torch.from_numpy(x).to(dev))
+    assert oq.rel_l2(yq.cpu().numpy(), ow.w8a8_matmul(q_w, sc_w, x, protect_k=8)) <= F32_TOL
+    disable_w8a8(store)
+    assert torch.equal(store.matmul("L0.q", torch.from_numpy(x).to(dev)), base)
