@@ -118,6 +118,76 @@ int qs_w8a8_gemm(const int8_t* qx, const float* act_scale, const int8_t* qw,
                  const float* w_scale, const float* side_x, const float* side_w, int P, void* y,
                  int y_dtype, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* ---- routed MoE ---------------------------------------------------------------------- */
+
+/* Router of Qwen3MoeDecodeRuntime.forward (src/mrun/engine/qwen3_moe_cuda.py:3702-3707):
+ * p = softmax(float(logits[t])), top-k (ties -> lower expert), optional renormalisation
+ * by the kept sum, weights stored as F32 or BF16.  E <= 1024, k <= 16. */
+int qs_moe_router(const void* logits, int logit_dtype, int64_t T, int E, int k, int norm_topk,
+                  int64_t* top_idx, void* top_w, int w_dtype, void* stream);
+
+/* Replaces grouped_route_tensors(_with_inverse) / _triton_route_{count,prefix,scatter}
+ * (src/mrun/engine/olmoe_cuda.py:989-1135, 131-182): expert-major queue of the T*k
+ * assignments in STABLE order (identical to the reference's CPU stable argsort):
+ * token_ids[q] = a / k, coef[q] = float(top_w[a]), counts[e], starts[e] (exclusive
+ * prefix), inverse[a] = q (nullable).  Expert ids must lie in [0, E); E <= 512. */
+int qs_moe_route(const void* top_idx, int idx_dtype, const void* top_w, int w_dtype, int64_t T,
+                 int k, int E, int64_t* token_ids, float* coef, int32_t* starts, int32_t* counts,
+                 int64_t* inverse, void* stream);
+
+/* Routed-row quantization (int8 analogue of quantize_fp8_activation,
+ * olmoe_cuda.py:1173-1176, with the W8A8 recipe of w8a8.py:118-121):
+ * row a of the output is source[rows[a]] (rows nullable = identity). */
+int qs_moe_gather_quant(const void* source, int src_dtype, int64_t ld_src, const int64_t* rows,
+                        int64_t A, int64_t H, int8_t* q, float* scale, void* stream);
+
+/* Replaces grouped_fp8_mm(_strided) / _grouped_fp8_strided_kernel / grouped_w4_mm_strided
+ * (olmoe_cuda.py:1197-1252, qwen3_moe_cuda.py:1910-2470) for int8 experts: for every
+ * group g with rows [starts[g], starts[g]+counts[g]) and weights
+ * w + slot(g)*w_stride ([N_w, K] int8 rows; slot(g) = slots ? slots[g] : g):
+ *   out[row, n] = (float(acc) * a_scale[row]) * w_scale[slot(g)*ws_stride + n]
+ * (F32/BF16); swiglu != 0: N_w = 2N, out[row, n] = bf16(bf16(silu(bf16(gate))) * bf16(up))
+ * with gate from weight row n and up from row n + N.  K % 64 == 0. */
+int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* w,
+                           int64_t w_stride, const float* w_scale, int64_t ws_stride,
+                           const int32_t* starts, const int32_t* counts, const int32_t* slots,
+                           int G, int64_t N, int64_t K, int swiglu, void* out, int out_dtype,
+                           void* stream);
+
+/* Replaces stable_route_reduce / _stable_route_reduce_kernel (qwen3_moe_cuda.py:2561-2664,
+ * 2160-2182): out[t, h] = sum over rank r = 0..k-1 (in order) of
+ * float(y[inverse[t*k+r], h]) * coef[inverse[t*k+r]], each product rounded to fp32. */
+int qs_moe_route_reduce(const void* expert_out, int y_dtype, const float* coef,
+                        const int64_t* inverse, int64_t T, int k, int64_t H, float* out,
+                        void* stream);
+
+/* ---- packed int3 / int2 ("qrow3" / "qrow2") --------------------------------------------
+ * packed: uint8 [N, row_bytes], each row an LSB-first bitstream of K codes of `bits` bits
+ * (code k at bits [bits*k, bits*k + bits)); scales [N, K/G] (F32 or F16); zeros [N, K/G]
+ * (F16/F32) or nullptr with a fixed `offset`:  w[n,k] = (float(code) - zero) * scale.
+ * The reference layout is zeros = nullptr, offset 4 (int3) / 1 (int2), F32 scales, G = 128
+ * (src/mrun/engine/kernels/qstore_int3.py:30-56, qstore_int2.py:24-63); the asymmetric
+ * G = 64 variant passes F16 scales and F16 zero points. */
+
+/* Replaces _dequant_int3 / _dequant_int2 (src/mrun/engine/kernels/qstore.py:441-456):
+ * out[n,k] = (float(code) - zero) * scale in fp32, bit-exact.  bits 2, 3 or 4. */
+int qs_lowbit_dequant(const uint8_t* packed, int64_t row_bytes, const void* scales,
+                      int scale_dtype, const void* zeros, int zero_dtype, float offset, int bits,
+                      int group_size, float* out, int64_t N, int64_t K, void* stream);
+
+/* Workspace bytes qs_lowbit_gemv needs for these dimensions. */
+size_t qs_lowbit_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int group_size);
+
+/* Replaces QStoreInt3.matmul / QStoreInt2.matmul (qstore.py:1318-1341, 1451-1474):
+ * y[m,n] = sum_k x[m,k] * w[n,k] in fp32, y F32 [M, N].  x BF16 or F32; bits 2 or 3;
+ * group_size 64 or 128; K % group_size == 0; rows 4-byte aligned.  workspace: device
+ * memory of at least qs_lowbit_workspace_bytes(...) bytes, contents clobbered. */
+int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uint8_t* packed,
+                   int64_t row_bytes, const void* scales, int scale_dtype, const void* zeros,
+                   int zero_dtype, float offset, int bits, int group_size, float* y, int64_t ldy,
+                   int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -34,6 +34,9 @@ COMMON_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # products and sums round separately unless a kernel asks for fmaf explicitly (the
+    # reference's epilogues and reducers are unfused fp32 operations)
+    "-ffp-contract=off",
     "-Wno-unused-command-line-argument",
     f"-I{PKG_DIR.parent / 'include'}",
 ]

@@ -1,0 +1,482 @@
+// Routed-MoE hot path on gfx950: router, route compiler, routed-row quantization, ragged
+// grouped int8 GEMM (W8A8, optional fused SwiGLU epilogue, slot indirection) and the
+// fixed-rank-order reducer.
+//
+// Kernels
+//   k_moe_router      : one wave per token: fp32 softmax over E logits, top-k (ties ->
+//                       lower expert id), optional renormalisation, weights as fp32/bf16.
+//   k_moe_route       : one workgroup; expert histogram, exclusive prefix and a STABLE
+//                       expert-major scatter (wave ballots give each assignment its rank
+//                       among earlier same-expert assignments), so the queue order equals
+//                       the reference's stable argsort and is identical on every call.
+//   k_moe_gather_quant: per routed row, int8 per-token quantization of source[token_ids[a]]
+//                       (the W8A8 recipe: s = max|x|/127, 0 -> 1; rint; clamp +-127).
+//   k_moe_gemm<...>   : one workgroup per (group, 16-row tile of N); its waves split K, hold
+//                       their weight slice in VGPRs (streamed once from HBM with 128-bit
+//                       loads) and walk the group's rows 16 at a time with
+//                       v_mfma_i32_16x16x64_i8; LDS reduction over the K split; epilogue
+//                       (float(acc) * a_scale[row]) * w_scale[n] -> bf16/fp32, or the
+//                       paired SwiGLU of gate row n and up row n + N.
+//   k_moe_reduce      : out[t, :] = sum over rank r of float(y[inv[t*k + r], :]) *
+//                       coef[inv[t*k + r]], each product rounded, summed in rank order.
+#include "qs_common.h"
+
+namespace qs {
+
+// ----------------------------------------------------------------------------------
+// router
+// ----------------------------------------------------------------------------------
+template <int XT>
+__device__ __forceinline__ float ld(const void* p, int64_t i) {
+  if constexpr (XT == QS_F32) return static_cast<const float*>(p)[i];
+  else return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// E <= 1024 (16 per lane), k <= 16.
+template <int XT>
+__global__ __launch_bounds__(256) void k_moe_router(const void* __restrict__ logits, int T, int E,
+                                                    int k, int norm, int64_t* __restrict__ idx,
+                                                    void* __restrict__ w, int w_dtype) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float v[16];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? ld<XT>(logits, (int64_t)t * E + e) : -INFINITY;
+    mx = fmaxf(mx, v[j]);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? expf(v[j] - mx) : 0.f;
+    sum += v[j];
+  }
+  sum = wave_sum(sum);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = v[j] / sum;
+  float picked[16];
+  int pidx[16];
+  float tot = 0.f;
+  for (int r = 0; r < k; ++r) {
+    float best = -1.f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E && (v[j] > best || (v[j] == best && e < bi))) {
+        best = v[j];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ob = __shfl_xor(best, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ob > best || (ob == best && oi < bi)) {
+        best = ob;
+        bi = oi;
+      }
+    }
+    picked[r] = best;
+    pidx[r] = bi;
+    tot += best;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (lane + 64 * j == bi) v[j] = -2.f;  // exclude
+  }
+  if (lane == 0) {
+    // renormalisation divides by the fp32 sum of the kept weights, summed in rank order
+    float s = 0.f;
+    for (int r = 0; r < k; ++r) s += picked[r];
+    for (int r = 0; r < k; ++r) {
+      const float wr = norm ? picked[r] / s : picked[r];
+      idx[(int64_t)t * k + r] = pidx[r];
+      if (w_dtype == QS_F32)
+        static_cast<float*>(w)[(int64_t)t * k + r] = wr;
+      else
+        static_cast<uint16_t*>(w)[(int64_t)t * k + r] = f32_to_bf16_bits(wr);
+    }
+  }
+  (void)tot;
+}
+
+// ----------------------------------------------------------------------------------
+// route compiler (single workgroup, 1024 threads = 16 waves)
+// ----------------------------------------------------------------------------------
+constexpr int kRouteWaves = 16;
+constexpr int kRouteMaxE = 512;
+
+__device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
+
+template <int IT, int WT>
+__global__ __launch_bounds__(1024) void k_moe_route(const void* __restrict__ top_idx,
+                                                    const void* __restrict__ top_w, int A, int k,
+                                                    int E, int64_t* __restrict__ token_ids,
+                                                    float* __restrict__ coef,
+                                                    int32_t* __restrict__ starts,
+                                                    int32_t* __restrict__ counts,
+                                                    int64_t* __restrict__ inverse) {
+  __shared__ int cnt[kRouteWaves][kRouteMaxE];
+  __shared__ int base[kRouteMaxE];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  auto expert_of = [&](int i) -> int {
+    if constexpr (IT == QS_I64) return (int)static_cast<const int64_t*>(top_idx)[i];
+    else return static_cast<const int32_t*>(top_idx)[i];
+  };
+  for (int i = tid; i < kRouteWaves * kRouteMaxE; i += 1024) (&cnt[0][0])[i] = 0;
+  __syncthreads();
+  // wave w owns the contiguous assignment range [lo, hi)
+  const int segs = (A + 63) / 64;
+  const int per = (segs + kRouteWaves - 1) / kRouteWaves;
+  const int lo = wave * per * 64;
+  const int hi = min(A, (wave + 1) * per * 64);
+  for (int i = lo + lane; i < hi; i += 64) {
+    const int e = expert_of(i);
+    if (e >= 0 && e < E) atomicAdd(&cnt[wave][e], 1);
+  }
+  __syncthreads();
+  // per expert: total count, exclusive prefix over experts, per-wave bases
+  if (tid < E) {
+    int c = 0;
+    for (int w = 0; w < kRouteWaves; ++w) c += cnt[w][tid];
+    base[tid] = c;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = base[e];
+      counts[e] = c;
+      starts[e] = run;
+      base[e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  if (tid < E) {
+    int run = base[tid];
+    for (int w = 0; w < kRouteWaves; ++w) {
+      const int c = cnt[w][tid];
+      cnt[w][tid] = run;  // becomes wave w's cursor for expert tid
+      run += c;
+    }
+  }
+  __syncthreads();
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  for (int s0 = lo; s0 < hi; s0 += 64) {
+    const int i = s0 + lane;
+    const bool valid = i < hi;
+    const int e = valid ? expert_of(i) : -1;
+    const bool ok = valid && e >= 0 && e < E;
+    uint64_t match = ballot64(ok);
+    for (int b = 0; b < nbits; ++b) {
+      const uint64_t bb = ballot64(ok && ((e >> b) & 1));
+      match &= ((e >> b) & 1) ? bb : ~bb;
+    }
+    // match: lanes with the same expert (valid ones); my rank among lower lanes
+    const uint64_t lower = lane ? (~0ull >> (64 - lane)) : 0ull;
+    const int rank = __popcll(match & lower);
+    const int n_same = __popcll(match);
+    int dest = 0;
+    if (ok) dest = cnt[wave][e] + rank;
+    // the highest lane of each expert group advances the cursor (after everyone read it)
+    __builtin_amdgcn_wave_barrier();
+    if (ok && rank == n_same - 1) cnt[wave][e] += n_same;
+    __builtin_amdgcn_wave_barrier();
+    if (ok) {
+      token_ids[dest] = i / k;
+      float cw;
+      if constexpr (WT == QS_F32) cw = static_cast<const float*>(top_w)[i];
+      else cw = bf16_bits_to_f32(static_cast<const uint16_t*>(top_w)[i]);
+      coef[dest] = cw;
+      if (inverse) inverse[i] = dest;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// routed-row quantization
+// ----------------------------------------------------------------------------------
+template <int XT>
+__global__ __launch_bounds__(256) void k_moe_gather_quant(const void* __restrict__ src, int64_t lds_,
+                                                          const int64_t* __restrict__ rows, int H,
+                                                          int8_t* __restrict__ q,
+                                                          float* __restrict__ scale) {
+  const int64_t a = blockIdx.x;
+  const int64_t r = rows ? rows[a] : a;
+  const void* xr = static_cast<const char*>(src) + r * lds_ * (XT == QS_F32 ? 4 : 2);
+  float amax = 0.f;
+  for (int h = threadIdx.x; h < H; h += 256) amax = fmaxf(amax, fabsf(ld<XT>(xr, h)));
+  amax = wave_max(amax);
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float s = amax / 127.0f;
+  if (s == 0.f) s = 1.f;
+  if (threadIdx.x == 0) scale[a] = s;
+  for (int h = threadIdx.x; h < H; h += 256) {
+    float v = rintf(ld<XT>(xr, h) / s);
+    v = fminf(fmaxf(v, -127.f), 127.f);
+    q[a * H + h] = static_cast<int8_t>(v);
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// ragged grouped int8 GEMM
+// ----------------------------------------------------------------------------------
+struct MoeGemmParams {
+  const int8_t* a;       // [A, K] routed rows, expert-major
+  const float* as;       // [A]
+  const int8_t* w;       // group g weights at w + slot(g) * w_stride, [N_w, K] row-major
+  int64_t w_stride;      // bytes
+  const float* ws;       // group g scales at ws + slot(g) * ws_stride
+  int64_t ws_stride;     // floats
+  const int32_t* starts;
+  const int32_t* counts;
+  const int32_t* slots;  // nullable
+  int N;                 // output features (SwiGLU: half of the weight rows)
+  int K;
+  void* out;             // [A, N]
+  int out_dtype;
+};
+
+__device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + expf(-g))); }
+
+// P = 1: plain; P = 2: paired SwiGLU (plane 0 = gate row n, plane 1 = up row n + N).
+// KW waves per plane split K; each wave holds CH 64-k chunks of its 16 weight rows.
+template <int P, int KW, int CH>
+__global__ __launch_bounds__(P * KW * 64) void k_moe_gemm(MoeGemmParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int plane = wave % P;
+  const int ks = wave / P;
+  const int col = lane & 15, grp = lane >> 4;
+  const int g = blockIdx.y;
+  const int count = p.counts[g];
+  if (count == 0) return;
+  const int start = p.starts[g];
+  const int slot = p.slots ? p.slots[g] : g;
+  const int n0 = blockIdx.x * 16;
+  int n = n0 + col;
+  const bool nval = n < p.N;
+  n = nval ? n : p.N - 1;
+  const int wrow_idx = n + plane * p.N;
+  const int8_t* wrow = p.w + (int64_t)slot * p.w_stride + (int64_t)wrow_idx * p.K + 16 * grp;
+  const int C = p.K / 64;
+
+  // the wave's weight slice: chunks ks, ks + KW, ... (at most CH of them)
+  i32x4 wv[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int cc = ks + c * KW;
+    wv[c] = cc < C ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wrow + (int64_t)cc * 64))
+                   : i32x4{0, 0, 0, 0};
+  }
+  const float wsc = p.ws[(int64_t)slot * p.ws_stride + wrow_idx];
+
+  __shared__ i32x4 red[P * KW][64];
+  for (int m0 = 0; m0 < count; m0 += 16) {
+    const int m = m0 + col;
+    const bool mval = m < count;
+    const int8_t* arow = p.a + (int64_t)(start + (mval ? m : 0)) * p.K + 16 * grp;
+    i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int cc = ks + c * KW;
+      if (cc < C) {
+        const i32x4 av = mval ? *reinterpret_cast<const i32x4*>(arow + (int64_t)cc * 64) : i32x4{0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, wv[c], acc, 0, 0, 0);
+      }
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+      i32x4 tot[P];
+#pragma unroll
+      for (int pl = 0; pl < P; ++pl) {
+        i32x4 s = red[pl][lane];
+#pragma unroll
+        for (int k2 = 1; k2 < KW; ++k2) s += red[k2 * P + pl][lane];
+        tot[pl] = s;
+      }
+      const int no = n0 + col;
+      if (no < p.N) {
+        float sc[P];
+#pragma unroll
+        for (int pl = 0; pl < P; ++pl)
+          sc[pl] = p.ws[(int64_t)slot * p.ws_stride + no + pl * p.N];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int mr = m0 + 4 * grp + q;
+          if (mr < count) {
+            const int64_t row = start + mr;
+            const float a_s = p.as[row];
+            if constexpr (P == 2) {
+              const float gv = mul_rn(mul_rn(static_cast<float>(tot[0][q]), a_s), sc[0]);
+              const float uv = mul_rn(mul_rn(static_cast<float>(tot[1][q]), a_s), sc[1]);
+              const float gt = bf16_bits_to_f32(f32_to_bf16_bits(gv));
+              const float ut = bf16_bits_to_f32(f32_to_bf16_bits(uv));
+              const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f(gt)));
+              static_cast<uint16_t*>(p.out)[row * p.N + no] = f32_to_bf16_bits(mul_rn(sl, ut));
+            } else {
+              const float v = mul_rn(mul_rn(static_cast<float>(tot[0][q]), a_s), sc[0]);
+              if (p.out_dtype == QS_F32)
+                static_cast<float*>(p.out)[row * p.N + no] = v;
+              else
+                static_cast<uint16_t*>(p.out)[row * p.N + no] = f32_to_bf16_bits(v);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  (void)wsc;
+  (void)nval;
+}
+
+// ----------------------------------------------------------------------------------
+// stable rank-order reduce
+// ----------------------------------------------------------------------------------
+template <int YT>
+__global__ __launch_bounds__(256) void k_moe_reduce(const void* __restrict__ y,
+                                                    const float* __restrict__ coef,
+                                                    const int64_t* __restrict__ inv, int k,
+                                                    int H, float* __restrict__ out) {
+  const int64_t t = blockIdx.y;
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  if (h >= H) return;
+  float acc = 0.f;
+  for (int r = 0; r < k; ++r) {
+    const int64_t a = inv[t * k + r];
+    const float v = ld<YT>(y, a * H + h);
+    const float c = mul_rn(v, coef[a]);
+    acc = r == 0 ? c : add_rn(acc, c);
+  }
+  out[t * H + h] = acc;
+}
+
+}  // namespace qs
+
+using namespace qs;
+
+extern "C" int qs_moe_router(const void* logits, int logit_dtype, int64_t T, int E, int k,
+                             int norm_topk, int64_t* top_idx, void* top_w, int w_dtype,
+                             void* stream) {
+  if (!logits || !top_idx || !top_w) return fail(QS_ERR_INVALID, "moe_router: null pointer");
+  if (T < 0 || E < 1 || E > 1024 || k < 1 || k > 16 || k > E)
+    return fail(QS_ERR_LIMIT, "moe_router: need 1 <= E <= 1024, 1 <= k <= min(16, E)");
+  if (w_dtype != QS_F32 && w_dtype != QS_BF16) return fail(QS_ERR_INVALID, "moe_router: weight dtype F32 or BF16");
+  if (T == 0) return QS_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned blocks = (unsigned)cdiv(T, 4);
+  if (logit_dtype == QS_F32)
+    hipLaunchKernelGGL(k_moe_router<QS_F32>, dim3(blocks), dim3(256), 0, s, logits, (int)T, E, k, norm_topk, top_idx, top_w, w_dtype);
+  else if (logit_dtype == QS_BF16)
+    hipLaunchKernelGGL(k_moe_router<QS_BF16>, dim3(blocks), dim3(256), 0, s, logits, (int)T, E, k, norm_topk, top_idx, top_w, w_dtype);
+  else
+    return fail(QS_ERR_INVALID, "moe_router: logits F32 or BF16");
+  return hip_check(hipGetLastError(), "k_moe_router launch");
+}
+
+extern "C" int qs_moe_route(const void* top_idx, int idx_dtype, const void* top_w, int w_dtype,
+                            int64_t T, int k, int E, int64_t* token_ids, float* coef,
+                            int32_t* starts, int32_t* counts, int64_t* inverse, void* stream) {
+  if (!top_idx || !top_w || !token_ids || !coef || !starts || !counts)
+    return fail(QS_ERR_INVALID, "moe_route: null pointer");
+  if (T < 0 || k < 1 || E < 1) return fail(QS_ERR_INVALID, "moe_route: bad shape");
+  if (E > kRouteMaxE) return fail(QS_ERR_LIMIT, "moe_route: at most %d experts", kRouteMaxE);
+  if (T * k > (int64_t)1 << 28) return fail(QS_ERR_LIMIT, "moe_route: too many assignments");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int A = (int)(T * k);
+#define QS_ROUTE(IT, WT) \
+  hipLaunchKernelGGL((k_moe_route<IT, WT>), dim3(1), dim3(1024), 0, s, top_idx, top_w, A, k, E, token_ids, coef, starts, counts, inverse)
+  if (idx_dtype == QS_I64 && w_dtype == QS_F32) QS_ROUTE(QS_I64, QS_F32);
+  else if (idx_dtype == QS_I64 && w_dtype == QS_BF16) QS_ROUTE(QS_I64, QS_BF16);
+  else if (idx_dtype == QS_I32 && w_dtype == QS_F32) QS_ROUTE(QS_I32, QS_F32);
+  else if (idx_dtype == QS_I32 && w_dtype == QS_BF16) QS_ROUTE(QS_I32, QS_BF16);
+  else return fail(QS_ERR_INVALID, "moe_route: indices I32/I64, weights F32/BF16");
+#undef QS_ROUTE
+  return hip_check(hipGetLastError(), "k_moe_route launch");
+}
+
+extern "C" int qs_moe_gather_quant(const void* source, int src_dtype, int64_t ld_src,
+                                   const int64_t* rows, int64_t A, int64_t H, int8_t* q,
+                                   float* scale, void* stream) {
+  if (!source || !q || !scale) return fail(QS_ERR_INVALID, "moe_gather_quant: null pointer");
+  if (A < 0 || H <= 0 || ld_src < H) return fail(QS_ERR_INVALID, "moe_gather_quant: bad shape");
+  if (A == 0) return QS_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (src_dtype == QS_BF16)
+    hipLaunchKernelGGL(k_moe_gather_quant<QS_BF16>, dim3((unsigned)A), dim3(256), 0, s, source, ld_src, rows, (int)H, q, scale);
+  else if (src_dtype == QS_F32)
+    hipLaunchKernelGGL(k_moe_gather_quant<QS_F32>, dim3((unsigned)A), dim3(256), 0, s, source, ld_src, rows, (int)H, q, scale);
+  else
+    return fail(QS_ERR_INVALID, "moe_gather_quant: source F32 or BF16");
+  return hip_check(hipGetLastError(), "k_moe_gather_quant launch");
+}
+
+namespace {
+template <int P, int KW>
+void launch_moe_gemm(const MoeGemmParams& p, int G, hipStream_t s) {
+  const int C = p.K / 64;
+  const int ch = (C + KW - 1) / KW;
+  dim3 grid((unsigned)cdiv(p.N, 16), (unsigned)G);
+  if (ch <= 2) hipLaunchKernelGGL((k_moe_gemm<P, KW, 2>), grid, dim3(P * KW * 64), 0, s, p);
+  else if (ch <= 4) hipLaunchKernelGGL((k_moe_gemm<P, KW, 4>), grid, dim3(P * KW * 64), 0, s, p);
+  else hipLaunchKernelGGL((k_moe_gemm<P, KW, 8>), grid, dim3(P * KW * 64), 0, s, p);
+}
+}  // namespace
+
+extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* w,
+                                      int64_t w_stride, const float* w_scale, int64_t ws_stride,
+                                      const int32_t* starts, const int32_t* counts,
+                                      const int32_t* slots, int G, int64_t N, int64_t K,
+                                      int swiglu, void* out, int out_dtype, void* stream) {
+  if (!a || !a_scale || !w || !w_scale || !starts || !counts || !out)
+    return fail(QS_ERR_INVALID, "moe_grouped_gemm: null pointer");
+  if (G < 1 || G > 65535 || N <= 0 || K <= 0) return fail(QS_ERR_INVALID, "moe_grouped_gemm: bad shape");
+  if (K % 64 != 0 || K > 64 * 64 * 8) return fail(QS_ERR_UNSUPPORTED, "moe_grouped_gemm: K must be a multiple of 64, <= 32768");
+  if (!aligned(a, 16) || !aligned(w, 16) || w_stride % 16 != 0)
+    return fail(QS_ERR_UNSUPPORTED, "moe_grouped_gemm: operands must be 16-byte aligned");
+  if (swiglu && out_dtype != QS_BF16) return fail(QS_ERR_INVALID, "moe_grouped_gemm: SwiGLU output is BF16");
+  if (out_dtype != QS_BF16 && out_dtype != QS_F32) return fail(QS_ERR_INVALID, "moe_grouped_gemm: out F32 or BF16");
+  MoeGemmParams p{a, a_scale, w, w_stride, w_scale, ws_stride, starts, counts, slots, (int)N, (int)K, out, out_dtype};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int C = (int)(K / 64);
+  if (swiglu) {
+    if (C <= 16) launch_moe_gemm<2, 4>(p, G, s);
+    else launch_moe_gemm<2, 8>(p, G, s);
+  } else {
+    if (C <= 16) launch_moe_gemm<1, 4>(p, G, s);
+    else if (C <= 32) launch_moe_gemm<1, 8>(p, G, s);
+    else launch_moe_gemm<1, 16>(p, G, s);
+  }
+  return hip_check(hipGetLastError(), "k_moe_gemm launch");
+}
+
+extern "C" int qs_moe_route_reduce(const void* expert_out, int y_dtype, const float* coef,
+                                   const int64_t* inverse, int64_t T, int k, int64_t H,
+                                   float* out, void* stream) {
+  if (!expert_out || !coef || !inverse || !out) return fail(QS_ERR_INVALID, "moe_route_reduce: null pointer");
+  if (T < 0 || k < 1 || H <= 0 || T > 65535 * 1024) return fail(QS_ERR_INVALID, "moe_route_reduce: bad shape");
+  if (T == 0) return QS_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)cdiv(H, 256), (unsigned)T);
+  if (y_dtype == QS_BF16)
+    hipLaunchKernelGGL(k_moe_reduce<QS_BF16>, grid, dim3(256), 0, s, expert_out, coef, inverse, k, (int)H, out);
+  else if (y_dtype == QS_F32)
+    hipLaunchKernelGGL(k_moe_reduce<QS_F32>, grid, dim3(256), 0, s, expert_out, coef, inverse, k, (int)H, out);
+  else
+    return fail(QS_ERR_INVALID, "moe_route_reduce: expert output F32 or BF16");
+  return hip_check(hipGetLastError(), "k_moe_reduce launch");
+}

@@ -1,0 +1,131 @@
+"""Oracle: routed MoE with int8 experts (numpy, CPU).
+
+Restates (reference paths relative to /root/reference):
+* ``router``            -- qwen3_moe_cuda.py:3702-3707 (softmax fp32, top-k, renormalise,
+                           cast to the model dtype)
+* ``route_stable``      -- CPU branch of ``_grouped_route_tensors_impl`` olmoe_cuda.py:1063-1090
+                           (stable argsort, bincount, exclusive prefix, inverse)
+* ``quantize_rows``     -- per-row absmax/127 int8 codec (w8a8.py:118-121 recipe; the int8
+                           analogue of ``quantize_fp8_activation`` olmoe_cuda.py:1173-1176)
+* ``grouped_int8_mm``   -- per-group exact int GEMM with the epilogue
+                           ``(acc * a_scale[m]) * w_scale[n]`` (olmoe_cuda.py:185-238)
+* ``stable_route_reduce`` -- CPU branch qwen3_moe_cuda.py:2655-2664
+* ``moe_forward``       -- the W8A8-shaped expert flow of FP8ExpertBackend.moe
+                           (olmoe_cuda.py:1308-1420) with the stable reducer
+                           (qwen3_moe_cuda.py:2911-2920) and bf16 boundaries
+* ``moe_dense_reference`` -- per-expert float math of streamed_moe_forward
+                           (moe_safetensors.py:603-627), weights dequantized to fp32
+
+Pinned by (tests/test_oracle_moe.py): the reference KATs test_olmoe_cuda.py:73-112 and
+test_qwen3_moe_cuda.py:1140-1241 (counts/starts/token ids/coefficients, inverse bijection,
+reduce == index_add and invariance under within-group permutation); numpy/torch library
+routines for the router; exact integer brute force for the grouped GEMM; the dense fp32
+per-expert formulation for the whole layer (tolerance).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .qrow import round_bf16, silu_f32
+from .w8a8 import act_quant, int8_gemm
+
+
+def router(logits: np.ndarray, k: int, norm_topk: bool = True, bf16: bool = True):
+    p = np.asarray(logits, dtype=np.float32)
+    p = p - p.max(axis=-1, keepdims=True)
+    e = np.exp(p).astype(np.float32)
+    prob = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
+    order = np.argsort(-prob, axis=-1, kind="stable")[:, :k]
+    w = np.take_along_axis(prob, order, axis=-1).astype(np.float32)
+    if norm_topk:
+        w = (w / w.sum(axis=-1, keepdims=True)).astype(np.float32)
+    if bf16:
+        w = round_bf16(w)
+    return w, order.astype(np.int64)
+
+
+def route_stable(top_indices: np.ndarray, top_weights: np.ndarray, num_experts: int):
+    ti = np.asarray(top_indices).reshape(-1).astype(np.int64)
+    tw = np.asarray(top_weights, dtype=np.float32).reshape(-1)
+    rows, k = np.asarray(top_indices).shape
+    order = np.argsort(ti, kind="stable")
+    token_ids = (np.arange(rows * k) // k)[order].astype(np.int64)
+    coef = tw[order]
+    counts = np.bincount(ti, minlength=num_experts).astype(np.int32)
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]]).astype(np.int32)
+    inverse = np.empty(rows * k, dtype=np.int64)
+    inverse[order] = np.arange(rows * k)
+    return token_ids, coef, starts, counts, inverse
+
+
+def quantize_rows(x: np.ndarray):
+    return act_quant(np.asarray(x, dtype=np.float32))
+
+
+def grouped_int8_mm(rows_q, row_scales, weights, weight_scales, starts, counts, *, slots=None,
+                    swiglu: bool = False, out_bf16: bool = True, acc_out: list | None = None):
+    rows_q = np.asarray(rows_q)
+    G = len(starts)
+    n_w = weights.shape[1]
+    n_out = n_w // 2 if swiglu else n_w
+    out = np.zeros((rows_q.shape[0], n_out), dtype=np.float32)
+    for g in range(G):
+        s0, c = int(starts[g]), int(counts[g])
+        if c == 0:
+            continue
+        slot = g if slots is None else int(slots[g])
+        acc = int8_gemm(rows_q[s0 : s0 + c], weights[slot])
+        if acc_out is not None:
+            acc_out.append((g, acc))
+        v = (acc.astype(np.float32) * row_scales[s0 : s0 + c, None]).astype(np.float32) * weight_scales[slot][None, :]
+        v = v.astype(np.float32)
+        if swiglu:
+            gt = round_bf16(v[:, :n_out])
+            ut = round_bf16(v[:, n_out:])
+            out[s0 : s0 + c] = round_bf16(round_bf16(silu_f32(gt)) * ut)
+        else:
+            out[s0 : s0 + c] = round_bf16(v) if out_bf16 else v
+    return out
+
+
+def stable_route_reduce(expert_output, coefficients, inverse, rows: int, k: int):
+    eo = np.asarray(expert_output, dtype=np.float32)
+    cf = np.asarray(coefficients, dtype=np.float32)
+    inv = np.asarray(inverse).reshape(rows, k)
+    contrib = (eo[inv] * cf[inv][..., None]).astype(np.float32)
+    out = contrib[:, 0].copy()
+    for r in range(1, k):
+        out = (out + contrib[:, r]).astype(np.float32)
+    return out
+
+
+def moe_forward(source, top_indices, top_weights, gate_up, gate_up_scales, down, down_scales):
+    """int8 expert layer, returns bf16-rounded fp32 [T, H]."""
+    E = gate_up.shape[0]
+    rows, k = top_indices.shape
+    token_ids, coef, starts, counts, inverse = route_stable(top_indices, top_weights, E)
+    q, s = quantize_rows(np.asarray(source, dtype=np.float32)[token_ids])
+    act = grouped_int8_mm(q, s, gate_up, gate_up_scales, starts, counts, swiglu=True)
+    q2, s2 = quantize_rows(act)
+    y = grouped_int8_mm(q2, s2, down, down_scales, starts, counts)
+    return round_bf16(stable_route_reduce(y, coef, inverse, rows, k))
+
+
+def moe_dense_reference(source, top_indices, top_weights, gate_up, gate_up_scales, down, down_scales):
+    """Float per-expert math (moe_safetensors.py:603-627) on fp32-dequantized weights."""
+    x = np.asarray(source, dtype=np.float64)
+    T, H = x.shape
+    out = np.zeros((T, H), dtype=np.float64)
+    I = gate_up.shape[1] // 2
+    for e in np.unique(top_indices):
+        sel = top_indices == e
+        tok = sel.any(-1)
+        w_e = (np.asarray(top_weights, np.float64) * sel).sum(-1)[tok]
+        Wgu = gate_up[e].astype(np.float64) * gate_up_scales[e][:, None]
+        Wd = down[e].astype(np.float64) * down_scales[e][:, None]
+        gu = x[tok] @ Wgu.T
+        g, u = gu[:, :I], gu[:, I:]
+        act = g / (1 + np.exp(-g)) * u
+        out[tok] += w_e[:, None] * (act @ Wd.T)
+    return out

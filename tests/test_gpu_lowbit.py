@@ -1,0 +1,120 @@
+"""GPU parity of the packed int3/int2 kernels against the CPU oracle (through the C ABI)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import lowbit as ol
+from oracle import qrow as oq
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+
+
+def _lb():
+    from mrun_pub_amd import lowbit
+
+    return lowbit
+
+
+def _page(dev, packed, scales, K, bits, G, zeros=None):
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    return _lb().LowbitPage("w", bits, G, K, t(packed), t(scales), None if zeros is None else t(zeros))
+
+
+def _sym(rng, N, K, bits, G=128):
+    codes = rng.integers(1 if bits == 3 else 0, 8 if bits == 3 else 3, size=(N, K), dtype=np.uint8)
+    scales = rng.uniform(0.001, 0.02, size=(N, K // G)).astype(np.float32)
+    return ol.pack_codes(codes, bits), scales
+
+
+def _asym(rng, N, K, bits, G=64):
+    lvl = (1 << bits) - 1
+    codes = rng.integers(0, lvl + 1, size=(N, K), dtype=np.uint8)
+    s = (rng.uniform(0.5, 1.5, size=(N, K // G)) / lvl).astype(np.float16)
+    z = rng.uniform(0, lvl, size=(N, K // G)).astype(np.float16)
+    return ol.pack_codes(codes, bits), s, z
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("K,G", [(17, 4), (256, 128), (192, 64)])
+def test_dequant_bit_exact(dev, bits, K, G):
+    rng = np.random.default_rng(bits * K)
+    W = rng.standard_normal((9, K)).astype(np.float32)
+    packed, scales = (ol.quant_row_int3 if bits == 3 else ol.quant_row_int2)(W, G=G)
+    got = _lb().lowbit_dequant(_page(dev, packed, scales, K, bits, G)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ol.dequant(packed, scales, K, bits, G).view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_dequant_asym_bit_exact(dev, bits):
+    rng = np.random.default_rng(bits)
+    packed, s, z = _asym(rng, 33, 256, bits)
+    got = _lb().lowbit_dequant(_page(dev, packed, s, 256, bits, 64, z)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ol.dequant(packed, s, 256, bits, 64, zeros=z).view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("N,K", [(11008, 4096), (4096, 11008), (40, 384)])
+@pytest.mark.parametrize("m", [1, 8])
+def test_gemv_asym_g64_bf16_config5(dev, bits, N, K, m):
+    """G=64 asymmetric fp16 scale/zero, bf16 activations [1..8, K]."""
+    rng = np.random.default_rng(bits + N + m)
+    packed, s, z = _asym(rng, N, K, bits)
+    x = oq.round_bf16(rng.standard_normal((m, K)).astype(np.float32))
+    y = _lb().lowbit_matmul(_page(dev, packed, s, K, bits, 64, z), torch.from_numpy(x).to(dev).to(torch.bfloat16))
+    assert y.dtype == torch.float32 and y.shape == (m, N)
+    ref = ol.lowbit_matmul(packed, s, x, K, bits, 64, zeros=z)
+    assert oq.rel_l2(y.cpu().numpy(), ref) <= F32_TOL
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("m", [1, 3, 7, 20])
+def test_gemv_reference_layout(dev, bits, xdt, m):
+    """Reference layout: symmetric codes, fixed offset, fp32 scales, G=128; fp32 output."""
+    rng = np.random.default_rng(bits * 100 + m)
+    N, K = 1000, 1024
+    packed, scales = _sym(rng, N, K, bits)
+    x = rng.standard_normal((m, K)).astype(np.float32)
+    xt = torch.from_numpy(x).to(xdt)
+    y = _lb().lowbit_matmul(_page(dev, packed, scales, K, bits, 128), xt.to(dev))
+    ref = ol.lowbit_matmul(packed, scales, xt.float().numpy(), K, bits, 128)
+    assert oq.rel_l2(y.cpu().numpy(), ref) <= F32_TOL
+
+
+def test_rows_independent_of_batch(dev):
+    rng = np.random.default_rng(9)
+    packed, s, z = _asym(rng, 512, 1024, 3)
+    x = torch.from_numpy(rng.standard_normal((8, 1024)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    page = _page(dev, packed, s, 1024, 3, 64, z)
+    full = _lb().lowbit_matmul(page, x)
+    for r in (0, 3, 7):
+        assert torch.equal(_lb().lowbit_matmul(page, x[r : r + 1])[0], full[r])
+
+
+def test_reference_store_reader(dev, tmp_path):
+    # the same on-disk layout the reference's QStoreInt3 test writes (test_qstore_int3.py:24-56)
+    import json
+
+    rng = np.random.default_rng(1)
+    W = rng.standard_normal((70, 256)).astype(np.float32)
+    packed, scales = ol.quant_row_int3(W, G=128)
+    d = tmp_path / "toy-int3"
+    d.mkdir()
+    (d / "weights.i3").write_bytes(packed.tobytes())
+    (d / "scales.f32").write_bytes(scales.tobytes())
+    (d / "extras.f32").write_bytes(np.zeros(1, np.float32).tobytes())
+    (d / "manifest.json").write_text(json.dumps({
+        "model_name": "toy", "arch": "qwen2", "dtype": "int3", "group_size": 128, "config": {},
+        "blocks": {"W": {"kind": "qrow3", "shape": [70, 256], "w_off": 0, "row_bytes": packed.shape[1],
+                         "s_off": 0, "n_groups": scales.shape[1], "group_size": 128},
+                   "W2": {"alias": "W"}}}))
+    store = _lb().DeviceLowbitQStore(d, device=dev)
+    x = rng.standard_normal((3, 256)).astype(np.float32)
+    y = store.matmul("W2", torch.from_numpy(x).to(dev))
+    assert oq.rel_l2(y.cpu().numpy(), ol.lowbit_matmul(packed, scales, x, 256, 3, 128)) <= F32_TOL
+    assert np.array_equal(store.weight("W").cpu().numpy(), ol.dequant(packed, scales, 256, 3, 128))

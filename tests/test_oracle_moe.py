@@ -1,0 +1,125 @@
+"""Pins the MoE oracle (CPU) against the reference's own KATs and closed forms."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import moe as om
+from oracle import qrow as oq
+
+
+def test_reference_kat_grouped_route_tensors():
+    # reference tests/test_olmoe_cuda.py:73-91
+    indices = np.array([[3, 1], [1, 2], [3, 2]], dtype=np.int64)
+    weights = np.array([[0.7, 0.3], [0.6, 0.4], [0.8, 0.2]], dtype=np.float32)
+    token_ids, coef, starts, counts, inverse = om.route_stable(indices, weights, 5)
+    assert counts.tolist() == [0, 2, 2, 2, 0]
+    assert starts.tolist() == [0, 0, 2, 4, 6]
+    assert token_ids.tolist() == [0, 1, 1, 2, 0, 2]
+    np.testing.assert_array_equal(coef, np.array([0.3, 0.6, 0.4, 0.2, 0.7, 0.8], np.float32))
+
+
+def test_reference_kat_inverse_bijection():
+    # reference tests/test_olmoe_cuda.py:94-112
+    indices = np.array([[3, 1], [1, 2], [3, 2]], dtype=np.int64)
+    weights = np.array([[0.7, 0.3], [0.6, 0.4], [0.8, 0.2]], dtype=np.float32)
+    token_ids, coef, starts, counts, inverse = om.route_stable(indices, weights, 5)
+    assert sorted(inverse.tolist()) == list(range(indices.size))
+    for original, dest in enumerate(inverse.tolist()):
+        token, rank = divmod(original, indices.shape[1])
+        expert = int(indices[token, rank])
+        assert token_ids[dest] == token
+        assert starts[expert] <= dest < starts[expert] + counts[expert]
+        assert coef[dest] == weights[token, rank]
+
+
+def test_reference_kat_compact_route():
+    # reference tests/test_qwen3_moe_cuda.py:1140-1153
+    top = np.array([[7, 2], [9, 7]])
+    sel = np.array([2, 7, 9])
+    compact = np.searchsorted(sel, top)
+    token_ids, coef, starts, counts, _ = om.route_stable(compact, np.array([[0.7, 0.3], [0.6, 0.4]], np.float32), 3)
+    assert counts.tolist() == [1, 2, 1] and starts.tolist() == [0, 1, 3]
+    assert sorted(token_ids.tolist()) == [0, 0, 1, 1]
+
+
+def test_reference_kat_stable_reduce_equals_index_add_and_is_order_invariant():
+    # reference tests/test_qwen3_moe_cuda.py:1155-1241
+    top = np.array([[2, 0], [1, 2]])
+    w = np.array([[0.7, 0.3], [0.6, 0.4]], np.float32)
+    token_ids, coef, starts, counts, inverse = om.route_stable(top, w, 3)
+    eo = np.array([[1.0, 2.0], [3.0, 4.0], [5.0, 6.0], [7.0, 8.0]], np.float32)
+    expected = torch.zeros((2, 2), dtype=torch.float32)
+    expected.index_add_(0, torch.from_numpy(token_ids), torch.from_numpy(eo * coef[:, None]))
+    got = om.stable_route_reduce(eo, coef, inverse, 2, 2)
+    np.testing.assert_allclose(got, expected.numpy(), rtol=1e-6, atol=0)
+    # reverse the two rows of expert group 2, carrying the inverse along
+    perm = np.array([0, 1, 3, 2])
+    old_to_new = np.empty_like(perm)
+    old_to_new[perm] = np.arange(4)
+    again = om.stable_route_reduce(eo[perm], coef[perm], old_to_new[inverse], 2, 2)
+    assert np.array_equal(again, got)
+
+
+def test_stable_route_is_a_stable_sort_on_random_routes():
+    rng = np.random.default_rng(0)
+    top = np.stack([rng.permutation(16)[:4] for _ in range(50)])
+    w = rng.random(top.shape).astype(np.float32)
+    token_ids, coef, starts, counts, inverse = om.route_stable(top, w, 16)
+    flat = top.reshape(-1)
+    # queue rows of one expert keep ascending original assignment order
+    for e in range(16):
+        rows = np.nonzero(flat == e)[0]
+        assert inverse[rows].tolist() == list(range(starts[e], starts[e] + counts[e]))
+
+
+def test_router_matches_torch_library_routines():
+    rng = np.random.default_rng(1)
+    logits = rng.standard_normal((64, 128)).astype(np.float32)
+    w, idx = om.router(logits, 8)
+    p = torch.softmax(torch.from_numpy(logits), dim=-1)
+    tw, ti = p.topk(8, dim=-1)
+    tw = (tw / tw.sum(-1, keepdim=True)).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(idx, ti.numpy())
+    np.testing.assert_allclose(w, tw, rtol=1e-2, atol=1e-3)  # bf16 rounding of ulp-level differences
+
+
+def test_grouped_int8_mm_brute_force_and_slots():
+    rng = np.random.default_rng(2)
+    E, N, K = 3, 8, 64
+    w = rng.integers(-127, 128, size=(E, N, K), dtype=np.int8)
+    ws = rng.uniform(0.5, 1.5, size=(E, N)).astype(np.float32) / 127
+    counts = np.array([2, 0, 3], np.int32)
+    starts = np.array([0, 2, 2], np.int32)
+    a = rng.integers(-127, 128, size=(5, K), dtype=np.int8)
+    asc = rng.uniform(0.1, 1.0, size=5).astype(np.float32)
+    out = om.grouped_int8_mm(a, asc, w, ws, starts, counts, out_bf16=False)
+    for g, (s0, c) in enumerate(zip(starts, counts)):
+        for m in range(c):
+            for n in range(N):
+                acc = int(np.dot(a[s0 + m].astype(np.int64), w[g, n].astype(np.int64)))
+                assert out[s0 + m, n] == np.float32(np.float32(np.float32(acc) * asc[s0 + m]) * ws[g, n])
+    # slot indirection == compact weights
+    slots = np.array([2, 0, 1])
+    w_phys = w[[1, 2, 0]]
+    ws_phys = ws[[1, 2, 0]]
+    assert np.array_equal(
+        om.grouped_int8_mm(a, asc, w_phys, ws_phys, starts, counts, slots=slots, out_bf16=False), out
+    )
+
+
+def test_moe_forward_close_to_dense_float_reference():
+    rng = np.random.default_rng(3)
+    T, E, k, H, I = 16, 8, 2, 128, 64
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    w, idx = om.router(logits, k)
+    gu = rng.integers(-127, 128, size=(E, 2 * I, H), dtype=np.int8)
+    gus = (rng.uniform(0.5, 1.5, size=(E, 2 * I)) / 127 / np.sqrt(H)).astype(np.float32)
+    dn = rng.integers(-127, 128, size=(E, H, I), dtype=np.int8)
+    dns = (rng.uniform(0.5, 1.5, size=(E, H)) / 127 / np.sqrt(I)).astype(np.float32)
+    x = oq.round_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    got = om.moe_forward(x, idx, w, gu, gus, dn, dns)
+    ref = om.moe_dense_reference(x, idx, w, gu, gus, dn, dns)
+    # W8A8 quantisation of activations + bf16 boundaries: a few percent
+    assert oq.rel_l2(got, ref) < 0.05
