@@ -112,6 +112,115 @@ def cpu_baseline(seconds: float = 12.0, m: int = 1) -> dict:
     }
 
 
+def _graph_time(torch, stream, fn, calls: int, reps: int = 5) -> float:
+    """Seconds per call of ``fn`` (one launch sequence), captured ``calls`` times in a graph."""
+    with torch.cuda.stream(stream):
+        fn(0)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(calls):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / (reps * calls)
+
+
+def secondary_measurements(torch, dev, stream) -> dict:
+    """Configs 1, 3, 4, 5 of BASELINE.json, measured with HIP graphs on one stream."""
+    from mrun_pub_amd import lowbit, moe, qrow, w8a8
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    res = {}
+
+    # config 1: fp32 decode GEMV [1,1024] x [4096,1024], 128 distinct weight copies (> MALL)
+    n, k, copies = 4096, 1024, 128
+    codes = torch.randint(-127, 128, (copies, n, k), dtype=torch.int8, device=dev, generator=gen)
+    scales = (torch.rand(copies, n, device=dev, generator=gen) + 0.5) / 127
+    x = torch.randn(1, k, device=dev, generator=gen)
+    t = _graph_time(torch, stream, lambda i: qrow.qrow_matmul(codes[i % copies], scales[i % copies], x), 64)
+    b = n * k + n * 4 + 4 * k + 4 * n
+    res["config1_fp32_gemv"] = {"us_per_call": round(t * 1e6, 3), "GB/s": round(b / t / 1e9, 1),
+                                "hbm_frac": round(b / t / 1e9 / HBM_PEAK_GBS, 4), "bytes": b}
+    del codes, scales
+
+    # config 3: W8A8 prefill, W [14336,4096], M in {512, 2048}, 0.1% outlier channels x20
+    N, K = 14336, 4096
+    qw = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen)
+    sw = (torch.rand(N, device=dev, generator=gen) + 0.5) / 127
+    for M in (512, 2048):
+        xb = torch.randn(M, K, device=dev, generator=gen)
+        xb[:, torch.randperm(K, device=dev, generator=gen)[:4]] *= 20.0
+        xb = xb.to(torch.bfloat16)
+        qx, asc = w8a8.quantize_activation(xb)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        from mrun_pub_amd import _native as nat
+
+        def gemm(_i):
+            nat.call("qs_w8a8_gemm", nat.ptr(qx), nat.ptr(asc), nat.ptr(qw), nat.ptr(sw), None, None, 0,
+                     nat.ptr(y), nat.QS_BF16, M, N, K, nat.stream_of(dev))
+
+        tg = _graph_time(torch, stream, gemm, 10)
+        tf = _graph_time(torch, stream, lambda i: w8a8.w8a8_matmul(qw, sw, xb, protect_k=8, out_dtype=torch.bfloat16), 10)
+        ops = 2 * M * N * K
+        res[f"config3_w8a8_m{M}"] = {
+            "gemm_us": round(tg * 1e6, 2), "gemm_TOPS": round(ops / tg / 1e12, 1),
+            "mfma_frac": round(ops / tg / 5.0e15, 4),
+            "w8a8_matmul_protect8_us": round(tf * 1e6, 2), "end_to_end_TOPS": round(ops / tf / 1e12, 1),
+        }
+    del qw, sw
+
+    # config 4: routed MoE, 128 experts top-8, H 2048, I 768, T in {64, 512}
+    E, topk, H, I = 128, 8, 2048, 768
+    layer = moe.Int8ExpertLayer.from_arrays(
+        torch.randint(-127, 128, (E, 2 * I, H), dtype=torch.int8, device=dev, generator=gen),
+        (torch.rand(E, 2 * I, device=dev, generator=gen) + 0.5) / 127,
+        torch.randint(-127, 128, (E, H, I), dtype=torch.int8, device=dev, generator=gen),
+        (torch.rand(E, H, device=dev, generator=gen) + 0.5) / 127, dev)
+    backend = moe.Int8ExpertBackend([layer])
+    page_bytes = layer.layout.gate_up_codes_bytes + layer.layout.gate_up_scales_bytes + \
+        layer.layout.down_codes_bytes + layer.layout.down_scales_bytes
+    for T in (64, 512):
+        logits = torch.randn(T, E, device=dev, generator=gen)
+        xs = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16)
+        tw, ti = moe.route_topk(logits, topk)
+        active = int(torch.unique(ti).numel())
+        tt = _graph_time(torch, stream, lambda i: backend.moe(0, xs, ti, tw), 10)
+        byts = active * page_bytes + T * H * 2 * 2
+        ops = 2 * T * topk * (2 * I * H + H * I)
+        res[f"config4_moe_t{T}"] = {"us": round(tt * 1e6, 2), "GB/s": round(byts / tt / 1e9, 1),
+                                    "hbm_frac": round(byts / tt / 1e9 / HBM_PEAK_GBS, 4),
+                                    "TOPS": round(ops / tt / 1e12, 2), "active_experts": active}
+    del layer, backend
+
+    # config 5: packed int3/int2 GEMV, G=64 fp16 scale+zero, [11008,4096] and [4096,11008]
+    for bits in (3, 2):
+        for (N5, K5) in ((11008, 4096), (4096, 11008)):
+            rb = K5 * bits // 8
+            ng = K5 // 64
+            copies = max(2, (512 << 20) // (N5 * rb) + 1)
+            packed = torch.randint(0, 256, (copies, N5, rb), dtype=torch.uint8, device=dev, generator=gen)
+            sc = ((torch.rand(copies, N5, ng, device=dev, generator=gen) + 0.5) / 7).to(torch.float16)
+            zp = (torch.rand(copies, N5, ng, device=dev, generator=gen) * 7).to(torch.float16)
+            pages = [lowbit.LowbitPage("w", bits, 64, K5, packed[c], sc[c], zp[c]) for c in range(copies)]
+            for M5 in (1, 8):
+                x5 = torch.randn(M5, K5, device=dev, generator=gen).to(torch.bfloat16)
+                t5 = _graph_time(torch, stream, lambda i: lowbit.lowbit_matmul(pages[i % copies], x5), 16)
+                b5 = N5 * rb + 2 * 2 * N5 * ng + 2 * M5 * K5 + 4 * M5 * N5
+                res[f"config5_int{bits}_{N5}x{K5}_m{M5}"] = {
+                    "us": round(t5 * 1e6, 2), "GB/s": round(b5 / t5 / 1e9, 1),
+                    "hbm_frac": round(b5 / t5 / 1e9 / HBM_PEAK_GBS, 4)}
+            del packed, sc, zp, pages
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +229,7 @@ def main() -> int:
     ap.add_argument("--m", type=int, default=1, help="decode tokens per pass (1, 4, 16, 32)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-secondary", action="store_true", help="skip configs 1/3/4/5")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -227,6 +337,9 @@ def main() -> int:
             "bytes_per_launch": swiglu_launch_bytes(m),
         },
     }
+    if not args.no_secondary:
+        del arena, pages, graph, sw_graph
+        out["secondary"] = secondary_measurements(torch, dev, stream)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds, m)
     print(json.dumps(out), flush=True)

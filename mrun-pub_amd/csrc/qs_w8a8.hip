@@ -68,25 +68,44 @@ __global__ __launch_bounds__(256) void k_act_quant(const void* __restrict__ x, i
   }
 }
 
+// Partial column maxima: block (bx, by) covers 256 columns x 64 rows and writes
+// part[by, k] = max over its rows of |x[m, k]|.
 template <int XT>
 __global__ __launch_bounds__(256) void k_col_absmax(const void* __restrict__ x, int64_t ldx,
-                                                    int M, int K, float* __restrict__ out) {
+                                                    int M, int K, float* __restrict__ part) {
   const int k = blockIdx.x * 256 + threadIdx.x;
   if (k >= K) return;
-  float amax = 0.f;
-  for (int m = 0; m < M; ++m) amax = fmaxf(amax, fabsf(load_x<XT>(x, (int64_t)m * ldx + k)));
-  out[k] = amax;
+  const int m0 = blockIdx.y * 64;
+  const int m1 = min(M, m0 + 64);
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int m = m0;
+  for (; m + 8 <= m1; m += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = fmaxf(a[j], fabsf(load_x<XT>(x, (int64_t)(m + j) * ldx + k)));
+  }
+  for (; m < m1; ++m) a[0] = fmaxf(a[0], fabsf(load_x<XT>(x, (int64_t)m * ldx + k)));
+  float r = a[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) r = fmaxf(r, a[j]);
+  part[(int64_t)blockIdx.y * K + k] = r;
 }
 
 // Single workgroup: kk rounds of a block-wide argmax over vals[0..K).  Selected entries
 // are excluded by index; ties go to the lower index.  Emits int64 indices (descending
 // value order) and the keep mask (1 everywhere, 0 at the selected columns).
-__global__ __launch_bounds__(1024) void k_topk(const float* __restrict__ vals, int K, int kk,
+// vals holds `parts` partial rows [parts, K]; they are first folded into row 0.
+__global__ __launch_bounds__(1024) void k_topk(float* __restrict__ vals, int K, int parts, int kk,
                                                int64_t* __restrict__ idx, float* __restrict__ keep) {
   __shared__ float bv[16];
   __shared__ int bi[16];
   __shared__ int chosen[64];
-  for (int k = threadIdx.x; k < K; k += 1024) keep[k] = 1.f;
+  for (int k = threadIdx.x; k < K; k += 1024) {
+    float v = vals[k];
+    for (int p = 1; p < parts; ++p) v = fmaxf(v, vals[(int64_t)p * K + k]);
+    vals[k] = v;
+    keep[k] = 1.f;
+  }
+  __syncthreads();
   for (int round = 0; round < kk; ++round) {
     float best = -1.f;
     int besti = 0x7fffffff;
@@ -393,17 +412,19 @@ extern "C" int qs_outlier_topk(const void* x, int x_dtype, int64_t ldx, int64_t 
   if (!x || !colmax || !idx || !keep) return fail(QS_ERR_INVALID, "outlier_topk: null pointer");
   if (M <= 0 || K <= 0 || ldx < K) return fail(QS_ERR_INVALID, "outlier_topk: bad shape");
   if (k < 1 || k > 64 || k > K) return fail(QS_ERR_LIMIT, "outlier_topk: k must be in 1..min(64, K)");
+  if (M > (int64_t)65535 * 64) return fail(QS_ERR_LIMIT, "outlier_topk: too many rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned blocks = (unsigned)cdiv(K, 256);
+  const int parts = (int)cdiv(M, 64);
+  const dim3 grid((unsigned)cdiv(K, 256), (unsigned)parts);
   if (x_dtype == QS_F32)
-    hipLaunchKernelGGL(k_col_absmax<QS_F32>, dim3(blocks), dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
+    hipLaunchKernelGGL(k_col_absmax<QS_F32>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
   else if (x_dtype == QS_BF16)
-    hipLaunchKernelGGL(k_col_absmax<QS_BF16>, dim3(blocks), dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
+    hipLaunchKernelGGL(k_col_absmax<QS_BF16>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
   else if (x_dtype == QS_F16)
-    hipLaunchKernelGGL(k_col_absmax<QS_F16>, dim3(blocks), dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
+    hipLaunchKernelGGL(k_col_absmax<QS_F16>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
   else
     return fail(QS_ERR_INVALID, "outlier_topk: dtype must be F32, BF16 or F16");
-  hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), 0, s, colmax, (int)K, k, idx, keep);
+  hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), 0, s, colmax, (int)K, parts, k, idx, keep);
   return hip_check(hipGetLastError(), "outlier_topk launch");
 }
 
