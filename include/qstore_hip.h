@@ -189,6 +189,31 @@ int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uint8_t* packe
                    int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+/* ---- pinned-host -> HBM page streaming -------------------------------------------------
+ * Replaces the CUDA prefetch ring _RingSlot / _RingPrefetch (src/mrun/engine/kernels/
+ * qstore.py:459-660: pinned staging, side-stream H2D, event + record_stream ordering) at
+ * the runtime level.  The ring is caller-owned device memory of slots * slot_bytes bytes
+ * (slot_bytes a multiple of 256); host sources must be pinned (hipHostMalloc / torch
+ * pin_memory).  Copies go out as page_bytes-sized hipMemcpyAsync calls on the pager's own
+ * copy stream (default priority).  Ordering is by events only: submit waits for the
+ * slot's last release, seal marks the slot ready, acquire makes a compute stream wait for
+ * ready, release marks the slot free once the compute stream's queued work is done. */
+typedef struct qs_pager qs_pager;
+
+int qs_pager_create(void* device_arena, size_t slot_bytes, int slots, size_t page_bytes,
+                    qs_pager** out);
+int qs_pager_destroy(qs_pager* pager);
+/* Device address of a slot (nullptr when out of range). */
+void* qs_pager_slot_ptr(qs_pager* pager, int slot);
+/* Queue host[0..bytes) -> slot[dst_offset..dst_offset+bytes) on the copy stream. */
+int qs_pager_submit(qs_pager* pager, int slot, const void* host, size_t bytes, size_t dst_offset);
+/* Mark the end of the slot's submissions (records its ready event). */
+int qs_pager_seal(qs_pager* pager, int slot);
+int qs_pager_acquire(qs_pager* pager, int slot, void* compute_stream);
+int qs_pager_release(qs_pager* pager, int slot, void* compute_stream);
+/* Block the host until every queued copy has landed. */
+int qs_pager_sync(qs_pager* pager);
+
 #ifdef __cplusplus
 }
 #endif

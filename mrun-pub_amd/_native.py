@@ -62,6 +62,14 @@ SIGNATURES: dict[str, tuple] = {
     "qs_lowbit_dequant": (_I, [_P, _L, _P, _I, _P, _I, ctypes.c_float, _I, _I, _P, _L, _L, _P]),
     "qs_lowbit_workspace_bytes": (ctypes.c_size_t, [_I, _L, _L, _L, _I]),
     "qs_lowbit_gemv": (_I, [_P, _I, _L, _P, _L, _P, _I, _P, _I, ctypes.c_float, _I, _I, _P, _L, _L, _L, _L, _P, ctypes.c_size_t, _P]),
+    "qs_pager_create": (_I, [_P, ctypes.c_size_t, _I, ctypes.c_size_t, ctypes.POINTER(_P)]),
+    "qs_pager_destroy": (_I, [_P]),
+    "qs_pager_slot_ptr": (_P, [_P, _I]),
+    "qs_pager_submit": (_I, [_P, _I, _P, ctypes.c_size_t, ctypes.c_size_t]),
+    "qs_pager_seal": (_I, [_P, _I]),
+    "qs_pager_acquire": (_I, [_P, _I, _P]),
+    "qs_pager_release": (_I, [_P, _I, _P]),
+    "qs_pager_sync": (_I, [_P]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -1,0 +1,120 @@
+// Pinned-host -> HBM page streamer (host code, HIP runtime API).
+//
+// A pager drives an HBM ring of `slots` equal-size slots (caller-owned device memory) and
+// owns one copy stream at the default priority.  submit() copies a byte range of pinned host memory into a slot as a
+// sequence of page-size hipMemcpyAsync calls on the copy stream, after the stream has
+// waited for the slot's "free" event (recorded by the last consumer), and records the
+// slot's "ready" event.  acquire() makes a compute stream wait for "ready"; release()
+// records "free" on the compute stream.  No call blocks the host and every cross-stream
+// dependency is an event, so a slot is never overwritten while a kernel still reads it
+// and never read before its copy has landed.
+#include <hip/hip_runtime.h>
+
+#include <new>
+#include <vector>
+
+#include "../../include/qstore_hip.h"
+
+namespace qs {
+int fail(int status, const char* fmt, ...);
+int hip_check(hipError_t e, const char* what);
+}  // namespace qs
+
+using qs::fail;
+using qs::hip_check;
+
+struct qs_pager {
+  size_t slot_bytes = 0;
+  size_t page_bytes = 0;
+  int slots = 0;
+  char* arena = nullptr;  // caller-owned, slot_bytes * slots bytes
+  hipStream_t copy = nullptr;
+  std::vector<hipEvent_t> ready, freed;
+  std::vector<int> used;  // a free event has been recorded at least once
+};
+
+extern "C" int qs_pager_create(void* device_arena, size_t slot_bytes, int slots,
+                               size_t page_bytes, qs_pager** out) {
+  if (!out || !device_arena || slot_bytes == 0 || slot_bytes % 256 || slots < 1 || slots > 64 ||
+      page_bytes == 0)
+    return fail(QS_ERR_INVALID, "pager_create: bad arguments");
+  qs_pager* p = new (std::nothrow) qs_pager();
+  if (!p) return fail(QS_ERR_HIP, "pager_create: out of host memory");
+  p->slot_bytes = slot_bytes;
+  p->page_bytes = page_bytes;
+  p->slots = slots;
+  p->arena = static_cast<char*>(device_arena);
+  int st = hip_check(hipStreamCreateWithFlags(&p->copy, hipStreamNonBlocking), "hipStreamCreate");
+  p->ready.assign(slots, nullptr);
+  p->freed.assign(slots, nullptr);
+  p->used.assign(slots, 0);
+  for (int i = 0; !st && i < slots; ++i) {
+    st = hip_check(hipEventCreateWithFlags(&p->ready[i], hipEventDisableTiming), "hipEventCreate");
+    if (!st) st = hip_check(hipEventCreateWithFlags(&p->freed[i], hipEventDisableTiming), "hipEventCreate");
+  }
+  if (st) {
+    qs_pager_destroy(p);
+    return st;
+  }
+  *out = p;
+  return QS_OK;
+}
+
+extern "C" int qs_pager_destroy(qs_pager* p) {
+  if (!p) return QS_OK;
+  if (p->copy) hipStreamSynchronize(p->copy);
+  for (auto e : p->ready)
+    if (e) hipEventDestroy(e);
+  for (auto e : p->freed)
+    if (e) hipEventDestroy(e);
+  if (p->copy) hipStreamDestroy(p->copy);
+  delete p;
+  return QS_OK;
+}
+
+extern "C" void* qs_pager_slot_ptr(qs_pager* p, int slot) {
+  if (!p || slot < 0 || slot >= p->slots) return nullptr;
+  return p->arena + p->slot_bytes * (size_t)slot;
+}
+
+extern "C" int qs_pager_submit(qs_pager* p, int slot, const void* host, size_t bytes,
+                               size_t dst_offset) {
+  if (!p || !host || slot < 0 || slot >= p->slots)
+    return fail(QS_ERR_INVALID, "pager_submit: bad arguments");
+  if (dst_offset + bytes > p->slot_bytes) return fail(QS_ERR_LIMIT, "pager_submit: range exceeds the slot");
+  if (p->used[slot]) {
+    int st = hip_check(hipStreamWaitEvent(p->copy, p->freed[slot], 0), "hipStreamWaitEvent(free)");
+    if (st) return st;
+  }
+  char* dst = p->arena + p->slot_bytes * (size_t)slot + dst_offset;
+  const char* src = static_cast<const char*>(host);
+  for (size_t off = 0; off < bytes; off += p->page_bytes) {
+    const size_t n = bytes - off < p->page_bytes ? bytes - off : p->page_bytes;
+    int st = hip_check(hipMemcpyAsync(dst + off, src + off, n, hipMemcpyHostToDevice, p->copy), "hipMemcpyAsync");
+    if (st) return st;
+  }
+  return QS_OK;
+}
+
+extern "C" int qs_pager_seal(qs_pager* p, int slot) {
+  if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_seal: bad arguments");
+  return hip_check(hipEventRecord(p->ready[slot], p->copy), "hipEventRecord(ready)");
+}
+
+extern "C" int qs_pager_acquire(qs_pager* p, int slot, void* compute_stream) {
+  if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_acquire: bad arguments");
+  return hip_check(hipStreamWaitEvent(static_cast<hipStream_t>(compute_stream), p->ready[slot], 0),
+                   "hipStreamWaitEvent(ready)");
+}
+
+extern "C" int qs_pager_release(qs_pager* p, int slot, void* compute_stream) {
+  if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_release: bad arguments");
+  p->used[slot] = 1;
+  return hip_check(hipEventRecord(p->freed[slot], static_cast<hipStream_t>(compute_stream)),
+                   "hipEventRecord(free)");
+}
+
+extern "C" int qs_pager_sync(qs_pager* p) {
+  if (!p) return fail(QS_ERR_INVALID, "pager_sync: null pager");
+  return hip_check(hipStreamSynchronize(p->copy), "hipStreamSynchronize(copy)");
+}

@@ -119,10 +119,10 @@ class DenseQStore:
         for name, out, inn, c_off, s_off in layout:
             codes, scales = self.reader.qrow(name)
             arena[c_off : c_off + out * inn].copy_(
-                torch.from_numpy(np.ascontiguousarray(codes).view(np.uint8).reshape(-1))
+                torch.from_numpy(np.array(codes, copy=True).view(np.uint8).reshape(-1))
             )
             arena[s_off : s_off + out * 4].copy_(
-                torch.from_numpy(np.ascontiguousarray(scales).view(np.uint8).reshape(-1))
+                torch.from_numpy(np.array(scales, copy=True).view(np.uint8).reshape(-1))
             )
             c = arena[c_off : c_off + out * inn].view(torch.int8).view(out, inn)
             s = arena[s_off : s_off + out * 4].view(torch.float32)
