@@ -14,7 +14,8 @@ dominant kernel (the paired gate/up + SwiGLU launch) timed on its own stream wit
 events; ``cpu_baseline`` is the reference CPU path (oracle/cpu_path.py) on a bounded
 sample of the same stack on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu] [--no-secondary]
+       python bench.py --profile {swiglu,stack,copy}   (eager launches for counter runs)
 """
 
 from __future__ import annotations
@@ -281,6 +282,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-secondary", action="store_true", help="skip configs 1/3/4/5")
+    ap.add_argument("--profile", choices=("swiglu", "stack", "copy"),
+                    help="eager launches only, for rocprofv3 counter runs: 28 paired gate/up+SwiGLU "
+                    "launches, one stack pass, or a plain 256 MiB device copy (counter calibration); x5")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -300,6 +304,15 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     m = args.m
+    if args.profile == "copy":
+        n = 256 << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": "copy", "launches": 5, "read_bytes": n, "write_bytes": n}), flush=True)
+        return 0
     arena, pages = build_stack(torch, dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
@@ -312,6 +325,17 @@ def main() -> int:
             qrow.fused_qrow_matmul(L["o"], x_h)
             qrow.fused_qrow_swiglu(L["gate"], L["up"], x_h)
             qrow.fused_qrow_matmul(L["down"], x_i)
+
+    if args.profile:
+        for _ in range(5):
+            if args.profile == "stack":
+                one_pass()
+            else:
+                for L in pages:
+                    qrow.fused_qrow_swiglu(L["gate"], L["up"], x_h)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": args.profile, "m": m, "swiglu_launch_bytes": swiglu_launch_bytes(m)}), flush=True)
+        return 0
 
     stream = torch.cuda.Stream(device=dev)
     with torch.cuda.stream(stream):
