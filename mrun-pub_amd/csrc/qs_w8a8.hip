@@ -68,6 +68,74 @@ __global__ __launch_bounds__(256) void k_act_quant(const void* __restrict__ x, i
   }
 }
 
+// One wave per row with the row held in registers between the max pass and the quantize
+// pass: lane l owns the 16-byte chunks l, l + 64, ... of the row (each wave instruction
+// reads 1 KiB contiguous).  Same arithmetic, element by element, as k_act_quant.
+// Requires K % E == 0, 16-byte aligned rows of x and keep, 8/4-byte aligned rows of q
+// and K <= 64 * CPL * E.
+template <int XT, int CPL>
+__global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x, int64_t ldx,
+                                                     const float* __restrict__ keep,
+                                                     int8_t* __restrict__ q, int64_t ldq,
+                                                     float* __restrict__ scale, int M, int K) {
+  constexpr int ES = XT == QS_F32 ? 4 : 2;
+  constexpr int E = 16 / ES;  // elements per 16-byte chunk
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const char* xr = static_cast<const char*>(x) + (int64_t)row * ldx * ES;
+  const int nch = K / E;
+  i32x4 v[CPL];
+  float amax = 0.f;
+  auto widen = [&](const i32x4& c, int e) -> float {
+    if constexpr (XT == QS_F32) return __int_as_float(c[e]);
+    const uint32_t d = static_cast<uint32_t>(c[e >> 1]);
+    const uint32_t h = (e & 1) ? (d >> 16) : (d & 0xffffu);
+    if constexpr (XT == QS_BF16) return bf16_bits_to_f32(h);
+    return f16_bits_to_f32(static_cast<uint16_t>(h));
+  };
+  auto keepv = [&](int ch, int e) -> float { return keep[ch * E + e]; };
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = c * 64 + lane;
+    if (ch < nch) {
+      v[c] = *reinterpret_cast<const i32x4*>(xr + (int64_t)ch * 16);
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        float f = widen(v[c], e);
+        if (keep) f = mul_rn(f, keepv(ch, e));
+        amax = fmaxf(amax, fabsf(f));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  float s = amax / 127.0f;  // IEEE division
+  if (s == 0.f) s = 1.f;
+  if (lane == 0) scale[row] = s;
+  int8_t* qr = q + (int64_t)row * ldq;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = c * 64 + lane;
+    if (ch < nch) {
+      uint32_t packed[E / 4];
+#pragma unroll
+      for (int j = 0; j < E / 4; ++j) packed[j] = 0;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        float f = widen(v[c], e);
+        if (keep) f = mul_rn(f, keepv(ch, e));
+        float r = rintf(f / s);  // IEEE division, round half to even
+        r = fminf(fmaxf(r, -127.f), 127.f);
+        packed[e >> 2] |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xffu) << (8 * (e & 3));
+      }
+      if constexpr (E == 8)
+        *reinterpret_cast<uint2*>(qr + (int64_t)ch * 8) = make_uint2(packed[0], packed[1]);
+      else
+        *reinterpret_cast<uint32_t*>(qr + (int64_t)ch * 4) = packed[0];
+    }
+  }
+}
+
 // Partial column maxima: block (bx, by) covers 256 columns x 64 rows and writes
 // part[by, k] = max over its rows of |x[m, k]|.
 template <int XT>
@@ -149,6 +217,102 @@ __global__ __launch_bounds__(1024) void k_topk(float* __restrict__ vals, int K, 
   }
 }
 
+// Single workgroup of 16 waves.  The partial maxima are folded into registers (wave w
+// owns columns [w*S, (w+1)*S), lane l the columns w*S + l + 64*e); every wave selects the
+// kk largest of its slice with kk rounds of a wave argmax, and wave 0 merges the 16
+// candidate lists the same way.  Ties go to the lower column index at every step, so the
+// result equals kk rounds of a global argmax.  K <= 16 * 64 * kTopkVpl.
+constexpr int kTopkVpl = 16;
+__global__ __launch_bounds__(1024) void k_topk_w(const float* __restrict__ vals, int K, int parts,
+                                                 int kk, int64_t* __restrict__ idx,
+                                                 float* __restrict__ keep) {
+  __shared__ float cv[16 * 64];
+  __shared__ int ci[16 * 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int S = (K + 15) / 16;
+  const int base = wave * S;
+  const float NEG = -__builtin_inff();
+  float v[kTopkVpl];
+#pragma unroll
+  for (int e = 0; e < kTopkVpl; ++e) {
+    const int off = e * 64 + lane;
+    const int k = base + off;
+    v[e] = NEG;
+    if (off < S && k < K) {
+      float m = vals[k];
+      for (int pp = 1; pp < parts; ++pp) m = fmaxf(m, vals[(int64_t)pp * K + k]);
+      v[e] = m;
+      keep[k] = 1.f;
+    }
+  }
+  auto argmax = [&](float& best, int& bi) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(best, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ov > best || (ov == best && oi < bi)) {
+        best = ov;
+        bi = oi;
+      }
+    }
+  };
+  for (int r = 0; r < kk; ++r) {
+    float best = NEG;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int e = 0; e < kTopkVpl; ++e) {
+      const int k = base + e * 64 + lane;
+      if (v[e] > best || (v[e] == best && k < bi)) {
+        best = v[e];
+        bi = k;
+      }
+    }
+    argmax(best, bi);
+    if (lane == 0) {
+      cv[wave * 64 + r] = best;
+      ci[wave * 64 + r] = bi;
+    }
+#pragma unroll
+    for (int e = 0; e < kTopkVpl; ++e)
+      if (base + e * 64 + lane == bi) v[e] = NEG;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // wave 0: merge 16 lists of kk candidates (entry j = w * kk + r, lane owns j = lane + 64 t)
+  float c[16];
+  int cidx[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    const int j = lane + 64 * t;
+    c[t] = NEG;
+    cidx[t] = 0x7fffffff;
+    if (j < 16 * kk) {
+      const int w = j / kk, r = j - (j / kk) * kk;
+      c[t] = cv[w * 64 + r];
+      cidx[t] = ci[w * 64 + r];
+    }
+  }
+  for (int r = 0; r < kk; ++r) {
+    float best = NEG;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+      if (c[t] > best || (c[t] == best && cidx[t] < bi)) {
+        best = c[t];
+        bi = cidx[t];
+      }
+    argmax(best, bi);
+    if (lane == 0) {
+      idx[r] = bi;
+      keep[bi] = 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+      if (cidx[t] == bi) c[t] = NEG;
+  }
+}
+
 template <int XT>
 __global__ __launch_bounds__(256) void k_gather_side(const void* __restrict__ x, int64_t ldx,
                                                      const int8_t* __restrict__ qw, int64_t ldw,
@@ -189,6 +353,7 @@ enum { EPI_I32 = 0, EPI_F32 = 1, EPI_BF16 = 2 };
 
 constexpr int kBK = 64;        // k bytes per step
 constexpr int kLdsRow = 80;    // padded LDS row (64 data + 16): conflict-free 16B reads
+constexpr int kSideLds = 16;   // side-path columns staged in LDS by the epilogue
 
 template <int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmParams p) {
@@ -288,6 +453,22 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmPara
     __syncthreads();
   }
 
+  // side-path operands of this tile in LDS (P <= kSideLds): xs[BM][16], wsT[16][BN]
+  const bool side_lds = EPI != EPI_I32 && p.P > 0 && p.P <= kSideLds;
+  float* xs = reinterpret_cast<float*>(&lds[0][0]);
+  float* ws = xs + BM * kSideLds;
+  if (side_lds) {
+    for (int i = tid; i < BM * p.P; i += NT) {
+      const int r = i / p.P, q = i - (i / p.P) * p.P;
+      xs[r * kSideLds + q] = bm + r < p.M ? p.xp[(int64_t)(bm + r) * p.P + q] : 0.f;
+    }
+    for (int i = tid; i < BN * p.P; i += NT) {
+      const int c = i / p.P, q = i - (i / p.P) * p.P;
+      ws[q * BN + c] = bn + c < p.N ? p.wp[(int64_t)(bn + c) * p.P + q] : 0.f;
+    }
+    __syncthreads();
+  }
+
   // epilogue
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -306,7 +487,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmPara
         } else {
           // reference order: (float(acc) * act_scale) * w_scale, added to the side path
           float v = mul_rn(mul_rn(static_cast<float>(acc[i][j][r]), p.as[row]), bsc);
-          if (p.P > 0) {
+          if (side_lds) {
+            float side = 0.f;
+            const float* xr = xs + (row - bm) * kSideLds;
+            const float* wr = ws + (col - bn);
+            for (int q = 0; q < p.P; ++q) side = fmaf(xr[q], wr[q * BN], side);
+            v = add_rn(side, v);
+          } else if (p.P > 0) {
             float side = 0.f;
             const float* xr = p.xp + (int64_t)row * p.P;
             const float* wr = p.wp + (int64_t)col * p.P;
@@ -389,6 +576,8 @@ int check_mnk(int64_t M, int64_t N, int64_t K) {
 
 using namespace qs;
 
+static constexpr int kQuantCpl = 16;  // 16-byte chunks per lane held by k_act_quant_w
+
 extern "C" int qs_act_quant_i8(const void* x, int x_dtype, int64_t ldx, const float* keep,
                                int8_t* q, float* scale, int64_t M, int64_t K, void* stream) {
   if (!x || !q || !scale) return fail(QS_ERR_INVALID, "act_quant: null pointer");
@@ -396,6 +585,21 @@ extern "C" int qs_act_quant_i8(const void* x, int x_dtype, int64_t ldx, const fl
   if (M > (1 << 30) || K > (1 << 30)) return fail(QS_ERR_LIMIT, "act_quant: dimension exceeds 2^30");
   if (M == 0) return QS_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int es = x_dtype == QS_F32 ? 4 : 2;
+  const int E = 16 / es;
+  const bool wave_path = (x_dtype == QS_F32 || x_dtype == QS_BF16 || x_dtype == QS_F16) && K % E == 0 &&
+                         K / E <= 64 * kQuantCpl && aligned(x, 16) && (ldx * es) % 16 == 0 &&
+                         (!keep || aligned(keep, 16)) && aligned(q, E == 8 ? 8 : 4);
+  if (wave_path) {
+    const dim3 grid((unsigned)cdiv(M, 4));
+    if (x_dtype == QS_F32)
+      hipLaunchKernelGGL((k_act_quant_w<QS_F32, kQuantCpl>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
+    else if (x_dtype == QS_BF16)
+      hipLaunchKernelGGL((k_act_quant_w<QS_BF16, kQuantCpl>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
+    else
+      hipLaunchKernelGGL((k_act_quant_w<QS_F16, kQuantCpl>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
+    return hip_check(hipGetLastError(), "k_act_quant_w launch");
+  }
   if (x_dtype == QS_F32)
     hipLaunchKernelGGL(k_act_quant<QS_F32>, dim3((unsigned)M), dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)K);
   else if (x_dtype == QS_BF16)
@@ -424,7 +628,10 @@ extern "C" int qs_outlier_topk(const void* x, int x_dtype, int64_t ldx, int64_t 
     hipLaunchKernelGGL(k_col_absmax<QS_F16>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
   else
     return fail(QS_ERR_INVALID, "outlier_topk: dtype must be F32, BF16 or F16");
-  hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), 0, s, colmax, (int)K, parts, k, idx, keep);
+  if (K <= 16 * 64 * kTopkVpl)
+    hipLaunchKernelGGL(k_topk_w, dim3(1), dim3(1024), 0, s, colmax, (int)K, parts, k, idx, keep);
+  else
+    hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), 0, s, colmax, (int)K, parts, k, idx, keep);
   return hip_check(hipGetLastError(), "outlier_topk launch");
 }
 

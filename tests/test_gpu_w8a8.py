@@ -47,21 +47,45 @@ def test_int8_gemm_extreme_values(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_act_quant_bit_exact(dev, dtype):
+@pytest.mark.parametrize("t,k", [(33, 4096), (9, 4100), (3, 20000), (5, 8), (70, 8192)])
+def test_act_quant_bit_exact(dev, dtype, t, k):
+    # wave-per-row kernel (K % chunk == 0, K within the register budget) and the
+    # workgroup-per-row kernel for the rest
     rng = np.random.default_rng(3)
-    x = rng.standard_normal((33, 4096)).astype(np.float32)
+    x = rng.standard_normal((t, k)).astype(np.float32)
     x[0] = 0.0
     x[1, :4] = [1.5, 2.5, -0.5, 127.0]
-    x[5, 7] = 2000.0
+    x[min(5, t - 1), 7] = 2000.0
     xt = torch.from_numpy(x).to(dtype)
     xs = xt.float().numpy()
-    keep = np.ones(4096, np.float32)
-    keep[[7, 99]] = 0.0
+    keep = np.ones(k, np.float32)
+    keep[[7, k // 2]] = 0.0
     for kp in (None, keep):
         q, s = _w().quantize_activation(xt.to(dev), None if kp is None else torch.from_numpy(kp).to(dev))
         qr, sr = ow.act_quant(xs, kp)
         assert np.array_equal(q.cpu().numpy(), qr)
         assert np.array_equal(s.cpu().numpy().view(np.uint32), sr.view(np.uint32))
+
+
+@pytest.mark.parametrize("t,k,kk", [(64, 4096, 8), (130, 512, 4), (3, 20000, 5), (1, 64, 64), (700, 1000, 13)])
+def test_outlier_topk_matches_oracle(dev, t, k, kk):
+    from mrun_pub_amd import _native as nat
+
+    rng = np.random.default_rng(t + k)
+    x = rng.standard_normal((t, k)).astype(np.float32)
+    x[:, rng.permutation(k)[: kk // 2 + 1]] *= 50.0
+    x[0, 1] = x[0, 2] = x[-1, 40] = 1000.0  # ties resolve to the lower column
+    xd = torch.from_numpy(x).to(dev)
+    colmax = torch.empty(((t + 63) // 64) * k, dtype=torch.float32, device=dev)
+    idx = torch.empty(kk, dtype=torch.int64, device=dev)
+    keep = torch.empty(k, dtype=torch.float32, device=dev)
+    nat.call("qs_outlier_topk", nat.ptr(xd), nat.QS_F32, k, t, k, kk, nat.ptr(colmax), nat.ptr(idx),
+             nat.ptr(keep), nat.stream_of(dev))
+    ref = ow.protect_topk(x, kk)
+    assert idx.cpu().numpy().tolist() == ref.tolist()
+    kref = np.ones(k, np.float32)
+    kref[ref] = 0.0
+    assert np.array_equal(keep.cpu().numpy(), kref)
 
 
 @pytest.mark.parametrize("t", [1, 17, 512])
@@ -72,7 +96,7 @@ def test_w8a8_no_protection_bit_exact(dev, t):
     assert np.array_equal(y.cpu().numpy().view(np.uint32), ow.w8a8_matmul(q_w, sc_w, x).view(np.uint32))
 
 
-@pytest.mark.parametrize("protect_k", [4, 8])
+@pytest.mark.parametrize("protect_k", [4, 8, 16, 24])
 def test_w8a8_outlier_protection(dev, protect_k):
     rng, q_w, sc_w = _weights(640, 4096, protect_k)
     x = rng.standard_normal((64, 4096)).astype(np.float32)
