@@ -7,14 +7,17 @@
 // with zero the reference's fixed offset (4 for int3, 1 for int2; scales fp32, G = 128) or
 // a per-group zero point (fp16 scale + fp16 zero, G = 64: the asymmetric variant).
 //
-// GEMV (k_lowbit_mfma): y[m,n] = sum_k x[m,k] w[n,k] in fp32.  Codes are widened to the
-// exact bf16 values OFF + code (OFF = 8 for 3-bit, 4 for 2-bit: bf16 bit pattern
-// 0x4100 | code << 4, resp. 0x4080 | code << 5 -- one bfe, one 24-bit multiply and one
-// and_or per PAIR of codes) and fed to v_mfma_f32_16x16x32_bf16 against bf16 activations
-// (products exact in fp32).  Each MFMA covers 32 codes of ONE group, so per group
+// All GEMV kernels compute y[m,n] = sum_k x[m,k] w[n,k] in fp32 the same way: codes are
+// widened to the exact bf16 values OFF + code (OFF = 8 for 3-bit, 4 for 2-bit: bf16 bit
+// pattern 0x4100 | code << 4, resp. 0x4080 | code << 5 -- one bfe, one 24-bit multiply and
+// one v_bitop3 per PAIR of codes) and multiplied with bf16 activations (products exact
+// in fp32); per group (or any piece of a group)
 //   sum_k x (code - z) = R - (OFF + z) * S0,     S0 = sum_{k in group} x[m,k],
 // and y += scale * (R - (OFF + z) * S0).  fp32 activations are split exactly into three
 // bf16 terms (x = h + m + l) that run as three activation rows and are summed at the end.
+//   k_lowbit_valu  decode (M <= 2 bf16 rows): one wave per weight row, v_dot2_f32_bf16
+//   k_lowbit_slot  M <= 16 rows: v_mfma_f32_16x16x32_bf16, one whole group per lane
+//   k_lowbit_mfma  any aligned-to-4 layout (fallback), four lanes per group
 #include "qs_common.h"
 
 namespace qs {
@@ -32,7 +35,22 @@ struct LowbitParams {
   float* y;            // [M, N]
   int64_t ldy;
   int M, N, K, ng;
+  uint32_t pair_mask, pair_base;  // code-pair -> bf16x2 (OFF + c) masks, set by pair_consts()
 };
+
+// (t * spread) & mask | base turns the 2*BITS-bit code pair t into two bf16 (OFF + c).
+// mask/base travel as kernel arguments (scalar registers) so that the and/or is a single
+// v_bitop3_b32 (table 0xEA = (a & b) | c).
+template <int BITS>
+__device__ __forceinline__ uint32_t pair_bf16(uint32_t t, uint32_t mask, uint32_t base) {
+  constexpr uint32_t spread = BITS == 3 ? 0x20010u : 0x80020u;
+  return __builtin_amdgcn_bitop3_b32(t * spread, mask, base, 0xEA);
+}
+
+inline void pair_consts(LowbitParams& p, int bits) {
+  p.pair_mask = bits == 3 ? 0x00700070u : 0x00600060u;
+  p.pair_base = bits == 3 ? 0x41004100u : 0x40804080u;
+}
 
 // Lane code extraction: the lane's G/4 codes (BITS*G/4 bits, at a 2- or 4-byte aligned
 // offset) are returned as a 64/96-bit little-endian field.
@@ -69,17 +87,14 @@ __device__ __forceinline__ void load_codes(const uint8_t* p, uint32_t (&f)[3]) {
 
 // 2 codes starting at bit position bp of the field -> packed bf16 pair (OFF + c).
 template <int BITS>
-__device__ __forceinline__ uint32_t code_pair(const uint32_t (&f)[3], int bp) {
+__device__ __forceinline__ uint32_t code_pair(const uint32_t (&f)[3], int bp, uint32_t mask, uint32_t base) {
   const int w = bp >> 5, o = bp & 31;
   uint32_t t;
   if (o + 2 * BITS <= 32)
     t = __builtin_amdgcn_ubfe(f[w], o, 2 * BITS);
   else
     t = __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(f[w + 1], f[w], o), 0, 2 * BITS);
-  if constexpr (BITS == 3)
-    return ((t * 0x20010u) & 0x00700070u) | 0x41004100u;  // 8 + c at bits 4-6 / 20-22
-  else
-    return ((t * 0x80020u) & 0x00600060u) | 0x40804080u;  // 4 + c at bits 5-6 / 21-22
+  return pair_bf16<BITS>(t, mask, base);  // int3: 8 + c at bits 4-6 / 20-22; int2: 4 + c at 5-6 / 21-22
 }
 
 template <int BITS, int G, int KW>
@@ -134,7 +149,7 @@ __global__ __launch_bounds__(KW * 64) void k_lowbit_mfma(LowbitParams p) {
         typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
         u32x4 b;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) b[d] = code_pair<BITS>(f[u], BITS * (8 * j + 2 * d));
+        for (int d = 0; d < 4; ++d) b[d] = code_pair<BITS>(f[u], BITS * (8 * j + 2 * d), p.pair_mask, p.pair_base);
         r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[u][j], __builtin_bit_cast(bf16x8, b), r, 0, 0, 0);
       }
       const float c = OFF + z[u];
@@ -160,6 +175,386 @@ __global__ __launch_bounds__(KW * 64) void k_lowbit_mfma(LowbitParams p) {
     const int m = 4 * g4 + q;
     if (m < p.M) p.y[(int64_t)m * p.ldy + no] = t[q];
   }
+}
+
+// ----------------------------------------------------------------------------------
+// Slotted GEMV (k_lowbit_slot): the per-group MFMA formulation with one WHOLE group per
+// lane, so that a lane reads its codes as contiguous 8-byte words and many groups are in
+// flight per wave.  Wave = 16 weight rows (lane l: row l & 15, slot l >> 4).  Step t covers
+// the groups gb = 4t .. 4t+3 of the workgroup's range; slot s holds the CB code bytes of
+// group gb + s of its row (B operand: 8 codes per MFMA, G/8 MFMAs per group).  The A
+// operand keeps the four groups apart: A row i = 4*mi + slot carries activation row mi
+// only in the k-block of that slot (zeros elsewhere), so D[4*mi + q][n] is the sum over
+// group gb + q alone and
+//   y[m, n] += scale[n, gb+q] * (D - (OFF + zero[n, gb+q]) * S0[m, gb+q]).
+// Four activation rows per pass, MP passes (M <= 16).  The workgroup's activations (its
+// K range, all rows) and their group sums S0 sit in LDS; codes and the per-group scale /
+// zero point stream through registers, D steps per batch, double-buffered.
+// Requirements (else k_lowbit_mfma): 8-byte aligned rows and K ranges that fit in LDS.
+// ----------------------------------------------------------------------------------
+template <int BITS, int G>
+struct SlotCfg {
+  static constexpr int CB = BITS * G / 8;  // code bytes per row per group: 24, 16, 48, 32
+  static constexpr int DW = CB / 8;        // 8-byte words per lane per step
+  static constexpr int D = 96 / CB;        // steps per register batch (96 bytes per lane)
+  static constexpr int SUB = G / 8;        // MFMAs per group
+};
+
+// Scale / zero-point storage: SM 0 = fp32 scales, 1 = fp16; ZM 0 = fixed offset,
+// 1 = fp16 zero points, 2 = fp32.  Compile-time so that every load in the main loop is
+// unconditional (addresses clamped into range, invalid data zeroed by selects) and the
+// compiler can keep whole batches in flight.
+template <int SM, int ZM>
+__device__ __forceinline__ void load_sz(const LowbitParams& p, int64_t i, float& sc, float& z) {
+  if constexpr (SM == 1) sc = f16_bits_to_f32(__builtin_nontemporal_load(static_cast<const uint16_t*>(p.scales) + i));
+  else sc = __builtin_nontemporal_load(static_cast<const float*>(p.scales) + i);
+  if constexpr (ZM == 0) z = p.offset;
+  else if constexpr (ZM == 1) z = f16_bits_to_f32(__builtin_nontemporal_load(static_cast<const uint16_t*>(p.zeros) + i));
+  else z = __builtin_nontemporal_load(static_cast<const float*>(p.zeros) + i);
+}
+
+template <int BITS, int G, int MP, int SM, int ZM>
+__global__ __launch_bounds__(256) void k_lowbit_slot(LowbitParams p, int gps, float* __restrict__ part) {
+  using C = SlotCfg<BITS, G>;
+  constexpr float OFF = BITS == 3 ? 8.f : 4.f;
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int gbeg = blockIdx.y * gps;
+  const int gend = min(p.ng, gbeg + gps);
+  const int GR = gend - gbeg;                 // groups in this workgroup's range
+  const int GRP = (GR + 3) & ~3;              // padded S0 row
+  const int KR = GR * G;                      // activations per row in range
+  const int M = p.M;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);                       // [M][KR]
+  float* s0 = reinterpret_cast<float*>(lds + (((size_t)M * KR * 2 + 15) & ~(size_t)15));  // [M][GRP]
+
+  const int col = lane & 15, slot = lane >> 4;
+  const int nrow = blockIdx.x * 64 + 16 * wave + col;
+  const int n = min(nrow, p.N - 1);
+  const uint8_t* rowp = p.packed + (int64_t)n * p.row_bytes;
+  const int64_t sidx = (int64_t)n * p.ng;
+  const int steps = (GR + 3) / 4;
+  const int nbatch = (steps + C::D - 1) / C::D;
+  // A-operand role of this lane: row i = col, k-block = slot -> activation row mi = col >> 2
+  // when col & 3 == slot
+  const bool arole = (col & 3) == slot;
+  const int ami = col >> 2;
+
+  u32x2 cw[2][C::D][C::DW];
+  float rs[2][C::D], rz[2][C::D];
+  auto gload = [&](int b, int t0) {
+#pragma unroll
+    for (int d = 0; d < C::D; ++d) {
+      const int g = gbeg + 4 * (t0 + d) + slot;
+      const bool ok = g < gend;
+      const int gc = ok ? g : gend - 1;
+      const u32x2* src = reinterpret_cast<const u32x2*>(rowp + (int64_t)gc * C::CB);
+#pragma unroll
+      for (int w = 0; w < C::DW; ++w) cw[b][d][w] = __builtin_nontemporal_load(src + w);
+      float sc, z;
+      load_sz<SM, ZM>(p, sidx + gc, sc, z);
+      rs[b][d] = ok ? sc : 0.f;
+      rz[b][d] = OFF + z;
+    }
+  };
+  gload(0, 0);  // the first codes are in flight while the activations are staged
+
+  // activations of the range -> LDS (16-byte pieces); each piece's 8 values are summed and
+  // the G/8 pieces of a group (consecutive lanes) combined by a fixed butterfly -> S0
+  const int pieces = KR / 8;
+  for (int q0 = 0; q0 < M * pieces; q0 += 256) {
+    const int q = q0 + tid;
+    i32x4 v = i32x4{0, 0, 0, 0};
+    int m = 0, c = 0;
+    if (q < M * pieces) {
+      m = q / pieces;
+      c = q - m * pieces;
+      v = *reinterpret_cast<const i32x4*>(p.x + (int64_t)m * p.ldx + (int64_t)gbeg * G + c * 8);
+      reinterpret_cast<i32x4*>(xs)[q] = v;
+    }
+    float t = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t dv = static_cast<uint32_t>(v[e]);
+      t += bf16_bits_to_f32(dv & 0xffffu);
+      t += bf16_bits_to_f32(dv >> 16);
+    }
+#pragma unroll
+    for (int off = 1; off < G / 8; off <<= 1) t += __shfl_xor(t, off, 64);
+    if (q < M * pieces && c % (G / 8) == 0) s0[m * GRP + c / (G / 8)] = t;
+  }
+  for (int q = tid; q < M * GRP; q += 256)
+    if (q - (q / GRP) * GRP >= GR) s0[q] = 0.f;
+  __syncthreads();
+
+  f32x4 y[MP];
+#pragma unroll
+  for (int pp = 0; pp < MP; ++pp) y[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int b, int t0) {
+#pragma unroll
+    for (int d = 0; d < C::D; ++d) {
+      const int t = min(t0 + d, steps - 1);  // steps past the end carry zero scales
+      uint32_t f[2 * C::DW + 1];
+#pragma unroll
+      for (int w = 0; w < C::DW; ++w) {
+        f[2 * w] = cw[b][d][w].x;
+        f[2 * w + 1] = cw[b][d][w].y;
+      }
+      f[2 * C::DW] = 0u;
+      f32x4 r[MP];
+#pragma unroll
+      for (int pp = 0; pp < MP; ++pp) r[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // activation block of this lane: group 4t + slot of the range (clamped; unused
+      // lanes and groups are zeroed below)
+      const int ga = min(4 * t + slot, GR - 1);
+#pragma unroll
+      for (int h = 0; h < C::SUB; ++h) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 bw;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int bp = BITS * (8 * h + 2 * e);
+          const int wi = bp >> 5, o = bp & 31;
+          uint32_t tt;
+          if (o + 2 * BITS <= 32)
+            tt = __builtin_amdgcn_ubfe(f[wi], o, 2 * BITS);
+          else
+            tt = __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(f[wi + 1], f[wi], o), 0, 2 * BITS);
+          bw[e] = pair_bf16<BITS>(tt, p.pair_mask, p.pair_base);
+        }
+#pragma unroll
+        for (int pp = 0; pp < MP; ++pp) {
+          const int m = 4 * pp + ami;
+          const bool use = arole && m < M;
+          const int mc = m < M ? m : 0;
+          i32x4 xv = *reinterpret_cast<const i32x4*>(xs + mc * KR + ga * G + 8 * h);
+          xv = use ? xv : i32x4{0, 0, 0, 0};
+          r[pp] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv),
+                                                          __builtin_bit_cast(bf16x8, bw), r[pp], 0, 0, 0);
+        }
+      }
+      // scale / zero point of groups 4t + q of this row live in lanes col + 16 q
+      float sq[4], cq[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sq[q] = __shfl(rs[b][d], col + 16 * q, 64);
+        cq[q] = __shfl(rz[b][d], col + 16 * q, 64);
+      }
+#pragma unroll
+      for (int pp = 0; pp < MP; ++pp) {
+        const int m = min(4 * pp + slot, M - 1);  // D row 4*(l>>4)+q: activation row l >> 4
+        const f32x4 sm = *reinterpret_cast<const f32x4*>(s0 + m * GRP + 4 * t);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) y[pp][q] = fmaf(sq[q], fmaf(-cq[q], sm[q], r[pp][q]), y[pp][q]);
+      }
+    }
+  };
+
+  for (int bt = 0; bt < nbatch; bt += 2) {
+    if (bt + 1 < nbatch) gload(1, (bt + 1) * C::D);
+    compute(0, bt * C::D);
+    if (bt + 2 < nbatch) gload(0, (bt + 2) * C::D);
+    if (bt + 1 < nbatch) compute(1, (bt + 1) * C::D);
+  }
+
+  if (nrow >= p.N) return;
+#pragma unroll
+  for (int pp = 0; pp < MP; ++pp) {
+    const int m = 4 * pp + slot;
+    if (m >= M) continue;
+    // lane (n, mi) holds the four group partials of row m in y[pp][0..3]: sum them in order
+    const float v = add_rn(add_rn(add_rn(y[pp][0], y[pp][1]), y[pp][2]), y[pp][3]);
+    if (part)
+      part[((int64_t)blockIdx.y * 16 + m) * p.N + nrow] = v;
+    else
+      p.y[(int64_t)m * p.ldy + nrow] = v;
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// Decode GEMV for M <= 2 bf16 activation rows (k_lowbit_valu): one wave per weight row,
+// rows dealt round-robin to the waves of a persistent grid, the next row's codes in
+// flight while the current one is reduced.  Lane l reads the LB-byte piece l + 64 j of
+// the row (int3: 12 bytes = 32 codes, int2: 16 bytes = 64 codes): every wave load is one
+// contiguous run of 64 * LB bytes.  Codes become bf16 (OFF + c) pairs (as for the MFMA
+// kernels) and meet the activations in v_dot2_f32_bf16; per piece
+//   y += scale * (R_piece - (OFF + zero) * S_piece),   S_piece = sum of x over the piece,
+// which sums to the per-group formula because a piece never straddles a group.  The
+// activations and the per-piece sums live in LDS, one copy per workgroup.
+// ----------------------------------------------------------------------------------
+constexpr int kValuThreads = 512;  // 8 waves: one staged copy of x serves 8 row streams
+
+template <int BITS>
+struct ValuCfg {
+  static constexpr int LB = BITS == 3 ? 12 : 16;  // bytes per lane piece
+  static constexpr int CPL = LB * 8 / BITS;       // codes per piece: 32 / 64
+  static constexpr int NW = LB / 4;               // dwords per piece
+};
+
+template <int BITS, int G, int MB, int J, int SM, int ZM>
+__global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
+  using C = ValuCfg<BITS>;
+  constexpr float OFF = BITS == 3 ? 8.f : 4.f;
+  constexpr int W = kValuThreads / 64;
+  typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int K = p.K, M = p.M;
+  const int npc = K / C::CPL;  // pieces per row
+  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);                                           // [MB][K]
+  float* ps = reinterpret_cast<float*>(lds + (((size_t)MB * K * 2 + 15) & ~(size_t)15));     // [MB][npc]
+
+  // wave-uniform row stream (scalar registers): rows wave_id + i * nwaves
+  const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * W + (tid >> 6));
+  const int nwaves = gridDim.x * W;
+  const int ng = p.ng;
+  // per-lane constants: piece j of this lane, its byte offset, scale index, LDS offsets
+  int poff[J], pgrp[J], pxo[J];
+  bool pval[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int pc = lane + 64 * j;
+    pval[j] = pc < npc;
+    const int pcc = pval[j] ? pc : npc - 1;
+    poff[j] = pcc * C::LB;
+    pgrp[j] = pcc * C::CPL / G;
+    pxo[j] = pcc * C::CPL;
+  }
+
+  constexpr int R = J == 1 ? 4 : (J == 2 ? 2 : 1);  // rows per register batch
+  uint32_t cw[2][R][J][C::NW];
+  float rs[2][R][J], rz[2][R][J];
+  // batch bt = rows wave_id + (bt * R + i) * nwaves, i < R (rows past N load row N-1)
+  auto gload = [&](int b, int bt) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int row = min(wave_id + (bt * R + i) * nwaves, p.N - 1);
+      const uint8_t* rp = p.packed + (int64_t)row * p.row_bytes;
+      const int64_t sb = (int64_t)row * ng;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        if constexpr (BITS == 3) {
+          const u32x3 v = __builtin_nontemporal_load(reinterpret_cast<const u32x3*>(rp + poff[j]));
+          cw[b][i][j][0] = v.x;
+          cw[b][i][j][1] = v.y;
+          cw[b][i][j][2] = v.z;
+        } else {
+          const i32x4 v = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(rp + poff[j]));
+#pragma unroll
+          for (int w = 0; w < 4; ++w) cw[b][i][j][w] = static_cast<uint32_t>(v[w]);
+        }
+        float sc, z;
+        load_sz<SM, ZM>(p, sb + pgrp[j], sc, z);
+        rs[b][i][j] = pval[j] ? sc : 0.f;
+        rz[b][i][j] = OFF + z;
+      }
+    }
+  };
+  const int nrows = wave_id < p.N ? (p.N - 1 - wave_id) / nwaves + 1 : 0;  // rows of this wave
+  const int nbt = (nrows + R - 1) / R;
+  if (nbt > 0) gload(0, 0);  // the first rows' codes are in flight during the staging
+
+  // activations -> LDS, per-piece sums -> LDS
+  for (int q = tid; q < M * (K / 8); q += kValuThreads) {
+    const int m = q / (K / 8), c = q - (q / (K / 8)) * (K / 8);
+    reinterpret_cast<i32x4*>(xs)[q] = *reinterpret_cast<const i32x4*>(p.x + (int64_t)m * p.ldx + c * 8);
+  }
+  __syncthreads();
+  for (int q = tid; q < M * npc; q += kValuThreads) {
+    const int m = q / npc, c = q - (q / npc) * npc;
+    const i32x4* xp = reinterpret_cast<const i32x4*>(xs + m * K + c * C::CPL);
+    float t = 0.f;
+    for (int v = 0; v < C::CPL / 8; ++v) {
+      const i32x4 d = xp[v];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        t += bf16_bits_to_f32(static_cast<uint32_t>(d[e]) & 0xffffu);
+        t += bf16_bits_to_f32(static_cast<uint32_t>(d[e]) >> 16);
+      }
+    }
+    ps[q] = t;
+  }
+  __syncthreads();
+
+  auto compute = [&](int b, int bt) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int row = wave_id + (bt * R + i) * nwaves;
+      if (row >= p.N) break;
+      float acc[MB];
+#pragma unroll
+      for (int m = 0; m < MB; ++m) acc[m] = 0.f;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        float r[MB];
+#pragma unroll
+        for (int m = 0; m < MB; ++m) r[m] = 0.f;
+#pragma unroll
+        for (int v = 0; v < C::CPL / 8; ++v) {  // 8 codes per step: 4 bf16 pairs
+          uint32_t bw[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int bp = BITS * (8 * v + 2 * e);
+            const int wi = bp >> 5, o = bp & 31;
+            uint32_t tt;
+            if (o + 2 * BITS <= 32 || wi + 1 >= C::NW)
+              tt = __builtin_amdgcn_ubfe(cw[b][i][j][wi], o, 2 * BITS);
+            else
+              tt = __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(cw[b][i][j][wi + 1], cw[b][i][j][wi], o), 0, 2 * BITS);
+            bw[e] = pair_bf16<BITS>(tt, p.pair_mask, p.pair_base);
+          }
+#pragma unroll
+          for (int m = 0; m < MB; ++m) {
+            if (m < M) {
+              const i32x4 xv = *reinterpret_cast<const i32x4*>(xs + m * K + pxo[j] + 8 * v);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                // copy the element out first: bit-casting a vector element expression reads
+                // element 0 of the whole vector with this compiler
+                const uint32_t xe = static_cast<uint32_t>(xv[e]);
+                r[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, bw[e]),
+                                                       __builtin_bit_cast(bf16x2, xe), r[m], false);
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+          if (m < M) acc[m] = fmaf(rs[b][i][j], fmaf(-rz[b][i][j], ps[m * npc + pxo[j] / C::CPL], r[m]), acc[m]);
+      }
+#pragma unroll
+      for (int m = 0; m < MB; ++m) {
+        const float v = wave_sum(acc[m]);
+        if (lane == 0 && m < M) p.y[(int64_t)m * p.ldy + row] = v;
+      }
+    }
+  };
+
+  for (int bt = 0; bt < nbt; bt += 2) {
+    if (bt + 1 < nbt) gload(1, bt + 1);
+    compute(0, bt);
+    if (bt + 2 < nbt) gload(0, bt + 2);
+    if (bt + 1 < nbt) compute(1, bt + 1);
+  }
+}
+
+// y[m, n] = sum over t < rpx (activation split terms), then over splits s, of
+// part[s][rpx*m + t][n] -- fixed order.
+__global__ __launch_bounds__(256) void k_lowbit_reduce(const float* __restrict__ part, int S, int rpx,
+                                                       int M, int N, float* __restrict__ y, int64_t ldy) {
+  const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const int64_t m = i / N, n = i - m * N;
+  float acc = 0.f;
+  for (int t = 0; t < rpx; ++t) {
+    float v = 0.f;
+    for (int s = 0; s < S; ++s) v = add_rn(v, part[((int64_t)s * 16 + rpx * m + t) * N + n]);
+    acc = t == 0 ? v : add_rn(acc, v);
+  }
+  y[m * ldy + n] = acc;
 }
 
 // x (f32 or bf16) -> bf16 activation rows: bf16 x is copied; fp32 row m becomes rows
@@ -228,6 +623,50 @@ __global__ __launch_bounds__(256) void k_lowbit_dequant(LowbitParams p, int bits
 }
 
 namespace {
+constexpr size_t kSlotLds = 64 * 1024;  // activations + group sums of one workgroup's K range
+
+template <int BITS, int G, int SM, int ZM>
+void launch_slot_sz(int mp, dim3 grid, size_t lds, hipStream_t s, const LowbitParams& p, int gps, float* part) {
+  if (mp == 1) hipLaunchKernelGGL((k_lowbit_slot<BITS, G, 1, SM, ZM>), grid, dim3(256), lds, s, p, gps, part);
+  else if (mp == 2) hipLaunchKernelGGL((k_lowbit_slot<BITS, G, 2, SM, ZM>), grid, dim3(256), lds, s, p, gps, part);
+  else if (mp == 3) hipLaunchKernelGGL((k_lowbit_slot<BITS, G, 3, SM, ZM>), grid, dim3(256), lds, s, p, gps, part);
+  else hipLaunchKernelGGL((k_lowbit_slot<BITS, G, 4, SM, ZM>), grid, dim3(256), lds, s, p, gps, part);
+}
+
+// Two storage layouts get the slotted kernel: fp16 scale + fp16 zero point (the
+// asymmetric G64 variant) and fp32 scales with the fixed offset (the reference layout).
+template <int BITS, int G>
+void launch_slot(int mp, dim3 grid, size_t lds, hipStream_t s, const LowbitParams& p, int gps, float* part) {
+  if (p.scale_f16) launch_slot_sz<BITS, G, 1, 1>(mp, grid, lds, s, p, gps, part);
+  else launch_slot_sz<BITS, G, 0, 0>(mp, grid, lds, s, p, gps, part);
+}
+
+template <int BITS, int G, int MB, int J>
+void launch_valu_j(unsigned grid, size_t lds, hipStream_t s, const LowbitParams& p) {
+  if (p.scale_f16) hipLaunchKernelGGL((k_lowbit_valu<BITS, G, MB, J, 1, 1>), dim3(grid), dim3(kValuThreads), lds, s, p);
+  else hipLaunchKernelGGL((k_lowbit_valu<BITS, G, MB, J, 0, 0>), dim3(grid), dim3(kValuThreads), lds, s, p);
+}
+
+template <int BITS, int G, int MB>
+void launch_valu_mb(int J, unsigned grid, size_t lds, hipStream_t s, const LowbitParams& p) {
+  if (J == 1) launch_valu_j<BITS, G, MB, 1>(grid, lds, s, p);
+  else if (J == 2) launch_valu_j<BITS, G, MB, 2>(grid, lds, s, p);
+  else if (J == 3) launch_valu_j<BITS, G, MB, 3>(grid, lds, s, p);
+  else if (J == 4) launch_valu_j<BITS, G, MB, 4>(grid, lds, s, p);
+  else launch_valu_j<BITS, G, MB, 6>(grid, lds, s, p);
+}
+
+template <int BITS>
+void launch_valu(int J, int M, int G, unsigned grid, size_t lds, hipStream_t s, const LowbitParams& p) {
+  if (G == 64) {
+    if (M == 1) launch_valu_mb<BITS, 64, 1>(J, grid, lds, s, p);
+    else launch_valu_mb<BITS, 64, 2>(J, grid, lds, s, p);
+  } else {
+    if (M == 1) launch_valu_mb<BITS, 128, 1>(J, grid, lds, s, p);
+    else launch_valu_mb<BITS, 128, 2>(J, grid, lds, s, p);
+  }
+}
+
 template <int BITS, int G>
 void launch_lowbit(const LowbitParams& p, hipStream_t s) {
   const dim3 grid((unsigned)cdiv(p.N, 16));
@@ -252,6 +691,8 @@ int check_lowbit(const void* packed, int64_t row_bytes, const void* scales, int 
 
 using namespace qs;
 
+static constexpr int kLowbitMaxSplit = 8;  // K splits of k_lowbit_slot (partial-sum planes)
+
 extern "C" int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uint8_t* packed,
                               int64_t row_bytes, const void* scales, int scale_dtype,
                               const void* zeros, int zero_dtype, float offset, int bits,
@@ -272,22 +713,75 @@ extern "C" int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uin
   if (!workspace || workspace_bytes < need)
     return fail(QS_ERR_INVALID, "lowbit_gemv: workspace of %zu bytes required", need);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // workspace: bf16 rows [mb*rows_per_x, K] | s0 [mb*rows_per_x, ng] | y3 [mb*3, N]
+  const int cb = bits * group_size / 8;
+  (void)cb;
+  const bool tiled = row_bytes % 8 == 0 && aligned(packed, 8) && aligned(workspace, 16);
+  // workspace: bf16 rows [16, K] | s0 [16, ng] | partial sums [kLowbitMaxSplit, 16, N]
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   uint16_t* xb = reinterpret_cast<uint16_t*>(ws);
   const size_t xb_bytes = ((size_t)16 * K * 2 + 255) / 256 * 256;
   float* s0 = reinterpret_cast<float*>(ws + xb_bytes);
   const size_t s0_bytes = ((size_t)16 * ng * 4 + 255) / 256 * 256;
   float* y3 = reinterpret_cast<float*>(ws + xb_bytes + s0_bytes);
+  {
+    // decode: M <= 2 bf16 rows, one wave per weight row
+    const int cpl = bits == 3 ? 32 : 64;
+    const int J = (int)cdiv(cdiv(K, cpl), 64);
+    const size_t lds = (((size_t)2 * K * 2 + 15) & ~(size_t)15) + (size_t)2 * (K / cpl) * 4;
+    const bool layout = (scale_dtype == QS_F16 && zeros && zero_dtype == QS_F16) || (scale_dtype == QS_F32 && !zeros);
+    const int lb = bits == 3 ? 12 : 16;
+    if (x_dtype == QS_BF16 && M <= 2 && layout && K % cpl == 0 && group_size % cpl == 0 && J <= 6 && J != 5 &&
+        row_bytes % lb == 0 && aligned(packed, 16) && aligned(x, 16) && ldx % 8 == 0 && lds <= 64 * 1024) {
+      LowbitParams p{};
+      p.x = static_cast<const uint16_t*>(x);
+      p.ldx = ldx;
+      p.packed = packed;
+      p.row_bytes = row_bytes;
+      p.scales = scales;
+      p.zeros = zeros;
+      p.scale_f16 = scale_dtype == QS_F16;
+      p.zero_f16 = zero_dtype == QS_F16;
+      p.offset = offset;
+      p.y = y;
+      p.ldy = ldy;
+      p.M = (int)M;
+      p.N = (int)N;
+      p.K = (int)K;
+      p.ng = ng;
+      pair_consts(p, bits);
+      const int64_t wpb = kValuThreads / 64;
+      const unsigned grid = (unsigned)(cdiv(N, wpb) < 512 ? cdiv(N, wpb) : 512);
+      if (bits == 3) launch_valu<3>(J, (int)M, group_size, grid, lds, s, p);
+      else launch_valu<2>(J, (int)M, group_size, grid, lds, s, p);
+      return hip_check(hipGetLastError(), "k_lowbit_valu launch");
+    }
+  }
   for (int64_t m0 = 0; m0 < M; m0 += mb) {
     const int mm = (int)((M - m0) < mb ? (M - m0) : mb);
     const int rows = mm * rows_per_x;
     const void* xm = static_cast<const char*>(x) + m0 * ldx * (x_dtype == QS_F32 ? 4 : 2);
-    hipLaunchKernelGGL(k_lowbit_prep, dim3((unsigned)cdiv((int64_t)mm * K, 256)), dim3(256), 0, s, xm, x_dtype, ldx, mm, (int)K, xb);
-    hipLaunchKernelGGL(k_group_sums, dim3((unsigned)cdiv((int64_t)rows * ng, 4)), dim3(256), 0, s, xb, rows, (int)K, group_size, s0);
+    // slotted kernel: K split so that each workgroup's activations + group sums fit in LDS
+    const int tiles = (int)cdiv(N, 64);
+    int S = (int)cdiv(512, tiles);
+    S = S < 1 ? 1 : (S > kLowbitMaxSplit ? kLowbitMaxSplit : S);
+    int gps = (int)cdiv(ng, S);
+    auto lds_of = [&](int g) {
+      return (((size_t)rows * g * group_size * 2 + 15) & ~(size_t)15) + (size_t)rows * ((g + 3) & ~3) * 4;
+    };
+    while (lds_of(gps) > kSlotLds && S < kLowbitMaxSplit) gps = (int)cdiv(ng, ++S);
+    S = (int)cdiv(ng, gps);
+    const bool slot_layout = (scale_dtype == QS_F16 && zeros && zero_dtype == QS_F16) ||
+                             (scale_dtype == QS_F32 && !zeros);
+    const bool slot = tiled && slot_layout && lds_of(gps) <= kSlotLds;
+    // bf16 activations that are 16-byte aligned feed the slotted kernel directly
+    const bool x_direct = slot && x_dtype == QS_BF16 && aligned(xm, 16) && ldx % 8 == 0;
+    if (!x_direct)
+      hipLaunchKernelGGL(k_lowbit_prep, dim3((unsigned)cdiv((int64_t)mm * K, 256)), dim3(256), 0, s, xm, x_dtype, ldx, mm, (int)K, xb);
+    if (!slot)
+      hipLaunchKernelGGL(k_group_sums, dim3((unsigned)cdiv((int64_t)rows * ng, 4)), dim3(256), 0, s, xb, rows, (int)K, group_size, s0);
     LowbitParams p{};
-    p.x = xb;
-    p.ldx = K;
+    p.x = x_direct ? static_cast<const uint16_t*>(xm) : xb;
+    p.ldx = x_direct ? ldx : K;
     p.s0 = s0;
     p.packed = packed;
     p.row_bytes = row_bytes;
@@ -300,6 +794,24 @@ extern "C" int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uin
     p.N = (int)N;
     p.K = (int)K;
     p.ng = ng;
+    pair_consts(p, bits);
+    if (slot) {
+      const bool direct = S == 1 && x_dtype == QS_BF16;
+      p.y = y + m0 * ldy;
+      p.ldy = ldy;
+      float* part = direct ? nullptr : y3;
+      const dim3 grid((unsigned)tiles, (unsigned)S);
+      const int mp = (rows + 3) / 4;
+      const size_t lds = lds_of(gps);
+      if (bits == 3 && group_size == 64) launch_slot<3, 64>(mp, grid, lds, s, p, gps, part);
+      else if (bits == 3) launch_slot<3, 128>(mp, grid, lds, s, p, gps, part);
+      else if (group_size == 64) launch_slot<2, 64>(mp, grid, lds, s, p, gps, part);
+      else launch_slot<2, 128>(mp, grid, lds, s, p, gps, part);
+      if (!direct)
+        hipLaunchKernelGGL(k_lowbit_reduce, dim3((unsigned)cdiv((int64_t)mm * N, 256)), dim3(256), 0, s, y3, S,
+                           rows_per_x, mm, (int)N, y + m0 * ldy, ldy);
+      continue;
+    }
     if (x_dtype == QS_BF16) {
       p.y = y + m0 * ldy;
       p.ldy = ldy;
@@ -323,7 +835,7 @@ extern "C" size_t qs_lowbit_workspace_bytes(int x_dtype, int64_t M, int64_t N, i
   const int64_t ng = group_size > 0 ? K / group_size : 0;
   const size_t xb = ((size_t)16 * K * 2 + 255) / 256 * 256;
   const size_t s0 = ((size_t)16 * ng * 4 + 255) / 256 * 256;
-  const size_t y3 = (size_t)15 * N * 4;
+  const size_t y3 = (size_t)kLowbitMaxSplit * 16 * N * 4;
   return xb + s0 + y3;
 }
 

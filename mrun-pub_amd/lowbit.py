@@ -81,8 +81,13 @@ def lowbit_dequant(page: LowbitPage) -> torch.Tensor:
 
 
 @torch.inference_mode()
-def lowbit_matmul(page: LowbitPage, x: torch.Tensor) -> torch.Tensor:
-    """``x[..., in] @ W.T`` in fp32 (``QStoreInt3.matmul`` contract), fp32 ``[..., out]``."""
+def lowbit_matmul(page: LowbitPage, x: torch.Tensor, *, row_stable: bool = False) -> torch.Tensor:
+    """``x[..., in] @ W.T`` in fp32 (``QStoreInt3.matmul`` contract), fp32 ``[..., out]``.
+
+    ``row_stable=True`` runs every activation row as its own M = 1 product, so row b of a
+    batch equals the single-row result bit for bit (``matmul_row_stable``,
+    qstore.py:1343-1380); otherwise rows share launches and the kernel choice depends on M.
+    """
     _check(page)
     K = page.in_features
     if int(x.shape[-1]) != K:
@@ -96,14 +101,17 @@ def lowbit_matmul(page: LowbitPage, x: torch.Tensor) -> torch.Tensor:
     y = torch.empty((M, N), dtype=torch.float32, device=device)
     if M:
         xdt = nat.dtype_code(x2.dtype)
-        wsb = int(nat.load().qs_lowbit_workspace_bytes(xdt, M, N, K, page.group_size))
+        chunk = 1 if row_stable else M
+        wsb = int(nat.load().qs_lowbit_workspace_bytes(xdt, chunk, N, K, page.group_size))
         ws = torch.empty(wsb, dtype=torch.uint8, device=device)
-        nat.call(
-            "qs_lowbit_gemv", nat.ptr(x2), xdt, K, nat.ptr(page.packed), page.row_bytes, nat.ptr(page.scales),
-            nat.dtype_code(page.scales.dtype), nat.ptr(page.zeros),
-            nat.dtype_code(page.zeros.dtype) if page.zeros is not None else nat.QS_F32, page._offset(),
-            page.bits, page.group_size, nat.ptr(y), N, M, N, K, nat.ptr(ws), wsb, nat.stream_of(device),
-        )
+        for m0 in range(0, M, chunk):
+            mm = min(chunk, M - m0)
+            nat.call(
+                "qs_lowbit_gemv", nat.ptr(x2[m0:]), xdt, K, nat.ptr(page.packed), page.row_bytes, nat.ptr(page.scales),
+                nat.dtype_code(page.scales.dtype), nat.ptr(page.zeros),
+                nat.dtype_code(page.zeros.dtype) if page.zeros is not None else nat.QS_F32, page._offset(),
+                page.bits, page.group_size, nat.ptr(y[m0:]), N, mm, N, K, nat.ptr(ws), wsb, nat.stream_of(device),
+            )
     return y.reshape(*x.shape[:-1], N)
 
 
@@ -170,10 +178,10 @@ class DeviceLowbitQStore:
         return lowbit_matmul(self.page(name), x)
 
     def matmul_row_stable(self, name: str, x: torch.Tensor) -> torch.Tensor:
-        """Every row is an independent MFMA row: batched rows equal B=1 rows bit for bit."""
+        """Each row runs as its own product: batched rows equal B=1 rows bit for bit."""
         if x.ndim < 2 or int(x.shape[0]) <= 0:
             raise ValueError("row-stable matmul input must have shape [B, ..., in]")
-        return lowbit_matmul(self.page(name), x)
+        return lowbit_matmul(self.page(name), x, row_stable=True)
 
     def row_blocks(self, name: str, bs: int = 8192):
         W = self.weight(name)

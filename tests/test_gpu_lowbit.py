@@ -86,14 +86,32 @@ def test_gemv_reference_layout(dev, bits, xdt, m):
     assert oq.rel_l2(y.cpu().numpy(), ref) <= F32_TOL
 
 
+@pytest.mark.parametrize("bits,K", [(3, 320), (2, 320), (3, 64), (2, 8192)])
+@pytest.mark.parametrize("m", [1, 5])
+def test_gemv_odd_layouts(dev, bits, K, m):
+    """Rows that are not 16-byte multiples (int3 K=320: 120-byte rows) take the unstaged
+    kernel; the rest exercise partial chunks and K splits of the staged kernel."""
+    rng = np.random.default_rng(bits * K + m)
+    packed, s, z = _asym(rng, 77, K, bits)
+    x = oq.round_bf16(rng.standard_normal((m, K)).astype(np.float32))
+    for xdt in (torch.bfloat16, torch.float32):
+        y = _lb().lowbit_matmul(_page(dev, packed, s, K, bits, 64, z), torch.from_numpy(x).to(dev).to(xdt))
+        ref = ol.lowbit_matmul(packed, s, x, K, bits, 64, zeros=z)
+        assert oq.rel_l2(y.cpu().numpy(), ref) <= F32_TOL
+
+
 def test_rows_independent_of_batch(dev):
     rng = np.random.default_rng(9)
     packed, s, z = _asym(rng, 512, 1024, 3)
     x = torch.from_numpy(rng.standard_normal((8, 1024)).astype(np.float32)).to(dev).to(torch.bfloat16)
     page = _page(dev, packed, s, 1024, 3, 64, z)
-    full = _lb().lowbit_matmul(page, x)
+    full = _lb().lowbit_matmul(page, x, row_stable=True)
     for r in (0, 3, 7):
         assert torch.equal(_lb().lowbit_matmul(page, x[r : r + 1])[0], full[r])
+    for xdt in (torch.float32, torch.bfloat16):  # batched rows agree within tolerance too
+        xb = x.to(xdt)
+        ref = _lb().lowbit_matmul(page, xb, row_stable=True)
+        assert oq.rel_l2(_lb().lowbit_matmul(page, xb).cpu().numpy(), ref.cpu().numpy()) <= F32_TOL
 
 
 def test_reference_store_reader(dev, tmp_path):
