@@ -382,15 +382,18 @@ __device__ __forceinline__ void valu_chunk(i32x4 w, float sc, const uint8_t* xs,
 // activations are staged in LDS per workgroup while the codes are in flight.
 // For plain linears tile_begin of linear i holds its first global row; all rows of a
 // wave belong to one linear (each linear's rows are padded to a multiple of R).
+// Waves per workgroup of the VALU GEMV: the activations staged in LDS serve 8 rows.
+constexpr int kGemvWaves = 8;
+
 template <int XT, int MB, int U, int R, bool SWI>
-__global__ __launch_bounds__(256) void k_gemv_valu(QrowParams p, int rows) {
+__global__ __launch_bounds__(kGemvWaves * 64) void k_gemv_valu(QrowParams p, int rows) {
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
   constexpr int ES = XElem<XT>::size;
   constexpr int P = SWI ? 2 : R;
   const int lane = threadIdx.x & 63;
   const int K = p.K;
   const int M = p.M;  // <= MB
-  const int r0 = ((int)blockIdx.x * 4 + (threadIdx.x >> 6)) * (SWI ? 1 : R);
+  const int r0 = ((int)blockIdx.x * kGemvWaves + (threadIdx.x >> 6)) * (SWI ? 1 : R);
   const bool live = r0 < rows;
   const int rr = live ? r0 : 0;
   int li = 0;
@@ -424,7 +427,7 @@ __global__ __launch_bounds__(256) void k_gemv_valu(QrowParams p, int rows) {
   }
   // stage the activations (M rows x K) in LDS while the codes are in flight
   const int row16 = K * ES / 16;
-  for (int i = threadIdx.x; i < M * row16; i += 256) {
+  for (int i = threadIdx.x; i < M * row16; i += kGemvWaves * 64) {
     const int m = i / row16;
     const int c = i - m * row16;
     reinterpret_cast<i32x4*>(xs)[i] = *reinterpret_cast<const i32x4*>(
@@ -635,18 +638,18 @@ template <int XT, int MB, int R, bool SWI>
 void launch_valu_r(const QrowParams& q, int rows, int blocks, size_t lds, hipStream_t s) {
   const int chunks = (q.K + 1023) / 1024;
   if (chunks <= 2)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 2, R, SWI>), dim3(blocks), dim3(256), lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 2, R, SWI>), dim3(blocks), dim3(kGemvWaves * 64), lds, s, q, rows);
   else if (chunks <= 4)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 4, R, SWI>), dim3(blocks), dim3(256), lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 4, R, SWI>), dim3(blocks), dim3(kGemvWaves * 64), lds, s, q, rows);
   else if (chunks <= 8)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 8, R, SWI>), dim3(blocks), dim3(256), lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 8, R, SWI>), dim3(blocks), dim3(kGemvWaves * 64), lds, s, q, rows);
   else
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 12, R, SWI>), dim3(blocks), dim3(256), lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 12, R, SWI>), dim3(blocks), dim3(kGemvWaves * 64), lds, s, q, rows);
 }
 
 template <int XT, int MB, bool SWI>
 void launch_valu_mb(const QrowParams& q, int R, int rows, size_t lds, hipStream_t s) {
-  const int blocks = (int)cdiv(cdiv(rows, R), 4);
+  const int blocks = (int)cdiv(cdiv(rows, R), kGemvWaves);
   if constexpr (SWI) {
     launch_valu_r<XT, MB, 1, true>(q, rows, blocks, lds, s);
   } else {
