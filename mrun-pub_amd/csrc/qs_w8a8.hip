@@ -353,7 +353,7 @@ enum { EPI_I32 = 0, EPI_F32 = 1, EPI_BF16 = 2 };
 
 constexpr int kBK = 64;        // k bytes per step
 constexpr int kLdsRow = 80;    // padded LDS row (64 data + 16): conflict-free 16B reads
-constexpr int kSideLds = 16;   // side-path columns staged in LDS by the epilogue
+constexpr int kSideLds = 16;   // side-path columns per LDS staging in the epilogue
 
 template <int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmParams p) {
@@ -453,57 +453,67 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmPara
     __syncthreads();
   }
 
-  // side-path operands of this tile in LDS (P <= kSideLds): xs[BM][16], wsT[16][BN]
-  const bool side_lds = EPI != EPI_I32 && p.P > 0 && p.P <= kSideLds;
-  float* xs = reinterpret_cast<float*>(&lds[0][0]);
-  float* ws = xs + BM * kSideLds;
-  if (side_lds) {
-    for (int i = tid; i < BM * p.P; i += NT) {
-      const int r = i / p.P, q = i - (i / p.P) * p.P;
-      xs[r * kSideLds + q] = bm + r < p.M ? p.xp[(int64_t)(bm + r) * p.P + q] : 0.f;
+  // Epilogue.  The side path (P protected columns, fp32) runs on the matrix cores:
+  // side[32x32 tile] = xs[rows][P] . ws[P][cols] with v_mfma_f32_32x32x2_f32, whose
+  // accumulator layout is the int32 one, so each lane adds side[r] to its own outputs.
+  // Operands go through LDS in chunks of kSideLds columns (zero padded); with
+  // P <= kSideLds one staging serves every tile.
+  const int nsc = (EPI != EPI_I32 && p.P > 0) ? (p.P + kSideLds - 1) / kSideLds : 0;
+  float* xs = reinterpret_cast<float*>(&lds[0][0]);  // [BM][kSideLds]
+  float* ws = xs + BM * kSideLds;                     // [kSideLds][BN]
+  auto stage_side = [&](int q0) {
+    for (int t = tid; t < BM * kSideLds; t += NT) {
+      const int r = t / kSideLds, q = q0 + (t - (t / kSideLds) * kSideLds);
+      xs[t] = (bm + r < p.M && q < p.P) ? p.xp[(int64_t)(bm + r) * p.P + q] : 0.f;
     }
-    for (int i = tid; i < BN * p.P; i += NT) {
-      const int c = i / p.P, q = i - (i / p.P) * p.P;
-      ws[q * BN + c] = bn + c < p.N ? p.wp[(int64_t)(bn + c) * p.P + q] : 0.f;
+    for (int t = tid; t < BN * kSideLds; t += NT) {
+      const int c = t / kSideLds, qq = t - (t / kSideLds) * kSideLds, q = q0 + qq;
+      ws[qq * BN + c] = (bn + c < p.N && q < p.P) ? p.wp[(int64_t)(bn + c) * p.P + q] : 0.f;
     }
+  };
+  if (nsc == 1) {
+    stage_side(0);
     __syncthreads();
   }
-
-  // epilogue
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const int col = bn + wn * WN + 32 * j + (lane & 31);
-      if (col >= p.N) continue;
+      const int lr = wm * WM + 32 * i;  // tile row / column offsets within the block
+      const int lc = wn * WN + 32 * j;
+      f32x16 side = {};
+      for (int c = 0; c < nsc; ++c) {
+        if (nsc > 1) {
+          __syncthreads();
+          stage_side(c * kSideLds);
+          __syncthreads();
+        }
+        const int qn = min(kSideLds, p.P - c * kSideLds);
+        for (int s2 = 0; s2 < qn; s2 += 2) {
+          const float xa = xs[(lr + (lane & 31)) * kSideLds + s2 + (lane >> 5)];
+          const float wb = ws[(s2 + (lane >> 5)) * BN + lc + (lane & 31)];
+          side = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, wb, side, 0, 0, 0);
+        }
+      }
+      const int col = bn + lc + (lane & 31);
       float bsc = 0.f;
-      if constexpr (EPI != EPI_I32) bsc = p.bs[col];
+      if constexpr (EPI != EPI_I32) bsc = col < p.N ? p.bs[col] : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = bm + wm * WM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row >= p.M) continue;
-        if constexpr (EPI == EPI_I32) {
-          static_cast<int32_t*>(p.c)[(int64_t)row * p.ldc + col] = acc[i][j][r];
-        } else {
-          // reference order: (float(acc) * act_scale) * w_scale, added to the side path
-          float v = mul_rn(mul_rn(static_cast<float>(acc[i][j][r]), p.as[row]), bsc);
-          if (side_lds) {
-            float side = 0.f;
-            const float* xr = xs + (row - bm) * kSideLds;
-            const float* wr = ws + (col - bn);
-            for (int q = 0; q < p.P; ++q) side = fmaf(xr[q], wr[q * BN], side);
-            v = add_rn(side, v);
-          } else if (p.P > 0) {
-            float side = 0.f;
-            const float* xr = p.xp + (int64_t)row * p.P;
-            const float* wr = p.wp + (int64_t)col * p.P;
-            for (int q = 0; q < p.P; ++q) side = fmaf(xr[q], wr[q], side);
-            v = add_rn(side, v);
+        const int row = bm + lr + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < p.M && col < p.N) {
+          if constexpr (EPI == EPI_I32) {
+            static_cast<int32_t*>(p.c)[(int64_t)row * p.ldc + col] = acc[i][j][r];
+          } else {
+            // reference order: (float(acc) * act_scale) * w_scale, added to the side path
+            float v = mul_rn(mul_rn(static_cast<float>(acc[i][j][r]), p.as[row]), bsc);
+            if (nsc) v = add_rn(side[r], v);
+            if constexpr (EPI == EPI_F32)
+              static_cast<float*>(p.c)[(int64_t)row * p.ldc + col] = v;
+            else
+              static_cast<uint16_t*>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16_bits(v);
           }
-          if constexpr (EPI == EPI_F32)
-            static_cast<float*>(p.c)[(int64_t)row * p.ldc + col] = v;
-          else
-            static_cast<uint16_t*>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16_bits(v);
         }
       }
     }
