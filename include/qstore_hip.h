@@ -95,8 +95,7 @@ int qs_act_quant_i8(const void* x, int x_dtype, int64_t ldx, const float* keep, 
 
 /* Outlier column selection of w8a8_matmul (w8a8.py:98-102): colmax[k] = max_m |x[m,k]|,
  * idx = the k largest (1 <= k <= 64, ties -> lower column), keep = 1 except 0 at idx.
- * colmax is caller-provided workspace of ceil(M/64) * K floats; colmax[0..K) holds the
- * column maxima on return. */
+ * colmax is caller-provided workspace of K floats and holds the column maxima on return. */
 int qs_outlier_topk(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int k,
                     float* colmax, int64_t* idx, float* keep, void* stream);
 

@@ -94,17 +94,23 @@ __global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x,
     if constexpr (XT == QS_BF16) return bf16_bits_to_f32(h);
     return f16_bits_to_f32(static_cast<uint16_t>(h));
   };
-  auto keepv = [&](int ch, int e) -> float { return keep[ch * E + e]; };
+  // keep mask of chunk ch: E floats at keep + ch*E (16-byte aligned), read as float4s
+  auto keep4 = [&](int ch, int h) -> f32x4 { return reinterpret_cast<const f32x4*>(keep + ch * E)[h]; };
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int ch = c * 64 + lane;
     if (ch < nch) {
       v[c] = *reinterpret_cast<const i32x4*>(xr + (int64_t)ch * 16);
+      if (keep) {
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        float f = widen(v[c], e);
-        if (keep) f = mul_rn(f, keepv(ch, e));
-        amax = fmaxf(amax, fabsf(f));
+        for (int h = 0; h < E / 4; ++h) {
+          const f32x4 kv = keep4(ch, h);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(mul_rn(widen(v[c], 4 * h + e), kv[e])));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) amax = fmaxf(amax, fabsf(widen(v[c], e)));
       }
     }
   }
@@ -120,10 +126,13 @@ __global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x,
       uint32_t packed[E / 4];
 #pragma unroll
       for (int j = 0; j < E / 4; ++j) packed[j] = 0;
+      f32x4 kv[E / 4];
+#pragma unroll
+      for (int h = 0; h < E / 4; ++h) kv[h] = keep ? keep4(ch, h) : f32x4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         float f = widen(v[c], e);
-        if (keep) f = mul_rn(f, keepv(ch, e));
+        if (keep) f = mul_rn(f, kv[e >> 2][e & 3]);
         float r = rintf(f / s);  // IEEE division, round half to even
         r = fminf(fmaxf(r, -127.f), 127.f);
         packed[e >> 2] |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xffu) << (8 * (e & 3));
@@ -136,8 +145,8 @@ __global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x,
   }
 }
 
-// Partial column maxima: block (bx, by) covers 256 columns x 64 rows and writes
-// part[by, k] = max over its rows of |x[m, k]|.
+// Column maxima: block (bx, by) covers 256 columns x 64 rows and folds the max over its
+// rows of |x[m, k]| into colmax[k] (zeroed beforehand by k_fill_zero).
 template <int XT>
 __global__ __launch_bounds__(256) void k_col_absmax(const void* __restrict__ x, int64_t ldx,
                                                     int M, int K, float* __restrict__ part) {
@@ -155,7 +164,14 @@ __global__ __launch_bounds__(256) void k_col_absmax(const void* __restrict__ x, 
   float r = a[0];
 #pragma unroll
   for (int j = 1; j < 8; ++j) r = fmaxf(r, a[j]);
-  part[(int64_t)blockIdx.y * K + k] = r;
+  // non-negative floats order like their bit patterns: an integer max is the float max,
+  // exact and independent of the order in which the row blocks arrive
+  atomicMax(reinterpret_cast<unsigned int*>(part) + k, __float_as_uint(r));
+}
+
+__global__ __launch_bounds__(256) void k_fill_zero(float* __restrict__ p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0.f;
 }
 
 // Single workgroup: kk rounds of a block-wide argmax over vals[0..K).  Selected entries
@@ -630,6 +646,7 @@ extern "C" int qs_outlier_topk(const void* x, int x_dtype, int64_t ldx, int64_t 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int parts = (int)cdiv(M, 64);
   const dim3 grid((unsigned)cdiv(K, 256), (unsigned)parts);
+  hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, s, colmax, (int)K);
   if (x_dtype == QS_F32)
     hipLaunchKernelGGL(k_col_absmax<QS_F32>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
   else if (x_dtype == QS_BF16)
@@ -639,9 +656,9 @@ extern "C" int qs_outlier_topk(const void* x, int x_dtype, int64_t ldx, int64_t 
   else
     return fail(QS_ERR_INVALID, "outlier_topk: dtype must be F32, BF16 or F16");
   if (K <= 16 * 64 * kTopkVpl)
-    hipLaunchKernelGGL(k_topk_w, dim3(1), dim3(1024), 0, s, colmax, (int)K, parts, k, idx, keep);
+    hipLaunchKernelGGL(k_topk_w, dim3(1), dim3(1024), 0, s, colmax, (int)K, 1, k, idx, keep);
   else
-    hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), 0, s, colmax, (int)K, parts, k, idx, keep);
+    hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), 0, s, colmax, (int)K, 1, k, idx, keep);
   return hip_check(hipGetLastError(), "outlier_topk launch");
 }
 

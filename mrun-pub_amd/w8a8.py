@@ -124,7 +124,7 @@ def w8a8_matmul(
     idx = None
     if protect_idx is None and protect_k > 0:
         k = min(int(protect_k), inn)
-        colmax = torch.empty(((T + 63) // 64) * inn, dtype=torch.float32, device=device)
+        colmax = torch.empty(inn, dtype=torch.float32, device=device)
         idx = torch.empty(k, dtype=torch.int64, device=device)
         keep = torch.empty(inn, dtype=torch.float32, device=device)
         nat.call("qs_outlier_topk", nat.ptr(x2), xdt, inn, T, inn, k, nat.ptr(colmax), nat.ptr(idx), nat.ptr(keep), stream)

@@ -76,7 +76,7 @@ def test_outlier_topk_matches_oracle(dev, t, k, kk):
     x[:, rng.permutation(k)[: kk // 2 + 1]] *= 50.0
     x[0, 1] = x[0, 2] = x[-1, 40] = 1000.0  # ties resolve to the lower column
     xd = torch.from_numpy(x).to(dev)
-    colmax = torch.empty(((t + 63) // 64) * k, dtype=torch.float32, device=dev)
+    colmax = torch.empty(k, dtype=torch.float32, device=dev)
     idx = torch.empty(kk, dtype=torch.int64, device=dev)
     keep = torch.empty(k, dtype=torch.float32, device=dev)
     nat.call("qs_outlier_topk", nat.ptr(xd), nat.QS_F32, k, t, k, kk, nat.ptr(colmax), nat.ptr(idx),
@@ -86,6 +86,7 @@ def test_outlier_topk_matches_oracle(dev, t, k, kk):
     kref = np.ones(k, np.float32)
     kref[ref] = 0.0
     assert np.array_equal(keep.cpu().numpy(), kref)
+    assert np.array_equal(colmax.cpu().numpy(), np.abs(x).max(axis=0))
 
 
 @pytest.mark.parametrize("t", [1, 17, 512])
