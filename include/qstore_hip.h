@@ -147,7 +147,8 @@ int qs_moe_gather_quant(const void* source, int src_dtype, int64_t ld_src, const
  * w + slot(g)*w_stride ([N_w, K] int8 rows; slot(g) = slots ? slots[g] : g):
  *   out[row, n] = (float(acc) * a_scale[row]) * w_scale[slot(g)*ws_stride + n]
  * (F32/BF16); swiglu != 0: N_w = 2N, out[row, n] = bf16(bf16(silu(bf16(gate))) * bf16(up))
- * with gate from weight row n and up from row n + N.  K % 64 == 0. */
+ * with gate from weight row n and up from row n + N.  K % 64 == 0, K <= 8192 with SwiGLU,
+ * K <= 16384 without. */
 int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* w,
                            int64_t w_stride, const float* w_scale, int64_t ws_stride,
                            const int32_t* starts, const int32_t* counts, const int32_t* slots,

@@ -11,7 +11,8 @@
 //                       the reference's stable argsort and is identical on every call.
 //   k_moe_gather_quant: per routed row, int8 per-token quantization of source[token_ids[a]]
 //                       (the W8A8 recipe: s = max|x|/127, 0 -> 1; rint; clamp +-127).
-//   k_moe_gemm<...>   : one workgroup per (group, 16-row tile of N); its waves split K, hold
+//   k_moe_gemm<...>   : one workgroup per (group, 4 consecutive 16-row tiles of N, the next
+//                       tile's weights loading while the current one is reduced); its waves split K, hold
 //                       their weight slice in VGPRs (streamed once from HBM with 128-bit
 //                       loads) and walk the group's rows 16 at a time with
 //                       v_mfma_i32_16x16x64_i8; LDS reduction over the K split; epilogue
@@ -253,7 +254,7 @@ __device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + ex
 
 // P = 1: plain; P = 2: paired SwiGLU (plane 0 = gate row n, plane 1 = up row n + N).
 // KW waves per plane split K; each wave holds CH 64-k chunks of its 16 weight rows.
-template <int P, int KW, int CH>
+template <int P, int KW, int CH, int NT>
 __global__ __launch_bounds__(P * KW * 64) void k_moe_gemm(MoeGemmParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -265,83 +266,103 @@ __global__ __launch_bounds__(P * KW * 64) void k_moe_gemm(MoeGemmParams p) {
   if (count == 0) return;
   const int start = p.starts[g];
   const int slot = p.slots ? p.slots[g] : g;
-  const int n0 = blockIdx.x * 16;
-  int n = n0 + col;
-  const bool nval = n < p.N;
-  n = nval ? n : p.N - 1;
-  const int wrow_idx = n + plane * p.N;
-  const int8_t* wrow = p.w + (int64_t)slot * p.w_stride + (int64_t)wrow_idx * p.K + 16 * grp;
   const int C = p.K / 64;
+  const int ntiles = (p.N + 15) / 16;
+  const int tile0 = blockIdx.x * NT;
+  const int8_t* wexp = p.w + (int64_t)slot * p.w_stride + 16 * grp;
 
-  // the wave's weight slice: chunks ks, ks + KW, ... (at most CH of them)
-  i32x4 wv[CH];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int cc = ks + c * KW;
-    wv[c] = cc < C ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wrow + (int64_t)cc * 64))
-                   : i32x4{0, 0, 0, 0};
-  }
-  const float wsc = p.ws[(int64_t)slot * p.ws_stride + wrow_idx];
-
-  __shared__ i32x4 red[P * KW][64];
-  for (int m0 = 0; m0 < count; m0 += 16) {
-    const int m = m0 + col;
-    const bool mval = m < count;
-    const int8_t* arow = p.a + (int64_t)(start + (mval ? m : 0)) * p.K + 16 * grp;
-    i32x4 acc = {0, 0, 0, 0};
+  // the wave's weight slice of one 16-row tile: chunks ks, ks + KW, ... (at most CH);
+  // two slices in registers so that tile t + 1 streams in while tile t is reduced
+  i32x4 wv[2][CH];
+  auto wload = [&](int b, int t) {
+    const int n = min(t * 16 + col, p.N - 1);
+    const int8_t* wrow = wexp + (int64_t)(n + plane * p.N) * p.K;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int cc = ks + c * KW;
-      if (cc < C) {
-        const i32x4 av = mval ? *reinterpret_cast<const i32x4*>(arow + (int64_t)cc * 64) : i32x4{0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, wv[c], acc, 0, 0, 0);
-      }
+      wv[b][c] = cc < C ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wrow + (int64_t)cc * 64))
+                        : i32x4{0, 0, 0, 0};
     }
-    red[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0) {
-      i32x4 tot[P];
+  };
+
+  __shared__ i32x4 red[P * KW][64];
+  if (tile0 < ntiles) wload(0, tile0);
+  // epilogue operands of the first tile / row block, requested with the weights so that
+  // the reduction does not wait for a second memory round trip
+  float sc0[P], as0[4];
+  {
+    const int no = min(tile0 * 16 + col, p.N - 1);
 #pragma unroll
-      for (int pl = 0; pl < P; ++pl) {
-        i32x4 s = red[pl][lane];
+    for (int pl = 0; pl < P; ++pl) sc0[pl] = p.ws[(int64_t)slot * p.ws_stride + no + pl * p.N];
 #pragma unroll
-        for (int k2 = 1; k2 < KW; ++k2) s += red[k2 * P + pl][lane];
-        tot[pl] = s;
+    for (int q = 0; q < 4; ++q) as0[q] = p.as[start + min(4 * grp + q, count - 1)];
+  }
+#pragma unroll
+  for (int ti = 0; ti < NT; ++ti) {
+    const int t = tile0 + ti;
+    if (t >= ntiles) break;
+    const int b = ti & 1;
+    if (ti + 1 < NT && t + 1 < ntiles) wload(b ^ 1, t + 1);
+    const int n0 = t * 16;
+    for (int m0 = 0; m0 < count; m0 += 16) {
+      const int m = m0 + col;
+      const bool mval = m < count;
+      const int8_t* arow = p.a + (int64_t)(start + (mval ? m : 0)) * p.K + 16 * grp;
+      i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int cc = ks + c * KW;
+        if (cc < C) {
+          const i32x4 av = mval ? *reinterpret_cast<const i32x4*>(arow + (int64_t)cc * 64) : i32x4{0, 0, 0, 0};
+          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, wv[b][c], acc, 0, 0, 0);
+        }
       }
-      const int no = n0 + col;
-      if (no < p.N) {
-        float sc[P];
+      red[wave][lane] = acc;
+      __syncthreads();
+      // the K-split partial sums of 16 rows x 16 tokens, reduced and finished by the
+      // first wave of each plane group
+      if (wave == 0) {
+        i32x4 tot[P];
 #pragma unroll
-        for (int pl = 0; pl < P; ++pl)
-          sc[pl] = p.ws[(int64_t)slot * p.ws_stride + no + pl * p.N];
+        for (int pl = 0; pl < P; ++pl) {
+          i32x4 s = red[pl][lane];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int mr = m0 + 4 * grp + q;
-          if (mr < count) {
-            const int64_t row = start + mr;
-            const float a_s = p.as[row];
-            if constexpr (P == 2) {
-              const float gv = mul_rn(mul_rn(static_cast<float>(tot[0][q]), a_s), sc[0]);
-              const float uv = mul_rn(mul_rn(static_cast<float>(tot[1][q]), a_s), sc[1]);
-              const float gt = bf16_bits_to_f32(f32_to_bf16_bits(gv));
-              const float ut = bf16_bits_to_f32(f32_to_bf16_bits(uv));
-              const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f(gt)));
-              static_cast<uint16_t*>(p.out)[row * p.N + no] = f32_to_bf16_bits(mul_rn(sl, ut));
-            } else {
-              const float v = mul_rn(mul_rn(static_cast<float>(tot[0][q]), a_s), sc[0]);
-              if (p.out_dtype == QS_F32)
-                static_cast<float*>(p.out)[row * p.N + no] = v;
-              else
-                static_cast<uint16_t*>(p.out)[row * p.N + no] = f32_to_bf16_bits(v);
+          for (int k2 = 1; k2 < KW; ++k2) s += red[k2 * P + pl][lane];
+          tot[pl] = s;
+        }
+        const int no = n0 + col;
+        if (no < p.N) {
+          float sc[P];
+#pragma unroll
+          for (int pl = 0; pl < P; ++pl)
+            sc[pl] = ti == 0 ? sc0[pl] : p.ws[(int64_t)slot * p.ws_stride + no + pl * p.N];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int mr = m0 + 4 * grp + q;
+            if (mr < count) {
+              const int64_t row = start + mr;
+              const float a_s = m0 == 0 ? as0[q] : p.as[row];
+              if constexpr (P == 2) {
+                const float gv = mul_rn(mul_rn(static_cast<float>(tot[0][q]), a_s), sc[0]);
+                const float uv = mul_rn(mul_rn(static_cast<float>(tot[1][q]), a_s), sc[1]);
+                const float gt = bf16_bits_to_f32(f32_to_bf16_bits(gv));
+                const float ut = bf16_bits_to_f32(f32_to_bf16_bits(uv));
+                const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f(gt)));
+                static_cast<uint16_t*>(p.out)[row * p.N + no] = f32_to_bf16_bits(mul_rn(sl, ut));
+              } else {
+                const float v = mul_rn(mul_rn(static_cast<float>(tot[0][q]), a_s), sc[0]);
+                if (p.out_dtype == QS_F32)
+                  static_cast<float*>(p.out)[row * p.N + no] = v;
+                else
+                  static_cast<uint16_t*>(p.out)[row * p.N + no] = f32_to_bf16_bits(v);
+              }
             }
           }
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
-  (void)wsc;
-  (void)nval;
 }
 
 // ----------------------------------------------------------------------------------
@@ -426,14 +447,18 @@ extern "C" int qs_moe_gather_quant(const void* source, int src_dtype, int64_t ld
 }
 
 namespace {
+constexpr int kMoeTilesPerBlock = 1;  // 16-row tiles per workgroup, streamed back to back
+
 template <int P, int KW>
 void launch_moe_gemm(const MoeGemmParams& p, int G, hipStream_t s) {
   const int C = p.K / 64;
   const int ch = (C + KW - 1) / KW;
-  dim3 grid((unsigned)cdiv(p.N, 16), (unsigned)G);
-  if (ch <= 2) hipLaunchKernelGGL((k_moe_gemm<P, KW, 2>), grid, dim3(P * KW * 64), 0, s, p);
-  else if (ch <= 4) hipLaunchKernelGGL((k_moe_gemm<P, KW, 4>), grid, dim3(P * KW * 64), 0, s, p);
-  else hipLaunchKernelGGL((k_moe_gemm<P, KW, 8>), grid, dim3(P * KW * 64), 0, s, p);
+  constexpr int NT = kMoeTilesPerBlock;
+  dim3 grid((unsigned)cdiv(cdiv(p.N, 16), NT), (unsigned)G);
+  if (ch <= 2) hipLaunchKernelGGL((k_moe_gemm<P, KW, 2, NT>), grid, dim3(P * KW * 64), 0, s, p);
+  else if (ch <= 4) hipLaunchKernelGGL((k_moe_gemm<P, KW, 4, NT>), grid, dim3(P * KW * 64), 0, s, p);
+  else if (ch <= 8) hipLaunchKernelGGL((k_moe_gemm<P, KW, 8, NT>), grid, dim3(P * KW * 64), 0, s, p);
+  else hipLaunchKernelGGL((k_moe_gemm<P, KW, 16, NT>), grid, dim3(P * KW * 64), 0, s, p);
 }
 }  // namespace
 
@@ -445,7 +470,8 @@ extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, con
   if (!a || !a_scale || !w || !w_scale || !starts || !counts || !out)
     return fail(QS_ERR_INVALID, "moe_grouped_gemm: null pointer");
   if (G < 1 || G > 65535 || N <= 0 || K <= 0) return fail(QS_ERR_INVALID, "moe_grouped_gemm: bad shape");
-  if (K % 64 != 0 || K > 64 * 64 * 8) return fail(QS_ERR_UNSUPPORTED, "moe_grouped_gemm: K must be a multiple of 64, <= 32768");
+  if (K % 64 != 0 || K > (swiglu ? 8192 : 16384))
+    return fail(QS_ERR_UNSUPPORTED, "moe_grouped_gemm: K must be a multiple of 64, <= 8192 (SwiGLU) / 16384");
   if (!aligned(a, 16) || !aligned(w, 16) || w_stride % 16 != 0)
     return fail(QS_ERR_UNSUPPORTED, "moe_grouped_gemm: operands must be 16-byte aligned");
   if (swiglu && out_dtype != QS_BF16) return fail(QS_ERR_INVALID, "moe_grouped_gemm: SwiGLU output is BF16");
@@ -453,12 +479,13 @@ extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, con
   MoeGemmParams p{a, a_scale, w, w_stride, w_scale, ws_stride, starts, counts, slots, (int)N, (int)K, out, out_dtype};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int C = (int)(K / 64);
+  // K split so that each wave holds at most 16 chunks of 64 k of its tile (<= 1024 threads)
   if (swiglu) {
-    if (C <= 16) launch_moe_gemm<2, 4>(p, G, s);
+    if (C <= 32) launch_moe_gemm<2, 4>(p, G, s);
     else launch_moe_gemm<2, 8>(p, G, s);
   } else {
-    if (C <= 16) launch_moe_gemm<1, 4>(p, G, s);
-    else if (C <= 32) launch_moe_gemm<1, 8>(p, G, s);
+    if (C <= 32) launch_moe_gemm<1, 4>(p, G, s);
+    else if (C <= 128) launch_moe_gemm<1, 8>(p, G, s);
     else launch_moe_gemm<1, 16>(p, G, s);
   }
   return hip_check(hipGetLastError(), "k_moe_gemm launch");
