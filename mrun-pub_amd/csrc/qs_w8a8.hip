@@ -8,7 +8,7 @@
 //   k_col_absmax     : max over rows of |x[:, k]| (outlier column detection).
 //   k_topk           : the k largest column maxima (ties -> lower column index).
 //   k_gather_side    : xp[m, p] = x[m, idx[p]], wp[n, p] = float(qw[n, idx[p]]) * sw[n].
-//   k_gemm_i8<...>   : C = A[M,K] . B[N,K]^T with v_mfma_i32_32x32x32_i8, 64-byte K
+//   k_gemm_i8<...>   : C = A[M,K] . B[N,K]^T with v_mfma_i32_32x32x32_i8, 128/64-byte K
 //                      steps staged through padded, double-buffered LDS tiles, an XCD-aware
 //                      tile order, and one of three epilogues: raw int32, or
 //                      y = side + (float(acc) * a_scale[m]) * b_scale[n] in fp32 / bf16.
@@ -367,18 +367,21 @@ struct GemmParams {
 
 enum { EPI_I32 = 0, EPI_F32 = 1, EPI_BF16 = 2 };
 
-constexpr int kBK = 64;        // k bytes per step
-constexpr int kLdsRow = 80;    // padded LDS row (64 data + 16): conflict-free 16B reads
+constexpr int kBK = 64;        // default k bytes per step; LDS rows padded by 16 bytes
 constexpr int kSideLds = 16;   // side-path columns per LDS staging in the epilogue
 
-template <int BM, int BN, int WM, int WN, int EPI>
+template <int BM, int BN, int WM, int WN, int EPI, int BK = kBK>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmParams p) {
   constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
   constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int FM = WM / 32, FN = WN / 32;
-  constexpr int A_CH = BM * 4 / NT, B_CH = BN * 4 / NT;  // 16-byte chunks per thread
-  static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for the thread count");
-  __shared__ __attribute__((aligned(16))) int8_t lds[2][(BM + BN) * kLdsRow];
+  constexpr int LROW = BK + 16;                            // padded LDS row
+  constexpr int RC = BK / 16;                              // 16-byte chunks per tile row
+  constexpr int A_CH = BM * RC / NT, B_CH = BN * RC / NT;  // 16-byte chunks per thread
+  static_assert(A_CH >= 1 && B_CH >= 1 && BM * RC % NT == 0 && BN * RC % NT == 0,
+                "tile too small for the thread count");
+  static_assert(2 * (BM + BN) * LROW >= (BM + BN) * kSideLds * 4, "epilogue staging needs the tile LDS");
+  __shared__ __attribute__((aligned(16))) int8_t lds[2][(BM + BN) * LROW];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -404,22 +407,22 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmPara
 #pragma unroll
   for (int i = 0; i < A_CH; ++i) {
     const int c = tid + i * NT;
-    const int r = c >> 2, col = (c & 3) * 16;
+    const int r = c / RC, col = (c % RC) * 16;
     const int gr = bm + r < p.M ? bm + r : p.M - 1;
     ga[i] = p.a + (int64_t)gr * p.lda + col;
-    la[i] = r * kLdsRow + col;
+    la[i] = r * LROW + col;
   }
 #pragma unroll
   for (int i = 0; i < B_CH; ++i) {
     const int c = tid + i * NT;
-    const int r = c >> 2, col = (c & 3) * 16;
+    const int r = c / RC, col = (c % RC) * 16;
     const int gr = bn + r < p.N ? bn + r : p.N - 1;
     gb[i] = p.b + (int64_t)gr * p.ldb + col;
-    lb[i] = (BM + r) * kLdsRow + col;
+    lb[i] = (BM + r) * LROW + col;
   }
   i32x4 ra[A_CH], rb[B_CH];
   auto gload = [&](int kt) {
-    const int64_t ko = (int64_t)kt * kBK;
+    const int64_t ko = (int64_t)kt * BK;
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const i32x4*>(ga[i] + ko);
 #pragma unroll
@@ -440,7 +443,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmPara
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  const int KT = p.K / kBK;
+  const int KT = p.K / BK;
   gload(0);
   lstore(0);
   __syncthreads();
@@ -451,14 +454,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmPara
     const int buf = kt & 1;
     if (kt + 1 < KT) gload(kt + 1);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < BK / 32; ++ks) {
       i32x4 fa[FM], fb[FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        fa[i] = *reinterpret_cast<const i32x4*>(&lds[buf][(arow + 32 * i) * kLdsRow + 32 * ks + kh]);
+        fa[i] = *reinterpret_cast<const i32x4*>(&lds[buf][(arow + 32 * i) * LROW + 32 * ks + kh]);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        fb[j] = *reinterpret_cast<const i32x4*>(&lds[buf][(brow + 32 * j) * kLdsRow + 32 * ks + kh]);
+        fb[j] = *reinterpret_cast<const i32x4*>(&lds[buf][(brow + 32 * j) * LROW + 32 * ks + kh]);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -562,18 +565,27 @@ __global__ __launch_bounds__(256) void k_gemm_i8_generic(GemmParams p, int epi) 
 
 namespace {
 
-template <int EPI>
-void launch_gemm(const GemmParams& p, hipStream_t s) {
+// Tile shapes (measured on MI355X, 14336 x 4096 weights): 256 x 256 blocks of 8 waves
+// (128 x 64 each) for large products, 128 x 128 blocks of 8 waves (64 x 32) otherwise;
+// 128-byte K steps when K allows, else 64.
+template <int EPI, int BK>
+void launch_gemm_bk(const GemmParams& p, hipStream_t s) {
   const bool big = (int64_t)p.M * p.N >= (int64_t)1024 * 8192;
   if (big) {
     constexpr int BM = 256, BN = 256;
     const int G = (int)(cdiv(p.M, BM) * cdiv(p.N, BN));
-    hipLaunchKernelGGL((k_gemm_i8<BM, BN, 128, 64, EPI>), dim3(G), dim3(8 * 64), 0, s, p);
+    hipLaunchKernelGGL((k_gemm_i8<BM, BN, 128, 64, EPI, BK>), dim3(G), dim3(8 * 64), 0, s, p);
   } else {
     constexpr int BM = 128, BN = 128;
     const int G = (int)(cdiv(p.M, BM) * cdiv(p.N, BN));
-    hipLaunchKernelGGL((k_gemm_i8<BM, BN, 64, 64, EPI>), dim3(G), dim3(4 * 64), 0, s, p);
+    hipLaunchKernelGGL((k_gemm_i8<BM, BN, 64, 32, EPI, BK>), dim3(G), dim3(8 * 64), 0, s, p);
   }
+}
+
+template <int EPI>
+void launch_gemm(const GemmParams& p, hipStream_t s) {
+  if (p.K % 128 == 0) launch_gemm_bk<EPI, 128>(p, s);
+  else launch_gemm_bk<EPI, 64>(p, s);
 }
 
 int run_gemm(const GemmParams& p, int epi, hipStream_t s) {
