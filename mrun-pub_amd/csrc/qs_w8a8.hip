@@ -233,6 +233,31 @@ __global__ __launch_bounds__(1024) void k_topk(float* __restrict__ vals, int K, 
   }
 }
 
+// One step of a wave argmax over (value desc, index asc) on the DPP network.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void argmax_dpp_step(float& best, int& bi) {
+  const int vb = __float_as_int(best);
+  const float ov = __int_as_float(__builtin_amdgcn_update_dpp(vb, vb, CTRL, ROW_MASK, 0xf, false));
+  const int oi = __builtin_amdgcn_update_dpp(bi, bi, CTRL, ROW_MASK, 0xf, false);
+  if (ov > best || (ov == best && oi < bi)) {
+    best = ov;
+    bi = oi;
+  }
+}
+
+// Wave argmax: quad swaps, row half-mirror and mirror, then row broadcasts 15 and 31
+// carry the winner to lane 63, which is broadcast to all lanes.
+__device__ __forceinline__ void wave_argmax_dpp(float& best, int& bi) {
+  argmax_dpp_step<0xB1, 0xf>(best, bi);   // quad_perm [1,0,3,2]
+  argmax_dpp_step<0x4E, 0xf>(best, bi);   // quad_perm [2,3,0,1]
+  argmax_dpp_step<0x141, 0xf>(best, bi);  // row_half_mirror
+  argmax_dpp_step<0x140, 0xf>(best, bi);  // row_mirror
+  argmax_dpp_step<0x142, 0xa>(best, bi);  // row_bcast:15
+  argmax_dpp_step<0x143, 0xc>(best, bi);  // row_bcast:31
+  best = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best), 63));
+  bi = __builtin_amdgcn_readlane(bi, 63);
+}
+
 // Single workgroup of 16 waves.  The partial maxima are folded into registers (wave w
 // owns columns [w*S, (w+1)*S), lane l the columns w*S + l + 64*e); every wave selects the
 // kk largest of its slice with kk rounds of a wave argmax, and wave 0 merges the 16
@@ -262,17 +287,7 @@ __global__ __launch_bounds__(1024) void k_topk_w(const float* __restrict__ vals,
       keep[k] = 1.f;
     }
   }
-  auto argmax = [&](float& best, int& bi) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(best, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (ov > best || (ov == best && oi < bi)) {
-        best = ov;
-        bi = oi;
-      }
-    }
-  };
+  auto argmax = [&](float& best, int& bi) { wave_argmax_dpp(best, bi); };
   for (int r = 0; r < kk; ++r) {
     float best = NEG;
     int bi = 0x7fffffff;
@@ -326,6 +341,121 @@ __global__ __launch_bounds__(1024) void k_topk_w(const float* __restrict__ vals,
 #pragma unroll
     for (int t = 0; t < 16; ++t)
       if (cidx[t] == bi) c[t] = NEG;
+  }
+}
+
+// Top-k by radix selection (single workgroup, 1024 threads, K <= 1024 * kRadixVpt).
+// Every column gets the 64-bit key (value bits << 32) | ~index: values are >= 0, so the
+// key order is value descending, then index ascending, and all keys are distinct.  The
+// kk-th largest key T is found one byte at a time from the top (histogram of the byte
+// among the keys that match the prefix found so far, then a suffix scan over the 256
+// bins); the selection is every key >= T, exactly kk columns.  The value bytes settle T
+// unless the value at the threshold is tied, in which case the index bytes follow.  The
+// kk selected keys are finally ranked against each other to emit idx in order.
+constexpr int kRadixVpt = 16;
+// Adds one count per active lane to hist[bin].  Lanes that share the leader's bin are
+// combined into one LDS atomic per round; the rounds stop once a round combines fewer
+// than 8 lanes (spread bins), and the remaining lanes add one atomic each.  The first
+// digit of float keys lands in one or two bins, where per-lane atomics serialise.
+__device__ __forceinline__ void hist_add_wave(unsigned* hist, bool active, unsigned bin) {
+  unsigned long long act = __ballot(active);
+  const int lane = threadIdx.x & 63;
+  while (act) {
+    const int leader = __builtin_ctzll(act);
+    const unsigned lb = __builtin_amdgcn_readlane(bin, leader);
+    const unsigned long long same = __ballot(((act >> lane) & 1ull) && bin == lb);
+    const int n = __popcll(same);
+    if (lane == leader) atomicAdd(&hist[lb], (unsigned)n);
+    act &= ~same;
+    if (n < 8) break;
+  }
+  if ((act >> lane) & 1ull) atomicAdd(&hist[bin], 1u);
+}
+
+__global__ __launch_bounds__(1024) void k_topk_radix(const float* __restrict__ vals, int K, int kk,
+                                                     int64_t* __restrict__ idx, float* __restrict__ keep) {
+  __shared__ unsigned hist[256];
+  __shared__ unsigned long long s_prefix;  // bytes of T found so far (top bytes)
+  __shared__ unsigned s_need;               // keys still to take inside the prefix bucket
+  __shared__ unsigned s_bucket;             // keys in the prefix bucket
+  __shared__ unsigned wsum[4];
+  __shared__ int s_nsel;
+  __shared__ unsigned long long sel[64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  unsigned long long key[kRadixVpt];
+#pragma unroll
+  for (int e = 0; e < kRadixVpt; ++e) {
+    const int k = tid + 1024 * e;
+    // columns past K are never counted or selected
+    const unsigned v = k < K ? __float_as_uint(vals[k]) : 0u;
+    key[e] = ((unsigned long long)v << 32) | (unsigned)(~(unsigned)k);
+    if (k < K) keep[k] = 1.f;
+  }
+  if (tid == 0) {
+    s_prefix = 0ull;
+    s_need = (unsigned)kk;
+    s_nsel = 0;
+  }
+  unsigned long long mask = 0ull;
+  for (int pass = 0; pass < 8; ++pass) {
+    const int shift = 56 - 8 * pass;
+    if (tid < 256) hist[tid] = 0u;
+    __syncthreads();
+    const unsigned long long prefix = s_prefix;
+#pragma unroll
+    for (int e = 0; e < kRadixVpt; ++e)
+      if (1024 * e < K)  // block-uniform: skip register rows that hold no column
+        hist_add_wave(hist, tid + 1024 * e < K && (key[e] & mask) == prefix,
+                      (unsigned)(key[e] >> shift) & 255u);
+    __syncthreads();
+    // suffix scan: thread t < 256 takes bin 255 - t; inclusive prefix over t
+    unsigned h = 0, c = 0;
+    if (tid < 256) {
+      h = hist[255 - tid];
+      c = h;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const unsigned o = __shfl_up(c, off, 64);
+        if (lane >= off) c += o;
+      }
+      if (lane == 63) wsum[wave] = c;
+    }
+    __syncthreads();
+    if (tid < 256) {
+      unsigned base = 0;
+      for (int w = 0; w < wave; ++w) base += wsum[w];
+      const unsigned incl = base + c, excl = incl - h;
+      const unsigned need = s_need;
+      if (excl < need && incl >= need) {  // exactly one bin holds the need-th key
+        s_prefix = prefix | ((unsigned long long)(255 - tid) << shift);
+        s_need = need - excl;
+        s_bucket = h;
+      }
+    }
+    __syncthreads();
+    mask |= 0xffull << shift;
+    // the whole bucket is taken: T is its smallest key, no further bytes needed
+    if (s_need == s_bucket) break;
+  }
+  // T: the smallest selected key; with a full bucket, every key of the bucket qualifies
+  const unsigned long long prefix = s_prefix;
+  const bool full = s_need == s_bucket;
+#pragma unroll
+  for (int e = 0; e < kRadixVpt; ++e) {
+    const bool take = tid + 1024 * e < K && (full ? ((key[e] & mask) >= prefix) : (key[e] >= prefix));
+    if (take) {
+      const int slot = atomicAdd(&s_nsel, 1);
+      if (slot < 64) sel[slot] = key[e];
+    }
+  }
+  __syncthreads();
+  if (tid < kk) {
+    const unsigned long long my = sel[tid];
+    int rank = 0;
+    for (int j = 0; j < kk; ++j) rank += sel[j] > my;
+    const int col = (int)(~(unsigned)my);
+    idx[rank] = col;
+    keep[col] = 0.f;
   }
 }
 
@@ -667,8 +797,8 @@ extern "C" int qs_outlier_topk(const void* x, int x_dtype, int64_t ldx, int64_t 
     hipLaunchKernelGGL(k_col_absmax<QS_F16>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
   else
     return fail(QS_ERR_INVALID, "outlier_topk: dtype must be F32, BF16 or F16");
-  if (K <= 16 * 64 * kTopkVpl)
-    hipLaunchKernelGGL(k_topk_w, dim3(1), dim3(1024), 0, s, colmax, (int)K, 1, k, idx, keep);
+  if (K <= 1024 * kRadixVpt)
+    hipLaunchKernelGGL(k_topk_radix, dim3(1), dim3(1024), 0, s, colmax, (int)K, k, idx, keep);
   else
     hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), 0, s, colmax, (int)K, 1, k, idx, keep);
   return hip_check(hipGetLastError(), "outlier_topk launch");
