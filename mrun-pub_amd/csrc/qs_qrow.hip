@@ -13,10 +13,12 @@
 //                                 K is split across the waves of a workgroup and reduced
 //                                 through LDS in a fixed order.  Used for 3 <= M.
 //   k_gemv_valu<...>            : M <= 2 decode rows (any activation dtype) and every
-//                                 fp32-activation call: one wave per weight row(s), 1 KiB
-//                                 contiguous row segments per instruction, activations in
-//                                 LDS, VALU dequant + fma / v_dot2, fixed-order wave
-//                                 butterfly.  Also the row-stable (batch invariant) lane.
+//                                 fp32-activation call: one wave per weight row, 1 KiB
+//                                 contiguous row segments per instruction issued in row
+//                                 order through a 4-chunk window, exact-width tail,
+//                                 activations in LDS, VALU dequant + fma / v_dot2,
+//                                 fixed-order DPP wave sum.  Also the row-stable (batch
+//                                 invariant) lane.
 //   k_generic                   : any shape / alignment, one wave per output row.
 //
 // MFMA operand mapping (16x16x32, wave64): lane l supplies row (l & 15) of A and
@@ -298,14 +300,11 @@ __global__ __launch_bounds__(P * KW * 64) void k_w8a16(QrowParams p) {
 // VALU GEMV for small M (and every fp32-activation call)
 // ----------------------------------------------------------------------------------
 // One wave per weight row: lane l reads the 16 contiguous codes at k = 1024*c + 16*l
-// (one wave instruction = one 1 KiB contiguous row segment) and the whole row is in
-// flight at once.  The M <= MB activation rows are staged in LDS per workgroup while
-// the codes are in flight.
+// (one wave instruction = one 1 KiB contiguous row segment).  The M <= MB activation
+// rows are staged in LDS per workgroup while the codes are in flight.
 //   fp32 x : w = float(code)*scale, fma per element        (QStore fp32 contract)
 //   bf16 x : w = bf16(float(code)*scale), v_dot2_f32_bf16   (W8A16 contract)
 //   fp16 x : w = fp16(float(code)*scale), v_dot2_f32_f16
-// Each row's sum is lane-local in chunk/element order, then a fixed butterfly across
-// the wave: the result of a row never depends on M or on the other rows.
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
@@ -314,86 +313,86 @@ struct XElem {
   static constexpr int size = XT == QS_F32 ? 4 : 2;
 };
 
-// Dot of one 16-code chunk (already in registers) with the activations of the MB rows.
-template <int XT, int MB>
-__device__ __forceinline__ void valu_chunk(i32x4 w, float sc, const uint8_t* xs, int K, int k,
-                                           int M, float (&acc)[MB]) {
+// Dot of NW code words (4 codes each, in registers) at k .. k + 4*NW with the
+// activations of the MB rows staged in LDS.
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x3 __attribute__((ext_vector_type(3)));
+
+template <int XT, int MB, int NW>
+__device__ __forceinline__ void valu_words(const int (&w)[4], float sc, const uint8_t* xs, int K,
+                                           int k, int M, float (&acc)[MB]) {
   constexpr int ES = XElem<XT>::size;
-  if constexpr (XT == QS_F32) {
-    float wf[16];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) wf[4 * j + e] = byte_f32(w[j], e) * sc;
+  for (int j = 0; j < NW; ++j) {
+    const int d = w[j];
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
-      if (m < M) {
-        const f32x4* xp = reinterpret_cast<const f32x4*>(xs + ((int64_t)m * K + k) * ES);
+      if (m >= M) continue;
+      const uint8_t* xp = xs + ((int64_t)m * K + k + 4 * j) * ES;
+      if constexpr (XT == QS_F32) {
+        const f32x4 xv = *reinterpret_cast<const f32x4*>(xp);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x4 xv = xp[j];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[m] = fmaf(xv[e], wf[4 * j + e], acc[m]);
+        for (int e = 0; e < 4; ++e) acc[m] = fmaf(xv[e], byte_f32(d, e) * sc, acc[m]);
+      } else {
+        const u32x2 xv = *reinterpret_cast<const u32x2*>(xp);
+        // copy the elements out first: a bit_cast of an element expression of an
+        // ext_vector can read element 0
+        const unsigned x0 = xv[0], x1 = xv[1];
+        if constexpr (XT == QS_BF16) {
+          bf16x2 a, b;
+          a[0] = static_cast<__bf16>(byte_f32(d, 0) * sc);
+          a[1] = static_cast<__bf16>(byte_f32(d, 1) * sc);
+          b[0] = static_cast<__bf16>(byte_f32(d, 2) * sc);
+          b[1] = static_cast<__bf16>(byte_f32(d, 3) * sc);
+          acc[m] = __builtin_amdgcn_fdot2_f32_bf16(a, __builtin_bit_cast(bf16x2, x0), acc[m], false);
+          acc[m] = __builtin_amdgcn_fdot2_f32_bf16(b, __builtin_bit_cast(bf16x2, x1), acc[m], false);
+        } else {
+          f16x2 a, b;
+          a[0] = static_cast<_Float16>(byte_f32(d, 0) * sc);
+          a[1] = static_cast<_Float16>(byte_f32(d, 1) * sc);
+          b[0] = static_cast<_Float16>(byte_f32(d, 2) * sc);
+          b[1] = static_cast<_Float16>(byte_f32(d, 3) * sc);
+          acc[m] = __builtin_amdgcn_fdot2(a, __builtin_bit_cast(f16x2, x0), acc[m], false);
+          acc[m] = __builtin_amdgcn_fdot2(b, __builtin_bit_cast(f16x2, x1), acc[m], false);
         }
-      }
-    }
-  } else if constexpr (XT == QS_BF16) {
-    bf16x8 w0, w1;
-    deq16_bf16(w, sc, w0, w1);
-#pragma unroll
-    for (int m = 0; m < MB; ++m) {
-      if (m < M) {
-        const bf16x8* xp = reinterpret_cast<const bf16x8*>(xs + ((int64_t)m * K + k) * ES);
-        const bf16x8 x0 = xp[0], x1 = xp[1];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[m] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w0[2 * j], w0[2 * j + 1]},
-                                                   bf16x2{x0[2 * j], x0[2 * j + 1]}, acc[m], false);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[m] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{w1[2 * j], w1[2 * j + 1]},
-                                                   bf16x2{x1[2 * j], x1[2 * j + 1]}, acc[m], false);
-      }
-    }
-  } else {
-    f16x8 w0, w1;
-    deq16_f16(w, sc, w0, w1);
-#pragma unroll
-    for (int m = 0; m < MB; ++m) {
-      if (m < M) {
-        const f16x8* xp = reinterpret_cast<const f16x8*>(xs + ((int64_t)m * K + k) * ES);
-        const f16x8 x0 = xp[0], x1 = xp[1];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[m] = __builtin_amdgcn_fdot2(f16x2{w0[2 * j], w0[2 * j + 1]},
-                                          f16x2{x0[2 * j], x0[2 * j + 1]}, acc[m], false);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[m] = __builtin_amdgcn_fdot2(f16x2{w1[2 * j], w1[2 * j + 1]},
-                                          f16x2{x1[2 * j], x1[2 * j + 1]}, acc[m], false);
       }
     }
   }
 }
 
-// One wave owns R consecutive rows (SWI: gate row n and up row n, R = 1) and requests
-// all of their codes up front, row after row; rows are then consumed in the same order,
-// so the dequant/dot work of row 0 runs while the later rows are still arriving.  The
-// activations are staged in LDS per workgroup while the codes are in flight.
-// For plain linears tile_begin of linear i holds its first global row; all rows of a
-// wave belong to one linear (each linear's rows are padded to a multiple of R).
-// Waves per workgroup of the VALU GEMV: the activations staged in LDS serve 8 rows.
-constexpr int kGemvWaves = 8;
+// Decode GEMV, one wave per output row (SWI: gate row n and up row n).  Load order per
+// wave: its share of the activations, then the row's tail (K mod 1024 bytes as one
+// exact-width 4/8/12-byte load per lane; 16 = a ragged tail read by the lanes it
+// covers), then the full 1 KiB chunks in row order, at most kGemvWindow of them in
+// flight; each later chunk is requested after the chunk kGemvWindow before it has been
+// consumed.  Scheduling barriers keep that issue order, so the wait before chunk c
+// covers chunks <= c only and the dequant/dot work of early chunks runs while later
+// ones are still arriving.  Chunk slots past the row (U is a bucket >= K/1024) load
+// one uniform address and are not consumed, which keeps every wait count static.
+// Sums are lane-local in a fixed order (tail, then chunks), then reduced with
+// wave_sum_dpp: a row's result never depends on M or on the other rows.
+template <bool SWI, int MB>
+struct GemvShape {
+  // 8 waves share one staged activation copy; the paired SwiGLU grid is larger than
+  // one resident round and drains with less tail in small workgroups.
+  static constexpr int waves = SWI ? (MB == 1 ? 2 : 4) : 8;
+};
+constexpr int kGemvWindow = 4;
 
-template <int XT, int MB, int U, int R, bool SWI>
-__global__ __launch_bounds__(kGemvWaves * 64) void k_gemv_valu(QrowParams p, int rows) {
+template <int XT, int MB, int U, int TB, bool SWI>
+__global__ __launch_bounds__((GemvShape<SWI, MB>::waves * 64)) void k_gemv_valu(QrowParams p, int rows) {
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+  constexpr int WPB = GemvShape<SWI, MB>::waves;
+  constexpr int NT = WPB * 64;
   constexpr int ES = XElem<XT>::size;
-  constexpr int P = SWI ? 2 : R;
-  const int lane = threadIdx.x & 63;
-  const int K = p.K;
-  const int M = p.M;  // <= MB
-  const int r0 = ((int)blockIdx.x * kGemvWaves + (threadIdx.x >> 6)) * (SWI ? 1 : R);
+  constexpr int P = SWI ? 2 : 1;
+  constexpr int XMAX16 = MB * (U * 1024 + (TB ? 1024 : 0)) * ES / 16;
+  constexpr int XL = (XMAX16 + NT - 1) / NT;
+  constexpr bool XREG = XL <= 6;  // activations fit a few registers: load them first
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int K = p.K, M = p.M;
+  const int F = K >> 10;
+  const int r0 = (int)blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool live = r0 < rows;
   const int rr = live ? r0 : 0;
   int li = 0;
@@ -402,78 +401,123 @@ __global__ __launch_bounds__(kGemvWaves * 64) void k_gemv_valu(QrowParams p, int
     for (int j = 1; j < 4; ++j)
       if (j < p.n_lin && rr >= p.lin[j].tile_begin) li = j;
   }
-  const int n0 = rr - p.lin[li].tile_begin;
-  const int N = p.lin[li].N;
+  const int n = rr - p.lin[li].tile_begin;
+  const int row16 = K * ES / 16;
+  const uint8_t* xg = static_cast<const uint8_t*>(p.x);
 
-  i32x4 wv[P][U];
+  i32x4 xr[XREG ? XL : 1];
+  if constexpr (XREG) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      int idx = tid + i * NT;
+      idx = idx < M * row16 ? idx : 0;
+      const int m = idx / row16, c = idx - m * row16;
+      xr[i] = *reinterpret_cast<const i32x4*>(xg + ((int64_t)m * p.ldx * ES + (int64_t)c * 16));
+    }
+  }
+  const int8_t* wrow[P];
   float sc[P];
 #pragma unroll
   for (int pl = 0; pl < P; ++pl) {
     const QrowLin& L = p.lin[SWI ? pl : li];
-    int n = SWI ? n0 : n0 + pl;
-    n = n < N ? n : N - 1;
-    const int8_t* wrow = L.codes + (int64_t)n * K + 16 * lane;
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      wv[pl][u] = (u * 1024 + 16 * lane < K)
-                      ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wrow + u * 1024))
-                      : i32x4{0, 0, 0, 0};
+    wrow[pl] = L.codes + (int64_t)n * K;
+    sc[pl] = L.scales[n];
   }
+  const int rem = K - (F << 10);
+  int tw[P][4];
+  if constexpr (TB != 0) {
 #pragma unroll
-  for (int pl = 0; pl < P; ++pl) {
-    int n = SWI ? n0 : n0 + pl;
-    n = n < N ? n : N - 1;
-    sc[pl] = p.lin[SWI ? pl : li].scales[n];
+    for (int pl = 0; pl < P; ++pl) {
+      const int8_t* t = wrow[pl] + (F << 10);
+      if constexpr (TB == 16) {
+        const i32x4 v = __builtin_nontemporal_load(
+            reinterpret_cast<const i32x4*>(16 * lane < rem ? t + 16 * lane : wrow[pl]));
+        tw[pl][0] = v[0]; tw[pl][1] = v[1]; tw[pl][2] = v[2]; tw[pl][3] = v[3];
+      } else if constexpr (TB == 12) {
+        const u32x3 v = __builtin_nontemporal_load(reinterpret_cast<const u32x3*>(t + 12 * lane));
+        tw[pl][0] = v[0]; tw[pl][1] = v[1]; tw[pl][2] = v[2]; tw[pl][3] = 0;
+      } else if constexpr (TB == 8) {
+        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(t + 8 * lane));
+        tw[pl][0] = v[0]; tw[pl][1] = v[1]; tw[pl][2] = 0; tw[pl][3] = 0;
+      } else {
+        const unsigned v = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(t + 4 * lane));
+        tw[pl][0] = v; tw[pl][1] = 0; tw[pl][2] = 0; tw[pl][3] = 0;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
-  // stage the activations (M rows x K) in LDS while the codes are in flight
-  const int row16 = K * ES / 16;
-  for (int i = threadIdx.x; i < M * row16; i += kGemvWaves * 64) {
-    const int m = i / row16;
-    const int c = i - m * row16;
-    reinterpret_cast<i32x4*>(xs)[i] = *reinterpret_cast<const i32x4*>(
-        static_cast<const uint8_t*>(p.x) + ((int64_t)m * p.ldx * ES + (int64_t)c * 16));
+  int wv[P][U][4];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl) {
+      const int8_t* a = c < F ? wrow[pl] + c * 1024 + 16 * lane : wrow[pl];
+      const i32x4 v = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a));
+      wv[pl][c][0] = v[0]; wv[pl][c][1] = v[1]; wv[pl][c][2] = v[2]; wv[pl][c][3] = v[3];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+#pragma unroll
+  for (int c = 0; c < (kGemvWindow < U ? kGemvWindow : U); ++c) load_chunk(c);
+
+  if constexpr (XREG) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const int idx = tid + i * NT;
+      if (idx < M * row16) reinterpret_cast<i32x4*>(xs)[idx] = xr[i];
+    }
+  } else {
+    for (int i = tid; i < M * row16; i += NT) {
+      const int m = i / row16, c = i - m * row16;
+      reinterpret_cast<i32x4*>(xs)[i] =
+          *reinterpret_cast<const i32x4*>(xg + ((int64_t)m * p.ldx * ES + (int64_t)c * 16));
+    }
   }
   __syncthreads();
   if (!live) return;
 
+  float acc[P][MB];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[pl][m] = 0.f;
+  if constexpr (TB == 16) {
+    if (16 * lane < rem) {
+#pragma unroll
+      for (int pl = 0; pl < P; ++pl) valu_words<XT, MB, 4>(tw[pl], sc[pl], xs, K, (F << 10) + 16 * lane, M, acc[pl]);
+    }
+  } else if constexpr (TB != 0) {
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl) valu_words<XT, MB, TB / 4>(tw[pl], sc[pl], xs, K, (F << 10) + TB * lane, M, acc[pl]);
+  }
+#pragma unroll
+  for (int c = 0; c < U; ++c) {
+    if (c < F) {
+#pragma unroll
+      for (int pl = 0; pl < P; ++pl) valu_words<XT, MB, 4>(wv[pl][c], sc[pl], xs, K, c * 1024 + 16 * lane, M, acc[pl]);
+    }
+    if (c + kGemvWindow < U) load_chunk(c + kGemvWindow);
+  }
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[pl][m] = wave_sum_dpp(acc[pl][m]);
+  if (lane != 0) return;
   const QrowLin& L = p.lin[li];
-  float acc_g[MB];
 #pragma unroll
-  for (int pl = 0; pl < P; ++pl) {
-    float acc[MB];
-#pragma unroll
-    for (int m = 0; m < MB; ++m) acc[m] = 0.f;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = u * 1024 + 16 * lane;
-      if (k < K) valu_chunk<XT, MB>(wv[pl][u], sc[pl], xs, K, k, M, acc);
-    }
+  for (int m = 0; m < MB; ++m) {
+    if (m >= M) continue;
+    const int64_t yi = (int64_t)m * L.ldy + n;
     if constexpr (SWI) {
-      if (pl == 0) {
-#pragma unroll
-        for (int m = 0; m < MB; ++m) acc_g[m] = wave_sum(acc[m]);
-        continue;
-      }
-    }
-    const int n = n0 + (SWI ? 0 : pl);
-#pragma unroll
-    for (int m = 0; m < MB; ++m) {
-      const float v = wave_sum(acc[m]);
-      if (lane == 0 && m < M && n < N) {
-        const int64_t yi = (int64_t)m * L.ldy + n;
-        if constexpr (SWI) {
-          const float gt = bf16_bits_to_f32(f32_to_bf16_bits(acc_g[m]));
-          const float ut = bf16_bits_to_f32(f32_to_bf16_bits(v));
-          const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f32(gt)));
-          static_cast<uint16_t*>(L.y)[yi] = f32_to_bf16_bits(sl * ut);
-        } else if constexpr (XT == QS_F32) {
-          static_cast<float*>(L.y)[yi] = v;
-        } else if constexpr (XT == QS_BF16) {
-          static_cast<uint16_t*>(L.y)[yi] = f32_to_bf16_bits(v);
-        } else {
-          static_cast<uint16_t*>(L.y)[yi] = f32_to_f16_bits(v);
-        }
-      }
+      const float gt = bf16_bits_to_f32(f32_to_bf16_bits(acc[0][m]));
+      const float ut = bf16_bits_to_f32(f32_to_bf16_bits(acc[1][m]));
+      const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f32(gt)));
+      static_cast<uint16_t*>(L.y)[yi] = f32_to_bf16_bits(sl * ut);
+    } else if constexpr (XT == QS_F32) {
+      static_cast<float*>(L.y)[yi] = acc[0][m];
+    } else if constexpr (XT == QS_BF16) {
+      static_cast<uint16_t*>(L.y)[yi] = f32_to_bf16_bits(acc[0][m]);
+    } else {
+      static_cast<uint16_t*>(L.y)[yi] = f32_to_f16_bits(acc[0][m]);
     }
   }
 }
@@ -634,50 +678,54 @@ bool valu_eligible(const QrowParams& p, int x_dtype) {
   return true;
 }
 
-template <int XT, int MB, int R, bool SWI>
-void launch_valu_r(const QrowParams& q, int rows, int blocks, size_t lds, hipStream_t s) {
-  const int chunks = (q.K + 1023) / 1024;
-  if (chunks <= 2)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 2, R, SWI>), dim3(blocks), dim3(kGemvWaves * 64), lds, s, q, rows);
-  else if (chunks <= 4)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 4, R, SWI>), dim3(blocks), dim3(kGemvWaves * 64), lds, s, q, rows);
-  else if (chunks <= 8)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 8, R, SWI>), dim3(blocks), dim3(kGemvWaves * 64), lds, s, q, rows);
+// Tail kind of a K: 0 (K % 1024 == 0), 4/8/12 bytes per lane (K % 256 == 0), else 16.
+int gemv_tail(int64_t K) {
+  const int64_t rem = K % 1024;
+  if (rem == 0) return 0;
+  if (rem % 256 == 0) return (int)(rem / 64);
+  return 16;
+}
+
+template <int XT, int MB, int TB, bool SWI>
+void launch_valu_tb(const QrowParams& q, int rows, size_t lds, hipStream_t s) {
+  constexpr int WPB = GemvShape<SWI, MB>::waves;
+  const dim3 grid((unsigned)cdiv(rows, WPB)), block(WPB * 64);
+  const int F = q.K >> 10;
+  if (F <= 1)
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 1, TB, SWI>), grid, block, lds, s, q, rows);
+  else if (F <= 2)
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 2, TB, SWI>), grid, block, lds, s, q, rows);
+  else if (F <= 4)
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 4, TB, SWI>), grid, block, lds, s, q, rows);
+  else if (F <= 8)
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 8, TB, SWI>), grid, block, lds, s, q, rows);
   else
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 12, R, SWI>), dim3(blocks), dim3(kGemvWaves * 64), lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 12, TB, SWI>), grid, block, lds, s, q, rows);
 }
 
 template <int XT, int MB, bool SWI>
-void launch_valu_mb(const QrowParams& q, int R, int rows, size_t lds, hipStream_t s) {
-  const int blocks = (int)cdiv(cdiv(rows, R), kGemvWaves);
-  if constexpr (SWI) {
-    launch_valu_r<XT, MB, 1, true>(q, rows, blocks, lds, s);
-  } else {
-    if (R == 4) launch_valu_r<XT, MB, 4, false>(q, rows, blocks, lds, s);
-    else if (R == 2) launch_valu_r<XT, MB, 2, false>(q, rows, blocks, lds, s);
-    else launch_valu_r<XT, MB, 1, false>(q, rows, blocks, lds, s);
+void launch_valu_mb(const QrowParams& q, int rows, size_t lds, hipStream_t s) {
+  switch (gemv_tail(q.K)) {
+    case 0: launch_valu_tb<XT, MB, 0, SWI>(q, rows, lds, s); break;
+    case 4: launch_valu_tb<XT, MB, 4, SWI>(q, rows, lds, s); break;
+    case 8: launch_valu_tb<XT, MB, 8, SWI>(q, rows, lds, s); break;
+    case 12: launch_valu_tb<XT, MB, 12, SWI>(q, rows, lds, s); break;
+    default: launch_valu_tb<XT, MB, 16, SWI>(q, rows, lds, s); break;
   }
 }
 
 // VALU path: rows of x in batches of MB (each batch one launch).  Every row is reduced
-// in the same order whatever M is.  R rows per wave: more when there are rows to spare,
-// and only while the wave's codes stay within a modest register budget.
+// in the same order whatever M is.
 int run_valu(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool swiglu) {
   const int es = x_dtype == QS_F32 ? 4 : 2;
   const int mb = valu_mb(x_dtype, p.K, M);
-  int64_t total = 0;
-  for (int i = 0; i < p.n_lin; ++i) total += p.lin[i].N;
-  const int chunks = (p.K + 1023) / 1024;
-  int R = 1;
-  (void)chunks;
-  (void)total;
   int rows = 0;
   if (swiglu) {
     rows = p.lin[0].N;
   } else {
     for (int i = 0; i < p.n_lin; ++i) {
       p.lin[i].tile_begin = rows;
-      rows += (int)cdiv(p.lin[i].N, R) * R;
+      rows += p.lin[i].N;
     }
   }
   for (int64_t m0 = 0; m0 < M; m0 += mb) {
@@ -688,18 +736,18 @@ int run_valu(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool swiglu) {
       if (p.lin[i].y) q.lin[i].y = static_cast<char*>(p.lin[i].y) + m0 * p.lin[i].ldy * es;
     const size_t lds = (size_t)q.M * q.K * es;
     if (swiglu) {
-      if (mb == 2) launch_valu_mb<QS_BF16, 2, true>(q, 1, rows, lds, s);
-      else launch_valu_mb<QS_BF16, 1, true>(q, 1, rows, lds, s);
+      if (mb == 2) launch_valu_mb<QS_BF16, 2, true>(q, rows, lds, s);
+      else launch_valu_mb<QS_BF16, 1, true>(q, rows, lds, s);
     } else if (x_dtype == QS_F32) {
-      if (mb == 4) launch_valu_mb<QS_F32, 4, false>(q, R, rows, lds, s);
-      else if (mb == 2) launch_valu_mb<QS_F32, 2, false>(q, R, rows, lds, s);
-      else launch_valu_mb<QS_F32, 1, false>(q, R, rows, lds, s);
+      if (mb == 4) launch_valu_mb<QS_F32, 4, false>(q, rows, lds, s);
+      else if (mb == 2) launch_valu_mb<QS_F32, 2, false>(q, rows, lds, s);
+      else launch_valu_mb<QS_F32, 1, false>(q, rows, lds, s);
     } else if (x_dtype == QS_BF16) {
-      if (mb == 2) launch_valu_mb<QS_BF16, 2, false>(q, R, rows, lds, s);
-      else launch_valu_mb<QS_BF16, 1, false>(q, R, rows, lds, s);
+      if (mb == 2) launch_valu_mb<QS_BF16, 2, false>(q, rows, lds, s);
+      else launch_valu_mb<QS_BF16, 1, false>(q, rows, lds, s);
     } else {
-      if (mb == 2) launch_valu_mb<QS_F16, 2, false>(q, R, rows, lds, s);
-      else launch_valu_mb<QS_F16, 1, false>(q, R, rows, lds, s);
+      if (mb == 2) launch_valu_mb<QS_F16, 2, false>(q, rows, lds, s);
+      else launch_valu_mb<QS_F16, 1, false>(q, rows, lds, s);
     }
   }
   return hip_check(hipGetLastError(), "k_gemv_valu launch");
