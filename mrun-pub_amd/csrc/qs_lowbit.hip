@@ -527,7 +527,7 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
       }
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
-        const float v = wave_sum(acc[m]);
+        const float v = wave_sum_dpp(acc[m]);
         if (lane == 0 && m < M) p.y[(int64_t)m * p.ldy + row] = v;
       }
     }
