@@ -148,12 +148,14 @@ int qs_moe_gather_quant(const void* source, int src_dtype, int64_t ld_src, const
  *   out[row, n] = (float(acc) * a_scale[row]) * w_scale[slot(g)*ws_stride + n]
  * (F32/BF16); swiglu != 0: N_w = 2N, out[row, n] = bf16(bf16(silu(bf16(gate))) * bf16(up))
  * with gate from weight row n and up from row n + N.  K % 64 == 0, K <= 8192 with SwiGLU,
- * K <= 16384 without. */
+ * K <= 16384 without.  max_rows is the reference's max_rows argument
+ * (qwen3_moe_cuda.py:2257-2310, callers pass the routed row count, :2747): a bound on
+ * counts[g] used only to size the row tile (0 = unknown); results do not depend on it. */
 int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* w,
                            int64_t w_stride, const float* w_scale, int64_t ws_stride,
                            const int32_t* starts, const int32_t* counts, const int32_t* slots,
-                           int G, int64_t N, int64_t K, int swiglu, void* out, int out_dtype,
-                           void* stream);
+                           int G, int64_t N, int64_t K, int64_t max_rows, int swiglu, void* out,
+                           int out_dtype, void* stream);
 
 /* Replaces stable_route_reduce / _stable_route_reduce_kernel (qwen3_moe_cuda.py:2561-2664,
  * 2160-2182): out[t, h] = sum over rank r = 0..k-1 (in order) of

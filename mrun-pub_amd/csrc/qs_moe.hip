@@ -11,13 +11,16 @@
 //                       the reference's stable argsort and is identical on every call.
 //   k_moe_gather_quant: per routed row, int8 per-token quantization of source[token_ids[a]]
 //                       (the W8A8 recipe: s = max|x|/127, 0 -> 1; rint; clamp +-127).
-//   k_moe_gemm<...>   : one workgroup per (group, 4 consecutive 16-row tiles of N, the next
-//                       tile's weights loading while the current one is reduced); its waves split K, hold
-//                       their weight slice in VGPRs (streamed once from HBM with 128-bit
-//                       loads) and walk the group's rows 16 at a time with
-//                       v_mfma_i32_16x16x64_i8; LDS reduction over the K split; epilogue
-//                       (float(acc) * a_scale[row]) * w_scale[n] -> bf16/fp32, or the
-//                       paired SwiGLU of gate row n and up row n + N.
+//   k_moe_stream<...> : one workgroup per (group, 8 waves of output rows).  The group's
+//                       routed rows (up to 16*MT at a time) are staged once in LDS; each
+//                       wave streams its weight rows (16 rows of gate and up for SwiGLU,
+//                       16-64 rows otherwise) over the full K through a window of 64-byte
+//                       chunks in flight and multiplies them with v_mfma_i32_16x16x64_i8
+//                       against every 16-row tile of the staged rows; epilogue (float(acc) * a_scale[row]) * w_scale[n] ->
+//                       bf16/fp32, or the paired SwiGLU of gate row n and up row n + N.
+//   k_moe_gemm<...>   : K beyond what the LDS tile holds: one workgroup per (group, 16-row
+//                       tile); its waves split K, hold their weight slice in VGPRs and
+//                       walk the group's rows 16 at a time, LDS reduction over the split.
 //   k_moe_reduce      : out[t, :] = sum over rank r of float(y[inv[t*k + r], :]) *
 //                       coef[inv[t*k + r]], each product rounded, summed in rank order.
 #include "qs_common.h"
@@ -365,6 +368,161 @@ __global__ __launch_bounds__(P * KW * 64) void k_moe_gemm(MoeGemmParams p) {
   }
 }
 
+// Streaming grouped GEMM.  Each wave owns RW output rows over the full K: SwiGLU
+// (P = 2): 16 rows n0 .. n0 + 15 of gate and the same rows + N of up; plain (P = 1):
+// NB consecutive 16-row tiles.  Its NB weight tiles are the B operands of
+// v_mfma_i32_16x16x64_i8: lane l loads bytes 64c + 16(l >> 4) .. +16 of tile row l & 15
+// for k-chunk c (column l & 15, k-block l >> 4).  The A operand is the same k range of
+// staged row (l & 15) of a 16-row tile of the group, read once from LDS per chunk and
+// shared by the NB tiles (rows padded by 16 bytes, so the 16 rows of a read fall in
+// distinct banks).  The chunk loads run W chunks ahead of the MFMAs, issued in k order;
+// slots past the last chunk reload it (static wait counts).  Staged rows past the
+// group's count hold stale LDS data: their MFMA columns are never stored.
+constexpr int kMoeWaves = 8;
+
+template <int P, int NB>
+struct MoeStreamCfg {
+  static constexpr int RW = P == 2 ? 16 : 16 * NB;  // output rows per wave
+  static constexpr int W = 16 / NB;                  // chunks in flight (16 loads per wave)
+};
+
+template <int P, int NB, int MT>
+__global__ __launch_bounds__(kMoeWaves * 64) void k_moe_stream(MoeGemmParams p) {
+  static_assert(P == 1 || NB == 2, "SwiGLU streams the gate and up tiles of one row block");
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int MC = 16 * MT;
+  constexpr int NT = kMoeWaves * 64;
+  constexpr int W = MoeStreamCfg<P, NB>::W;
+  constexpr int RW = MoeStreamCfg<P, NB>::RW;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, q = lane >> 4;
+  const int g = blockIdx.y;
+  const int count = p.counts[g];
+  if (count == 0) return;
+  const int start = p.starts[g];
+  const int slot = p.slots ? p.slots[g] : g;
+  const int K = p.K, C = K >> 6;
+  const int xstride = K + 16;
+  int8_t* xs = reinterpret_cast<int8_t*>(lds);                 // [MC][K + 16]
+  float* asl = reinterpret_cast<float*>(lds + MC * xstride);   // [MC]
+  const int n0 = (blockIdx.x * kMoeWaves + wave) * RW;
+  const bool live = n0 < p.N;
+  const int8_t* wexp = p.w + (int64_t)slot * p.w_stride;
+  const int8_t* wr[NB];
+  float wsc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    // weight row of tile b for this lane's column
+    const int nb = P == 2 ? min(n0 + col, p.N - 1) + b * p.N : min(n0 + 16 * b + col, p.N - 1);
+    wr[b] = wexp + (int64_t)nb * K + 16 * q;
+    wsc[b] = p.ws[(int64_t)slot * p.ws_stride + nb];
+  }
+  const int ppr = K >> 4;  // 16-byte pieces per row
+
+  for (int m0 = 0; m0 < count; m0 += MC) {
+    const int mc = min(MC, count - m0);
+    i32x4 wv[W][NB];
+#pragma unroll
+    for (int u = 0; u < W; ++u) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        wv[u][b] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wr[b] + (int64_t)min(u, C - 1) * 64));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // routed rows m0 .. m0 + mc of the group and their scales -> LDS, 8 loads in flight
+    const int tot = mc * ppr;
+    const int8_t* arows = p.a + (int64_t)(start + m0) * K;
+    for (int i0 = 0; i0 < tot; i0 += 8 * NT) {
+      i32x4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        int i = i0 + j * NT + tid;
+        i = i < tot ? i : 0;
+        const int t = i / ppr, pc = i - t * ppr;
+        v[j] = *reinterpret_cast<const i32x4*>(arows + (int64_t)t * K + pc * 16);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + j * NT + tid;
+        if (i < tot) {
+          const int t = i / ppr, pc = i - t * ppr;
+          *reinterpret_cast<i32x4*>(xs + t * xstride + pc * 16) = v[j];
+        }
+      }
+    }
+    if (tid < mc) asl[tid] = p.as[start + m0 + tid];
+    __syncthreads();
+
+    i32x4 acc[MT][NB];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[mt][b] = i32x4{0, 0, 0, 0};
+    for (int c0 = 0; c0 < C; c0 += W) {
+#pragma unroll
+      for (int u = 0; u < W; ++u) {
+        const int c = c0 + u;
+        if (c < C) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            if (mt * 16 < mc) {
+              const i32x4 av = *reinterpret_cast<const i32x4*>(xs + (mt * 16 + col) * xstride + c * 64 + 16 * q);
+#pragma unroll
+              for (int b = 0; b < NB; ++b)
+                acc[mt][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, wv[u][b], acc[mt][b], 0, 0, 0);
+            }
+          }
+        }
+        const int cn = min(c + W, C - 1);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          wv[u][b] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wr[b] + (int64_t)cn * 64));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    // lane l holds D[row 4(l >> 4) + r of the tile][column l & 15]
+    if (live) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int ml = mt * 16 + 4 * q + r;
+          if (ml >= mc) continue;
+          const int64_t row = start + m0 + ml;
+          const float a_s = asl[ml];
+          if constexpr (P == 2) {
+            const int no = n0 + col;
+            if (no < p.N) {
+              const float gv = mul_rn(mul_rn(static_cast<float>(acc[mt][0][r]), a_s), wsc[0]);
+              const float uv = mul_rn(mul_rn(static_cast<float>(acc[mt][1][r]), a_s), wsc[1]);
+              const float gt = bf16_bits_to_f32(f32_to_bf16_bits(gv));
+              const float ut = bf16_bits_to_f32(f32_to_bf16_bits(uv));
+              const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f(gt)));
+              static_cast<uint16_t*>(p.out)[row * p.N + no] = f32_to_bf16_bits(mul_rn(sl, ut));
+            }
+          } else {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+              const int no = n0 + 16 * b + col;
+              if (no < p.N) {
+                const float v = mul_rn(mul_rn(static_cast<float>(acc[mt][b][r]), a_s), wsc[b]);
+                if (p.out_dtype == QS_F32)
+                  static_cast<float*>(p.out)[row * p.N + no] = v;
+                else
+                  static_cast<uint16_t*>(p.out)[row * p.N + no] = f32_to_bf16_bits(v);
+              }
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();  // the next pass overwrites the staged rows
+  }
+}
+
 // ----------------------------------------------------------------------------------
 // stable rank-order reduce
 // ----------------------------------------------------------------------------------
@@ -448,6 +606,7 @@ extern "C" int qs_moe_gather_quant(const void* source, int src_dtype, int64_t ld
 
 namespace {
 constexpr int kMoeTilesPerBlock = 1;  // 16-row tiles per workgroup, streamed back to back
+constexpr size_t kMoeStreamLds = 144 * 1024;  // staged routed rows of k_moe_stream
 
 template <int P, int KW>
 void launch_moe_gemm(const MoeGemmParams& p, int G, hipStream_t s) {
@@ -460,13 +619,30 @@ void launch_moe_gemm(const MoeGemmParams& p, int G, hipStream_t s) {
   else if (ch <= 8) hipLaunchKernelGGL((k_moe_gemm<P, KW, 8, NT>), grid, dim3(P * KW * 64), 0, s, p);
   else hipLaunchKernelGGL((k_moe_gemm<P, KW, 16, NT>), grid, dim3(P * KW * 64), 0, s, p);
 }
+
+// LDS bytes of k_moe_stream for MT row tiles; 0 when it does not fit.
+size_t moe_stream_lds(int MT, int64_t K) {
+  const size_t b = (size_t)16 * MT * (size_t)(K + 16) + (size_t)16 * MT * 4;
+  return b <= kMoeStreamLds ? b : 0;
+}
+
+template <int P, int NB>
+void launch_moe_stream(const MoeGemmParams& p, int G, int MT, hipStream_t s) {
+  constexpr int RW = MoeStreamCfg<P, NB>::RW;
+  const dim3 grid((unsigned)cdiv(p.N, RW * kMoeWaves), (unsigned)G), block(kMoeWaves * 64);
+  const size_t lds = moe_stream_lds(MT, p.K);
+  if (MT == 4) hipLaunchKernelGGL((k_moe_stream<P, NB, 4>), grid, block, lds, s, p);
+  else if (MT == 2) hipLaunchKernelGGL((k_moe_stream<P, NB, 2>), grid, block, lds, s, p);
+  else hipLaunchKernelGGL((k_moe_stream<P, NB, 1>), grid, block, lds, s, p);
+}
 }  // namespace
 
 extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* w,
                                       int64_t w_stride, const float* w_scale, int64_t ws_stride,
                                       const int32_t* starts, const int32_t* counts,
                                       const int32_t* slots, int G, int64_t N, int64_t K,
-                                      int swiglu, void* out, int out_dtype, void* stream) {
+                                      int64_t max_rows, int swiglu, void* out, int out_dtype,
+                                      void* stream) {
   if (!a || !a_scale || !w || !w_scale || !starts || !counts || !out)
     return fail(QS_ERR_INVALID, "moe_grouped_gemm: null pointer");
   if (G < 1 || G > 65535 || N <= 0 || K <= 0) return fail(QS_ERR_INVALID, "moe_grouped_gemm: bad shape");
@@ -476,8 +652,24 @@ extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, con
     return fail(QS_ERR_UNSUPPORTED, "moe_grouped_gemm: operands must be 16-byte aligned");
   if (swiglu && out_dtype != QS_BF16) return fail(QS_ERR_INVALID, "moe_grouped_gemm: SwiGLU output is BF16");
   if (out_dtype != QS_BF16 && out_dtype != QS_F32) return fail(QS_ERR_INVALID, "moe_grouped_gemm: out F32 or BF16");
+  if (max_rows < 0) return fail(QS_ERR_INVALID, "moe_grouped_gemm: max_rows must be >= 0");
   MoeGemmParams p{a, a_scale, w, w_stride, w_scale, ws_stride, starts, counts, slots, (int)N, (int)K, out, out_dtype};
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // Streaming kernel: row tiles sized for twice the mean rows per group (max_rows / G),
+  // so that most groups take one pass over their weights; 0 = unknown -> 2 tiles.
+  const int64_t mean = max_rows > 0 ? cdiv(max_rows, G) : 16;
+  int MT = 2 * mean <= 16 ? 1 : (2 * mean <= 32 ? 2 : 4);
+  while (MT > 1 && !moe_stream_lds(MT, K)) MT /= 2;
+  // Plain products over short groups (one 16-row tile) read faster as many small
+  // workgroups that each take whole rows (the K-split kernel) than as long streams.
+  if (moe_stream_lds(MT, K) && (swiglu || MT > 1)) {
+    // plain: row tiles per wave so that a wave streams about 48 KB or more
+    if (swiglu) launch_moe_stream<2, 2>(p, G, MT, s);
+    else if (K <= 1024) launch_moe_stream<1, 4>(p, G, MT, s);
+    else if (K <= 2048) launch_moe_stream<1, 2>(p, G, MT, s);
+    else launch_moe_stream<1, 1>(p, G, MT, s);
+    return hip_check(hipGetLastError(), "k_moe_stream launch");
+  }
   const int C = (int)(K / 64);
   // K split so that each wave holds at most 16 chunks of 64 k of its tile (<= 1024 threads)
   if (swiglu) {

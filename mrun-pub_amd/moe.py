@@ -64,7 +64,7 @@ def route_topk(
 # ---- route compiler ----------------------------------------------------------------------
 
 
-def _route_impl(top_indices, top_weights, num_experts: int, include_inverse: bool):
+def _route_impl(top_indices, top_weights, num_experts: int, include_inverse: bool, coef_f32: bool = False):
     started = time.perf_counter()
     if top_indices.ndim != 2 or top_weights.shape != top_indices.shape:
         raise ValueError("route tensors must both have shape [rows, top_k]")
@@ -88,7 +88,8 @@ def _route_impl(top_indices, top_weights, num_experts: int, include_inverse: boo
         nat.ptr(counts), nat.ptr(inverse), nat.stream_of(device),
     )
     # coefficients keep the routing-weight dtype, as the reference's index_select does
-    coef = coef if tw.dtype == torch.float32 else coef.to(tw.dtype)
+    # (the kernel's fp32 copy of a bf16 weight is exact, so coef_f32 loses nothing)
+    coef = coef if (tw.dtype == torch.float32 or coef_f32) else coef.to(tw.dtype)
     return token_ids, coef, starts, counts, inverse, time.perf_counter() - started
 
 
@@ -233,6 +234,7 @@ def grouped_int8_mm(
     counts: torch.Tensor,
     *,
     group_slots: torch.Tensor | None = None,
+    max_rows: int | None = None,
     swiglu: bool = False,
     out_dtype: torch.dtype = torch.bfloat16,
 ) -> tuple[torch.Tensor, str]:
@@ -240,7 +242,10 @@ def grouped_int8_mm(
 
     ``weights[slot(g)]`` is ``[N, K]`` int8 (``weights`` may be a strided view into an
     expert-page arena); ``swiglu=True`` treats rows ``[0, N/2)`` as gate and ``[N/2, N)``
-    as up and returns ``bf16(silu(gate) * up)`` of width ``N/2``.
+    as up and returns ``bf16(silu(gate) * up)`` of width ``N/2``.  ``max_rows`` bounds
+    every group's row count as in the reference's grouped kernels
+    (qwen3_moe_cuda.py:2257-2310); it defaults to the routed row count, as its callers
+    pass (:2747), and only sizes the kernel's row tile.
     """
     G, n_w, K = _grouped_contract(rows_q, weights, weight_scales, starts, counts, group_slots)
     device = nat.require_device(rows_q, row_scales, weights, weight_scales, starts, counts, group_slots)
@@ -251,10 +256,13 @@ def grouped_int8_mm(
     st = starts.to(torch.int32).contiguous()
     ct = counts.to(torch.int32).contiguous()
     sl = None if group_slots is None else group_slots.to(torch.int32).contiguous()
+    rows_bound = int(rows_q.shape[0]) if max_rows is None else int(max_rows)
+    if rows_bound < 0:
+        raise ValueError("max_rows must be non-negative")
     nat.call(
         "qs_moe_grouped_gemm_i8", nat.ptr(rows_q), nat.ptr(row_scales), nat.ptr(weights), int(weights.stride(0)),
         nat.ptr(weight_scales), int(weight_scales.stride(0)), nat.ptr(st), nat.ptr(ct), nat.ptr(sl), G, n_out, K,
-        int(bool(swiglu)), nat.ptr(out), nat.dtype_code(out_dtype), nat.stream_of(device),
+        rows_bound, int(bool(swiglu)), nat.ptr(out), nat.dtype_code(out_dtype), nat.stream_of(device),
     )
     return out, IMPL_GROUPED
 
@@ -338,6 +346,14 @@ class Int8ExpertBackend:
         self.layers = layers
         self.dtype = dtype
         self.stats = {"grouped_kernel_calls": 0, "route_compiler_calls": 0, "expert_assignments": 0}
+        self._experts: dict[tuple[torch.device, int], torch.Tensor] = {}
+
+    def _expert_ids(self, device: torch.device, E: int) -> torch.Tensor:
+        key = (device, E)
+        ids = self._experts.get(key)
+        if ids is None:
+            ids = self._experts[key] = torch.arange(E, device=device)
+        return ids
 
     @torch.inference_mode()
     def moe(
@@ -352,9 +368,8 @@ class Int8ExpertBackend:
         del prefill
         page = self.layers[layer]
         E = page.num_experts
-        token_ids, coef, starts, counts, inverse, _ = grouped_route_tensors_with_inverse(
-            top_indices, top_weights, num_experts=E
-        )
+        # fp32 coefficients: the reduce widens them to fp32 anyway
+        token_ids, coef, starts, counts, inverse, _ = _route_impl(top_indices, top_weights, E, True, coef_f32=True)
         rows_q, rows_s = quantize_rows(source, token_ids)
         activated, _ = grouped_int8_mm(
             rows_q, rows_s, page.gate_up, page.gate_up_scales, starts, counts, swiglu=True
@@ -365,7 +380,7 @@ class Int8ExpertBackend:
         )
         out = stable_route_reduce(
             expert_output, coef, token_ids, counts, top_indices,
-            torch.arange(E, device=source.device), inverse_assignments=inverse,
+            self._expert_ids(source.device, E), inverse_assignments=inverse,
         )
         self.stats["grouped_kernel_calls"] += 2
         self.stats["route_compiler_calls"] += 1

@@ -101,7 +101,7 @@ def _layer(rng, E, H, I):
 
 
 @pytest.mark.parametrize("swiglu", [False, True])
-@pytest.mark.parametrize("H", [256, 4096, 12288])  # K = H: 4-, 8- and 16-wave K splits
+@pytest.mark.parametrize("H", [256, 4096, 12288])  # K = H: streamed (256, 4096), K-split (12288)
 def test_grouped_gemm_matches_oracle(dev, swiglu, H):
     if swiglu and H > 8192:
         pytest.skip("the SwiGLU kernel takes K <= 8192 (its K splits stop at 8 waves)")
@@ -121,6 +121,32 @@ def test_grouped_gemm_matches_oracle(dev, swiglu, H):
         assert oq.rel_l2(out.float().cpu().numpy(), ref) <= 1e-3
     else:
         # int32 accumulators exact + closed-form epilogue: bit-exact bf16
+        assert np.array_equal(out.float().cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("swiglu", [False, True])
+@pytest.mark.parametrize("max_rows", [0, 16, 400, 4000])  # row tiles of 32, 16, 64, 64 rows
+@pytest.mark.parametrize("H", [256, 2048])
+def test_grouped_gemm_row_tiles(dev, swiglu, max_rows, H):
+    """Skewed routing (expert 0 takes every token): groups longer than one row tile take
+    several passes; max_rows only changes the tiling, never the result."""
+    rng = np.random.default_rng(11)
+    E, I, T, k = 8, 96, 200, 2
+    gu, gus, dn, dns = _layer(rng, E, H, I)
+    top = np.stack([np.concatenate([[0], 1 + rng.permutation(E - 1)[: k - 1]]) for _ in range(T)]).astype(np.int64)
+    tok, coef, starts, counts, inv = om.route_stable(top, np.ones((T, k), np.float32), E)
+    assert counts.max() == T
+    a = rng.integers(-127, 128, size=(T * k, H), dtype=np.int8)
+    asc = rng.uniform(0.01, 0.1, size=T * k).astype(np.float32)
+    layer = _moe().Int8ExpertLayer.from_arrays(*(torch.from_numpy(v) for v in (gu, gus, dn, dns)), dev)
+    out, _ = _moe().grouped_int8_mm(
+        _t(a, dev), _t(asc, dev), layer.gate_up, layer.gate_up_scales, _t(starts, dev), _t(counts, dev),
+        max_rows=max_rows, swiglu=swiglu,
+    )
+    ref = om.grouped_int8_mm(a, asc, gu, gus, starts, counts, swiglu=swiglu)
+    if swiglu:
+        assert oq.rel_l2(out.float().cpu().numpy(), ref) <= 1e-3
+    else:
         assert np.array_equal(out.float().cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
 
