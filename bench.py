@@ -221,11 +221,18 @@ def secondary_measurements(torch, dev, stream) -> dict:
 
         tg = _graph_time(torch, stream, gemm, 10)
         tf = _graph_time(torch, stream, lambda i: w8a8.w8a8_matmul(qw, sw, xb, protect_k=8, out_dtype=torch.bfloat16), 10)
+        # the int32 GEMM alone, and the vendor library's int8 GEMM (torch._int_mm, hipBLASLt)
+        # on the same operands: a reference point for the MFMA fraction, not part of the path
+        ti = _graph_time(torch, stream, lambda i: w8a8._int8_gemm(qx, qw, True), 10)
+        wt = qw.t()
+        tv = _graph_time(torch, stream, lambda i: torch._int_mm(qx, wt), 10)
         ops = 2 * M * N * K
         res[f"config3_w8a8_m{M}"] = {
             "gemm_us": round(tg * 1e6, 2), "gemm_TOPS": round(ops / tg / 1e12, 1),
             "mfma_frac": round(ops / tg / 5.0e15, 4),
             "w8a8_matmul_protect8_us": round(tf * 1e6, 2), "end_to_end_TOPS": round(ops / tf / 1e12, 1),
+            "int32_gemm_TOPS": round(ops / ti / 1e12, 1),
+            "hipblaslt_int_mm_TOPS": round(ops / tv / 1e12, 1),
         }
     del qw, sw
 
