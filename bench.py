@@ -136,7 +136,7 @@ def _graph_time(torch, stream, fn, calls: int, reps: int = 5) -> float:
 def paged_measurement(torch, dev, pages, x_h, x_i, passes: int = 6) -> dict:
     """Config 2 as BASELINE words it: the same stack streamed from pinned host memory in
     2 MiB pages through the HBM slot ring (PCIe-inclusive; never the headline value)."""
-    from mrun_pub_amd.paged import PAGE_BYTES, PagedQStore, PinnedHostTier
+    from mrun_pub_amd.paged import PAGE_BYTES, TRANSFER_BYTES, PagedQStore, PinnedHostTier
 
     tier = PinnedHostTier.from_pages({p.name: p for L in pages for p in L.values()})
     torch.cuda.synchronize()
@@ -176,6 +176,8 @@ def paged_measurement(torch, dev, pages, x_h, x_i, passes: int = 6) -> dict:
         "h2d_GB/s": round(moved / dt / 1e9, 2),
         "raw_pinned_h2d_GB/s": round(raw_gbs, 2),
         "page_bytes": PAGE_BYTES,
+        "pages_per_pass": (st["h2d_pages"] - h0["h2d_pages"]) // passes,
+        "max_transfer_bytes": TRANSFER_BYTES,
         "slots": 4,
         "depth": 3,
         "hits": st["hits"] - h0["hits"],

@@ -196,13 +196,15 @@ int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uint8_t* packe
  * qstore.py:459-660: pinned staging, side-stream H2D, event + record_stream ordering) at
  * the runtime level.  The ring is caller-owned device memory of slots * slot_bytes bytes
  * (slot_bytes a multiple of 256); host sources must be pinned (hipHostMalloc / torch
- * pin_memory).  Copies go out as page_bytes-sized hipMemcpyAsync calls on the pager's own
- * copy stream (default priority).  Ordering is by events only: submit waits for the
- * slot's last release, seal marks the slot ready, acquire makes a compute stream wait for
- * ready, release marks the slot free once the compute stream's queued work is done. */
+ * pin_memory).  A submitted range is a run of contiguous host pages; it goes out as
+ * hipMemcpyAsync transfers of at most max_transfer bytes on the pager's own copy stream
+ * (default priority).  submit waits on the host for the slot's last release to have
+ * fired on the GPU (blocking only while that consumer is still queued, i.e. when the host
+ * is a whole ring ahead), seal marks the slot ready, acquire makes a compute stream wait
+ * for ready, release marks the slot free once the compute stream's queued work is done. */
 typedef struct qs_pager qs_pager;
 
-int qs_pager_create(void* device_arena, size_t slot_bytes, int slots, size_t page_bytes,
+int qs_pager_create(void* device_arena, size_t slot_bytes, int slots, size_t max_transfer,
                     qs_pager** out);
 int qs_pager_destroy(qs_pager* pager);
 /* Device address of a slot (nullptr when out of range). */

@@ -1,13 +1,16 @@
 // Pinned-host -> HBM page streamer (host code, HIP runtime API).
 //
 // A pager drives an HBM ring of `slots` equal-size slots (caller-owned device memory) and
-// owns one copy stream at the default priority.  submit() copies a byte range of pinned host memory into a slot as a
-// sequence of page-size hipMemcpyAsync calls on the copy stream, after the stream has
-// waited for the slot's "free" event (recorded by the last consumer), and records the
-// slot's "ready" event.  acquire() makes a compute stream wait for "ready"; release()
-// records "free" on the compute stream.  No call blocks the host and every cross-stream
-// dependency is an event, so a slot is never overwritten while a kernel still reads it
-// and never read before its copy has landed.
+// owns one copy stream at the default priority.  submit() copies a byte range of pinned
+// host memory (a run of contiguous host pages) into a slot on the copy stream once the
+// slot's "free" event (recorded by the last consumer) has fired, as transfers of at most
+// max_transfer bytes: each hipMemcpyAsync carries a fixed cost, and 2 MiB transfers reach
+// only about 60% of the link rate that 16 MiB and larger ones do.  seal() records the
+// slot's "ready" event; acquire() makes a compute stream wait for "ready"; release()
+// records "free" on the compute stream.  Only submit() can block the host, and only while
+// the slot's last consumer is still queued on the GPU (the host is a whole ring ahead), so
+// a slot is never overwritten while a kernel still reads it and never read before its
+// copy has landed.
 #include <hip/hip_runtime.h>
 
 #include <new>
@@ -25,7 +28,7 @@ using qs::hip_check;
 
 struct qs_pager {
   size_t slot_bytes = 0;
-  size_t page_bytes = 0;
+  size_t max_transfer = 0;
   int slots = 0;
   char* arena = nullptr;  // caller-owned, slot_bytes * slots bytes
   hipStream_t copy = nullptr;
@@ -34,14 +37,14 @@ struct qs_pager {
 };
 
 extern "C" int qs_pager_create(void* device_arena, size_t slot_bytes, int slots,
-                               size_t page_bytes, qs_pager** out) {
+                               size_t max_transfer, qs_pager** out) {
   if (!out || !device_arena || slot_bytes == 0 || slot_bytes % 256 || slots < 1 || slots > 64 ||
-      page_bytes == 0)
+      max_transfer == 0)
     return fail(QS_ERR_INVALID, "pager_create: bad arguments");
   qs_pager* p = new (std::nothrow) qs_pager();
   if (!p) return fail(QS_ERR_HIP, "pager_create: out of host memory");
   p->slot_bytes = slot_bytes;
-  p->page_bytes = page_bytes;
+  p->max_transfer = max_transfer;
   p->slots = slots;
   p->arena = static_cast<char*>(device_arena);
   int st = hip_check(hipStreamCreateWithFlags(&p->copy, hipStreamNonBlocking), "hipStreamCreate");
@@ -83,13 +86,20 @@ extern "C" int qs_pager_submit(qs_pager* p, int slot, const void* host, size_t b
     return fail(QS_ERR_INVALID, "pager_submit: bad arguments");
   if (dst_offset + bytes > p->slot_bytes) return fail(QS_ERR_LIMIT, "pager_submit: range exceeds the slot");
   if (p->used[slot]) {
-    int st = hip_check(hipStreamWaitEvent(p->copy, p->freed[slot], 0), "hipStreamWaitEvent(free)");
+    // The slot's last consumer must be done before the copy overwrites it.  The wait is
+    // taken on the host (a query, and a block only when the host is a whole ring ahead of
+    // the GPU): a copy stream made to wait on a compute-stream event can stall the host
+    // inside the following hipMemcpyAsync until that event fires, and the link then
+    // idles between blocks.
+    hipError_t q = hipEventQuery(p->freed[slot]);
+    if (q == hipErrorNotReady) q = hipEventSynchronize(p->freed[slot]);
+    int st = hip_check(q, "slot free event");
     if (st) return st;
   }
   char* dst = p->arena + p->slot_bytes * (size_t)slot + dst_offset;
   const char* src = static_cast<const char*>(host);
-  for (size_t off = 0; off < bytes; off += p->page_bytes) {
-    const size_t n = bytes - off < p->page_bytes ? bytes - off : p->page_bytes;
+  for (size_t off = 0; off < bytes; off += p->max_transfer) {
+    const size_t n = bytes - off < p->max_transfer ? bytes - off : p->max_transfer;
     int st = hip_check(hipMemcpyAsync(dst + off, src + off, n, hipMemcpyHostToDevice, p->copy), "hipMemcpyAsync");
     if (st) return st;
   }

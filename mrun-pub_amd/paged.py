@@ -13,11 +13,15 @@ Differences of design, same observable contract:
   threads; here the pageable->pinned copy is paid once, so the steady state is bounded by
   the PCIe link alone.
 * The HBM side is a fixed ring of ``slots`` equal slots in one device allocation.  A
-  block travels as ``page_bytes`` (2 MiB) ``hipMemcpyAsync`` pieces on the pager's copy
-  stream (``csrc/qs_pager.cpp``); the compute stream waits on the slot's ready event,
+  block is a run of contiguous ``page_bytes`` (2 MiB) pages of the tier and travels as
+  transfers of up to ``transfer_bytes`` (64 MiB, so one transfer per block) on the
+  pager's copy stream (``csrc/qs_pager.cpp``): one 2 MiB copy per page would cap the
+  link at about 60% of its rate; the compute stream waits on the slot's ready event,
   the fused kernel reads codes and scales in place from the slot, and the slot's free
-  event is recorded right after, so the next copy into that slot is ordered behind the
-  kernel on the GPU.  No host thread ever blocks on the GPU.
+  event is recorded right after.  The next copy into that slot is issued once the free
+  event has fired: the host checks it, and blocks only when it has run a whole ring
+  ahead of the GPU.  Taking that dependency on the copy stream instead stalls the host
+  inside ``hipMemcpyAsync`` and leaves the link idle between blocks (35 vs 50 GB/s).
 * A hit consumes the identical int8 codes and fp32 scales through the identical kernels
   as the resident ``DenseQStore``, so paged results equal resident results bit for bit.
 
@@ -43,6 +47,7 @@ from .qrow import CompactQRowPage
 from .store import QStoreReader
 
 PAGE_BYTES = 2 << 20
+TRANSFER_BYTES = 64 << 20
 IMPL_PAGED = "hip-gfx950-paged-ring-v1"
 
 
@@ -135,7 +140,7 @@ class RingPrefetch:
     """Successor-oracle prefetch ring over HBM slots (qstore.py:486-660 ``_RingPrefetch``)."""
 
     def __init__(self, tier: PinnedHostTier, device: torch.device, *, slots: int = 3, depth: int = 2,
-                 page_bytes: int = PAGE_BYTES):
+                 page_bytes: int = PAGE_BYTES, transfer_bytes: int = TRANSFER_BYTES):
         if device.type != "cuda":
             raise RuntimeError("ring prefetch requires a HIP device")
         self.tier = tier
@@ -144,10 +149,13 @@ class RingPrefetch:
         self.n_slots = max(2, int(slots))
         self.slot_bytes = tier.max_slot_bytes
         self.page_bytes = int(page_bytes)
+        self.transfer_bytes = int(transfer_bytes)
+        if self.page_bytes <= 0 or self.transfer_bytes <= 0:
+            raise ValueError("page_bytes and transfer_bytes must be positive")
         self.arena = torch.empty(self.slot_bytes * self.n_slots, dtype=torch.uint8, device=device)
         handle = ctypes.c_void_p()
         with torch.cuda.device(device):
-            nat.call("qs_pager_create", nat.ptr(self.arena), self.slot_bytes, self.n_slots, self.page_bytes,
+            nat.call("qs_pager_create", nat.ptr(self.arena), self.slot_bytes, self.n_slots, self.transfer_bytes,
                      ctypes.byref(handle))
         self._pager = handle
         self.held = [0] * self.n_slots
@@ -162,6 +170,7 @@ class RingPrefetch:
             "evicted_unused": 0,
             "successor_entries": 0,
             "h2d_bytes": 0,
+            "h2d_pages": 0,
         }
 
     # -- lifecycle -----------------------------------------------------------------
@@ -270,6 +279,7 @@ class RingPrefetch:
         nat.call("qs_pager_seal", self._pager, slot)
         self.inflight[name] = slot
         self.stats["h2d_bytes"] += b.span
+        self.stats["h2d_pages"] += -(-b.span // self.page_bytes)
 
 
 class PagedQStore:
@@ -291,6 +301,7 @@ class PagedQStore:
         slots: int = 3,
         depth: int = 2,
         page_bytes: int = PAGE_BYTES,
+        transfer_bytes: int = TRANSFER_BYTES,
         enable_prefetch_ring: bool = True,
     ) -> None:
         self.device = torch.device(device)
@@ -305,7 +316,8 @@ class PagedQStore:
         else:
             self.reader = store if isinstance(store, QStoreReader) else QStoreReader(store)
             self.tier = PinnedHostTier.from_reader(self.reader)
-        self.ring = RingPrefetch(self.tier, self.device, slots=slots, depth=depth, page_bytes=page_bytes)
+        self.ring = RingPrefetch(self.tier, self.device, slots=slots, depth=depth, page_bytes=page_bytes,
+                                 transfer_bytes=transfer_bytes)
         self.prefetch = bool(enable_prefetch_ring)
         self.stats = DenseQStoreStats()
 
@@ -313,7 +325,8 @@ class PagedQStore:
     def enable_ring(self, *, slots: int | None = None, depth: int = 2) -> None:
         if slots is not None and max(2, int(slots)) != self.ring.n_slots:
             self.ring.close()
-            self.ring = RingPrefetch(self.tier, self.device, slots=slots, depth=depth, page_bytes=self.ring.page_bytes)
+            self.ring = RingPrefetch(self.tier, self.device, slots=slots, depth=depth, page_bytes=self.ring.page_bytes,
+                                     transfer_bytes=self.ring.transfer_bytes)
         self.ring.depth = max(1, int(depth))
         self.prefetch = True
 
