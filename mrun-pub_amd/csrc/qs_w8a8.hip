@@ -510,7 +510,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmPara
   constexpr int A_CH = BM * RC / NT, B_CH = BN * RC / NT;  // 16-byte chunks per thread
   static_assert(A_CH >= 1 && B_CH >= 1 && BM * RC % NT == 0 && BN * RC % NT == 0,
                 "tile too small for the thread count");
-  static_assert(2 * (BM + BN) * LROW >= (BM + BN) * kSideLds * 4, "epilogue staging needs the tile LDS");
+  static_assert(2 * (BM + BN) * LROW >= (BM + BN) * (kSideLds + 1) * 4, "epilogue staging needs the tile LDS");
   __shared__ __attribute__((aligned(16))) int8_t lds[2][(BM + BN) * LROW];
 
   const int tid = threadIdx.x;
@@ -620,10 +620,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmPara
       ws[qq * BN + c] = (bn + c < p.N && q < p.P) ? p.wp[(int64_t)(bn + c) * p.P + q] : 0.f;
     }
   };
-  if (nsc == 1) {
-    stage_side(0);
-    __syncthreads();
+  // the block's activation and weight scales, staged once: read per output from LDS
+  // instead of one dependent L2 round trip per output row
+  float* asl = ws + kSideLds * BN;  // [BM]
+  float* bsl = asl + BM;            // [BN]
+  if constexpr (EPI != EPI_I32) {
+    for (int t = tid; t < BM; t += NT) asl[t] = bm + t < p.M ? p.as[bm + t] : 0.f;
+    for (int t = tid; t < BN; t += NT) bsl[t] = bn + t < p.N ? p.bs[bn + t] : 0.f;
   }
+  if (nsc == 1) stage_side(0);
+  if (EPI != EPI_I32) __syncthreads();
   typedef float f32x16 __attribute__((ext_vector_type(16)));
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -647,16 +653,17 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmPara
       }
       const int col = bn + lc + (lane & 31);
       float bsc = 0.f;
-      if constexpr (EPI != EPI_I32) bsc = col < p.N ? p.bs[col] : 0.f;
+      if constexpr (EPI != EPI_I32) bsc = bsl[lc + (lane & 31)];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = bm + lr + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int lrow = lr + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int row = bm + lrow;
         if (row < p.M && col < p.N) {
           if constexpr (EPI == EPI_I32) {
             static_cast<int32_t*>(p.c)[(int64_t)row * p.ldc + col] = acc[i][j][r];
           } else {
             // reference order: (float(acc) * act_scale) * w_scale, added to the side path
-            float v = mul_rn(mul_rn(static_cast<float>(acc[i][j][r]), p.as[row]), bsc);
+            float v = mul_rn(mul_rn(static_cast<float>(acc[i][j][r]), asl[lrow]), bsc);
             if (nsc) v = add_rn(side[r], v);
             if constexpr (EPI == EPI_F32)
               static_cast<float*>(p.c)[(int64_t)row * p.ldc + col] = v;

@@ -97,6 +97,18 @@ def test_w8a8_no_protection_bit_exact(dev, t):
     assert np.array_equal(y.cpu().numpy().view(np.uint32), ow.w8a8_matmul(q_w, sc_w, x).view(np.uint32))
 
 
+@pytest.mark.parametrize("t,n", [(300, 1000), (17, 640), (1030, 8200), (2048, 2048)])
+def test_w8a8_bf16_out_bit_exact(dev, t, n):
+    """bf16 output = RNE of the bit-exact fp32 result; ragged M and N edges of both tile
+    shapes (the row strips leave through LDS except at a ragged N edge)."""
+    rng, q_w, sc_w = _weights(n, 512, t)
+    x = rng.standard_normal((t, 512)).astype(np.float32)
+    y = _w().w8a8_matmul(torch.from_numpy(q_w).to(dev), torch.from_numpy(sc_w).to(dev), torch.from_numpy(x).to(dev),
+                         out_dtype=torch.bfloat16)
+    ref = torch.from_numpy(ow.w8a8_matmul(q_w, sc_w, x)).to(torch.bfloat16)
+    assert torch.equal(y.cpu(), ref)
+
+
 @pytest.mark.parametrize("protect_k", [4, 8, 16, 24])
 def test_w8a8_outlier_protection(dev, protect_k):
     rng, q_w, sc_w = _weights(640, 4096, protect_k)
