@@ -238,6 +238,19 @@ def secondary_measurements(torch, dev, stream) -> dict:
         }
     del qw, sw
 
+    # decode-step neighbour: fused W8A16 lm_head + top-2 (no logits in memory), the
+    # 151,936 x 1536 head of the config-2 model family, one bf16 decode row, 2 copies
+    V, Kh, hc = 151936, 1536, 2
+    hcodes = torch.randint(-127, 128, (hc, V, Kh), dtype=torch.int8, device=dev, generator=gen)
+    hscales = (torch.rand(hc, V, device=dev, generator=gen) + 0.5) / 127
+    hx = torch.randn(1, Kh, device=dev, generator=gen).to(torch.bfloat16)
+    hpages = [qrow.CompactQRowPage("lm_head", 0, V, Kh, hcodes[i], hscales[i]) for i in range(hc)]
+    th = _graph_time(torch, stream, lambda i: qrow.fused_qrow_top2(hpages[i % hc], hx), 8)
+    hb = V * Kh + V * 4 + Kh * 2
+    res["head_top2_m1"] = {"us": round(th * 1e6, 2), "GB/s": round(hb / th / 1e9, 1),
+                           "hbm_frac": round(hb / th / 1e9 / HBM_PEAK_GBS, 4), "bytes": hb}
+    del hcodes, hscales, hpages
+
     # config 4: routed MoE, 128 experts top-8, H 2048, I 768, T in {64, 512}
     E, topk, H, I = 128, 8, 2048, 768
     layer = moe.Int8ExpertLayer.from_arrays(

@@ -85,6 +85,29 @@ int qs_qrow_swiglu(const void* x, int64_t ldx, const int8_t* gate_codes,
                    const float* gate_scales, const int8_t* up_codes, const float* up_scales,
                    void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* Replaces fused_qrow_top2 / _qrow_w8a16_block_top2_kernel / _reduce_top2_blocks_kernel
+ * (src/mrun/engine/kernels/dense_qstore_cuda.py:578-674, 1239-1317): the two best rows of
+ * the first row_count rows of a head page for every activation row, with no logits in
+ * memory.  Logits follow qs_qrow_matmul's weight contract (W8A16 for BF16/F16 x, fp32 for
+ * F32 x) with fp32 sums.  out_indices[m][0..1] (int32) = start_row + row, out_values[m][0..1]
+ * the logits: the first is the largest (lowest index on ties), the second the largest of
+ * the other rows.  workspace: qs_qrow_top2_workspace_bytes(M, row_count) bytes of device
+ * memory for the per-block candidates.  row_count >= 2. */
+size_t qs_qrow_top2_workspace_bytes(int64_t M, int64_t row_count);
+int qs_qrow_top2(const void* x, int x_dtype, int64_t ldx, const int8_t* codes, const float* scales,
+                 int64_t M, int64_t row_count, int64_t K, int64_t start_row, void* workspace,
+                 size_t workspace_bytes, int32_t* out_indices, float* out_values, void* stream);
+
+/* Replaces _rerank_qrow_candidates_fp32 (dense_qstore_cuda.py:1189-1236): candidates[m][c]
+ * (int64 global rows, 1 <= C <= 16) scored as sum_k float(x[m][k]) * (float(code) * scale)
+ * in fp32; out_indices[m] (int64) is the best candidate (lowest index on ties) and
+ * out_values[m] its score.  A candidate outside [start_row, start_row + page_rows) scores
+ * -inf. */
+int qs_qrow_rerank_fp32(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
+                        const float* scales, int64_t page_rows, int64_t K, int64_t start_row,
+                        const int64_t* candidates, int C, int64_t M, int64_t* out_indices,
+                        float* out_values, void* stream);
+
 /* ---- W8A8 (int8 weights x per-token int8 activations) ------------------------------ */
 
 /* Activation quantizer of w8a8_matmul (src/mrun/engine/kernels/w8a8.py:118-121):

@@ -40,6 +40,25 @@ __device__ __forceinline__ float byte_f32(int d, int b) {
   return static_cast<float>(static_cast<signed char>(d >> (8 * b)));
 }
 
+// float(signed byte B of d) as ONE v_cvt_f32_i32 with an SDWA sign-extending byte
+// select.  byte_f32 computes the same value, but whether the compiler folds the byte
+// extraction into the conversion depends on the surrounding code (when it does not, each
+// code costs a v_bfe_i32 more, about one VALU op per weight byte on the GEMV paths).
+template <int B>
+__device__ __forceinline__ float sbyte_f32(int d) {
+  static_assert(B >= 0 && B < 4, "byte index");
+  float r;
+  if constexpr (B == 0)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(d));
+  else if constexpr (B == 1)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(d));
+  else if constexpr (B == 2)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(d));
+  else
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(d));
+  return r;
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }

@@ -331,8 +331,10 @@ __device__ __forceinline__ void valu_words(const int (&w)[4], float sc, const ui
       const uint8_t* xp = xs + ((int64_t)m * K + k + 4 * j) * ES;
       if constexpr (XT == QS_F32) {
         const f32x4 xv = *reinterpret_cast<const f32x4*>(xp);
+        const float w4[4] = {sbyte_f32<0>(d) * sc, sbyte_f32<1>(d) * sc, sbyte_f32<2>(d) * sc,
+                             sbyte_f32<3>(d) * sc};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[m] = fmaf(xv[e], byte_f32(d, e) * sc, acc[m]);
+        for (int e = 0; e < 4; ++e) acc[m] = fmaf(xv[e], w4[e], acc[m]);
       } else {
         const u32x2 xv = *reinterpret_cast<const u32x2*>(xp);
         // copy the elements out first: a bit_cast of an element expression of an
@@ -340,18 +342,18 @@ __device__ __forceinline__ void valu_words(const int (&w)[4], float sc, const ui
         const unsigned x0 = xv[0], x1 = xv[1];
         if constexpr (XT == QS_BF16) {
           bf16x2 a, b;
-          a[0] = static_cast<__bf16>(byte_f32(d, 0) * sc);
-          a[1] = static_cast<__bf16>(byte_f32(d, 1) * sc);
-          b[0] = static_cast<__bf16>(byte_f32(d, 2) * sc);
-          b[1] = static_cast<__bf16>(byte_f32(d, 3) * sc);
+          a[0] = static_cast<__bf16>(sbyte_f32<0>(d) * sc);
+          a[1] = static_cast<__bf16>(sbyte_f32<1>(d) * sc);
+          b[0] = static_cast<__bf16>(sbyte_f32<2>(d) * sc);
+          b[1] = static_cast<__bf16>(sbyte_f32<3>(d) * sc);
           acc[m] = __builtin_amdgcn_fdot2_f32_bf16(a, __builtin_bit_cast(bf16x2, x0), acc[m], false);
           acc[m] = __builtin_amdgcn_fdot2_f32_bf16(b, __builtin_bit_cast(bf16x2, x1), acc[m], false);
         } else {
           f16x2 a, b;
-          a[0] = static_cast<_Float16>(byte_f32(d, 0) * sc);
-          a[1] = static_cast<_Float16>(byte_f32(d, 1) * sc);
-          b[0] = static_cast<_Float16>(byte_f32(d, 2) * sc);
-          b[1] = static_cast<_Float16>(byte_f32(d, 3) * sc);
+          a[0] = static_cast<_Float16>(sbyte_f32<0>(d) * sc);
+          a[1] = static_cast<_Float16>(sbyte_f32<1>(d) * sc);
+          b[0] = static_cast<_Float16>(sbyte_f32<2>(d) * sc);
+          b[1] = static_cast<_Float16>(sbyte_f32<3>(d) * sc);
           acc[m] = __builtin_amdgcn_fdot2(a, __builtin_bit_cast(f16x2, x0), acc[m], false);
           acc[m] = __builtin_amdgcn_fdot2(b, __builtin_bit_cast(f16x2, x1), acc[m], false);
         }
@@ -379,9 +381,14 @@ struct GemvShape {
 };
 constexpr int kGemvWindow = 4;
 
+// The row work of one wave, shared by the store and top-2 launches: every thread of the
+// workgroup calls it (it stages the activations and passes one barrier).  On return the
+// wave's row sums are in acc (wave-uniform), n / li name the row and its linear, and the
+// result says whether the wave had a row.
 template <int XT, int MB, int U, int TB, bool SWI>
-__global__ __launch_bounds__((GemvShape<SWI, MB>::waves * 64)) void k_gemv_valu(QrowParams p, int rows) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+__device__ __forceinline__ bool gemv_wave_rows(const QrowParams& p, int rows, uint8_t* xs,
+                                               float (&acc)[SWI ? 2 : 1][MB], int& n_out,
+                                               int& li_out) {
   constexpr int WPB = GemvShape<SWI, MB>::waves;
   constexpr int NT = WPB * 64;
   constexpr int ES = XElem<XT>::size;
@@ -473,13 +480,13 @@ __global__ __launch_bounds__((GemvShape<SWI, MB>::waves * 64)) void k_gemv_valu(
     }
   }
   __syncthreads();
-  if (!live) return;
-
-  float acc[P][MB];
+  n_out = n;
+  li_out = li;
 #pragma unroll
   for (int pl = 0; pl < P; ++pl)
 #pragma unroll
     for (int m = 0; m < MB; ++m) acc[pl][m] = 0.f;
+  if (!live) return false;
   if constexpr (TB == 16) {
     if (16 * lane < rem) {
 #pragma unroll
@@ -501,6 +508,17 @@ __global__ __launch_bounds__((GemvShape<SWI, MB>::waves * 64)) void k_gemv_valu(
   for (int pl = 0; pl < P; ++pl)
 #pragma unroll
     for (int m = 0; m < MB; ++m) acc[pl][m] = wave_sum_dpp(acc[pl][m]);
+  return true;
+}
+
+template <int XT, int MB, int U, int TB, bool SWI>
+__global__ __launch_bounds__((GemvShape<SWI, MB>::waves * 64)) void k_gemv_valu(QrowParams p, int rows) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+  const int lane = threadIdx.x & 63;
+  const int M = p.M;
+  float acc[SWI ? 2 : 1][MB];
+  int n, li;
+  if (!gemv_wave_rows<XT, MB, U, TB, SWI>(p, rows, xs, acc, n, li)) return;
   if (lane != 0) return;
   const QrowLin& L = p.lin[li];
 #pragma unroll
@@ -519,6 +537,177 @@ __global__ __launch_bounds__((GemvShape<SWI, MB>::waves * 64)) void k_gemv_valu(
     } else {
       static_cast<uint16_t*>(L.y)[yi] = f32_to_f16_bits(acc[0][m]);
     }
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// head top-2 (fused_qrow_top2, dense_qstore_cuda.py:578-674, 1239-1317)
+// ----------------------------------------------------------------------------------
+// Order of candidates: larger value first, lower index on ties; the second is the best
+// candidate other than the first.  Rows past the semantic row count never compete.
+__device__ __forceinline__ bool top2_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void top2_push(float v, int i, float& v1, int& i1, float& v2, int& i2) {
+  if (top2_better(v, i, v1, i1)) {
+    v2 = v1;
+    i2 = i1;
+    v1 = v;
+    i1 = i;
+  } else if (top2_better(v, i, v2, i2)) {
+    v2 = v;
+    i2 = i;
+  }
+}
+
+// Workgroup epilogue: wave w's logits (one row each) -> this block's first and second
+// per activation row, written to part_v / part_i [M][nblk][2].
+template <int WPB, int MB>
+__device__ __forceinline__ void block_top2(const float (&acc)[MB], bool has_row, int index, int M,
+                                           float* part_v, int* part_i) {
+  __shared__ float tv[WPB][MB];
+  __shared__ int ti[WPB][MB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      tv[wave][m] = has_row ? acc[m] : -INFINITY;
+      ti[wave][m] = has_row ? index : INT_MAX;
+    }
+  }
+  __syncthreads();
+  if (tid < M && tid < MB) {
+    float v1 = -INFINITY, v2 = -INFINITY;
+    int i1 = INT_MAX, i2 = INT_MAX;
+#pragma unroll
+    for (int w = 0; w < WPB; ++w) top2_push(tv[w][tid], ti[w][tid], v1, i1, v2, i2);
+    const int64_t o = ((int64_t)tid * gridDim.x + blockIdx.x) * 2;
+    part_v[o] = v1;
+    part_i[o] = i1;
+    part_v[o + 1] = v2;
+    part_i[o + 1] = i2;
+  }
+}
+
+// Fused W8A16 / fp32 head GEMV + top-2: the decode GEMV's row work (one wave per row of
+// the semantic prefix), no logits written.
+template <int XT, int MB, int U, int TB>
+__global__ __launch_bounds__((GemvShape<false, MB>::waves * 64)) void k_gemv_top2(QrowParams p, int rows,
+                                                                                   int start_row, float* part_v,
+                                                                                   int* part_i) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+  float acc[1][MB];
+  int n, li;
+  const bool has = gemv_wave_rows<XT, MB, U, TB, false>(p, rows, xs, acc, n, li);
+  block_top2<GemvShape<false, MB>::waves, MB>(acc[0], has, start_row + n, p.M, part_v, part_i);
+}
+
+// Any K / alignment: one wave per row, one activation row per launch (x points at it),
+// the same arithmetic contract as k_generic.
+__global__ __launch_bounds__(256) void k_generic_top2(QrowParams p, int x_dtype, int rows, int start_row,
+                                                      float* part_v, int* part_i) {
+  const int lane = threadIdx.x & 63;
+  const int n = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const bool has = n < rows;
+  const int8_t* w = p.lin[0].codes + (int64_t)(has ? n : 0) * p.K;
+  const float s = p.lin[0].scales[has ? n : 0];
+  float acc = 0.f;
+  for (int k = lane; k < p.K; k += 64) {
+    float wf = static_cast<float>(w[k]) * s;
+    float xf;
+    if (x_dtype == QS_F32) {
+      xf = static_cast<const float*>(p.x)[k];
+    } else if (x_dtype == QS_BF16) {
+      wf = bf16_bits_to_f32(f32_to_bf16_bits(wf));
+      xf = bf16_bits_to_f32(static_cast<const uint16_t*>(p.x)[k]);
+    } else {
+      wf = f16_bits_to_f32(f32_to_f16_bits(wf));
+      xf = f16_bits_to_f32(static_cast<const uint16_t*>(p.x)[k]);
+    }
+    acc = fmaf(xf, wf, acc);
+  }
+  float a[1] = {wave_sum_dpp(acc)};
+  block_top2<4, 1>(a, has, start_row + n, 1, part_v, part_i);
+}
+
+// Candidates [M][C] of the blocks -> first and second per row.
+__global__ __launch_bounds__(256) void k_top2_reduce(const float* __restrict__ part_v,
+                                                     const int* __restrict__ part_i, int C,
+                                                     int* __restrict__ out_i, float* __restrict__ out_v) {
+  __shared__ float sv[256][2];
+  __shared__ int si[256][2];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  float v1 = -INFINITY, v2 = -INFINITY;
+  int i1 = INT_MAX, i2 = INT_MAX;
+  for (int c = tid; c < C; c += 256)
+    top2_push(part_v[(int64_t)m * C + c], part_i[(int64_t)m * C + c], v1, i1, v2, i2);
+  sv[tid][0] = v1;
+  si[tid][0] = i1;
+  sv[tid][1] = v2;
+  si[tid][1] = i2;
+  __syncthreads();
+  for (int h = 128; h >= 1; h >>= 1) {
+    if (tid < h) {
+      float a1 = sv[tid][0], a2 = sv[tid][1];
+      int b1 = si[tid][0], b2 = si[tid][1];
+      top2_push(sv[tid + h][0], si[tid + h][0], a1, b1, a2, b2);
+      top2_push(sv[tid + h][1], si[tid + h][1], a1, b1, a2, b2);
+      sv[tid][0] = a1;
+      si[tid][0] = b1;
+      sv[tid][1] = a2;
+      si[tid][1] = b2;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    out_v[2 * m] = sv[0][0];
+    out_i[2 * m] = si[0][0];
+    out_v[2 * m + 1] = sv[0][1];
+    out_i[2 * m + 1] = si[0][1];
+  }
+}
+
+// FP32 candidate rerank (_rerank_qrow_candidates_fp32, dense_qstore_cuda.py:1189-1236):
+// score = sum_k float(x[k]) * (float(code[k]) * scale), fp32; best score wins, lower
+// index on ties.  Wave c of workgroup m scores candidate c of row m.
+__global__ __launch_bounds__(1024) void k_rerank_fp32(const void* __restrict__ x, int x_dtype, int64_t ldx,
+                                                      const int8_t* __restrict__ codes,
+                                                      const float* __restrict__ scales, int page_rows, int K,
+                                                      int64_t start_row, const int64_t* __restrict__ cand, int C,
+                                                      int64_t* __restrict__ out_i, float* __restrict__ out_v) {
+  __shared__ float sv[16];
+  __shared__ int64_t si[16];
+  const int m = blockIdx.x, lane = threadIdx.x & 63, c = threadIdx.x >> 6;
+  const int64_t idx = cand[(int64_t)m * C + c];
+  const int64_t local = idx - start_row;
+  const bool ok = local >= 0 && local < page_rows;
+  const int8_t* w = codes + (ok ? local : 0) * (int64_t)K;
+  const float s = scales[ok ? local : 0];
+  float acc = 0.f;
+  for (int k = lane; k < K; k += 64) {
+    float xf;
+    if (x_dtype == QS_F32) xf = static_cast<const float*>(x)[(int64_t)m * ldx + k];
+    else if (x_dtype == QS_BF16) xf = bf16_bits_to_f32(static_cast<const uint16_t*>(x)[(int64_t)m * ldx + k]);
+    else xf = f16_bits_to_f32(static_cast<const uint16_t*>(x)[(int64_t)m * ldx + k]);
+    acc = fmaf(xf, static_cast<float>(w[k]) * s, acc);
+  }
+  acc = wave_sum_dpp(acc);
+  if (lane == 0) {
+    sv[c] = ok ? acc : -INFINITY;
+    si[c] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float bv = sv[0];
+    int64_t bi = si[0];
+    for (int j = 1; j < C; ++j)
+      if (sv[j] > bv || (sv[j] == bv && si[j] < bi)) {
+        bv = sv[j];
+        bi = si[j];
+      }
+    out_v[m] = bv;
+    out_i[m] = bi;
   }
 }
 
@@ -753,6 +942,40 @@ int run_valu(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool swiglu) {
   return hip_check(hipGetLastError(), "k_gemv_valu launch");
 }
 
+template <int XT, int MB, int TB>
+void launch_top2_tb(const QrowParams& q, int rows, int start_row, float* pv, int* pi, size_t lds,
+                    hipStream_t s) {
+  constexpr int WPB = GemvShape<false, MB>::waves;
+  const dim3 grid((unsigned)cdiv(rows, WPB)), block(WPB * 64);
+  const int F = q.K >> 10;
+  if (F <= 1)
+    hipLaunchKernelGGL((k_gemv_top2<XT, MB, 1, TB>), grid, block, lds, s, q, rows, start_row, pv, pi);
+  else if (F <= 2)
+    hipLaunchKernelGGL((k_gemv_top2<XT, MB, 2, TB>), grid, block, lds, s, q, rows, start_row, pv, pi);
+  else if (F <= 4)
+    hipLaunchKernelGGL((k_gemv_top2<XT, MB, 4, TB>), grid, block, lds, s, q, rows, start_row, pv, pi);
+  else if (F <= 8)
+    hipLaunchKernelGGL((k_gemv_top2<XT, MB, 8, TB>), grid, block, lds, s, q, rows, start_row, pv, pi);
+  else
+    hipLaunchKernelGGL((k_gemv_top2<XT, MB, 12, TB>), grid, block, lds, s, q, rows, start_row, pv, pi);
+}
+
+template <int XT, int MB>
+void launch_top2_mb(const QrowParams& q, int rows, int start_row, float* pv, int* pi, size_t lds,
+                    hipStream_t s) {
+  switch (gemv_tail(q.K)) {
+    case 0: launch_top2_tb<XT, MB, 0>(q, rows, start_row, pv, pi, lds, s); break;
+    case 4: launch_top2_tb<XT, MB, 4>(q, rows, start_row, pv, pi, lds, s); break;
+    case 8: launch_top2_tb<XT, MB, 8>(q, rows, start_row, pv, pi, lds, s); break;
+    case 12: launch_top2_tb<XT, MB, 12>(q, rows, start_row, pv, pi, lds, s); break;
+    default: launch_top2_tb<XT, MB, 16>(q, rows, start_row, pv, pi, lds, s); break;
+  }
+}
+
+// Candidate blocks of the head top-2 for `rows` semantic rows (the generic path's 4-row
+// blocks; the fused path uses 8-row blocks, so this bounds both).
+int64_t top2_blocks(int64_t rows) { return cdiv(rows, 4); }
+
 // Runs one set of linears sharing x, M <= 32 rows at a time for the MFMA path.
 int run_linears(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool row_stable) {
   if (M == 0) return QS_OK;
@@ -925,4 +1148,93 @@ extern "C" int qs_qrow_swiglu(const void* x, int64_t ldx, const int8_t* gate_cod
   p.M = (int)M;
   hipLaunchKernelGGL(k_generic_swiglu, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, s, p);
   return hip_check(hipGetLastError(), "k_generic_swiglu launch");
+}
+
+extern "C" size_t qs_qrow_top2_workspace_bytes(int64_t M, int64_t row_count) {
+  if (M <= 0 || row_count <= 0) return 0;
+  return (size_t)(M * top2_blocks(row_count) * 2) * (sizeof(float) + sizeof(int));
+}
+
+extern "C" int qs_qrow_top2(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
+                            const float* scales, int64_t M, int64_t row_count, int64_t K,
+                            int64_t start_row, void* workspace, size_t workspace_bytes,
+                            int32_t* out_indices, float* out_values, void* stream) {
+  if (!codes || !scales || !out_indices || !out_values) return fail(QS_ERR_INVALID, "qrow_top2: null pointer");
+  int st = validate_common(x, x_dtype, ldx, M, K);
+  if (st) return st;
+  if (row_count < 2 || row_count > INT_MAX - 1) return fail(QS_ERR_INVALID, "qrow_top2: row_count must be >= 2");
+  if (start_row < 0 || start_row + row_count > INT_MAX) return fail(QS_ERR_LIMIT, "qrow_top2: indices exceed int32");
+  if (M == 0) return QS_OK;
+  if (M > 65535) return fail(QS_ERR_LIMIT, "qrow_top2: at most 65535 activation rows");
+  if (!workspace || workspace_bytes < qs_qrow_top2_workspace_bytes(M, row_count))
+    return fail(QS_ERR_INVALID, "qrow_top2: workspace smaller than qs_qrow_top2_workspace_bytes()");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int es = x_dtype == QS_F32 ? 4 : 2;
+  const int64_t nblk_max = top2_blocks(row_count);
+  float* pv = static_cast<float*>(workspace);
+  int* pi = reinterpret_cast<int*>(pv + M * nblk_max * 2);
+  QrowParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.K = (int)K;
+  p.n_lin = 1;
+  p.lin[0] = QrowLin{codes, scales, nullptr, 0, (int)row_count, 0};
+  const int rows = (int)row_count;
+  int C;
+  if (valu_eligible(p, x_dtype)) {
+    const int mb = valu_mb(x_dtype, K, M);
+    const int nblk = (int)cdiv(rows, GemvShape<false, 1>::waves);
+    C = 2 * nblk;
+    for (int64_t m0 = 0; m0 < M; m0 += mb) {
+      QrowParams q = p;
+      q.M = (int)((M - m0) < mb ? (M - m0) : mb);
+      q.x = static_cast<const char*>(x) + m0 * ldx * es;
+      float* qv = pv + m0 * C;
+      int* qi = pi + m0 * C;
+      const size_t lds = (size_t)q.M * K * es;
+      if (x_dtype == QS_F32) {
+        if (mb == 4) launch_top2_mb<QS_F32, 4>(q, rows, (int)start_row, qv, qi, lds, s);
+        else if (mb == 2) launch_top2_mb<QS_F32, 2>(q, rows, (int)start_row, qv, qi, lds, s);
+        else launch_top2_mb<QS_F32, 1>(q, rows, (int)start_row, qv, qi, lds, s);
+      } else if (x_dtype == QS_BF16) {
+        if (mb == 2) launch_top2_mb<QS_BF16, 2>(q, rows, (int)start_row, qv, qi, lds, s);
+        else launch_top2_mb<QS_BF16, 1>(q, rows, (int)start_row, qv, qi, lds, s);
+      } else {
+        if (mb == 2) launch_top2_mb<QS_F16, 2>(q, rows, (int)start_row, qv, qi, lds, s);
+        else launch_top2_mb<QS_F16, 1>(q, rows, (int)start_row, qv, qi, lds, s);
+      }
+    }
+  } else {
+    const int nblk = (int)nblk_max;
+    C = 2 * nblk;
+    for (int64_t m = 0; m < M; ++m) {
+      QrowParams q = p;
+      q.M = 1;
+      q.x = static_cast<const char*>(x) + m * ldx * es;
+      hipLaunchKernelGGL(k_generic_top2, dim3((unsigned)nblk), dim3(256), 0, s, q, x_dtype, rows,
+                         (int)start_row, pv + m * C, pi + m * C);
+    }
+  }
+  st = hip_check(hipGetLastError(), "qrow top-2 launch");
+  if (st) return st;
+  hipLaunchKernelGGL(k_top2_reduce, dim3((unsigned)M), dim3(256), 0, s, pv, pi, C, out_indices, out_values);
+  return hip_check(hipGetLastError(), "k_top2_reduce launch");
+}
+
+extern "C" int qs_qrow_rerank_fp32(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
+                                   const float* scales, int64_t page_rows, int64_t K, int64_t start_row,
+                                   const int64_t* candidates, int C, int64_t M, int64_t* out_indices,
+                                   float* out_values, void* stream) {
+  if (!codes || !scales || !candidates || !out_indices || !out_values)
+    return fail(QS_ERR_INVALID, "qrow_rerank: null pointer");
+  int st = validate_common(x, x_dtype, ldx, M, K);
+  if (st) return st;
+  if (C < 1 || C > 16) return fail(QS_ERR_LIMIT, "qrow_rerank: 1..16 candidates per row");
+  if (page_rows < 1 || page_rows > INT_MAX) return fail(QS_ERR_INVALID, "qrow_rerank: bad page_rows");
+  if (M == 0) return QS_OK;
+  if (M > 65535) return fail(QS_ERR_LIMIT, "qrow_rerank: at most 65535 activation rows");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_rerank_fp32, dim3((unsigned)M), dim3(64 * C), 0, s, x, x_dtype, ldx, codes, scales,
+                     (int)page_rows, (int)K, start_row, candidates, C, out_indices, out_values);
+  return hip_check(hipGetLastError(), "k_rerank_fp32 launch");
 }

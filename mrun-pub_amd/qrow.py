@@ -25,6 +25,9 @@ from . import _native as nat
 IMPL_W8A16 = "hip-gfx950-w8a16-qrow-v1"
 IMPL_FP32 = "hip-gfx950-qrow-fp32-v1"
 IMPL_SWIGLU = "hip-gfx950-paired-w8a16-swiglu-bf16-v1"
+IMPL_TOP2 = "hip-gfx950-w8a16-qrow-block-top2-v1"
+IMPL_TOP2_FP32 = "hip-gfx950-qrow-fp32-block-top2-v1"
+IMPL_RERANK_SUFFIX = "+fp32-candidate-rerank-v1"
 
 _ACT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
@@ -258,3 +261,142 @@ def fused_qrow_swiglu(
             nat.stream_of(device),
         )
     return y.reshape(*activations.shape[:-1], n), IMPL_SWIGLU
+
+
+# ---- head: fused top-2 and fp32 candidate rerank ----------------------------------------------
+
+
+def _semantic_row_count(page: CompactQRowPage, value: int | None) -> int:
+    """Same checks and messages as dense_qstore_cuda.py:67-76."""
+    if value is None:
+        return page.out_features
+    if isinstance(value, bool) or not isinstance(value, int):
+        raise TypeError("semantic_row_count must be an integer or None")
+    row_count = int(value)
+    if row_count < 2 or row_count > page.out_features:
+        raise ValueError("semantic_row_count must select at least two rows inside the compact page")
+    return row_count
+
+
+def _check_head(page: CompactQRowPage, activations: torch.Tensor) -> None:
+    if activations.ndim < 2 or activations.shape[-1] != page.in_features:
+        raise ValueError("activation shape does not match compact head page")
+    if page.codes.device != activations.device or page.scales.device != activations.device:
+        raise ValueError("head page and activations must use one device")
+
+
+@torch.inference_mode()
+def fused_qrow_top2(
+    page: CompactQRowPage,
+    activations: torch.Tensor,
+    *,
+    semantic_row_count: int | None = None,
+    require_triton: bool = False,
+    block_m: int = 16,
+    block_n: int = 64,
+) -> tuple[torch.Tensor, torch.Tensor, str, int]:
+    """Drop-in for ``fused_qrow_top2`` (dense_qstore_cuda.py:1239-1317).
+
+    Returns ``(indices, values, implementation, working_bytes)``: the two best rows of the
+    semantic prefix of the page per activation row (int32 global row indices, fp32
+    logits), without materializing logits.  ``require_triton`` and the tile arguments
+    keep the reference's signature and checks; the native kernel picks its own tiles.
+    """
+    del require_triton
+    _check_head(page, activations)
+    if block_m not in {16, 32, 64} or block_n != 64:
+        raise ValueError("supported head tiles are block_m in {16,32,64}, block_n=64")
+    row_count = _semantic_row_count(page, semantic_row_count)
+    if activations.dtype not in _ACT_DTYPES:
+        raise ValueError(f"activation dtype {activations.dtype} not supported")
+    n, k = _check_codes(page.codes, page.scales)
+    device = nat.require_device(activations, page.codes)
+    flat = activations.reshape(-1, k)
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    m = int(flat.shape[0])
+    out_i = torch.empty((m, 2), dtype=torch.int32, device=device)
+    out_v = torch.empty((m, 2), dtype=torch.float32, device=device)
+    ws_bytes = int(nat.load().qs_qrow_top2_workspace_bytes(m, row_count))
+    if m:
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+        nat.call(
+            "qs_qrow_top2", nat.ptr(flat), nat.dtype_code(flat.dtype), k, nat.ptr(page.codes),
+            nat.ptr(page.scales), m, row_count, k, int(page.start_row), nat.ptr(ws), ws_bytes,
+            nat.ptr(out_i), nat.ptr(out_v), nat.stream_of(device),
+        )
+    shape = (*activations.shape[:-1], 2)
+    tag = IMPL_TOP2_FP32 if activations.dtype == torch.float32 else IMPL_TOP2
+    working = ws_bytes + m * 2 * (4 + 4)
+    return out_i.reshape(shape), out_v.reshape(shape), tag, int(working)
+
+
+def _rerank(page: CompactQRowPage, activations: torch.Tensor, candidate_indices: torch.Tensor,
+            *, validate_candidate_bounds: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """Checks and messages of dense_qstore_cuda.py:1189-1210; scoring on the device."""
+    if activations.ndim < 2 or activations.shape[-1] != page.in_features:
+        raise ValueError("activation shape does not match compact head page")
+    if candidate_indices.shape[:-1] != activations.shape[:-1]:
+        raise ValueError("candidate rows must match the activation prefix shape")
+    if candidate_indices.shape[-1] < 1:
+        raise ValueError("at least one candidate is required")
+    if candidate_indices.device != activations.device:
+        raise ValueError("candidate indices and activations must use one device")
+    if page.codes.device != activations.device or page.scales.device != activations.device:
+        raise ValueError("head page and activations must use one device")
+    if activations.dtype not in _ACT_DTYPES:
+        raise ValueError(f"activation dtype {activations.dtype} not supported")
+    n, k = _check_codes(page.codes, page.scales)
+    device = nat.require_device(activations, page.codes)
+    flat = activations.reshape(-1, k)
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    m = int(flat.shape[0])
+    cand = candidate_indices.reshape(m, -1).to(torch.long).contiguous()
+    c = int(cand.shape[1])
+    if validate_candidate_bounds:
+        local = cand - int(page.start_row)
+        if bool(((local < 0) | (local >= page.out_features)).any().item()):
+            raise ValueError("candidate index falls outside the compact head page")
+    out_i = torch.empty(m, dtype=torch.long, device=device)
+    out_v = torch.empty(m, dtype=torch.float32, device=device)
+    if m:
+        nat.call(
+            "qs_qrow_rerank_fp32", nat.ptr(flat), nat.dtype_code(flat.dtype), k, nat.ptr(page.codes),
+            nat.ptr(page.scales), n, k, int(page.start_row), nat.ptr(cand), c, m, nat.ptr(out_i),
+            nat.ptr(out_v), nat.stream_of(device),
+        )
+    shape = activations.shape[:-1]
+    return out_i.reshape(shape), out_v.reshape(shape)
+
+
+@torch.inference_mode()
+def rerank_qrow_candidates_fp32(
+    page: CompactQRowPage, activations: torch.Tensor, candidate_indices: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Drop-in for ``rerank_qrow_candidates_fp32`` (dense_qstore_cuda.py:1174-1186): score a
+    shortlist in fp32 with exact dequant; returns ``(best_indices, best_values)``."""
+    return _rerank(page, activations, candidate_indices, validate_candidate_bounds=True)
+
+
+@torch.inference_mode()
+def fused_qrow_reranked_argmax(
+    page: CompactQRowPage,
+    activations: torch.Tensor,
+    *,
+    semantic_row_count: int | None = None,
+    require_triton: bool = False,
+    block_m: int = 16,
+    block_n: int = 64,
+) -> tuple[torch.Tensor, torch.Tensor, str, int]:
+    """Drop-in for ``fused_qrow_reranked_argmax`` (dense_qstore_cuda.py:1332-1374): fused
+    top-two search, then fp32 reranking of the two candidates."""
+    candidates, _, implementation, working = fused_qrow_top2(
+        page, activations, semantic_row_count=semantic_row_count, require_triton=require_triton,
+        block_m=block_m, block_n=block_n,
+    )
+    # the candidates come from the masked kernel above: no bounds revalidation (no sync)
+    indices, values = _rerank(page, activations, candidates, validate_candidate_bounds=False)
+    rows = activations.numel() // page.in_features
+    rerank_bytes = rows * (2 * 8 + 8 + 4)
+    return indices, values, implementation + IMPL_RERANK_SUFFIX, int(working + rerank_bytes)

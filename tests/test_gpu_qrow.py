@@ -169,3 +169,101 @@ def test_errors_are_reference_exceptions(dev):
         fused_qrow_matmul(page, torch.zeros((1, 16), device=dev), block_m=8)
     with pytest.raises(ValueError, match="BF16"):
         fused_qrow_swiglu(page, page, torch.zeros((1, 16), device=dev))
+
+
+# ---- head: fused top-2 and fp32 rerank ---------------------------------------------------------
+
+
+def _page(codes, scales, dev, start_row=0):
+    from mrun_pub_amd.qrow import CompactQRowPage
+
+    n, k = codes.shape
+    return CompactQRowPage("lm_head", start_row, start_row + n, k, _dev(codes, dev), _dev(scales, dev))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_top2_reference_kat(dev, dtype):
+    """reference tests/test_dense_qstore_cuda.py:246-287 on the device (K=4: generic path)."""
+    codes = np.array(
+        [[1, 0, 0, 0], [0, 1, 0, 0], [0, 0, 1, 0], [0, 0, 0, 1], [1, 1, 0, 0], [-1, 0, 1, 0], [1, 1, 0, 0]],
+        dtype=np.int8,
+    )
+    page = _page(codes, np.ones(7, np.float32), dev, start_row=11)
+    x = torch.tensor([[2.0, 3.0, -1.0, 0.5], [-2.0, 0.0, 4.0, 1.0]], device=dev).to(dtype)
+    q = _qrow()
+    cand, vals, tag, _ = q.fused_qrow_top2(page, x)
+    assert cand.cpu().tolist() == [[15, 17], [16, 13]] and cand.dtype == torch.int32
+    assert vals.cpu().tolist() == [[5.0, 5.0], [6.0, 4.0]]
+    assert tag.startswith("hip-gfx950")
+    best, best_v = q.rerank_qrow_candidates_fp32(page, x, cand)
+    assert best.cpu().tolist() == [15, 16] and best_v.cpu().tolist() == [5.0, 6.0]
+    fused, _, ftag, _ = q.fused_qrow_reranked_argmax(page, x)
+    assert torch.equal(fused, best) and ftag.endswith("+fp32-candidate-rerank-v1")
+
+
+def test_top2_semantic_row_count_kat(dev):
+    """reference tests/test_dense_qstore_cuda.py:289-311: padding rows never compete."""
+    page = _page(np.array([[2, 0], [0, 2], [1, 1], [100, 100]], np.int8), np.ones(4, np.float32), dev)
+    x = torch.ones((1, 2), device=dev)
+    q = _qrow()
+    assert int(q.fused_qrow_reranked_argmax(page, x)[0].item()) == 3
+    assert int(q.fused_qrow_reranked_argmax(page, x, semantic_row_count=3)[0].item()) == 0
+    for invalid, error in ((True, TypeError), (1, ValueError), (5, ValueError), (2.5, TypeError)):
+        with pytest.raises(error, match="semantic_row_count"):
+            q.fused_qrow_top2(page, x, semantic_row_count=invalid)
+    with pytest.raises(ValueError, match="head tiles"):
+        q.fused_qrow_top2(page, x, block_n=32)
+    with pytest.raises(ValueError, match="outside the compact head page"):
+        q.rerank_qrow_candidates_fp32(page, x, torch.tensor([[4]], device=dev))
+
+
+def _exact_head(v, k, m, seed):
+    """Codes x scale 2^-6 x activations on a 1/16 grid: every product and sum is exact in
+    fp32 and the weights are exact in bf16/fp16, so logits (and their ties) are exact."""
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(-127, 128, size=(v, k), dtype=np.int8)
+    scales = np.full(v, 2.0 ** -6, np.float32)
+    x = (rng.integers(-8, 9, size=(m, k)) / 16.0).astype(np.float32)
+    return codes, scales, x
+
+
+@pytest.mark.parametrize("v,k", [(5000, 1536), (4099, 1024), (3001, 2304), (777, 8960), (600, 1000)])
+@pytest.mark.parametrize("m", [1, 2, 5])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_top2_exact_heads(dev, v, k, m, dtype):
+    """Every row tail kind (none, 4/8/12-byte, ragged -> generic path), batches of MB rows."""
+    codes, scales, x = _exact_head(v, k, m, seed=v + k + m)
+    start, rows = 37, v - 3
+    page = _page(codes, scales, dev, start_row=start)
+    cand, vals, _, _ = _qrow().fused_qrow_top2(page, _dev(x, dev, dtype), semantic_row_count=rows)
+    dname = {torch.bfloat16: "bf16", torch.float32: "fp32", torch.float16: "fp16"}[dtype]
+    ri, rv = oq.qrow_top2(oq.head_logits(codes, scales, x, dname), start_row=start, row_count=rows)
+    assert np.array_equal(cand.cpu().numpy(), ri)
+    assert np.array_equal(vals.cpu().numpy(), rv)
+    best, bv = _qrow().rerank_qrow_candidates_fp32(page, _dev(x, dev, dtype), cand)
+    oi, ov = oq.rerank_fp32(codes, scales, x, ri, start_row=start)
+    assert np.array_equal(best.cpu().numpy(), oi) and np.array_equal(bv.cpu().numpy(), ov)
+
+
+def test_top2_full_vocabulary_decode(dev):
+    """A 151,936 x 1536 int8 head (Qwen2-1.5B's lm_head shape), one bf16 decode row."""
+    codes, scales, x = _exact_head(151936, 1536, 1, seed=9)
+    page = _page(codes, scales, dev)
+    cand, vals, _, _ = _qrow().fused_qrow_top2(page, _dev(x, dev, torch.bfloat16))
+    ri, rv = oq.qrow_top2(oq.head_logits(codes, scales, x, "bf16"))
+    assert np.array_equal(cand.cpu().numpy(), ri) and np.array_equal(vals.cpu().numpy(), rv)
+
+
+def test_top2_random_floats_within_tolerance(dev):
+    """General inputs: the chosen rows are the best up to fp32 summation order."""
+    rng, codes, scales = _case(20000, 1536, seed=4)
+    x = oq.round_bf16(rng.standard_normal((2, 1536)).astype(np.float32))
+    page = _page(codes, scales, dev)
+    cand, vals, _, _ = _qrow().fused_qrow_top2(page, _dev(x, dev, torch.bfloat16))
+    L = oq.head_logits(codes, scales, x, "bf16").astype(np.float64)
+    ci, cv = cand.cpu().numpy(), vals.cpu().numpy()
+    for m in range(2):
+        top = np.sort(L[m])[::-1]
+        tol = 1e-5 * np.abs(L[m]).max()
+        assert abs(L[m, ci[m, 0]] - top[0]) <= tol and abs(L[m, ci[m, 1]] - top[1]) <= tol
+        assert np.allclose(cv[m], L[m, ci[m]], rtol=0, atol=tol) and ci[m, 0] != ci[m, 1]

@@ -125,3 +125,49 @@ def test_row_stable_equals_batched_in_oracle():
     full = oq.qrow_matmul_w8a16(q, s, x)
     for m in range(5):
         np.testing.assert_array_equal(oq.qrow_matmul_w8a16(q, s, x[m : m + 1])[0], full[m])
+
+
+# ---- head top-2 and fp32 rerank ------------------------------------------------------------
+
+
+def _kat_head():
+    # reference tests/test_dense_qstore_cuda.py:246-266 (page rows 11..17, unit scales)
+    codes = np.array(
+        [[1, 0, 0, 0], [0, 1, 0, 0], [0, 0, 1, 0], [0, 0, 0, 1], [1, 1, 0, 0], [-1, 0, 1, 0], [1, 1, 0, 0]],
+        dtype=np.int8,
+    )
+    x = np.array([[2.0, 3.0, -1.0, 0.5], [-2.0, 0.0, 4.0, 1.0]], dtype=np.float32)
+    return codes, np.ones(7, np.float32), x
+
+
+def test_top2_and_rerank_reference_kat():
+    codes, scales, x = _kat_head()
+    idx, val = oq.qrow_top2(oq.head_logits(codes, scales, x, "fp32"), start_row=11)
+    assert idx.tolist() == [[15, 17], [16, 13]]  # test_dense_qstore_cuda.py:281
+    assert val.tolist() == [[5.0, 5.0], [6.0, 4.0]]
+    best, best_v = oq.rerank_fp32(codes, scales, x, idx, start_row=11)
+    assert best.tolist() == [15, 16] and best_v.tolist() == [5.0, 6.0]  # :283-284
+
+
+def test_top2_semantic_row_count_masks_padding_kat():
+    # reference tests/test_dense_qstore_cuda.py:289-311
+    codes = np.array([[2, 0], [0, 2], [1, 1], [100, 100]], dtype=np.int8)
+    scales = np.ones(4, np.float32)
+    x = np.ones((1, 2), np.float32)
+    logits = oq.head_logits(codes, scales, x, "fp32")
+    for rows, want in ((None, 3), (3, 0)):
+        cand, _ = oq.qrow_top2(logits, row_count=rows)
+        best, _ = oq.rerank_fp32(codes, scales, x, cand)
+        assert int(best[0]) == want
+
+
+def test_top2_matches_a_stable_sort():
+    # discrete logits with many ties: the first two of a (value desc, index asc) sort
+    rng = np.random.default_rng(5)
+    for _ in range(50):
+        L = rng.integers(-4, 5, size=(3, 37)).astype(np.float32)
+        idx, val = oq.qrow_top2(L, start_row=100)
+        for m in range(3):
+            order = np.lexsort((np.arange(37), -L[m]))
+            assert idx[m].tolist() == [100 + int(order[0]), 100 + int(order[1])]
+            assert val[m].tolist() == [float(L[m, order[0]]), float(L[m, order[1]])]
