@@ -385,10 +385,12 @@ constexpr int kGemvWindow = 4;
 // workgroup calls it (it stages the activations and passes one barrier).  On return the
 // wave's row sums are in acc (wave-uniform), n / li name the row and its linear, and the
 // result says whether the wave had a row.
+// blk is the 8-row (SWI: 2-row) block of this call; stage = false skips the activation
+// staging when an earlier call of the same workgroup has already filled xs.
 template <int XT, int MB, int U, int TB, bool SWI>
 __device__ __forceinline__ bool gemv_wave_rows(const QrowParams& p, int rows, uint8_t* xs,
                                                float (&acc)[SWI ? 2 : 1][MB], int& n_out,
-                                               int& li_out) {
+                                               int& li_out, int blk, bool stage) {
   constexpr int WPB = GemvShape<SWI, MB>::waves;
   constexpr int NT = WPB * 64;
   constexpr int ES = XElem<XT>::size;
@@ -399,7 +401,7 @@ __device__ __forceinline__ bool gemv_wave_rows(const QrowParams& p, int rows, ui
   const int tid = threadIdx.x, lane = tid & 63;
   const int K = p.K, M = p.M;
   const int F = K >> 10;
-  const int r0 = (int)blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r0 = blk * WPB + __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool live = r0 < rows;
   const int rr = live ? r0 : 0;
   int li = 0;
@@ -413,7 +415,7 @@ __device__ __forceinline__ bool gemv_wave_rows(const QrowParams& p, int rows, ui
   const uint8_t* xg = static_cast<const uint8_t*>(p.x);
 
   i32x4 xr[XREG ? XL : 1];
-  if constexpr (XREG) {
+  if (XREG && stage) {
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
       int idx = tid + i * NT;
@@ -466,20 +468,22 @@ __device__ __forceinline__ bool gemv_wave_rows(const QrowParams& p, int rows, ui
 #pragma unroll
   for (int c = 0; c < (kGemvWindow < U ? kGemvWindow : U); ++c) load_chunk(c);
 
-  if constexpr (XREG) {
+  if (stage) {
+    if constexpr (XREG) {
 #pragma unroll
-    for (int i = 0; i < XL; ++i) {
-      const int idx = tid + i * NT;
-      if (idx < M * row16) reinterpret_cast<i32x4*>(xs)[idx] = xr[i];
+      for (int i = 0; i < XL; ++i) {
+        const int idx = tid + i * NT;
+        if (idx < M * row16) reinterpret_cast<i32x4*>(xs)[idx] = xr[i];
+      }
+    } else {
+      for (int i = tid; i < M * row16; i += NT) {
+        const int m = i / row16, c = i - m * row16;
+        reinterpret_cast<i32x4*>(xs)[i] =
+            *reinterpret_cast<const i32x4*>(xg + ((int64_t)m * p.ldx * ES + (int64_t)c * 16));
+      }
     }
-  } else {
-    for (int i = tid; i < M * row16; i += NT) {
-      const int m = i / row16, c = i - m * row16;
-      reinterpret_cast<i32x4*>(xs)[i] =
-          *reinterpret_cast<const i32x4*>(xg + ((int64_t)m * p.ldx * ES + (int64_t)c * 16));
-    }
+    __syncthreads();
   }
-  __syncthreads();
   n_out = n;
   li_out = li;
 #pragma unroll
@@ -518,7 +522,7 @@ __global__ __launch_bounds__((GemvShape<SWI, MB>::waves * 64)) void k_gemv_valu(
   const int M = p.M;
   float acc[SWI ? 2 : 1][MB];
   int n, li;
-  if (!gemv_wave_rows<XT, MB, U, TB, SWI>(p, rows, xs, acc, n, li)) return;
+  if (!gemv_wave_rows<XT, MB, U, TB, SWI>(p, rows, xs, acc, n, li, (int)blockIdx.x, true)) return;
   if (lane != 0) return;
   const QrowLin& L = p.lin[li];
 #pragma unroll
@@ -561,46 +565,69 @@ __device__ __forceinline__ void top2_push(float v, int i, float& v1, int& i1, fl
   }
 }
 
-// Workgroup epilogue: wave w's logits (one row each) -> this block's first and second
-// per activation row, written to part_v / part_i [M][nblk][2].
+// Workgroup epilogue: each wave's running first/second per activation row -> this
+// workgroup's first and second, written to part_v / part_i [M][gridDim.x][2].
 template <int WPB, int MB>
-__device__ __forceinline__ void block_top2(const float (&acc)[MB], bool has_row, int index, int M,
-                                           float* part_v, int* part_i) {
-  __shared__ float tv[WPB][MB];
-  __shared__ int ti[WPB][MB];
+__device__ __forceinline__ void block_top2(const float (&v1)[MB], const int (&i1)[MB], const float (&v2)[MB],
+                                           const int (&i2)[MB], int M, float* part_v, int* part_i) {
+  __shared__ float tv[WPB][MB][2];
+  __shared__ int ti[WPB][MB][2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (lane == 0) {
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
-      tv[wave][m] = has_row ? acc[m] : -INFINITY;
-      ti[wave][m] = has_row ? index : INT_MAX;
+      tv[wave][m][0] = v1[m];
+      ti[wave][m][0] = i1[m];
+      tv[wave][m][1] = v2[m];
+      ti[wave][m][1] = i2[m];
     }
   }
   __syncthreads();
   if (tid < M && tid < MB) {
-    float v1 = -INFINITY, v2 = -INFINITY;
-    int i1 = INT_MAX, i2 = INT_MAX;
+    float a1 = -INFINITY, a2 = -INFINITY;
+    int b1 = INT_MAX, b2 = INT_MAX;
 #pragma unroll
-    for (int w = 0; w < WPB; ++w) top2_push(tv[w][tid], ti[w][tid], v1, i1, v2, i2);
+    for (int w = 0; w < WPB; ++w) {
+      top2_push(tv[w][tid][0], ti[w][tid][0], a1, b1, a2, b2);
+      top2_push(tv[w][tid][1], ti[w][tid][1], a1, b1, a2, b2);
+    }
     const int64_t o = ((int64_t)tid * gridDim.x + blockIdx.x) * 2;
-    part_v[o] = v1;
-    part_i[o] = i1;
-    part_v[o + 1] = v2;
-    part_i[o + 1] = i2;
+    part_v[o] = a1;
+    part_i[o] = b1;
+    part_v[o + 1] = a2;
+    part_i[o + 1] = b2;
   }
 }
 
 // Fused W8A16 / fp32 head GEMV + top-2: the decode GEMV's row work (one wave per row of
-// the semantic prefix), no logits written.
+// the semantic prefix), no logits written.  Persistent: workgroup g takes the 8-row
+// blocks g, g + G, ... (G = gridDim.x), stages the activations once and keeps each
+// wave's running first/second in registers.
 template <int XT, int MB, int U, int TB>
 __global__ __launch_bounds__((GemvShape<false, MB>::waves * 64)) void k_gemv_top2(QrowParams p, int rows,
                                                                                    int start_row, float* part_v,
                                                                                    int* part_i) {
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
-  float acc[1][MB];
-  int n, li;
-  const bool has = gemv_wave_rows<XT, MB, U, TB, false>(p, rows, xs, acc, n, li);
-  block_top2<GemvShape<false, MB>::waves, MB>(acc[0], has, start_row + n, p.M, part_v, part_i);
+  constexpr int WPB = GemvShape<false, MB>::waves;
+  const int nblk = (rows + WPB - 1) / WPB;
+  float v1[MB], v2[MB];
+  int i1[MB], i2[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    v1[m] = v2[m] = -INFINITY;
+    i1[m] = i2[m] = INT_MAX;
+  }
+  bool stage = true;
+  for (int blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
+    float acc[1][MB];
+    int n, li;
+    if (gemv_wave_rows<XT, MB, U, TB, false>(p, rows, xs, acc, n, li, blk, stage)) {
+#pragma unroll
+      for (int m = 0; m < MB; ++m) top2_push(acc[0][m], start_row + n, v1[m], i1[m], v2[m], i2[m]);
+    }
+    stage = false;
+  }
+  block_top2<WPB, MB>(v1, i1, v2, i2, p.M, part_v, part_i);
 }
 
 // Any K / alignment: one wave per row, one activation row per launch (x points at it),
@@ -627,8 +654,9 @@ __global__ __launch_bounds__(256) void k_generic_top2(QrowParams p, int x_dtype,
     }
     acc = fmaf(xf, wf, acc);
   }
-  float a[1] = {wave_sum_dpp(acc)};
-  block_top2<4, 1>(a, has, start_row + n, 1, part_v, part_i);
+  float v1[1] = {has ? wave_sum_dpp(acc) : -INFINITY}, v2[1] = {-INFINITY};
+  int i1[1] = {has ? start_row + n : INT_MAX}, i2[1] = {INT_MAX};
+  block_top2<4, 1>(v1, i1, v2, i2, 1, part_v, part_i);
 }
 
 // Candidates [M][C] of the blocks -> first and second per row.
@@ -942,11 +970,18 @@ int run_valu(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool swiglu) {
   return hip_check(hipGetLastError(), "k_gemv_valu launch");
 }
 
+// Workgroups of the persistent top-2 launch: 4 resident 8-wave workgroups per CU.
+constexpr int kTop2Grid = 1024;
+int top2_grid(int rows) {
+  const int nblk = (int)cdiv(rows, GemvShape<false, 1>::waves);
+  return nblk < kTop2Grid ? nblk : kTop2Grid;
+}
+
 template <int XT, int MB, int TB>
 void launch_top2_tb(const QrowParams& q, int rows, int start_row, float* pv, int* pi, size_t lds,
                     hipStream_t s) {
   constexpr int WPB = GemvShape<false, MB>::waves;
-  const dim3 grid((unsigned)cdiv(rows, WPB)), block(WPB * 64);
+  const dim3 grid((unsigned)top2_grid(rows)), block(WPB * 64);
   const int F = q.K >> 10;
   if (F <= 1)
     hipLaunchKernelGGL((k_gemv_top2<XT, MB, 1, TB>), grid, block, lds, s, q, rows, start_row, pv, pi);
@@ -1183,8 +1218,7 @@ extern "C" int qs_qrow_top2(const void* x, int x_dtype, int64_t ldx, const int8_
   int C;
   if (valu_eligible(p, x_dtype)) {
     const int mb = valu_mb(x_dtype, K, M);
-    const int nblk = (int)cdiv(rows, GemvShape<false, 1>::waves);
-    C = 2 * nblk;
+    C = 2 * top2_grid(rows);
     for (int64_t m0 = 0; m0 < M; m0 += mb) {
       QrowParams q = p;
       q.M = (int)((M - m0) < mb ? (M - m0) : mb);
