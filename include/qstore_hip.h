@@ -214,6 +214,22 @@ int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uint8_t* packe
                    int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+/* ---- offline codecs (store writer) --------------------------------------------------------
+ * Replaces _quant_row_int8 (src/mrun/engine/kernels/qstore_build.py:496-501): per row,
+ * s = max|W| / 127 (0 -> 1), q = clip(rint(W / s), +-127); W fp32 [N, K] (ldw), q int8
+ * [N, K] (ldq), scales fp32 [N].  Bit-exact with the numpy writer. */
+int qs_quant_rows_int8(const float* W, int64_t ldw, int64_t N, int64_t K, int8_t* q, int64_t ldq,
+                       float* scales, void* stream);
+/* Replaces _quant_row_int3 (qstore_int3.py:42-56, bits 3) and _quant_row_int2
+ * (qstore_int2.py:36-63, bits 2, TWN ternary) with their packers (:30-39, :24-33): per row
+ * and group of G columns, scales fp32 [N, ceil(K/G)] and LSB-first code streams packed
+ * [N, row_bytes = ceil(K*bits/8)].  codes is a workspace of N*K bytes (raw codes).
+ * Bit-exact with the numpy writer, including numpy's pairwise summation order in the
+ * int2 means and sums. */
+int qs_quant_rows_lowbit(const float* W, int64_t ldw, int64_t N, int64_t K, int bits, int G,
+                         uint8_t* packed, int64_t row_bytes, float* scales, uint8_t* codes,
+                         void* stream);
+
 /* ---- pinned-host -> HBM page streaming -------------------------------------------------
  * Replaces the CUDA prefetch ring _RingSlot / _RingPrefetch (src/mrun/engine/kernels/
  * qstore.py:459-660: pinned staging, side-stream H2D, event + record_stream ordering) at

@@ -52,6 +52,8 @@ SIGNATURES: dict[str, tuple] = {
     "qs_qrow_top2_workspace_bytes": (ctypes.c_size_t, [_L, _L]),
     "qs_qrow_top2": (_I, [_P, _I, _L, _P, _P, _L, _L, _L, _L, _P, ctypes.c_size_t, _P, _P, _P]),
     "qs_qrow_rerank_fp32": (_I, [_P, _I, _L, _P, _P, _L, _L, _L, _P, _I, _L, _P, _P, _P]),
+    "qs_quant_rows_int8": (_I, [_P, _L, _L, _L, _P, _L, _P, _P]),
+    "qs_quant_rows_lowbit": (_I, [_P, _L, _L, _L, _I, _I, _P, _L, _P, _P, _P]),
     "qs_act_quant_i8": (_I, [_P, _I, _L, _P, _P, _P, _L, _L, _P]),
     "qs_outlier_topk": (_I, [_P, _I, _L, _L, _L, _I, _P, _P, _P, _P]),
     "qs_w8a8_side_gather": (_I, [_P, _I, _L, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P]),

@@ -1,0 +1,214 @@
+// Offline QStore codecs on the device: the writer's row quantizers, bit-exact.
+//
+// Kernels
+//   k_quant_int8   : one wave per row: s = max|W| / 127 (0 -> 1), q = clip(rint(W / s), +-127)
+//                    (_quant_row_int8, src/mrun/engine/kernels/qstore_build.py:496-501).
+//   k_quant_groups : one thread per (row, group) of G columns, raw codes to a workspace:
+//                    bits 3: s = max|blk| / 3 (0 -> 1), code = clip(rint(blk / s), -3, 3) + 4
+//                    (_quant_row_int3, qstore_int3.py:42-56);
+//                    bits 2: TWN ternary, thr = 0.7 * mean|blk|, active = |blk| >= thr,
+//                    s = sum(|blk| * active) / count (no active -> 1; 0 -> 1),
+//                    code = (active ? sign(blk) : 0) + 1 (_quant_row_int2, qstore_int2.py:36-63).
+//   k_pack_codes   : one thread per output byte of the LSB-first row bitstream
+//                    (np.packbits(bitorder="little"), qstore_int3.py:30-39, qstore_int2.py:24-33).
+//
+// Arithmetic follows numpy's exactly:
+//   * float32 divisions by the literals 127.0 / 3.0 (numpy keeps float32 for a Python float
+//     operand) and by the per-element scale are IEEE single divisions (HIP's default float
+//     division is correctly rounded), np.round is round-half-even (rintf);
+//   * the float32 sums of mean() and sum() use numpy's pairwise summation order (8
+//     interleaved partial sums for n <= 128, combined as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)),
+//     the n % 8 tail added in order; longer runs split at n/2 rounded down to a multiple
+//     of 8), starting from the additive identity;
+//   * mean = float32(double(sum) / n) and s = float32(double(weighted) / count): numpy
+//     divides a float32 array by an integer count in float64 and casts the result back;
+//   * 0.7 * mean is a float32 product with 0.7 rounded to float32.
+#include "qs_common.h"
+
+namespace qs {
+
+// numpy's float32 pairwise sum of f(0) .. f(n-1) (loops_utils.h: FLOAT_pairwise_sum),
+// written as an explicit stack of halves so that it stays iterative on the device.
+template <typename F>
+__device__ float np_pairwise_sum(int n, F f) {
+  // ranges waiting to be summed: [start, len]; results combined in the same tree order
+  // through a second stack of partial sums.
+  int st_start[32], st_len[32], st_state[32];
+  float st_val[32];
+  int sp = 0;
+  st_start[0] = 0;
+  st_len[0] = n;
+  st_state[0] = 0;
+  float ret = 0.f;
+  while (sp >= 0) {
+    const int a = st_start[sp], len = st_len[sp];
+    if (len <= 128) {
+      float res;
+      if (len < 8) {
+        res = 0.f;
+        for (int i = 0; i < len; ++i) res += f(a + i);
+      } else {
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = f(a + j);
+        int i = 8;
+        for (; i < len - (len % 8); i += 8) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) r[j] += f(a + i + j);
+        }
+        res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        for (; i < len; ++i) res += f(a + i);
+      }
+      // pop and hand the result to the parent
+      --sp;
+      while (true) {
+        if (sp < 0) {
+          ret = res;
+          break;
+        }
+        if (st_state[sp] == 1) {  // left half done: remember it, descend into the right half
+          st_val[sp] = res;
+          st_state[sp] = 2;
+          const int n2 = st_len[sp] / 2 - (st_len[sp] / 2) % 8;
+          ++sp;
+          st_start[sp] = st_start[sp - 1] + n2;
+          st_len[sp] = st_len[sp - 1] - n2;
+          st_state[sp] = 0;
+          break;
+        }
+        // both halves done
+        res = st_val[sp] + res;
+        --sp;
+      }
+    } else {
+      // split: left half first
+      st_state[sp] = 1;
+      const int n2 = len / 2 - (len / 2) % 8;
+      ++sp;
+      st_start[sp] = a;
+      st_len[sp] = n2;
+      st_state[sp] = 0;
+    }
+  }
+  return ret;
+}
+
+__global__ __launch_bounds__(256) void k_quant_int8(const float* __restrict__ W, int64_t ldw, int N, int K,
+                                                    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const float* w = W + (int64_t)n * ldw;
+  float mx = 0.f;
+  for (int k = lane; k < K; k += 64) mx = fmaxf(mx, fabsf(w[k]));
+  mx = wave_max(mx);
+  float s = mx / 127.0f;
+  if (s == 0.f) s = 1.f;
+  if (lane == 0) scales[n] = s;
+  for (int k = lane; k < K; k += 64) {
+    float r = rintf(w[k] / s);
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    q[(int64_t)n * ldq + k] = static_cast<int8_t>(r);
+  }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void k_quant_groups(const float* __restrict__ W, int64_t ldw, int N, int K,
+                                                      int G, float* __restrict__ scales,
+                                                      uint8_t* __restrict__ codes) {
+  const int ng = (K + G - 1) / G;
+  const int64_t t = blockIdx.x * 256ll + threadIdx.x;
+  if (t >= (int64_t)N * ng) return;
+  const int n = (int)(t / ng), g = (int)(t - (int64_t)n * ng);
+  const int c0 = g * G, len = min(G, K - c0);
+  const float* w = W + (int64_t)n * ldw + c0;
+  uint8_t* out = codes + (int64_t)n * K + c0;
+  float s;
+  if constexpr (BITS == 3) {
+    float mx = 0.f;
+    for (int i = 0; i < len; ++i) mx = fmaxf(mx, fabsf(w[i]));
+    s = mx / 3.0f;
+    if (s == 0.f) s = 1.f;
+    for (int i = 0; i < len; ++i) {
+      float r = rintf(w[i] / s);
+      r = fminf(fmaxf(r, -3.f), 3.f);
+      out[i] = static_cast<uint8_t>(static_cast<int>(r) + 4);
+    }
+  } else {
+    const float sum_abs = np_pairwise_sum(len, [&](int i) { return fabsf(w[i]); });
+    const float mean = static_cast<float>(static_cast<double>(sum_abs) / len);
+    const float thr = 0.7f * mean;
+    int count = 0;
+    for (int i = 0; i < len; ++i) count += fabsf(w[i]) >= thr;
+    const float weighted = np_pairwise_sum(len, [&](int i) {
+      const float a = fabsf(w[i]);
+      return a >= thr ? a : 0.f;  // |w| * active (active is 0/1; a * 0 = +0)
+    });
+    s = count > 0 ? static_cast<float>(static_cast<double>(weighted) / count) : 1.f;
+    if (s == 0.f) s = 1.f;
+    for (int i = 0; i < len; ++i) {
+      const float v = w[i];
+      const int sg = v > 0.f ? 1 : (v < 0.f ? -1 : 0);
+      out[i] = static_cast<uint8_t>((fabsf(v) >= thr ? sg : 0) + 1);
+    }
+  }
+  scales[(int64_t)n * ng + g] = s;
+}
+
+// Output byte b of row n holds bits 8b .. 8b+7 of the row's code stream, code j at bits
+// [BITS*j, BITS*j + BITS), least significant bit first.
+template <int BITS>
+__global__ __launch_bounds__(256) void k_pack_codes(const uint8_t* __restrict__ codes, int N, int K,
+                                                    uint8_t* __restrict__ packed, int64_t row_bytes) {
+  const int64_t t = blockIdx.x * 256ll + threadIdx.x;
+  if (t >= (int64_t)N * row_bytes) return;
+  const int n = (int)(t / row_bytes);
+  const int64_t b = t - (int64_t)n * row_bytes;
+  const uint8_t* c = codes + (int64_t)n * K;
+  unsigned v = 0;
+  const int64_t bit0 = 8 * b;
+  for (int64_t j = bit0 / BITS; j < K && j * BITS < bit0 + 8; ++j) {
+    const int64_t sh = j * BITS - bit0;  // may be negative for the code straddling in
+    const unsigned code = c[j] & ((1u << BITS) - 1);
+    v |= sh >= 0 ? code << sh : code >> (-sh);
+  }
+  packed[t] = static_cast<uint8_t>(v & 0xffu);
+}
+
+}  // namespace qs
+
+using namespace qs;
+
+extern "C" int qs_quant_rows_int8(const float* W, int64_t ldw, int64_t N, int64_t K, int8_t* q,
+                                  int64_t ldq, float* scales, void* stream) {
+  if (!W || !q || !scales) return fail(QS_ERR_INVALID, "quant_rows_int8: null pointer");
+  if (N < 0 || K <= 0 || ldw < K || ldq < K) return fail(QS_ERR_INVALID, "quant_rows_int8: bad shape");
+  if (N > INT_MAX || K > INT_MAX) return fail(QS_ERR_LIMIT, "quant_rows_int8: dimension exceeds int32");
+  if (N == 0) return QS_OK;
+  hipLaunchKernelGGL(k_quant_int8, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     W, ldw, (int)N, (int)K, q, ldq, scales);
+  return hip_check(hipGetLastError(), "k_quant_int8 launch");
+}
+
+extern "C" int qs_quant_rows_lowbit(const float* W, int64_t ldw, int64_t N, int64_t K, int bits, int G,
+                                    uint8_t* packed, int64_t row_bytes, float* scales, uint8_t* codes,
+                                    void* stream) {
+  if (!W || !packed || !scales || !codes) return fail(QS_ERR_INVALID, "quant_rows_lowbit: null pointer");
+  if (bits != 2 && bits != 3) return fail(QS_ERR_UNSUPPORTED, "quant_rows_lowbit: bits must be 2 or 3");
+  if (N < 0 || K <= 0 || G <= 0 || ldw < K) return fail(QS_ERR_INVALID, "quant_rows_lowbit: bad shape");
+  if (row_bytes != (K * bits + 7) / 8) return fail(QS_ERR_INVALID, "quant_rows_lowbit: row_bytes must be ceil(K*bits/8)");
+  if (N * K > ((int64_t)1 << 40) || K > INT_MAX || G > (1 << 24))
+    return fail(QS_ERR_LIMIT, "quant_rows_lowbit: shape too large");
+  if (N == 0) return QS_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t ng = cdiv(K, G);
+  const unsigned gq = (unsigned)cdiv(N * ng, 256), gp = (unsigned)cdiv(N * row_bytes, 256);
+  if (bits == 3) {
+    hipLaunchKernelGGL(k_quant_groups<3>, dim3(gq), dim3(256), 0, s, W, ldw, (int)N, (int)K, G, scales, codes);
+    hipLaunchKernelGGL(k_pack_codes<3>, dim3(gp), dim3(256), 0, s, codes, (int)N, (int)K, packed, row_bytes);
+  } else {
+    hipLaunchKernelGGL(k_quant_groups<2>, dim3(gq), dim3(256), 0, s, W, ldw, (int)N, (int)K, G, scales, codes);
+    hipLaunchKernelGGL(k_pack_codes<2>, dim3(gp), dim3(256), 0, s, codes, (int)N, (int)K, packed, row_bytes);
+  }
+  return hip_check(hipGetLastError(), "qs_quant_rows_lowbit launch");
+}
