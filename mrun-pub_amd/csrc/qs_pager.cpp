@@ -38,7 +38,7 @@ struct qs_pager {
 
 extern "C" int qs_pager_create(void* device_arena, size_t slot_bytes, int slots,
                                size_t max_transfer, qs_pager** out) {
-  if (!out || !device_arena || slot_bytes == 0 || slot_bytes % 256 || slots < 1 || slots > 64 ||
+  if (!out || !device_arena || slot_bytes == 0 || slot_bytes % 256 || slots < 1 || slots > 65536 ||
       max_transfer == 0)
     return fail(QS_ERR_INVALID, "pager_create: bad arguments");
   qs_pager* p = new (std::nothrow) qs_pager();

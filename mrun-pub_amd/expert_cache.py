@@ -1,0 +1,514 @@
+"""Paged int8 experts: page store, pinned host tier and HBM slot cache with route prefetch.
+
+Mirrors the Qwen3 MoE page tier of the reference (src/mrun/engine/qwen3_moe_cuda.py):
+
+* ``PackedInt8ExpertStore`` -- ``PackedFP8ExpertStore`` (:780-840): one flat file of
+  ``[layers * experts, page_stride]`` pages in the ``ExpertPageLayout`` (:187-233) with
+  1-byte int8 codes and fp32 row scales; ``global_page`` / ``gather`` / ``view_pages``.
+* ``HostPageTier`` (:878-981): a budgeted pinned copy of pages, filled by one sequential
+  ``warm()`` pass or admitted on first miss, never evicted.
+* ``ExpertPageCache`` (:1221-1820): a device cache of ``capacity`` page slots with the
+  reference's ``global-lru-v1`` / ``layer-frequency-lru-v1`` eviction, decode protection,
+  the ``slot-indirect-v1`` binding (routed groups address cache slots directly through the
+  grouped GEMM's ``group_slots``) and the ``compact-copy-v1`` binding, and opt-in
+  route-history prefetch of the previous step's routes for layer + 1.
+
+Design for the device: the cache arena is the slot array of a ``qs_pager`` (csrc/
+qs_pager.cpp).  A miss is one H2D transfer straight from the pinned tier page into its
+cache slot (no staging copy when the tier holds the page), on the pager's copy stream;
+the compute stream waits on that slot's ready event; the slot's free event is recorded
+after the kernels that read it, and a later fill of that slot waits for it on the host.
+Route prefetches are the same transfers issued one layer early.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+from collections import Counter, OrderedDict
+from dataclasses import dataclass, fields
+from pathlib import Path
+from typing import Any
+
+import numpy as np
+import torch
+
+from . import _native as nat
+from .moe import ExpertPageLayout, Int8ExpertLayer
+
+STORE_SCHEMA = "mrun-hip-int8-expert-store-v1"
+STORE_CODEC = "int8-qrow-experts-v1"
+STORE_FILE = "experts.pages"
+
+GLOBAL_LRU_CACHE_POLICY = "global-lru-v1"
+LAYER_FREQUENCY_CACHE_POLICY = "layer-frequency-lru-v1"
+SUPPORTED_CACHE_POLICIES = frozenset({GLOBAL_LRU_CACHE_POLICY, LAYER_FREQUENCY_CACHE_POLICY})
+COMPACT_PAGE_BINDING_POLICY = "compact-copy-v1"
+SLOT_INDIRECT_PAGE_BINDING_POLICY = "slot-indirect-v1"
+DEFAULT_PAGE_BINDING_POLICY = SLOT_INDIRECT_PAGE_BINDING_POLICY
+SUPPORTED_PAGE_BINDING_POLICIES = frozenset({COMPACT_PAGE_BINDING_POLICY, SLOT_INDIRECT_PAGE_BINDING_POLICY})
+TRANSFER_BYTES = 64 << 20
+
+
+# ---- page store -----------------------------------------------------------------------------
+
+
+def write_int8_expert_store(store_dir: str | Path, gate_up, gate_up_scales, down, down_scales) -> Path:
+    """Write ``[L,E,2I,H]`` int8 / ``[L,E,2I]`` f32 / ``[L,E,H,I]`` int8 / ``[L,E,H]`` f32 arrays
+    as one page file plus ``manifest.json``; returns the store directory."""
+    gate_up = np.asarray(gate_up, dtype=np.int8)
+    down = np.asarray(down, dtype=np.int8)
+    gate_up_scales = np.asarray(gate_up_scales, dtype=np.float32)
+    down_scales = np.asarray(down_scales, dtype=np.float32)
+    L, E, two_i, H = gate_up.shape
+    I = two_i // 2
+    if two_i != 2 * I or down.shape != (L, E, H, I) or gate_up_scales.shape != (L, E, two_i) \
+            or down_scales.shape != (L, E, H):
+        raise ValueError("expert arrays disagree on [layers, experts, 2I, H] / [layers, experts, H, I]")
+    layout = ExpertPageLayout.create(H, I)
+    root = Path(store_dir)
+    root.mkdir(parents=True, exist_ok=True)
+    pages = np.lib.format.open_memmap(root / (STORE_FILE + ".npy"), mode="w+", dtype=np.uint8,
+                                      shape=(L * E, layout.page_stride))
+    for layer in range(L):
+        for expert in range(E):
+            row = pages[layer * E + expert]
+            row[:] = 0
+            lo = layout.gate_up_codes_offset
+            row[lo:lo + layout.gate_up_codes_bytes] = gate_up[layer, expert].reshape(-1).view(np.uint8)
+            lo = layout.gate_up_scales_offset
+            row[lo:lo + layout.gate_up_scales_bytes] = gate_up_scales[layer, expert].view(np.uint8)
+            lo = layout.down_codes_offset
+            row[lo:lo + layout.down_codes_bytes] = down[layer, expert].reshape(-1).view(np.uint8)
+            lo = layout.down_scales_offset
+            row[lo:lo + layout.down_scales_bytes] = down_scales[layer, expert].view(np.uint8)
+    pages.flush()
+    del pages
+    manifest = {
+        "schema_version": STORE_SCHEMA,
+        "codec": STORE_CODEC,
+        "layout": layout.as_dict(),
+        "layers": int(L),
+        "num_experts": int(E),
+        "data_file": STORE_FILE + ".npy",
+    }
+    (root / "manifest.json").write_text(json.dumps(manifest, indent=1, sort_keys=True), encoding="utf-8")
+    return root
+
+
+class PackedInt8ExpertStore:
+    """``[layers * experts, page_stride]`` int8 expert pages on disk (memory-mapped)."""
+
+    def __init__(self, store_dir: str | Path):
+        self.store_dir = Path(store_dir)
+        self.manifest = json.loads((self.store_dir / "manifest.json").read_text(encoding="utf-8"))
+        if self.manifest.get("schema_version") != STORE_SCHEMA:
+            raise ValueError("unsupported int8 expert store schema")
+        if self.manifest.get("codec") != STORE_CODEC:
+            raise ValueError("unsupported int8 expert store codec")
+        self.layout = ExpertPageLayout.from_dict(self.manifest["layout"])
+        self.layers = int(self.manifest["layers"])
+        self.experts = int(self.manifest["num_experts"])
+        self.data_path = self.store_dir / self.manifest["data_file"]
+        self._pages: np.ndarray | None = None
+        pages = self._ensure_pages()
+        if pages.shape != (self.layers * self.experts, self.layout.page_stride):
+            raise ValueError("expert page file does not match the manifest")
+
+    def _ensure_pages(self) -> np.ndarray:
+        if self._pages is None:
+            self._pages = np.load(self.data_path, mmap_mode="r", allow_pickle=False)
+        return self._pages
+
+    def global_page(self, layer: int, expert: int) -> int:
+        return layer * self.experts + expert
+
+    def page(self, gid: int) -> np.ndarray:
+        return self._ensure_pages()[gid]
+
+    def gather(self, layer: int, expert_ids: list[int], target: torch.Tensor) -> None:
+        if not expert_ids:
+            return
+        if target.device.type != "cpu" or target.dtype != torch.uint8:
+            raise ValueError("expert page staging target must be a CPU uint8 tensor")
+        view = target[: len(expert_ids)].numpy()
+        rows = layer * self.experts + np.asarray(expert_ids, dtype=np.int64)
+        np.take(self._ensure_pages(), rows, axis=0, out=view)
+
+    def view_pages(self, raw: torch.Tensor) -> Int8ExpertLayer:
+        """Expert-page views ``gate_up / gate_up_scales / down / down_scales`` over ``raw``
+        ``[groups, page_stride]`` (no copies)."""
+        if raw.dtype != torch.uint8 or raw.ndim != 2 or raw.shape[1] != self.layout.page_stride:
+            raise ValueError("expert pages must be uint8 [groups, page_stride]")
+        return Int8ExpertLayer(raw.reshape(-1), self.layout, int(raw.shape[0]))
+
+    def release(self) -> None:
+        self._pages = None
+
+
+class HostPageTier:
+    """Budgeted pinned host copy of expert pages (fill once, no eviction)."""
+
+    def __init__(self, store: PackedInt8ExpertStore, *, host_cache_mb: float, try_pin: bool = True):
+        self.store = store
+        stride = store.layout.page_stride
+        total_pages = store.layers * store.experts
+        capacity = min(total_pages, int(float(host_cache_mb) * 1e6) // stride)
+        if capacity < 1:
+            raise ValueError("host_cache_mb smaller than one expert page")
+        self.capacity = capacity
+        self.pinned = False
+        buf = None
+        if try_pin:
+            try:
+                buf = torch.empty((capacity, stride), dtype=torch.uint8, pin_memory=True)
+                self.pinned = True
+            except RuntimeError:
+                buf = None
+        if buf is None:
+            buf = torch.empty((capacity, stride), dtype=torch.uint8)
+        self.buf = buf
+        self._buf_np = buf.numpy()
+        self._rows = np.full(total_pages, -1, dtype=np.int64)
+        self._next_row = 0
+        self.stats = {"capacity_pages": capacity, "pinned": self.pinned, "warmed_pages": 0,
+                      "served_pages": 0, "admitted_pages": 0, "disk_pages": 0}
+
+    def warm(self) -> dict[str, Any]:
+        """Fill rows [next, capacity) with pages [next, capacity) in one sequential pass."""
+        pages = self.store._ensure_pages()
+        start, stop = self._next_row, self.capacity
+        chunk = max(1, (256 << 20) // self.store.layout.page_stride)
+        for lo in range(start, stop, chunk):
+            hi = min(stop, lo + chunk)
+            self._buf_np[lo:hi] = pages[lo:hi]
+        self._rows[start:stop] = np.arange(start, stop, dtype=np.int64)
+        self._next_row = stop
+        self.stats["warmed_pages"] = stop
+        return dict(self.stats)
+
+    def host_page(self, layer: int, expert: int) -> torch.Tensor | None:
+        """The tier's row for a page (admitting it while capacity remains), else None."""
+        gid = self.store.global_page(layer, expert)
+        row = int(self._rows[gid])
+        if row >= 0:
+            self.stats["served_pages"] += 1
+            return self.buf[row]
+        if self._next_row >= self.capacity:
+            self.stats["disk_pages"] += 1
+            return None
+        row = self._next_row
+        self._next_row += 1
+        np.copyto(self._buf_np[row], self.store.page(gid))
+        self._rows[gid] = row
+        self.stats["admitted_pages"] += 1
+        return self.buf[row]
+
+    def gather(self, layer: int, expert_ids: list[int], target: torch.Tensor) -> None:
+        """Fill ``target[:len(expert_ids)]`` from the tier where present, disk otherwise."""
+        view = target[: len(expert_ids)].numpy()
+        for i, expert in enumerate(expert_ids):
+            page = self.host_page(layer, expert)
+            np.copyto(view[i], page.numpy() if page is not None else
+                      self.store.page(self.store.global_page(layer, expert)))
+
+
+# ---- slot policy (host logic) ---------------------------------------------------------------
+
+
+@dataclass
+class PageCacheStats:
+    """Counters of qwen3_moe_cuda.py:983-1030 that this cache maintains."""
+
+    page_requests: int = 0
+    page_hits: int = 0
+    page_misses: int = 0
+    host_to_device_bytes: int = 0
+    layer_acquires: int = 0
+    active_experts_sum: int = 0
+    evictions: int = 0
+    same_layer_evictions: int = 0
+    over_quota_evictions: int = 0
+    fallback_evictions: int = 0
+    decode_protected_promotions: int = 0
+    decode_protected_demotions: int = 0
+
+    def as_dict(self) -> dict[str, Any]:
+        out = {f.name: getattr(self, f.name) for f in fields(self)}
+        out["hit_rate"] = self.page_hits / max(1, self.page_requests)
+        out["host_to_device_gb"] = self.host_to_device_bytes / 1e9
+        out["mean_active_experts"] = self.active_experts_sum / max(1, self.layer_acquires)
+        return out
+
+
+class SlotPolicy:
+    """Which cache slot holds which (layer, expert) page, and which page to evict.
+
+    ``global-lru-v1`` evicts the least recently used unprotected page;
+    ``layer-frequency-lru-v1`` first evicts within the incoming layer once it is at its
+    quota, then any layer above its quota, then falls back to global LRU
+    (qwen3_moe_cuda.py:1415-1488).  Pages requested by the current acquire are never
+    evicted; decode-protected pages lose protection when evicted.
+    """
+
+    def __init__(self, capacity: int, layers: int, policy: str, stats: PageCacheStats):
+        if policy not in SUPPORTED_CACHE_POLICIES:
+            raise ValueError(f"unsupported expert cache policy {policy!r}; "
+                             f"expected one of {sorted(SUPPORTED_CACHE_POLICIES)}")
+        self.capacity = capacity
+        self.policy = policy
+        self.stats = stats
+        self.entries: OrderedDict[tuple[int, int], int] = OrderedDict()
+        self.decode_protected: set[tuple[int, int]] = set()
+        self.free_slots = list(range(capacity - 1, -1, -1))
+        quota, remainder = divmod(capacity, layers)
+        self.layer_quotas = tuple(quota + (1 if layer < remainder else 0) for layer in range(layers))
+        self.layer_entry_counts = [0] * layers
+
+    def reset(self) -> None:
+        self.entries.clear()
+        self.decode_protected.clear()
+        self.free_slots = list(range(self.capacity - 1, -1, -1))
+        self.layer_entry_counts = [0] * len(self.layer_entry_counts)
+
+    def eviction_candidate(self, key, protected) -> tuple[tuple[int, int] | None, str]:
+        if self.policy == GLOBAL_LRU_CACHE_POLICY:
+            return next((c for c in self.entries if c not in protected), None), "fallback"
+        layer = key[0]
+        same_layer = next((c for c in self.entries if c[0] == layer and c not in protected), None)
+        if same_layer is not None and self.layer_entry_counts[layer] >= self.layer_quotas[layer]:
+            return same_layer, "same-layer"
+        over = next((c for c in self.entries if c not in protected
+                     and self.layer_entry_counts[c[0]] > self.layer_quotas[c[0]]), None)
+        if over is not None:
+            return over, "over-quota"
+        return next((c for c in self.entries if c not in protected), None), "fallback"
+
+    def reserve(self, key, protected) -> int:
+        if self.free_slots:
+            slot = self.free_slots.pop()
+        else:
+            victim, reason = self.eviction_candidate(key, protected)
+            if victim is None:
+                raise RuntimeError("expert cache cannot evict a page from the active set")
+            slot = self.entries.pop(victim)
+            if victim in self.decode_protected:
+                self.decode_protected.remove(victim)
+                self.stats.decode_protected_demotions += 1
+            self.layer_entry_counts[victim[0]] -= 1
+            self.stats.evictions += 1
+            if reason == "same-layer":
+                self.stats.same_layer_evictions += 1
+            elif reason == "over-quota":
+                self.stats.over_quota_evictions += 1
+            else:
+                self.stats.fallback_evictions += 1
+        self.entries[key] = slot
+        self.layer_entry_counts[key[0]] += 1
+        return slot
+
+
+# ---- device cache ---------------------------------------------------------------------------
+
+
+class ExpertPageCache:
+    """HBM cache of expert pages with slot binding for the grouped int8 GEMM."""
+
+    def __init__(
+        self,
+        store: PackedInt8ExpertStore,
+        *,
+        device: str | torch.device,
+        cache_mb: float,
+        max_active_pages: int,
+        host_tier: HostPageTier | None = None,
+        route_prefetch: bool | None = None,
+        cache_policy: str | None = None,
+        page_binding_policy: str | None = None,
+    ):
+        self.store = store
+        self.layout = store.layout
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("ExpertPageCache requires a HIP (cuda) device")
+        self.host_tier = host_tier
+        if route_prefetch is None:
+            route_prefetch = os.environ.get("MRUN_QWEN3_MOE_ROUTE_PREFETCH", "").strip() not in ("", "0")
+        self.route_prefetch = bool(route_prefetch)
+        policy = cache_policy if cache_policy is not None else \
+            os.environ.get("MRUN_QWEN3_MOE_CACHE_POLICY", GLOBAL_LRU_CACHE_POLICY)
+        binding = page_binding_policy if page_binding_policy is not None else \
+            os.environ.get("MRUN_QWEN3_MOE_PAGE_BINDING_POLICY", DEFAULT_PAGE_BINDING_POLICY)
+        self.page_binding_policy = str(binding).strip().lower()
+        if self.page_binding_policy not in SUPPORTED_PAGE_BINDING_POLICIES:
+            raise ValueError(f"unsupported expert page binding policy {self.page_binding_policy!r}; "
+                             f"expected one of {sorted(SUPPORTED_PAGE_BINDING_POLICIES)}")
+        stride = self.layout.page_stride
+        requested = int(float(cache_mb) * 1e6) // stride
+        self.capacity = min(store.layers * store.experts, max(int(max_active_pages), requested))
+        self.max_active_pages = int(max_active_pages)
+        self.stats = PageCacheStats()
+        self.policy = SlotPolicy(self.capacity, store.layers, str(policy).strip().lower(), self.stats)
+        self.cache_policy = self.policy.policy
+        self.cache = torch.empty((self.capacity, stride), dtype=torch.uint8, device=self.device)
+        # pinned staging for pages the host tier does not hold (read from the store file)
+        self.stage = torch.empty((self.max_active_pages, stride), dtype=torch.uint8, pin_memory=True)
+        self.compact = torch.empty((self.max_active_pages, stride), dtype=torch.uint8, device=self.device) \
+            if self.page_binding_policy == COMPACT_PAGE_BINDING_POLICY else None
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            nat.call("qs_pager_create", nat.ptr(self.cache), stride, self.capacity, TRANSFER_BYTES,
+                     ctypes.byref(handle))
+        self._pager = handle
+        self._pending_release: list[int] = []
+        self._stage_in_flight = False
+        self._prev_routes: dict[int, list[int]] = {}
+        self.prefetch_stats = {"prefetched_pages": 0, "prefetch_rounds": 0}
+
+    # -- reference surface ------------------------------------------------------------------
+    @property
+    def entries(self) -> OrderedDict:
+        return self.policy.entries
+
+    @property
+    def decode_protected(self) -> set:
+        return self.policy.decode_protected
+
+    @property
+    def device_bytes(self) -> int:
+        n = self.cache.numel() + (self.compact.numel() if self.compact is not None else 0)
+        return int(n)
+
+    def reset(self, *, clear_pages: bool) -> None:
+        self.synchronize()
+        self.stats.__init__()
+        self.prefetch_stats = {"prefetched_pages": 0, "prefetch_rounds": 0}
+        self._prev_routes.clear()
+        if clear_pages:
+            self.policy.reset()
+
+    def acquire_slot_binding(self, layer: int, top_indices: torch.Tensor, *, protect: bool = False):
+        """``(selected_experts, page views of the whole cache, slots)``: routed groups address
+        their cache slots directly (the grouped GEMM's ``group_slots``)."""
+        selected, slots = self._acquire_resident(layer, top_indices, protect=protect)
+        return selected, self.store.view_pages(self.cache), slots
+
+    def acquire(self, layer: int, top_indices: torch.Tensor, *, protect: bool = False):
+        """``(selected_experts, page views of a compact copy)`` (the compact binding)."""
+        selected, slots = self._acquire_resident(layer, top_indices, protect=protect)
+        if self.compact is None:
+            self.compact = torch.empty((self.max_active_pages, self.layout.page_stride), dtype=torch.uint8,
+                                       device=self.device)
+        n = int(selected.numel())
+        torch.index_select(self.cache, 0, slots, out=self.compact[:n])
+        return selected, self.store.view_pages(self.compact[:n])
+
+    def release(self) -> None:
+        """Mark the pages of the last acquire free once the work queued so far on the current
+        stream is done (also done implicitly by the next acquire)."""
+        stream = nat.stream_of(self.device)
+        for slot in self._pending_release:
+            nat.call("qs_pager_release", self._pager, slot, stream)
+        self._pending_release = []
+
+    def synchronize(self) -> None:
+        nat.call("qs_pager_sync", self._pager)
+
+    def close(self) -> None:
+        if self._pager is not None:
+            self.synchronize()
+            nat.call("qs_pager_destroy", self._pager)
+            self._pager = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- internals ----------------------------------------------------------------------------
+    def _fill(self, layer: int, misses: list[tuple[int, int]]) -> None:
+        """One H2D transfer per missing page into its slot (pager copy stream)."""
+        stride = self.layout.page_stride
+        staged: list[tuple[int, int]] = []
+        for expert, slot in misses:
+            src = self.host_tier.host_page(layer, expert) if self.host_tier is not None else None
+            if src is not None and self.host_tier.pinned:
+                nat.call("qs_pager_submit", self._pager, slot, src.data_ptr(), stride, 0)
+                nat.call("qs_pager_seal", self._pager, slot)
+            else:
+                staged.append((expert, slot))
+        if staged:
+            if self._stage_in_flight:  # the previous staging copies must have landed
+                self.synchronize()
+            rows = [e for e, _ in staged]
+            if self.host_tier is not None:
+                self.host_tier.gather(layer, rows, self.stage)
+            else:
+                self.store.gather(layer, rows, self.stage)
+            for i, (_, slot) in enumerate(staged):
+                nat.call("qs_pager_submit", self._pager, slot, self.stage[i].data_ptr(), stride, 0)
+                nat.call("qs_pager_seal", self._pager, slot)
+            self._stage_in_flight = True
+        self.stats.host_to_device_bytes += len(misses) * stride
+
+    def _acquire_resident(self, layer: int, top_indices: torch.Tensor, *, protect: bool):
+        self.release()  # the previous acquire's kernels are queued: its slots may be refilled after them
+        routed = [int(v) for v in top_indices.detach().cpu().reshape(-1)]
+        frequencies = Counter(routed)
+        expert_ids = sorted(frequencies)
+        if len(expert_ids) > self.max_active_pages:
+            raise RuntimeError(f"active expert set {len(expert_ids)} exceeds staging limit {self.max_active_pages}")
+        keys = [(int(layer), e) for e in expert_ids]
+        protected = set(keys)
+        admission = keys
+        if self.cache_policy == LAYER_FREQUENCY_CACHE_POLICY:
+            admission = sorted(keys, key=lambda k: (frequencies[k[1]], k[1]))
+        misses: list[tuple[int, int]] = []
+        for key in admission:
+            if key in self.policy.entries:
+                self.policy.entries.move_to_end(key)
+                continue
+            misses.append((key[1], self.policy.reserve(key, protected)))
+        if misses:
+            self._fill(int(layer), misses)
+        slot_list = [self.policy.entries[k] for k in keys]
+        stream = nat.stream_of(self.device)
+        for slot in slot_list:
+            nat.call("qs_pager_acquire", self._pager, slot, stream)
+        self._pending_release = list(slot_list)
+        self.stats.page_requests += len(keys)
+        self.stats.page_misses += len(misses)
+        self.stats.page_hits += len(keys) - len(misses)
+        self.stats.layer_acquires += 1
+        self.stats.active_experts_sum += len(keys)
+        if protect:
+            new = set(keys) - self.policy.decode_protected
+            self.policy.decode_protected.update(keys)
+            self.stats.decode_protected_promotions += len(new)
+        if self.route_prefetch:
+            self._prefetch_next_layer(int(layer), protected)
+            self._prev_routes[int(layer)] = expert_ids
+        selected = torch.tensor(expert_ids, dtype=torch.long, device=self.device)
+        slots = torch.tensor(slot_list, dtype=torch.long, device=self.device)
+        return selected, slots
+
+    def _prefetch_next_layer(self, layer: int, protected: set) -> None:
+        """Stage the previous step's routes for layer + 1 (qwen3_moe_cuda.py:1778-1815)."""
+        nxt = layer + 1
+        predicted = self._prev_routes.get(nxt)
+        if not predicted:
+            return
+        wanted = [e for e in predicted if (nxt, e) not in self.policy.entries][: self.max_active_pages]
+        fills: list[tuple[int, int]] = []
+        for expert in wanted:
+            try:
+                fills.append((expert, self.policy.reserve((nxt, expert), protected)))
+            except RuntimeError:
+                break  # the cache is saturated by the active set
+        if not fills:
+            return
+        self._fill(nxt, fills)
+        self.prefetch_stats["prefetched_pages"] += len(fills)
+        self.prefetch_stats["prefetch_rounds"] += 1

@@ -299,6 +299,13 @@ class ExpertPageLayout:
         return cls(hidden_size, intermediate_size, 0, gu_c, gu_s_off, gu_rows * 4, d_c_off, d_c, d_s_off,
                    hidden_size * 4, stride)
 
+    @classmethod
+    def from_dict(cls, payload: dict) -> "ExpertPageLayout":
+        return cls(**{name: int(payload[name]) for name in cls.__dataclass_fields__})
+
+    def as_dict(self) -> dict[str, int]:
+        return {name: int(getattr(self, name)) for name in self.__dataclass_fields__}
+
 
 class Int8ExpertLayer:
     """All experts of one layer in one HBM arena laid out as ``ExpertPageLayout`` pages."""
@@ -342,8 +349,14 @@ class Int8ExpertBackend:
     grouped down GEMM -> fixed rank-order reduce -> model dtype.
     """
 
-    def __init__(self, layers: list[Int8ExpertLayer], *, dtype: torch.dtype = torch.bfloat16):
-        self.layers = layers
+    def __init__(self, layers: list[Int8ExpertLayer] | None = None, *, dtype: torch.dtype = torch.bfloat16,
+                 page_cache=None):
+        """``layers``: resident expert layers; ``page_cache``: an ``expert_cache.ExpertPageCache``
+        serving the layers' pages from host memory instead (slot-indirect binding)."""
+        if not layers and page_cache is None:
+            raise ValueError("Int8ExpertBackend needs resident layers or a page cache")
+        self.layers = layers or []
+        self.page_cache = page_cache
         self.dtype = dtype
         self.stats = {"grouped_kernel_calls": 0, "route_compiler_calls": 0, "expert_assignments": 0}
         self._experts: dict[tuple[torch.device, int], torch.Tensor] = {}
@@ -365,6 +378,8 @@ class Int8ExpertBackend:
         *,
         prefill: bool = False,
     ) -> torch.Tensor:
+        if self.page_cache is not None:
+            return self._moe_paged(layer, source, top_indices, top_weights, prefill=prefill)
         del prefill
         page = self.layers[layer]
         E = page.num_experts
@@ -382,6 +397,33 @@ class Int8ExpertBackend:
             expert_output, coef, token_ids, counts, top_indices,
             self._expert_ids(source.device, E), inverse_assignments=inverse,
         )
+        self.stats["grouped_kernel_calls"] += 2
+        self.stats["route_compiler_calls"] += 1
+        self.stats["expert_assignments"] += int(top_indices.numel())
+        return out.to(self.dtype)
+
+    def _moe_paged(self, layer, source, top_indices, top_weights, *, prefill: bool) -> torch.Tensor:
+        """Same flow over the experts of this step only: the page cache binds each routed
+        expert (a compact group id) to its cache slot, and the grouped GEMMs read the pages
+        in place through ``group_slots``."""
+        cache = self.page_cache
+        selected, page, slots = cache.acquire_slot_binding(layer, top_indices, protect=not prefill)
+        compact = torch.searchsorted(selected, top_indices)
+        token_ids, coef, starts, counts, inverse, _ = _route_impl(
+            compact, top_weights, int(selected.numel()), True, coef_f32=True
+        )
+        rows_q, rows_s = quantize_rows(source, token_ids)
+        activated, _ = grouped_int8_mm(
+            rows_q, rows_s, page.gate_up, page.gate_up_scales, starts, counts, group_slots=slots, swiglu=True
+        )
+        act_q, act_s = quantize_rows(activated)
+        expert_output, _ = grouped_int8_mm(
+            act_q, act_s, page.down, page.down_scales, starts, counts, group_slots=slots, out_dtype=self.dtype
+        )
+        out = stable_route_reduce(
+            expert_output, coef, token_ids, counts, top_indices, selected, inverse_assignments=inverse,
+        )
+        cache.release()
         self.stats["grouped_kernel_calls"] += 2
         self.stats["route_compiler_calls"] += 1
         self.stats["expert_assignments"] += int(top_indices.numel())
