@@ -424,7 +424,7 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
     pxo[j] = pcc * C::CPL;
   }
 
-  constexpr int R = J == 1 ? 4 : (J == 2 ? 2 : 1);  // rows per register batch
+  constexpr int R = 1;  // rows per register batch
   uint32_t cw[2][R][J][C::NW];
   float rs[2][R][J], rz[2][R][J];
   // batch bt = rows wave_id + (bt * R + i) * nwaves, i < R (rows past N load row N-1)
@@ -455,10 +455,28 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
   };
   const int nrows = wave_id < p.N ? (p.N - 1 - wave_id) / nwaves + 1 : 0;  // rows of this wave
   const int nbt = (nrows + R - 1) / R;
+  // activations of long rows (J >= 3 pieces per lane): the first kXRegs pieces per thread
+  // are requested before the codes, so the staging below waits for them only, not for the
+  // codes in flight behind them (short rows keep the registers for occupancy instead)
+  constexpr int kXRegs = J >= 3 ? 6 : 0;
+  const int x16 = M * (K / 8);
+  i32x4 xr[kXRegs > 0 ? kXRegs : 1];
+#pragma unroll
+  for (int i = 0; i < kXRegs; ++i) {
+    int q = tid + i * kValuThreads;
+    q = q < x16 ? q : 0;
+    const int m = q / (K / 8), c = q - m * (K / 8);
+    xr[i] = *reinterpret_cast<const i32x4*>(p.x + (int64_t)m * p.ldx + c * 8);
+  }
   if (nbt > 0) gload(0, 0);  // the first rows' codes are in flight during the staging
 
   // activations -> LDS, per-piece sums -> LDS
-  for (int q = tid; q < M * (K / 8); q += kValuThreads) {
+#pragma unroll
+  for (int i = 0; i < kXRegs; ++i) {
+    const int q = tid + i * kValuThreads;
+    if (q < x16) reinterpret_cast<i32x4*>(xs)[q] = xr[i];
+  }
+  for (int q = tid + kXRegs * kValuThreads; q < x16; q += kValuThreads) {
     const int m = q / (K / 8), c = q - (q / (K / 8)) * (K / 8);
     reinterpret_cast<i32x4*>(xs)[q] = *reinterpret_cast<const i32x4*>(p.x + (int64_t)m * p.ldx + c * 8);
   }
@@ -750,7 +768,7 @@ extern "C" int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uin
       p.ng = ng;
       pair_consts(p, bits);
       const int64_t wpb = kValuThreads / 64;
-      const unsigned grid = (unsigned)(cdiv(N, wpb) < 512 ? cdiv(N, wpb) : 512);
+      const unsigned grid = (unsigned)(cdiv(N, wpb) < 1024 ? cdiv(N, wpb) : 1024);
       if (bits == 3) launch_valu<3>(J, (int)M, group_size, grid, lds, s, p);
       else launch_valu<2>(J, (int)M, group_size, grid, lds, s, p);
       return hip_check(hipGetLastError(), "k_lowbit_valu launch");
