@@ -385,6 +385,10 @@ __global__ __launch_bounds__(256) void k_lowbit_slot(LowbitParams p, int gps, fl
 // activations and the per-piece sums live in LDS, one copy per workgroup.
 // ----------------------------------------------------------------------------------
 constexpr int kValuThreads = 512;  // 8 waves: one staged copy of x serves 8 row streams
+// activation rows taken by the VALU kernel: its dot work grows with M while the unpack
+// does not, and from M = 4 on the MFMA slot kernel is faster
+constexpr int kValuMaxM = 2;
+constexpr size_t kValuLdsMax = 144 * 1024;     // staged activations + piece sums per workgroup
 
 template <int BITS>
 struct ValuCfg {
@@ -674,13 +678,14 @@ void launch_valu_mb(int J, unsigned grid, size_t lds, hipStream_t s, const Lowbi
   else launch_valu_j<BITS, G, MB, 6>(grid, lds, s, p);
 }
 
+// MB: activation rows per launch (1 or 2; p.M <= MB)
 template <int BITS>
-void launch_valu(int J, int M, int G, unsigned grid, size_t lds, hipStream_t s, const LowbitParams& p) {
+void launch_valu(int J, int MB, int G, unsigned grid, size_t lds, hipStream_t s, const LowbitParams& p) {
   if (G == 64) {
-    if (M == 1) launch_valu_mb<BITS, 64, 1>(J, grid, lds, s, p);
+    if (MB == 1) launch_valu_mb<BITS, 64, 1>(J, grid, lds, s, p);
     else launch_valu_mb<BITS, 64, 2>(J, grid, lds, s, p);
   } else {
-    if (M == 1) launch_valu_mb<BITS, 128, 1>(J, grid, lds, s, p);
+    if (MB == 1) launch_valu_mb<BITS, 128, 1>(J, grid, lds, s, p);
     else launch_valu_mb<BITS, 128, 2>(J, grid, lds, s, p);
   }
 }
@@ -745,11 +750,19 @@ extern "C" int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uin
     // decode: M <= 2 bf16 rows, one wave per weight row
     const int cpl = bits == 3 ? 32 : 64;
     const int J = (int)cdiv(cdiv(K, cpl), 64);
-    const size_t lds = (((size_t)2 * K * 2 + 15) & ~(size_t)15) + (size_t)2 * (K / cpl) * 4;
+    // activation rows per launch: the next power of two >= M, halved until x and the piece
+    // sums fit the LDS budget; larger M runs as several launches
+    auto lds_for = [&](int mbx) {
+      return (((size_t)mbx * K * 2 + 15) & ~(size_t)15) + (size_t)mbx * (K / cpl) * 4;
+    };
+    int mbv = M <= 1 ? 1 : 2;
+    while (mbv > 1 && lds_for(mbv) > kValuLdsMax) mbv /= 2;
+    const size_t lds = lds_for(mbv);
     const bool layout = (scale_dtype == QS_F16 && zeros && zero_dtype == QS_F16) || (scale_dtype == QS_F32 && !zeros);
     const int lb = bits == 3 ? 12 : 16;
-    if (x_dtype == QS_BF16 && M <= 2 && layout && K % cpl == 0 && group_size % cpl == 0 && J <= 6 && J != 5 &&
-        row_bytes % lb == 0 && aligned(packed, 16) && aligned(x, 16) && ldx % 8 == 0 && lds <= 64 * 1024) {
+    if (x_dtype == QS_BF16 && M <= kValuMaxM && layout && K % cpl == 0 && group_size % cpl == 0 && J <= 6 &&
+        J != 5 && row_bytes % lb == 0 && aligned(packed, 16) && aligned(x, 16) && ldx % 8 == 0 &&
+        lds <= kValuLdsMax) {
       LowbitParams p{};
       p.x = static_cast<const uint16_t*>(x);
       p.ldx = ldx;
@@ -769,8 +782,14 @@ extern "C" int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uin
       pair_consts(p, bits);
       const int64_t wpb = kValuThreads / 64;
       const unsigned grid = (unsigned)(cdiv(N, wpb) < 1024 ? cdiv(N, wpb) : 1024);
-      if (bits == 3) launch_valu<3>(J, (int)M, group_size, grid, lds, s, p);
-      else launch_valu<2>(J, (int)M, group_size, grid, lds, s, p);
+      for (int64_t m0 = 0; m0 < M; m0 += mbv) {
+        LowbitParams q = p;
+        q.M = (int)(M - m0 < mbv ? M - m0 : mbv);
+        q.x = p.x + m0 * ldx;
+        q.y = p.y + m0 * ldy;
+        if (bits == 3) launch_valu<3>(J, mbv, group_size, grid, lds, s, q);
+        else launch_valu<2>(J, mbv, group_size, grid, lds, s, q);
+      }
       return hip_check(hipGetLastError(), "k_lowbit_valu launch");
     }
   }
