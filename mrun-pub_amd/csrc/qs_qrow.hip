@@ -663,36 +663,52 @@ __global__ __launch_bounds__(256) void k_generic_top2(QrowParams p, int x_dtype,
 __global__ __launch_bounds__(256) void k_top2_reduce(const float* __restrict__ part_v,
                                                      const int* __restrict__ part_i, int C,
                                                      int* __restrict__ out_i, float* __restrict__ out_v) {
-  __shared__ float sv[256][2];
-  __shared__ int si[256][2];
-  const int m = blockIdx.x, tid = threadIdx.x;
+  // Partials come from the previous launch, so every read misses the cache: all U loads
+  // of a round are issued before any is merged.  (-inf, INT_MAX) pads are no-ops.
+  constexpr int U = 8;
+  __shared__ float sv[4][2];
+  __shared__ int si[4][2];
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* pv = part_v + (int64_t)m * C;
+  const int* pi = part_i + (int64_t)m * C;
   float v1 = -INFINITY, v2 = -INFINITY;
   int i1 = INT_MAX, i2 = INT_MAX;
-  for (int c = tid; c < C; c += 256)
-    top2_push(part_v[(int64_t)m * C + c], part_i[(int64_t)m * C + c], v1, i1, v2, i2);
-  sv[tid][0] = v1;
-  si[tid][0] = i1;
-  sv[tid][1] = v2;
-  si[tid][1] = i2;
-  __syncthreads();
-  for (int h = 128; h >= 1; h >>= 1) {
-    if (tid < h) {
-      float a1 = sv[tid][0], a2 = sv[tid][1];
-      int b1 = si[tid][0], b2 = si[tid][1];
-      top2_push(sv[tid + h][0], si[tid + h][0], a1, b1, a2, b2);
-      top2_push(sv[tid + h][1], si[tid + h][1], a1, b1, a2, b2);
-      sv[tid][0] = a1;
-      si[tid][0] = b1;
-      sv[tid][1] = a2;
-      si[tid][1] = b2;
+  for (int c0 = tid; c0 < C; c0 += 256 * U) {
+    float v[U];
+    int ix[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + 256 * u;
+      v[u] = c < C ? pv[c] : -INFINITY;
+      ix[u] = c < C ? pi[c] : INT_MAX;
     }
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U; ++u) top2_push(v[u], ix[u], v1, i1, v2, i2);
   }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float o1 = __shfl_xor(v1, off), o2 = __shfl_xor(v2, off);
+    const int j1 = __shfl_xor(i1, off), j2 = __shfl_xor(i2, off);
+    top2_push(o1, j1, v1, i1, v2, i2);
+    top2_push(o2, j2, v1, i1, v2, i2);
+  }
+  if (lane == 0) {
+    sv[wave][0] = v1;
+    si[wave][0] = i1;
+    sv[wave][1] = v2;
+    si[wave][1] = i2;
+  }
+  __syncthreads();
   if (tid == 0) {
-    out_v[2 * m] = sv[0][0];
-    out_i[2 * m] = si[0][0];
-    out_v[2 * m + 1] = sv[0][1];
-    out_i[2 * m + 1] = si[0][1];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      top2_push(sv[w][0], si[w][0], v1, i1, v2, i2);
+      top2_push(sv[w][1], si[w][1], v1, i1, v2, i2);
+    }
+    out_v[2 * m] = v1;
+    out_i[2 * m] = i1;
+    out_v[2 * m + 1] = v2;
+    out_i[2 * m + 1] = i2;
   }
 }
 
