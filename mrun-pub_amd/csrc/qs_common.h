@@ -83,22 +83,30 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t bits) {
 __device__ __forceinline__ void deq16_bf16(i32x4 w, float s, bf16x8& lo, bf16x8& hi) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      lo[4 * j + b] = static_cast<__bf16>(byte_f32(w[j], b) * s);
-      hi[4 * j + b] = static_cast<__bf16>(byte_f32(w[j + 2], b) * s);
-    }
+    const int a = w[j], b = w[j + 2];
+    lo[4 * j + 0] = static_cast<__bf16>(sbyte_f32<0>(a) * s);
+    lo[4 * j + 1] = static_cast<__bf16>(sbyte_f32<1>(a) * s);
+    lo[4 * j + 2] = static_cast<__bf16>(sbyte_f32<2>(a) * s);
+    lo[4 * j + 3] = static_cast<__bf16>(sbyte_f32<3>(a) * s);
+    hi[4 * j + 0] = static_cast<__bf16>(sbyte_f32<0>(b) * s);
+    hi[4 * j + 1] = static_cast<__bf16>(sbyte_f32<1>(b) * s);
+    hi[4 * j + 2] = static_cast<__bf16>(sbyte_f32<2>(b) * s);
+    hi[4 * j + 3] = static_cast<__bf16>(sbyte_f32<3>(b) * s);
   }
 }
 
 __device__ __forceinline__ void deq16_f16(i32x4 w, float s, f16x8& lo, f16x8& hi) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      lo[4 * j + b] = static_cast<_Float16>(byte_f32(w[j], b) * s);
-      hi[4 * j + b] = static_cast<_Float16>(byte_f32(w[j + 2], b) * s);
-    }
+    const int a = w[j], b = w[j + 2];
+    lo[4 * j + 0] = static_cast<_Float16>(sbyte_f32<0>(a) * s);
+    lo[4 * j + 1] = static_cast<_Float16>(sbyte_f32<1>(a) * s);
+    lo[4 * j + 2] = static_cast<_Float16>(sbyte_f32<2>(a) * s);
+    lo[4 * j + 3] = static_cast<_Float16>(sbyte_f32<3>(a) * s);
+    hi[4 * j + 0] = static_cast<_Float16>(sbyte_f32<0>(b) * s);
+    hi[4 * j + 1] = static_cast<_Float16>(sbyte_f32<1>(b) * s);
+    hi[4 * j + 2] = static_cast<_Float16>(sbyte_f32<2>(b) * s);
+    hi[4 * j + 3] = static_cast<_Float16>(sbyte_f32<3>(b) * s);
   }
 }
 

@@ -12,6 +12,11 @@
 //                                 (cvt_sdwa + mul + half a cvt_pk per weight byte).
 //                                 K is split across the waves of a workgroup and reduced
 //                                 through LDS in a fixed order.  Used for 3 <= M.
+//   k_w8a16_s<...>              : the same contract as a streaming kernel -- one wave per
+//                                 (tile, K slice) with a sliding window of chunks in
+//                                 flight, SwiGLU planes sharing a wave, activations in LDS
+//                                 when they are small.  Used for SwiGLU at 3 <= M and for
+//                                 long rows (K >= 4096) while the activations fit in LDS.
 //   k_gemv_valu<...>            : M <= 2 decode rows (any activation dtype) and every
 //                                 fp32-activation call: one wave per weight row, 1 KiB
 //                                 contiguous row segments per instruction issued in row
@@ -292,6 +297,209 @@ __global__ __launch_bounds__(P * KW * 64) void k_w8a16(QrowParams p) {
       for (int q = 0; q < 4; ++q) {
         const int m = 16 * t + 4 * grp + q;
         if (m < M) y[(int64_t)m * ldy + no] = H::out(out[0][t][q]);
+      }
+  }
+}
+
+// Streaming W8A16 MFMA kernel (3 <= M <= 32).  One wave per (16-row tile, K slice); the
+// P planes of a SwiGLU tile share the wave, so each activation fragment is loaded once
+// for both.  A wave walks its chunks ks, ks + KW, ks + 2*KW, ... (128 k each, the lane
+// mapping of k_w8a16) through a window of W chunks in flight: chunk i + W is requested
+// as soon as chunk i has been consumed, so the wave waits for memory once per slice
+// rather than once per batch of chunks.  Window slots past the slice load out of the
+// buffer's range (zero, no memory access), which keeps every wait count static.
+// Activation rows m >= M are zero and never stored.  The KW
+// slices of a tile are summed through LDS in a fixed order and KW depends on (N, K)
+// only, so within this kernel a row does not depend on the other rows of the batch.
+template <int P, int MT, int KW, int W, bool F16, bool XL>
+__global__ __launch_bounds__(KW * 64) void k_w8a16_s(QrowParams p) {
+  typedef HalfOps<F16> H;
+  typedef typename H::vec hvec;
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+
+  int li = 0;
+  if (P == 1) {
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      if (j < p.n_lin && (int)blockIdx.x >= p.lin[j].tile_begin) li = j;
+  }
+  const int tile = (int)blockIdx.x - p.lin[li].tile_begin;
+  const int N = p.lin[li].N;
+  const int K = p.K;
+  const int M = p.M;
+  const int n0 = tile * 16;
+  const int n = min(n0 + col, N - 1);  // clamped lanes compute a row that is not stored
+  // Buffer loads: a 32-bit lane offset plus a uniform chunk offset (the host checks that
+  // N*K and M*ldx*2 fit in 31 bits).  A slot past the slice loads at lane offset `wlim` /
+  // `xlim` with chunk offset 0: that lane offset alone is outside the buffer's range, so
+  // the load returns zero without touching memory.
+  __amdgpu_buffer_rsrc_t wr[P];
+  const float* srow[P];
+  const int wlim = N * K;
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) {
+    const QrowLin& L = p.lin[P == 2 ? pl : li];
+    wr[pl] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(L.codes), (short)0, wlim, 0x00020000);
+    srow[pl] = L.scales + n;
+  }
+  const int wlane = n * K + 32 * grp;
+  const int xlim = M * (int)p.ldx * 2;
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.x), (short)0, xlim, 0x00020000);
+  int xlane[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) xlane[t] = (min(16 * t + col, M - 1) * (int)p.ldx + 32 * grp) * 2;
+  const int C = K / 128;
+  const int nch = ks < C ? (C - 1 - ks) / KW + 1 : 0;  // chunks of this wave's slice
+
+  // XL: the M activation rows sit in LDS (row stride 2K + 16 bytes: the 16 rows of a
+  // fragment read fall in distinct banks), copied once per workgroup right after the
+  // weight window has been requested (the copy lands behind those loads, about when the
+  // first chunk can be consumed), and each chunk's fragments are read from LDS while the
+  // previous chunk is multiplied -- the vector-memory queue then carries only the HBM
+  // weight stream.
+  extern __shared__ __attribute__((aligned(16))) uint8_t xl[];
+  const int xstride = 2 * K + 16;
+
+  static_assert(!XL || W % 2 == 0, "the activation double buffer follows the slot parity");
+  i32x4 wv[W][P][2];
+  hvec xa[XL ? 2 : W][MT][4];
+  auto issue = [&](int slot, int i) {
+    const bool live = i < nch;
+    const int koff = (ks + i * KW) * 128;
+    if constexpr (!XL) {
+      const int xs = live ? 2 * koff : 0;
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // only the lanes of existing rows fetch; padded rows are zero
+          xa[slot][t][j] = hvec{};
+          if (16 * t + col < M)
+            xa[slot][t][j] = __builtin_bit_cast(
+                hvec, __builtin_amdgcn_raw_buffer_load_b128(xr, live ? xlane[t] + 16 * j : xlim, xs, 0));
+        }
+    }
+    const int ws = live ? koff : 0;
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        wv[slot][pl][h] = __builtin_bit_cast(
+            i32x4, __builtin_amdgcn_raw_buffer_load_b128(wr[pl], live ? wlane + 16 * h : wlim, ws, 0));
+  };
+  float sc[P];
+  f32x4 acc[P][MT];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[pl][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // activation fragments of chunk i from LDS into buffer b (XL)
+  auto xfrag = [&](int b, int i) {
+    const int koff = (ks + min(i, nch - 1) * KW) * 128;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = 16 * t + col;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xa[b][t][j] = hvec{};
+        if (m < M) xa[b][t][j] = *reinterpret_cast<const hvec*>(xl + m * xstride + 2 * (koff + 32 * grp + 8 * j));
+      }
+    }
+  };
+  auto consume = [&](int slot, int i) {
+    // chunk i = (multiple of W) + slot with W even: the buffer parity is static
+    const int xs = XL ? (slot & 1) : slot;
+    if constexpr (XL) xfrag(xs ^ 1, i + 1);
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        hvec b0, b1;
+        H::deq(wv[slot][pl][h], sc[pl], b0, b1);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acc[pl][t] = H::mma(xa[xs][t][2 * h], b0, acc[pl][t]);
+          acc[pl][t] = H::mma(xa[xs][t][2 * h + 1], b1, acc[pl][t]);
+        }
+      }
+  };
+
+  // W chunks in flight first, the row scales behind them
+#pragma unroll
+  for (int s = 0; s < W; ++s) {
+    issue(s, s);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) sc[pl] = *srow[pl];
+  if constexpr (XL) {
+    const int pieces = K / 8;  // 16-byte pieces per row
+    for (int q = threadIdx.x; q < M * pieces; q += KW * 64) {
+      const int m = q / pieces, c = q - m * pieces;
+      *reinterpret_cast<i32x4*>(xl + m * xstride + 16 * c) =
+          *reinterpret_cast<const i32x4*>(static_cast<const uint16_t*>(p.x) + (int64_t)m * p.ldx + 8 * c);
+    }
+    __syncthreads();
+    if (nch > 0) xfrag(0, 0);
+  }
+  for (int base = 0; base < nch; base += W) {
+#pragma unroll
+    for (int s = 0; s < W; ++s) {
+      if (base + s < nch) consume(s, base + s);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(s, base + s + W);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  if constexpr (KW > 1) {
+    __shared__ f32x4 red[KW][P][MT][64];
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) red[ks][pl][t][lane] = acc[pl][t];
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        f32x4 s = red[0][pl][t][lane];
+#pragma unroll
+        for (int k2 = 1; k2 < KW; ++k2) s += red[k2][pl][t][lane];
+        acc[pl][t] = s;
+      }
+  }
+
+  // store: lane holds D[m = 16t + 4*grp + q][n = n0 + col]
+  const int no = n0 + col;
+  if (no >= N) return;
+  if constexpr (P == 2) {
+    uint16_t* y = static_cast<uint16_t*>(p.lin[0].y);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = 16 * t + 4 * grp + q;
+        if (m < M) {
+          const float gt = bf16_bits_to_f32(f32_to_bf16_bits(acc[0][t][q]));
+          const float ut = bf16_bits_to_f32(f32_to_bf16_bits(acc[1][t][q]));
+          const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f32(gt)));
+          y[(int64_t)m * p.lin[0].ldy + no] = f32_to_bf16_bits(sl * ut);
+        }
+      }
+  } else {
+    uint16_t* y = static_cast<uint16_t*>(p.lin[li].y);
+    const int64_t ldy = p.lin[li].ldy;
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = 16 * t + 4 * grp + q;
+        if (m < M) y[(int64_t)m * ldy + no] = H::out(acc[0][t][q]);
       }
   }
 }
@@ -844,6 +1052,67 @@ int pick_kw(int64_t N, int64_t K) {
   return w;
 }
 
+// Streaming kernel: K slices per tile from (tiles, K) only, for about 2048 waves per
+// launch while every slice keeps at least four 128-k chunks (two for launches of fewer
+// than 1024 waves).  Two-plane (SwiGLU) waves hold more registers, so their workgroups
+// stop at 8 waves.
+int pick_kw_s(int64_t tiles, int64_t K, int P) {
+  const int64_t chunks = K / 128;
+  const int cap = P == 2 ? 8 : 16;
+  int w = 1;
+  while (w < cap && tiles * w < 2048 && (int64_t)4 * w <= chunks) w *= 2;
+  if (w < cap && tiles * w < 1024 && (int64_t)2 * w <= chunks) w *= 2;
+  return w;
+}
+
+// The streaming kernel addresses every operand with 31-bit buffer offsets.
+bool stream_fits(const QrowParams& q) {
+  if ((int64_t)q.M * q.ldx * 2 >= INT_MAX) return false;
+  for (int i = 0; i < q.n_lin; ++i)
+    if ((int64_t)q.lin[i].N * q.K >= INT_MAX) return false;
+  return true;
+}
+
+// LDS bytes for the activations of the streaming kernel, 0 when they are read from
+// L2: a copy per workgroup pays off while it is small next to the workgroup's weights --
+// up to 25 KB (M <= 8 rows of a 1536-wide layer), or up to 144 KB when the launch has
+// at most one workgroup per CU anyway (few, long tiles such as 1536 x 8960).
+size_t stream_xl_bytes(const QrowParams& q, int blocks) {
+  const size_t b = (size_t)q.M * (size_t)(2 * q.K + 16);
+  if (b <= 25 * 1024) return b;
+  if (blocks <= 256 && b <= 144 * 1024) return b;
+  return 0;
+}
+
+// Returns false (nothing launched) for a plain linear whose activations do not go to LDS.
+template <int P, int MT, int KW, bool F16>
+bool launch_w8a16_s_kw(const QrowParams& p, int blocks, hipStream_t s) {
+  const int64_t per = cdiv(p.K / 128, KW);  // chunks per slice
+  const size_t xl = stream_xl_bytes(p, blocks);
+  if (xl) {
+    hipLaunchKernelGGL((k_w8a16_s<P, MT, KW, 4, F16, true>), dim3(blocks), dim3(KW * 64), xl, s, p);
+    return true;
+  }
+  if constexpr (P == 2) {  // plain linears take the streaming kernel only with LDS activations
+    if (MT == 2 || per <= 2)
+      hipLaunchKernelGGL((k_w8a16_s<P, MT, KW, 2, F16, false>), dim3(blocks), dim3(KW * 64), 0, s, p);
+    else
+      hipLaunchKernelGGL((k_w8a16_s<P, MT, KW, 4, F16, false>), dim3(blocks), dim3(KW * 64), 0, s, p);
+    return true;
+  }
+  return false;
+}
+
+template <int P, int MT, bool F16>
+bool launch_w8a16_s(const QrowParams& p, int blocks, int kw, hipStream_t s) {
+  if (kw == 1) return launch_w8a16_s_kw<P, MT, 1, F16>(p, blocks, s);
+  if (kw == 2) return launch_w8a16_s_kw<P, MT, 2, F16>(p, blocks, s);
+  if (kw == 4) return launch_w8a16_s_kw<P, MT, 4, F16>(p, blocks, s);
+  if (kw == 8) return launch_w8a16_s_kw<P, MT, 8, F16>(p, blocks, s);
+  if constexpr (P == 1) return launch_w8a16_s_kw<P, MT, 16, F16>(p, blocks, s);
+  return false;
+}
+
 template <int P, int MT, int KW, bool F16>
 void launch_w8a16_kw(const QrowParams& p, int blocks, hipStream_t s) {
   const int u = (int)cdiv(p.K / 128, KW);
@@ -1048,8 +1317,19 @@ int run_linears(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool row_st
         blocks += (int)cdiv(q.lin[i].N, 16);
         nmax = q.lin[i].N > nmax ? q.lin[i].N : nmax;
       }
-      const int kw = pick_kw(nmax, q.K);
       const bool f16 = x_dtype == QS_F16;
+      // long rows with LDS-resident activations stream (few tiles, deep K); the rest
+      // keep the round-based kernel, which measured faster for 1536-wide layers
+      if (q.K >= 4096 && stream_fits(q) && stream_xl_bytes(q, blocks)) {
+        const int kw = pick_kw_s(blocks, q.K, 1);
+        bool done;
+        if (mm <= 16)
+          done = f16 ? launch_w8a16_s<1, 1, true>(q, blocks, kw, s) : launch_w8a16_s<1, 1, false>(q, blocks, kw, s);
+        else
+          done = f16 ? launch_w8a16_s<1, 2, true>(q, blocks, kw, s) : launch_w8a16_s<1, 2, false>(q, blocks, kw, s);
+        if (done) continue;
+      }
+      const int kw = pick_kw(nmax, q.K);
       if (mm <= 16)
         f16 ? launch_w8a16<1, 1, true>(q, blocks, kw, s) : launch_w8a16<1, 1, false>(q, blocks, kw, s);
       else
@@ -1188,6 +1468,14 @@ extern "C" int qs_qrow_swiglu(const void* x, int64_t ldx, const int8_t* gate_cod
       q.x = static_cast<const uint16_t*>(x) + m0 * ldx;
       q.lin[0].y = static_cast<uint16_t*>(y) + m0 * ldy;
       const int blocks = (int)cdiv(N, 16);
+      if (stream_fits(q)) {
+        const int kw = pick_kw_s(blocks, K, 2);
+        if (mm <= 16)
+          launch_w8a16_s<2, 1, false>(q, blocks, kw, s);
+        else
+          launch_w8a16_s<2, 2, false>(q, blocks, kw, s);
+        continue;
+      }
       const int kw = pick_kw(N, K);
       if (mm <= 16)
         launch_w8a16<2, 1, false>(q, blocks, kw, s);
