@@ -12,7 +12,8 @@ HIP graph; the timed region replays it K times.
 in/out, 1,315,084,288 B at M=1) / measured time per pass, in GB/s.  ``roofline`` is the
 dominant kernel (the paired gate/up + SwiGLU launch) timed on its own stream with HIP
 events; ``cpu_baseline`` is the reference CPU path (oracle/cpu_path.py) on a bounded
-sample of the same stack on this host's cores.
+sample of the same stack on this host's cores.  ``secondary`` holds the same stack at
+config 2's other batch sizes (M = 4, 16, 32) and configs 1, 3, 4 and 5, never ``value``.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--m 1] [--no-cpu] [--no-secondary]
        python bench.py --profile {swiglu,stack,copy}   (eager launches for counter runs)
@@ -435,9 +436,32 @@ def main() -> int:
         },
     }
     if not args.no_secondary:
+        # config 2's other batch sizes (M = 4, 16, 32): the same resident stack and graph
+        # protocol; M >= 3 runs the MFMA W8A16 kernels
+        batches = {}
+        for mm in (4, 16, 32):
+            if mm == m:
+                continue
+            xb_h = torch.randn(mm, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
+            xb_i = torch.randn(mm, INTER, device=dev, generator=gen).to(torch.bfloat16)
+
+            def pass_m(_i, xh=xb_h, xi=xb_i):
+                for L in pages:
+                    qrow.qrow_matmul_multi([(L[nm].codes, L[nm].scales) for nm in ("q", "k", "v")], xh)
+                    qrow.fused_qrow_matmul(L["o"], xh)
+                    qrow.fused_qrow_swiglu(L["gate"], L["up"], xh)
+                    qrow.fused_qrow_matmul(L["down"], xi)
+
+            tp = _graph_time(torch, stream, pass_m, 1, reps=10)
+            batches[f"config2_stack_m{mm}"] = {
+                "ms_per_pass": round(tp * 1e3, 4),
+                "GB/s": round(algorithmic_bytes_per_pass(mm) / tp / 1e9, 1),
+                "hbm_frac": round(algorithmic_bytes_per_pass(mm) / tp / 1e9 / HBM_PEAK_GBS, 4),
+            }
         paged = paged_measurement(torch, dev, pages, x_h, x_i)
         del arena, pages, graph, sw_graph
-        out["secondary"] = {"config2_paged_pinned_host": paged, **secondary_measurements(torch, dev, stream)}
+        out["secondary"] = {**batches, "config2_paged_pinned_host": paged,
+                            **secondary_measurements(torch, dev, stream)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds, m)
     print(json.dumps(out), flush=True)
