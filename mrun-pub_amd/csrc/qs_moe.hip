@@ -383,7 +383,6 @@ constexpr int kMoeWaves = 8;
 template <int P, int NB>
 struct MoeStreamCfg {
   static constexpr int RW = P == 2 ? 16 : 16 * NB;  // output rows per wave
-  static constexpr int W = 16 / NB;                  // chunks in flight (16 loads per wave)
 };
 
 template <int P, int NB, int MT>
@@ -392,7 +391,10 @@ __global__ __launch_bounds__(kMoeWaves * 64) void k_moe_stream(MoeGemmParams p) 
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int MC = 16 * MT;
   constexpr int NT = kMoeWaves * 64;
-  constexpr int W = MoeStreamCfg<P, NB>::W;
+  // chunks in flight: 4 weight loads per wave for one row tile, 8 for more (a small
+  // window keeps the kernel at 110-160 VGPRs, 3-4 waves per SIMD; 16 loads measured
+  // 3-13% slower at 2 waves per SIMD)
+  constexpr int W = (MT == 1 ? 4 : 8) / NB > 0 ? (MT == 1 ? 4 : 8) / NB : 1;
   constexpr int RW = MoeStreamCfg<P, NB>::RW;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
