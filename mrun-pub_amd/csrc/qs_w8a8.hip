@@ -500,6 +500,86 @@ enum { EPI_I32 = 0, EPI_F32 = 1, EPI_BF16 = 2 };
 constexpr int kBK = 64;        // default k bytes per step; LDS rows padded by 16 bytes
 constexpr int kSideLds = 16;   // side-path columns per LDS staging in the epilogue
 
+// Epilogue shared by the GEMM kernels: scales, the optional fp32 side path and the store.
+// `ws0` is the workgroup's LDS (at least (BM + BN) * (kSideLds + 1) floats), free once the
+// main loop's last barrier has passed.
+template <int BM, int BN, int WM, int WN, int EPI, int NT>
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, i32x16 (&acc)[WM / 32][WN / 32], float* ws0,
+                                              int bm, int bn, int wm, int wn, int tid, int lane) {
+  constexpr int FM = WM / 32, FN = WN / 32;
+  // Epilogue.  The side path (P protected columns, fp32) runs on the matrix cores:
+  // side[32x32 tile] = xs[rows][P] . ws[P][cols] with v_mfma_f32_32x32x2_f32, whose
+  // accumulator layout is the int32 one, so each lane adds side[r] to its own outputs.
+  // Operands go through LDS in chunks of kSideLds columns (zero padded); with
+  // P <= kSideLds one staging serves every tile.
+  const int nsc = (EPI != EPI_I32 && p.P > 0) ? (p.P + kSideLds - 1) / kSideLds : 0;
+  float* xs = ws0;  // [BM][kSideLds]
+  float* ws = xs + BM * kSideLds;                     // [kSideLds][BN]
+  auto stage_side = [&](int q0) {
+    for (int t = tid; t < BM * kSideLds; t += NT) {
+      const int r = t / kSideLds, q = q0 + (t - (t / kSideLds) * kSideLds);
+      xs[t] = (bm + r < p.M && q < p.P) ? p.xp[(int64_t)(bm + r) * p.P + q] : 0.f;
+    }
+    for (int t = tid; t < BN * kSideLds; t += NT) {
+      const int c = t / kSideLds, qq = t - (t / kSideLds) * kSideLds, q = q0 + qq;
+      ws[qq * BN + c] = (bn + c < p.N && q < p.P) ? p.wp[(int64_t)(bn + c) * p.P + q] : 0.f;
+    }
+  };
+  // the block's activation and weight scales, staged once: read per output from LDS
+  // instead of one dependent L2 round trip per output row
+  float* asl = ws + kSideLds * BN;  // [BM]
+  float* bsl = asl + BM;            // [BN]
+  if constexpr (EPI != EPI_I32) {
+    for (int t = tid; t < BM; t += NT) asl[t] = bm + t < p.M ? p.as[bm + t] : 0.f;
+    for (int t = tid; t < BN; t += NT) bsl[t] = bn + t < p.N ? p.bs[bn + t] : 0.f;
+  }
+  if (nsc == 1) stage_side(0);
+  if (EPI != EPI_I32) __syncthreads();
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int lr = wm * WM + 32 * i;  // tile row / column offsets within the block
+      const int lc = wn * WN + 32 * j;
+      f32x16 side = {};
+      for (int c = 0; c < nsc; ++c) {
+        if (nsc > 1) {
+          __syncthreads();
+          stage_side(c * kSideLds);
+          __syncthreads();
+        }
+        const int qn = min(kSideLds, p.P - c * kSideLds);
+        for (int s2 = 0; s2 < qn; s2 += 2) {
+          const float xa = xs[(lr + (lane & 31)) * kSideLds + s2 + (lane >> 5)];
+          const float wb = ws[(s2 + (lane >> 5)) * BN + lc + (lane & 31)];
+          side = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, wb, side, 0, 0, 0);
+        }
+      }
+      const int col = bn + lc + (lane & 31);
+      float bsc = 0.f;
+      if constexpr (EPI != EPI_I32) bsc = bsl[lc + (lane & 31)];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lrow = lr + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int row = bm + lrow;
+        if (row < p.M && col < p.N) {
+          if constexpr (EPI == EPI_I32) {
+            static_cast<int32_t*>(p.c)[(int64_t)row * p.ldc + col] = acc[i][j][r];
+          } else {
+            // reference order: (float(acc) * act_scale) * w_scale, added to the side path
+            float v = mul_rn(mul_rn(static_cast<float>(acc[i][j][r]), asl[lrow]), bsc);
+            if (nsc) v = add_rn(side[r], v);
+            if constexpr (EPI == EPI_F32)
+              static_cast<float*>(p.c)[(int64_t)row * p.ldc + col] = v;
+            else
+              static_cast<uint16_t*>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16_bits(v);
+          }
+        }
+      }
+    }
+}
+
 template <int BM, int BN, int WM, int WN, int EPI, int BK = kBK>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmParams p) {
   constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
@@ -602,77 +682,148 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmPara
     __syncthreads();
   }
 
-  // Epilogue.  The side path (P protected columns, fp32) runs on the matrix cores:
-  // side[32x32 tile] = xs[rows][P] . ws[P][cols] with v_mfma_f32_32x32x2_f32, whose
-  // accumulator layout is the int32 one, so each lane adds side[r] to its own outputs.
-  // Operands go through LDS in chunks of kSideLds columns (zero padded); with
-  // P <= kSideLds one staging serves every tile.
-  const int nsc = (EPI != EPI_I32 && p.P > 0) ? (p.P + kSideLds - 1) / kSideLds : 0;
-  float* xs = reinterpret_cast<float*>(&lds[0][0]);  // [BM][kSideLds]
-  float* ws = xs + BM * kSideLds;                     // [kSideLds][BN]
-  auto stage_side = [&](int q0) {
-    for (int t = tid; t < BM * kSideLds; t += NT) {
-      const int r = t / kSideLds, q = q0 + (t - (t / kSideLds) * kSideLds);
-      xs[t] = (bm + r < p.M && q < p.P) ? p.xp[(int64_t)(bm + r) * p.P + q] : 0.f;
-    }
-    for (int t = tid; t < BN * kSideLds; t += NT) {
-      const int c = t / kSideLds, qq = t - (t / kSideLds) * kSideLds, q = q0 + qq;
-      ws[qq * BN + c] = (bn + c < p.N && q < p.P) ? p.wp[(int64_t)(bn + c) * p.P + q] : 0.f;
-    }
-  };
-  // the block's activation and weight scales, staged once: read per output from LDS
-  // instead of one dependent L2 round trip per output row
-  float* asl = ws + kSideLds * BN;  // [BM]
-  float* bsl = asl + BM;            // [BN]
-  if constexpr (EPI != EPI_I32) {
-    for (int t = tid; t < BM; t += NT) asl[t] = bm + t < p.M ? p.as[bm + t] : 0.f;
-    for (int t = tid; t < BN; t += NT) bsl[t] = bn + t < p.N ? p.bs[bn + t] : 0.f;
+  gemm_epilogue<BM, BN, WM, WN, EPI, NT>(p, acc, reinterpret_cast<float*>(&lds[0][0]), bm, bn, wm, wn, tid, lane);
+}
+
+// LDS row swizzle of the DMA-fed tiles: 16-byte chunk c of tile row r sits in slot
+// c ^ dma_swz(r).  For the 16 consecutive rows one ds_read_b128 pass serves (64 banks)
+// and for the 8 of a 32-bank pass, the slots (with the row's bank phase) are distinct.
+__device__ __forceinline__ int dma_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// One wave's 1 KiB global -> LDS copy: lane l's 16 bytes at buffer offset voff + soff land
+// at dst + 16 l.  Kept out of the kernel template: in template-dependent code the host
+// compilation pass drops the kernel's launch stub over this builtin.
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, int8_t* dst, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
+
+// int8 GEMM with LDS fed by DMA: BM x BN blocks of 8 waves (the tiles of k_gemm_i8:
+// 256 x 256 with 128 x 64 per wave, or 128 x 128 with 64 x 32), 64-byte K steps, a ring
+// of four LDS stages.  Tile kt + 3 is
+// requested (buffer_load ... lds: global memory straight into LDS, 1 KiB per wave
+// instruction) while tile kt is multiplied, so loads have three steps to land and
+// neither staging registers nor ds_write instructions sit in the loop.  A DMA instruction
+// writes its 64 lanes' 16 bytes contiguously, so a wave instruction fills 16 tile rows
+// and the lane -> global chunk map carries the row swizzle.  One barrier per step: each
+// wave waits for its own copies of tile kt (vmcnt), then the barrier makes every wave's
+// copies visible and retires the stage read in step kt - 1, which the next copy reuses.
+// Needs K % 64 == 0, 16-byte aligned rows and 256 * ld < 2^31.
+template <int BM, int BN, int WM, int WN, int EPI>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(GemmParams p) {
+  constexpr int BK = 64, S = 4;
+  constexpr int WAVES_M = BM / WM, NW = WAVES_M * (BN / WN), NT = NW * 64;
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int TILE_A = BM * BK, TILE_B = BN * BK;  // bytes per operand per stage
+  constexpr int STAGE = TILE_A + TILE_B;
+  constexpr int JA = BM / 16 / NW, JB = BN / 16 / NW;  // 1 KiB copies per wave per stage
+  static_assert(JA >= 1 && JB >= 1 && JA * 16 * NW == BM && JB * 16 * NW == BN, "whole copies per wave");
+  static_assert(S * STAGE >= (BM + BN) * (kSideLds + 1) * 4, "epilogue staging needs the tile LDS");
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int G = tiles_m * tiles_n;
+  const int bid = blockIdx.x;
+  int lid = bid;
+  if ((G & 7) == 0) lid = (bid & 7) * (G >> 3) + (bid >> 3);
+  const int tm = lid % tiles_m, tn = lid / tiles_m;
+  const int bm = tm * BM, bn = tn * BN;
+
+  const int64_t arem = (int64_t)(p.M - bm) * p.lda, brem = (int64_t)(p.N - bn) * p.ldb;
+  const int alim = (int)(arem < INT_MAX ? arem : INT_MAX), blim = (int)(brem < INT_MAX ? brem : INT_MAX);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(p.a + (int64_t)bm * p.lda), (short)0, alim, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(p.b + (int64_t)bn * p.ldb), (short)0, blim, 0x00020000);
+  // DMA roles: copy j of this wave covers tile rows 16 * (J * wave + j) + 0..15 of its
+  // operand; lane l lands in row + (l >> 2), slot l & 3, and fetches chunk slot ^ swizzle.
+  int aoff[JA], boff[JB];
+#pragma unroll
+  for (int j = 0; j < JA; ++j) {
+    const int r = 16 * (JA * wave + j) + (lane >> 2);
+    aoff[j] = r * (int)p.lda + 16 * ((lane & 3) ^ dma_swz(r));
   }
-  if (nsc == 1) stage_side(0);
-  if (EPI != EPI_I32) __syncthreads();
-  typedef float f32x16 __attribute__((ext_vector_type(16)));
+#pragma unroll
+  for (int j = 0; j < JB; ++j) {
+    const int r = 16 * (JB * wave + j) + (lane >> 2);
+    boff[j] = r * (int)p.ldb + 16 * ((lane & 3) ^ dma_swz(r));
+  }
+  const int KT = p.K / BK;
+  // rows past M / N read as zero; steps past K load out of the buffer's range (zero, no
+  // memory access) into a stage that is not read again
+  auto dma = [&](int kt) {
+    const bool live = kt < KT;
+    const int ko = live ? kt * BK : 0;
+    int8_t* st = lds + (kt & (S - 1)) * STAGE;
+#pragma unroll
+    for (int j = 0; j < JA; ++j) lds_copy16(rsa, st + 1024 * (JA * wave + j), live ? aoff[j] : alim, ko);
+#pragma unroll
+    for (int j = 0; j < JB; ++j) lds_copy16(rsb, st + TILE_A + 1024 * (JB * wave + j), live ? boff[j] : blim, ko);
+  };
+
+  i32x16 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int lr = wm * WM + 32 * i;  // tile row / column offsets within the block
-      const int lc = wn * WN + 32 * j;
-      f32x16 side = {};
-      for (int c = 0; c < nsc; ++c) {
-        if (nsc > 1) {
-          __syncthreads();
-          stage_side(c * kSideLds);
-          __syncthreads();
-        }
-        const int qn = min(kSideLds, p.P - c * kSideLds);
-        for (int s2 = 0; s2 < qn; s2 += 2) {
-          const float xa = xs[(lr + (lane & 31)) * kSideLds + s2 + (lane >> 5)];
-          const float wb = ws[(s2 + (lane >> 5)) * BN + lc + (lane & 31)];
-          side = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, wb, side, 0, 0, 0);
-        }
-      }
-      const int col = bn + lc + (lane & 31);
-      float bsc = 0.f;
-      if constexpr (EPI != EPI_I32) bsc = bsl[lc + (lane & 31)];
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lrow = lr + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int row = bm + lrow;
-        if (row < p.M && col < p.N) {
-          if constexpr (EPI == EPI_I32) {
-            static_cast<int32_t*>(p.c)[(int64_t)row * p.ldc + col] = acc[i][j][r];
-          } else {
-            // reference order: (float(acc) * act_scale) * w_scale, added to the side path
-            float v = mul_rn(mul_rn(static_cast<float>(acc[i][j][r]), asl[lrow]), bsc);
-            if (nsc) v = add_rn(side[r], v);
-            if constexpr (EPI == EPI_F32)
-              static_cast<float*>(p.c)[(int64_t)row * p.ldc + col] = v;
-            else
-              static_cast<uint16_t*>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16_bits(v);
-          }
-        }
-      }
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  // fragment rows are 32-aligned bases + (lane & 31), so one swizzle serves them all
+  const int sl = dma_swz(lane & 31);
+  const int arow = (wm * WM + (lane & 31)) * BK, brow = TILE_A + (wn * WN + (lane & 31)) * BK;
+
+  static_assert(BK == 64, "the loop below takes two 32-byte slices per step");
+  auto frag = [&](i32x4 (&f)[FM + FN], int kt, int ks) {
+    const int8_t* st = lds + (kt & (S - 1)) * STAGE;
+    const int co = 16 * ((2 * ks + (lane >> 5)) ^ sl);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) f[i] = *reinterpret_cast<const i32x4*>(st + arow + 32 * BK * i + co);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) f[FM + j] = *reinterpret_cast<const i32x4*>(st + brow + 32 * BK * j + co);
+  };
+  auto mma = [&](const i32x4 (&f)[FM + FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[i], f[FM + j], acc[i][j], 0, 0, 0);
+  };
+  // Step kt: read slice 1 of tile kt, multiply slice 0 (read one step earlier), then the
+  // barrier for tile kt + 1 -- this wave's copies of kt + 1 done (vmcnt) and its reads of
+  // tile kt done (lgkmcnt), so the stage may be refilled -- the copy of tile kt + 4, the
+  // reads of slice 0 of tile kt + 1, and the MFMAs of slice 1 of tile kt, which cover the
+  // barrier and those reads.
+  i32x4 fa[FM + FN], fb[FM + FN];
+  dma(0);
+  dma(1);
+  dma(2);
+  constexpr int NEWER = 2 * (JA + JB);  // this wave's copies of the two newer stages
+  static_assert(NEWER == 8 || NEWER == 4, "wait counts below");
+  if constexpr (NEWER == 8)
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+  dma(3);
+  frag(fa, 0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    frag(fb, kt, 1);
+    mma(fa);
+    if (kt + 1 < KT) {
+      if constexpr (NEWER == 8)
+        asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      dma(kt + 4);
+      frag(fa, kt + 1, 0);
     }
+    mma(fb);
+  }
+  // every copy (including the ones past K) has landed before the epilogue reuses LDS
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  gemm_epilogue<BM, BN, WM, WN, EPI, NT>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn, tid, lane);
 }
 
 // Any shape: one thread per output, exact int32 accumulation.
@@ -705,6 +856,11 @@ namespace {
 // Tile shapes (measured on MI355X, 14336 x 4096 weights): 256 x 256 blocks of 8 waves
 // (128 x 64 each) for large products, 128 x 128 blocks of 8 waves (64 x 32) otherwise;
 // 128-byte K steps when K allows, else 64.
+#ifndef QS_GEMM_DMA
+#define QS_GEMM_DMA 1
+#endif
+constexpr bool kGemmDma = QS_GEMM_DMA != 0;  // large products take k_gemm_i8_dma
+
 template <int EPI, int BK>
 void launch_gemm_bk(const GemmParams& p, hipStream_t s) {
   const bool big = (int64_t)p.M * p.N >= (int64_t)1024 * 8192;
@@ -721,6 +877,19 @@ void launch_gemm_bk(const GemmParams& p, hipStream_t s) {
 
 template <int EPI>
 void launch_gemm(const GemmParams& p, hipStream_t s) {
+  const bool big = (int64_t)p.M * p.N >= (int64_t)1024 * 8192;
+  const bool dma_ok = p.K % 64 == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned(p.a, 16) &&
+                      aligned(p.b, 16) && 256 * p.lda < INT_MAX && 256 * p.ldb < INT_MAX;
+  if (kGemmDma && dma_ok) {
+    if (big) {
+      const int G = (int)(cdiv(p.M, 256) * cdiv(p.N, 256));
+      hipLaunchKernelGGL((k_gemm_i8_dma<256, 256, 128, 64, EPI>), dim3(G), dim3(512), 0, s, p);
+    } else {
+      const int G = (int)(cdiv(p.M, 128) * cdiv(p.N, 128));
+      hipLaunchKernelGGL((k_gemm_i8_dma<128, 128, 64, 32, EPI>), dim3(G), dim3(512), 0, s, p);
+    }
+    return;
+  }
   if (p.K % 128 == 0) launch_gemm_bk<EPI, 128>(p, s);
   else launch_gemm_bk<EPI, 64>(p, s);
 }
