@@ -11,7 +11,7 @@
 //                       the reference's stable argsort and is identical on every call.
 //   k_moe_gather_quant: per routed row, int8 per-token quantization of source[token_ids[a]]
 //                       (the W8A8 recipe: s = max|x|/127, 0 -> 1; rint; clamp +-127).
-//   k_moe_stream<...> : one workgroup per (group, 8 waves of output rows).  The group's
+//   k_moe_stream<...> : one workgroup per (group, 8 or 4 waves of output rows).  The group's
 //                       routed rows (up to 16*MT at a time) are staged once in LDS; each
 //                       wave streams its weight rows (16 rows of gate and up for SwiGLU,
 //                       16-64 rows otherwise) over the full K through a window of 64-byte
@@ -378,7 +378,10 @@ __global__ __launch_bounds__(P * KW * 64) void k_moe_gemm(MoeGemmParams p) {
 // distinct banks).  The chunk loads run W chunks ahead of the MFMAs, issued in k order;
 // slots past the last chunk reload it (static wait counts).  Staged rows past the
 // group's count hold stale LDS data: their MFMA columns are never stored.
-constexpr int kMoeWaves = 8;
+// waves per workgroup: 8 for SwiGLU (gate/up), 4 for plain products (more workgroups per
+// CU; the T=512 down projection 80 -> 74 us, while gate/up is fastest at 8)
+template <int P>
+constexpr int kMoeWaves = P == 2 ? 8 : 4;
 
 template <int P, int NB>
 struct MoeStreamCfg {
@@ -386,11 +389,11 @@ struct MoeStreamCfg {
 };
 
 template <int P, int NB, int MT>
-__global__ __launch_bounds__(kMoeWaves * 64) void k_moe_stream(MoeGemmParams p) {
+__global__ __launch_bounds__(kMoeWaves<P> * 64) void k_moe_stream(MoeGemmParams p) {
   static_assert(P == 1 || NB == 2, "SwiGLU streams the gate and up tiles of one row block");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int MC = 16 * MT;
-  constexpr int NT = kMoeWaves * 64;
+  constexpr int NT = kMoeWaves<P> * 64;
   // chunks in flight: 4 weight loads per wave for one row tile, 8 for more (a small
   // window keeps the kernel at 110-160 VGPRs, 3-4 waves per SIMD; 16 loads measured
   // 3-13% slower at 2 waves per SIMD)
@@ -408,7 +411,7 @@ __global__ __launch_bounds__(kMoeWaves * 64) void k_moe_stream(MoeGemmParams p) 
   const int xstride = K + 16;
   int8_t* xs = reinterpret_cast<int8_t*>(lds);                 // [MC][K + 16]
   float* asl = reinterpret_cast<float*>(lds + MC * xstride);   // [MC]
-  const int n0 = (blockIdx.x * kMoeWaves + wave) * RW;
+  const int n0 = (blockIdx.x * kMoeWaves<P> + wave) * RW;
   const bool live = n0 < p.N;
   const int8_t* wexp = p.w + (int64_t)slot * p.w_stride;
   const int8_t* wr[NB];
@@ -631,7 +634,7 @@ size_t moe_stream_lds(int MT, int64_t K) {
 template <int P, int NB>
 void launch_moe_stream(const MoeGemmParams& p, int G, int MT, hipStream_t s) {
   constexpr int RW = MoeStreamCfg<P, NB>::RW;
-  const dim3 grid((unsigned)cdiv(p.N, RW * kMoeWaves), (unsigned)G), block(kMoeWaves * 64);
+  const dim3 grid((unsigned)cdiv(p.N, RW * kMoeWaves<P>), (unsigned)G), block(kMoeWaves<P> * 64);
   const size_t lds = moe_stream_lds(MT, p.K);
   if (MT == 4) hipLaunchKernelGGL((k_moe_stream<P, NB, 4>), grid, block, lds, s, p);
   else if (MT == 2) hipLaunchKernelGGL((k_moe_stream<P, NB, 2>), grid, block, lds, s, p);
