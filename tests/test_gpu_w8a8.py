@@ -28,7 +28,21 @@ def _weights(out, inn, seed):
     return rng, q_w, sc_w
 
 
-@pytest.mark.parametrize("t,n,k", [(512, 1024, 4096), (96, 640, 384), (7, 33, 80), (5, 3, 4), (300, 256, 192)])
+@pytest.mark.parametrize(
+    "t,n,k",
+    [
+        (512, 1024, 4096),
+        (96, 640, 384),
+        (7, 33, 80),
+        (5, 3, 4),
+        (300, 256, 192),
+        # DMA-fed kernel edges: one and two 64-byte K steps (the copy ring runs past K),
+        # and the 256 x 256 tiles with ragged M and N
+        (40, 200, 64),
+        (260, 130, 128),
+        (1030, 8200, 64),
+    ],
+)
 def test_int8_gemm_int32_bit_exact(dev, t, n, k):
     rng = np.random.default_rng(t + n + k)
     qx = rng.integers(-128, 128, size=(t, k), dtype=np.int8)
