@@ -67,7 +67,9 @@ def test_matmul_fp32(dev, m, n, k):
 
 
 @pytest.mark.parametrize("m", [1, 4, 16, 32, 37])
-@pytest.mark.parametrize("n,k", [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (100, 192), (24, 40)])
+@pytest.mark.parametrize(
+    "n,k", [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (1000, 4096), (100, 192), (24, 40)]
+)
 def test_matmul_bf16_w8a16(dev, m, n, k):
     rng, codes, scales = _case(n, k, seed=m * 31 + n + k)
     x = oq.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
@@ -136,8 +138,8 @@ def test_multi_linear_equals_individual(dev):
         assert torch.allclose(o.float(), single.float(), rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("m", [1, 4, 32])
-@pytest.mark.parametrize("n,k", [(8960, 1536), (96, 64), (5, 4)])
+@pytest.mark.parametrize("m", [1, 4, 16, 32])
+@pytest.mark.parametrize("n,k", [(8960, 1536), (1000, 1536), (200, 128), (96, 64), (5, 4)])
 def test_swiglu(dev, m, n, k):
     rng = np.random.default_rng(m + n)
     gq = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
