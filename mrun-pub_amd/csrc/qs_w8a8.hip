@@ -5,7 +5,8 @@
 //   k_act_quant      : per row, s = max|x*keep| / 127 (0 -> 1), q = clamp(rint(x*keep / s))
 //                      -- one IEEE fp32 multiply/divide per element, round-half-even, the
 //                      exact recipe of the reference (bit-exact codes and scales).
-//   k_col_absmax     : max over rows of |x[:, k]| (outlier column detection).
+//   k_col_absmax(_rows): max over rows of |x[:, k]| (outlier column detection; one pass
+//                      without atomics for M <= 1024).
 //   k_topk           : the k largest column maxima (ties -> lower column index).
 //   k_gather_side    : xp[m, p] = x[m, idx[p]], wp[n, p] = float(qw[n, idx[p]]) * sw[n].
 //   k_gemm_i8<...>   : C = A[M,K] . B[N,K]^T with v_mfma_i32_32x32x32_i8, 128/64-byte K
@@ -68,22 +69,25 @@ __global__ __launch_bounds__(256) void k_act_quant(const void* __restrict__ x, i
   }
 }
 
-// One wave per row with the row held in registers between the max pass and the quantize
-// pass: lane l owns the 16-byte chunks l, l + 64, ... of the row (each wave instruction
-// reads 1 KiB contiguous).  Same arithmetic, element by element, as k_act_quant.
+// WPR waves per row (1, or 4 for short batches) with the row held in registers between
+// the max pass and the quantize pass: lane l of the row's wave wr owns the 16-byte chunks
+// (c * WPR + wr) * 64 + l (each wave instruction reads 1 KiB contiguous); the waves'
+// maxima meet in LDS.  Same arithmetic, element by element, as k_act_quant.
 // Requires K % E == 0, 16-byte aligned rows of x and keep, 8/4-byte aligned rows of q
-// and K <= 64 * CPL * E.
-template <int XT, int CPL>
+// and K <= 64 * WPR * CPL * E.
+template <int XT, int CPL, int WPR>
 __global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x, int64_t ldx,
                                                      const float* __restrict__ keep,
                                                      int8_t* __restrict__ q, int64_t ldq,
                                                      float* __restrict__ scale, int M, int K) {
   constexpr int ES = XT == QS_F32 ? 4 : 2;
   constexpr int E = 16 / ES;  // elements per 16-byte chunk
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= M) return;
-  const char* xr = static_cast<const char*>(x) + (int64_t)row * ldx * ES;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // WPR waves share a row: wave wr of the row takes chunks (c * WPR + wr) * 64 + lane
+  const int row = blockIdx.x * (4 / WPR) + wave / WPR, wr = wave % WPR;
+  const bool live = row < M;
+  if (WPR == 1 && !live) return;
+  const char* xr = static_cast<const char*>(x) + (int64_t)(live ? row : 0) * ldx * ES;
   const int nch = K / E;
   i32x4 v[CPL];
   float amax = 0.f;
@@ -98,8 +102,8 @@ __global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x,
   auto keep4 = [&](int ch, int h) -> f32x4 { return reinterpret_cast<const f32x4*>(keep + ch * E)[h]; };
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    const int ch = c * 64 + lane;
-    if (ch < nch) {
+    const int ch = (c * WPR + wr) * 64 + lane;
+    if (live && ch < nch) {
       v[c] = *reinterpret_cast<const i32x4*>(xr + (int64_t)ch * 16);
       if (keep) {
 #pragma unroll
@@ -115,13 +119,21 @@ __global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x,
     }
   }
   amax = wave_max(amax);
+  if constexpr (WPR > 1) {  // max is exact in any order
+    __shared__ float wmax[4];
+    if (lane == 0) wmax[wave] = amax;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < WPR; ++j) amax = fmaxf(amax, wmax[(wave / WPR) * WPR + j]);
+    if (!live) return;
+  }
   float s = amax / 127.0f;  // IEEE division
   if (s == 0.f) s = 1.f;
-  if (lane == 0) scale[row] = s;
+  if (lane == 0 && wr == 0) scale[row] = s;
   int8_t* qr = q + (int64_t)row * ldq;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
-    const int ch = c * 64 + lane;
+    const int ch = (c * WPR + wr) * 64 + lane;
     if (ch < nch) {
       uint32_t packed[E / 4];
 #pragma unroll
@@ -167,6 +179,35 @@ __global__ __launch_bounds__(256) void k_col_absmax(const void* __restrict__ x, 
   // non-negative floats order like their bit patterns: an integer max is the float max,
   // exact and independent of the order in which the row blocks arrive
   atomicMax(reinterpret_cast<unsigned int*>(part) + k, __float_as_uint(r));
+}
+
+// Column maxima in one pass for short batches: workgroup bx covers 64 columns with 16
+// row groups (rows g, g + 16, ...), combined through LDS; writes colmax[k] directly, so
+// no zero fill and no atomics.
+template <int XT>
+__global__ __launch_bounds__(1024) void k_col_absmax_rows(const void* __restrict__ x, int64_t ldx,
+                                                          int M, int K, float* __restrict__ colmax) {
+  __shared__ float red[16][64];
+  const int c = blockIdx.x * 64 + (threadIdx.x & 63), g = threadIdx.x >> 6;
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (c < K) {
+    int m = g;
+    for (; m + 7 * 16 < M; m += 8 * 16) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[j] = fmaxf(a[j], fabsf(load_x<XT>(x, (int64_t)(m + 16 * j) * ldx + c)));
+    }
+    for (; m < M; m += 16) a[0] = fmaxf(a[0], fabsf(load_x<XT>(x, (int64_t)m * ldx + c)));
+  }
+  float r = a[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) r = fmaxf(r, a[j]);
+  red[g][threadIdx.x & 63] = r;
+  __syncthreads();
+  if (g == 0 && c < K) {
+#pragma unroll
+    for (int j = 1; j < 16; ++j) r = fmaxf(r, red[j][threadIdx.x]);
+    colmax[c] = r;
+  }
 }
 
 __global__ __launch_bounds__(256) void k_fill_zero(float* __restrict__ p, int n) {
@@ -939,13 +980,25 @@ extern "C" int qs_act_quant_i8(const void* x, int x_dtype, int64_t ldx, const fl
                          K / E <= 64 * kQuantCpl && aligned(x, 16) && (ldx * es) % 16 == 0 &&
                          (!keep || aligned(keep, 16)) && aligned(q, E == 8 ? 8 : 4);
   if (wave_path) {
+    // up to 4096 rows, four waves share a row (more waves in flight: M=512 7.2 -> 5.0 us,
+    // M=2048 9.7 -> 8.4 us)
+    if (M <= 4096 && K / E <= 4 * 64 * (kQuantCpl / 4)) {
+      const dim3 grid((unsigned)M);
+      if (x_dtype == QS_F32)
+        hipLaunchKernelGGL((k_act_quant_w<QS_F32, kQuantCpl / 4, 4>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
+      else if (x_dtype == QS_BF16)
+        hipLaunchKernelGGL((k_act_quant_w<QS_BF16, kQuantCpl / 4, 4>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
+      else
+        hipLaunchKernelGGL((k_act_quant_w<QS_F16, kQuantCpl / 4, 4>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
+      return hip_check(hipGetLastError(), "k_act_quant_w launch");
+    }
     const dim3 grid((unsigned)cdiv(M, 4));
     if (x_dtype == QS_F32)
-      hipLaunchKernelGGL((k_act_quant_w<QS_F32, kQuantCpl>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
+      hipLaunchKernelGGL((k_act_quant_w<QS_F32, kQuantCpl, 1>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
     else if (x_dtype == QS_BF16)
-      hipLaunchKernelGGL((k_act_quant_w<QS_BF16, kQuantCpl>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
+      hipLaunchKernelGGL((k_act_quant_w<QS_BF16, kQuantCpl, 1>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
     else
-      hipLaunchKernelGGL((k_act_quant_w<QS_F16, kQuantCpl>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
+      hipLaunchKernelGGL((k_act_quant_w<QS_F16, kQuantCpl, 1>), grid, dim3(256), 0, s, x, ldx, keep, q, K, scale, (int)M, (int)K);
     return hip_check(hipGetLastError(), "k_act_quant_w launch");
   }
   if (x_dtype == QS_F32)
@@ -966,17 +1019,28 @@ extern "C" int qs_outlier_topk(const void* x, int x_dtype, int64_t ldx, int64_t 
   if (k < 1 || k > 64 || k > K) return fail(QS_ERR_LIMIT, "outlier_topk: k must be in 1..min(64, K)");
   if (M > (int64_t)65535 * 64) return fail(QS_ERR_LIMIT, "outlier_topk: too many rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int parts = (int)cdiv(M, 64);
-  const dim3 grid((unsigned)cdiv(K, 256), (unsigned)parts);
-  hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, s, colmax, (int)K);
-  if (x_dtype == QS_F32)
-    hipLaunchKernelGGL(k_col_absmax<QS_F32>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
-  else if (x_dtype == QS_BF16)
-    hipLaunchKernelGGL(k_col_absmax<QS_BF16>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
-  else if (x_dtype == QS_F16)
-    hipLaunchKernelGGL(k_col_absmax<QS_F16>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
-  else
+  if (x_dtype != QS_F32 && x_dtype != QS_BF16 && x_dtype != QS_F16)
     return fail(QS_ERR_INVALID, "outlier_topk: dtype must be F32, BF16 or F16");
+  if (M <= 1024) {
+    // one pass, one launch: up to 64 rows per thread
+    const dim3 grid((unsigned)cdiv(K, 64));
+    if (x_dtype == QS_F32)
+      hipLaunchKernelGGL(k_col_absmax_rows<QS_F32>, grid, dim3(1024), 0, s, x, ldx, (int)M, (int)K, colmax);
+    else if (x_dtype == QS_BF16)
+      hipLaunchKernelGGL(k_col_absmax_rows<QS_BF16>, grid, dim3(1024), 0, s, x, ldx, (int)M, (int)K, colmax);
+    else
+      hipLaunchKernelGGL(k_col_absmax_rows<QS_F16>, grid, dim3(1024), 0, s, x, ldx, (int)M, (int)K, colmax);
+  } else {
+    const int parts = (int)cdiv(M, 64);
+    const dim3 grid((unsigned)cdiv(K, 256), (unsigned)parts);
+    hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)cdiv(K, 256)), dim3(256), 0, s, colmax, (int)K);
+    if (x_dtype == QS_F32)
+      hipLaunchKernelGGL(k_col_absmax<QS_F32>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
+    else if (x_dtype == QS_BF16)
+      hipLaunchKernelGGL(k_col_absmax<QS_BF16>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
+    else
+      hipLaunchKernelGGL(k_col_absmax<QS_F16>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
+  }
   if (K <= 1024 * kRadixVpt)
     hipLaunchKernelGGL(k_topk_radix, dim3(1), dim3(1024), 0, s, colmax, (int)K, k, idx, keep);
   else
