@@ -413,6 +413,84 @@ __device__ __forceinline__ void hist_add_wave(unsigned* hist, bool active, unsig
   if ((act >> lane) & 1ull) atomicAdd(&hist[bin], 1u);
 }
 
+// One step of a wave-wide 64-bit maximum through DPP: lanes whose source lane is outside
+// the pattern (or whose row is masked off) keep their own value.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ unsigned long long dpp_max_u64(unsigned long long v) {
+  const int lo = (int)(unsigned)v, hi = (int)(unsigned)(v >> 32);
+  const unsigned olo = (unsigned)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWS, 0xf, false);
+  const unsigned ohi = (unsigned)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWS, 0xf, false);
+  const unsigned long long o = ((unsigned long long)ohi << 32) | olo;
+  return o > v ? o : v;
+}
+
+// Maximum over the wave, returned to every lane: row_shr 1, 2, 4, 8 leave each 16-lane
+// row's maximum in its lane 15; row_bcast 15 (rows 1, 3) and row_bcast 31 (rows 2, 3)
+// carry it to lane 63, which is read back as a scalar.
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+  v = dpp_max_u64<0x111, 0xf>(v);
+  v = dpp_max_u64<0x112, 0xf>(v);
+  v = dpp_max_u64<0x114, 0xf>(v);
+  v = dpp_max_u64<0x118, 0xf>(v);
+  v = dpp_max_u64<0x142, 0xa>(v);
+  v = dpp_max_u64<0x143, 0xc>(v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, 63);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), 63);
+  return ((unsigned long long)hi << 32) | lo;
+}
+
+// Small k (kk <= 16): the same 64-bit keys as k_topk_radix ((value bits << 32) | ~column:
+// larger value first, lower column on ties; keys are unique).  Each wave selects its own
+// top kk by kk rounds of a wave-wide maximum (the winning key is cleared in its lane),
+// then wave 0 selects the final kk from the 16 waves' candidates the same way: two
+// barriers instead of the radix select's eight passes.  Emits idx in descending key order
+// and the keep mask.
+template <int VPT>
+__global__ __launch_bounds__(1024) void k_topk_small(const float* __restrict__ vals, int K, int kk,
+                                                     int64_t* __restrict__ idx, float* __restrict__ keep) {
+  __shared__ unsigned long long cand[16 * 16];
+  __shared__ unsigned long long sel[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  unsigned long long key[VPT];
+#pragma unroll
+  for (int e = 0; e < VPT; ++e) {
+    const int k = tid + 1024 * e;
+    key[e] = k < K ? (((unsigned long long)__float_as_uint(vals[k]) << 32) | (unsigned)(~(unsigned)k)) : 0ull;
+    if (k < K) keep[k] = 1.f;
+  }
+  auto wave_top = [&](unsigned long long* keys, int n, int r) {
+    unsigned long long best = 0ull;
+    for (int e = 0; e < n; ++e) best = keys[e] > best ? keys[e] : best;
+    best = wave_max_u64(best);
+    for (int e = 0; e < n; ++e)
+      if (keys[e] == best) keys[e] = 0ull;
+    (void)r;
+    return best;
+  };
+  for (int r = 0; r < kk; ++r) {
+    const unsigned long long b = wave_top(key, VPT, r);
+    if (lane == 0) cand[wave * 16 + r] = b;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    unsigned long long c[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = lane + 64 * j;  // candidate (wave i / 16, rank i % 16)
+      c[j] = (i % 16) < kk ? cand[i] : 0ull;
+    }
+    for (int r = 0; r < kk; ++r) {
+      const unsigned long long b = wave_top(c, 4, r);
+      if (lane == 0) {
+        sel[r] = b;
+        idx[r] = (int64_t)(~(unsigned)(b & 0xffffffffull));
+      }
+    }
+  }
+  __syncthreads();  // every keep = 1 store precedes the zeros
+  if (tid < kk) keep[~(unsigned)(sel[tid] & 0xffffffffull)] = 0.f;
+}
+
 __global__ __launch_bounds__(1024) void k_topk_radix(const float* __restrict__ vals, int K, int kk,
                                                      int64_t* __restrict__ idx, float* __restrict__ keep) {
   __shared__ unsigned hist[256];
@@ -1041,7 +1119,11 @@ extern "C" int qs_outlier_topk(const void* x, int x_dtype, int64_t ldx, int64_t 
     else
       hipLaunchKernelGGL(k_col_absmax<QS_F16>, grid, dim3(256), 0, s, x, ldx, (int)M, (int)K, colmax);
   }
-  if (K <= 1024 * kRadixVpt)
+  if (k <= 16 && K <= 1024 * 4)
+    hipLaunchKernelGGL(k_topk_small<4>, dim3(1), dim3(1024), 0, s, colmax, (int)K, k, idx, keep);
+  else if (k <= 16 && K <= 1024 * 16)
+    hipLaunchKernelGGL(k_topk_small<16>, dim3(1), dim3(1024), 0, s, colmax, (int)K, k, idx, keep);
+  else if (K <= 1024 * kRadixVpt)
     hipLaunchKernelGGL(k_topk_radix, dim3(1), dim3(1024), 0, s, colmax, (int)K, k, idx, keep);
   else
     hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), 0, s, colmax, (int)K, 1, k, idx, keep);

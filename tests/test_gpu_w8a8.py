@@ -81,14 +81,18 @@ def test_act_quant_bit_exact(dev, dtype, t, k):
         assert np.array_equal(s.cpu().numpy().view(np.uint32), sr.view(np.uint32))
 
 
-@pytest.mark.parametrize("t,k,kk", [(64, 4096, 8), (130, 512, 4), (3, 20000, 5), (1, 64, 64), (700, 1000, 13)])
+@pytest.mark.parametrize(
+    "t,k,kk",
+    [(64, 4096, 8), (130, 512, 4), (3, 20000, 5), (1, 64, 64), (700, 1000, 13), (9, 12000, 16), (2, 4097, 16),
+     (4, 70, 16), (1, 16, 16), (33, 16384, 17)],
+)
 def test_outlier_topk_matches_oracle(dev, t, k, kk):
     from mrun_pub_amd import _native as nat
 
     rng = np.random.default_rng(t + k)
     x = rng.standard_normal((t, k)).astype(np.float32)
     x[:, rng.permutation(k)[: kk // 2 + 1]] *= 50.0
-    x[0, 1] = x[0, 2] = x[-1, 40] = 1000.0  # ties resolve to the lower column
+    x[0, 1] = x[0, 2] = x[-1, min(40, k - 1)] = 1000.0  # ties resolve to the lower column
     xd = torch.from_numpy(x).to(dev)
     colmax = torch.empty(k, dtype=torch.float32, device=dev)
     idx = torch.empty(kk, dtype=torch.int64, device=dev)
@@ -101,6 +105,22 @@ def test_outlier_topk_matches_oracle(dev, t, k, kk):
     kref[ref] = 0.0
     assert np.array_equal(keep.cpu().numpy(), kref)
     assert np.array_equal(colmax.cpu().numpy(), np.abs(x).max(axis=0))
+
+
+@pytest.mark.parametrize("k,kk", [(4096, 8), (10000, 16), (300, 3)])
+def test_outlier_topk_all_ties(dev, k, kk):
+    """Every column has the same maximum: the lowest kk column indices, in order."""
+    from mrun_pub_amd import _native as nat
+
+    x = np.ones((3, k), np.float32)
+    xd = torch.from_numpy(x).to(dev)
+    colmax = torch.empty(k, dtype=torch.float32, device=dev)
+    idx = torch.empty(kk, dtype=torch.int64, device=dev)
+    keep = torch.empty(k, dtype=torch.float32, device=dev)
+    nat.call("qs_outlier_topk", nat.ptr(xd), nat.QS_F32, k, 3, k, kk, nat.ptr(colmax), nat.ptr(idx),
+             nat.ptr(keep), nat.stream_of(dev))
+    assert idx.cpu().numpy().tolist() == list(range(kk)) == ow.protect_topk(x, kk).tolist()
+    assert keep.cpu().numpy()[:kk].sum() == 0 and keep.cpu().numpy()[kk:].min() == 1.0
 
 
 @pytest.mark.parametrize("t", [1, 17, 512])
