@@ -385,7 +385,12 @@ __global__ __launch_bounds__(256) void k_lowbit_slot(LowbitParams p, int gps, fl
 // kernels) and meet the activations in v_dot2_f32_bf16; per piece
 //   y += scale * (R_piece - (OFF + zero) * S_piece),   S_piece = sum of x over the piece,
 // which sums to the per-group formula because a piece never straddles a group.  The
-// activations and the per-piece sums live in LDS, one copy per workgroup.
+// activations and the per-piece sums live in LDS, one copy per workgroup.  The activations
+// are stored piece-transposed: 16-byte chunk v of piece c of row m sits at chunk
+// (m * CH + v) * 64J + c (CH chunks per piece, pieces padded to 64J), so the 64 lanes of
+// a wave (64 consecutive pieces) read 64 consecutive chunks -- with pieces laid end to
+// end, lane strides of 64 or 128 bytes put every lane of a 16-byte read on the same few
+// banks -- and each read is a per-lane base plus a constant offset.
 // ----------------------------------------------------------------------------------
 constexpr int kValuThreads = 512;  // 8 waves: one staged copy of x serves 8 row streams
 // activation rows taken by the VALU kernel: its dot work grows with M while the unpack
@@ -411,15 +416,17 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int K = p.K, M = p.M;
   const int npc = K / C::CPL;  // pieces per row
-  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);                                           // [MB][K]
-  float* ps = reinterpret_cast<float*>(lds + (((size_t)MB * K * 2 + 15) & ~(size_t)15));     // [MB][npc]
+  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);                                  // [MB][CH][PS] chunks
+  constexpr int CH = C::CPL / 8;  // 16-byte activation chunks per piece
+  constexpr int PS = 64 * J;      // piece stride of the transposed activations (>= npc)
+  float* ps = reinterpret_cast<float*>(lds + (size_t)MB * CH * PS * 16);                   // [MB][npc]
 
   // wave-uniform row stream (scalar registers): rows wave_id + i * nwaves
   const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * W + (tid >> 6));
   const int nwaves = gridDim.x * W;
   const int ng = p.ng;
   // per-lane constants: piece j of this lane, its byte offset, scale index, LDS offsets
-  int poff[J], pgrp[J], pxo[J];
+  int poff[J], pgrp[J], ppc[J];
   bool pval[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
@@ -428,7 +435,7 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
     const int pcc = pval[j] ? pc : npc - 1;
     poff[j] = pcc * C::LB;
     pgrp[j] = pcc * C::CPL / G;
-    pxo[j] = pcc * C::CPL;
+    ppc[j] = pcc;
   }
 
   constexpr int R = 1;  // rows per register batch
@@ -467,6 +474,11 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
   // codes in flight behind them (short rows keep the registers for occupancy instead)
   constexpr int kXRegs = J >= 3 ? 6 : 0;
   const int x16 = M * (K / 8);
+  // LDS chunk of activation chunk q (row-major order of x)
+  auto xpos = [&](int q) {
+    const int m = q / (K / 8), c = q - m * (K / 8);
+    return (m * CH + c % CH) * PS + c / CH;
+  };
   i32x4 xr[kXRegs > 0 ? kXRegs : 1];
 #pragma unroll
   for (int i = 0; i < kXRegs; ++i) {
@@ -481,19 +493,19 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
 #pragma unroll
   for (int i = 0; i < kXRegs; ++i) {
     const int q = tid + i * kValuThreads;
-    if (q < x16) reinterpret_cast<i32x4*>(xs)[q] = xr[i];
+    if (q < x16) reinterpret_cast<i32x4*>(xs)[xpos(q)] = xr[i];
   }
   for (int q = tid + kXRegs * kValuThreads; q < x16; q += kValuThreads) {
     const int m = q / (K / 8), c = q - (q / (K / 8)) * (K / 8);
-    reinterpret_cast<i32x4*>(xs)[q] = *reinterpret_cast<const i32x4*>(p.x + (int64_t)m * p.ldx + c * 8);
+    reinterpret_cast<i32x4*>(xs)[xpos(q)] = *reinterpret_cast<const i32x4*>(p.x + (int64_t)m * p.ldx + c * 8);
   }
   __syncthreads();
   for (int q = tid; q < M * npc; q += kValuThreads) {
     const int m = q / npc, c = q - (q / npc) * npc;
-    const i32x4* xp = reinterpret_cast<const i32x4*>(xs + m * K + c * C::CPL);
+    const i32x4* xp = reinterpret_cast<const i32x4*>(xs) + m * CH * PS + c;
     float t = 0.f;
-    for (int v = 0; v < C::CPL / 8; ++v) {
-      const i32x4 d = xp[v];
+    for (int v = 0; v < CH; ++v) {
+      const i32x4 d = xp[v * PS];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         t += bf16_bits_to_f32(static_cast<uint32_t>(d[e]) & 0xffffu);
@@ -534,7 +546,7 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
 #pragma unroll
           for (int m = 0; m < MB; ++m) {
             if (m < M) {
-              const i32x4 xv = *reinterpret_cast<const i32x4*>(xs + m * K + pxo[j] + 8 * v);
+              const i32x4 xv = reinterpret_cast<const i32x4*>(xs)[(m * CH + v) * PS + ppc[j]];
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 // copy the element out first: bit-casting a vector element expression reads
@@ -548,7 +560,7 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
         }
 #pragma unroll
         for (int m = 0; m < MB; ++m)
-          if (m < M) acc[m] = fmaf(rs[b][i][j], fmaf(-rz[b][i][j], ps[m * npc + pxo[j] / C::CPL], r[m]), acc[m]);
+          if (m < M) acc[m] = fmaf(rs[b][i][j], fmaf(-rz[b][i][j], ps[m * npc + ppc[j]], r[m]), acc[m]);
       }
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
@@ -755,8 +767,8 @@ extern "C" int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uin
     const int J = (int)cdiv(cdiv(K, cpl), 64);
     // activation rows per launch: the next power of two >= M, halved until x and the piece
     // sums fit the LDS budget; larger M runs as several launches
-    auto lds_for = [&](int mbx) {
-      return (((size_t)mbx * K * 2 + 15) & ~(size_t)15) + (size_t)mbx * (K / cpl) * 4;
+    auto lds_for = [&](int mbx) {  // transposed activations (pieces padded to 64 J) + piece sums
+      return (size_t)mbx * J * 64 * cpl * 2 + (size_t)mbx * (K / cpl) * 4;
     };
     int mbv = M <= 1 ? 1 : 2;
     while (mbv > 1 && lds_for(mbv) > kValuLdsMax) mbv /= 2;
