@@ -405,10 +405,17 @@ struct ValuCfg {
   static constexpr int NW = LB / 4;               // dwords per piece
 };
 
+// int2 pieces skip the OFF + c pairs: a code word w (16 codes) gives w & 0x33333333 and
+// (w >> 2) & 0x33333333, whose byte k holds codes (4k, 4k+2) and (4k+1, 4k+3) as the low
+// bits of two nibbles.  Read as FP4 (e2m1) those nibbles are 0, 0.5, 1, 1.5, so
+// v_cvt_scalef32_pk_bf16_fp4 with scale 2 turns each byte into an exact bf16 pair (c, c').
+// The activations are staged to match: per 16-code word, a chunk of the even-indexed x and
+// a chunk of the odd-indexed x.  That is 11 VALU ops per 16 codes before the dot products,
+// against 24 for the multiply / bitop3 pairs.
 template <int BITS, int G, int MB, int J, int SM, int ZM>
 __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
   using C = ValuCfg<BITS>;
-  constexpr float OFF = BITS == 3 ? 8.f : 4.f;
+  constexpr float OFF = BITS == 3 ? 8.f : 0.f;
   constexpr int W = kValuThreads / 64;
   typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -469,35 +476,59 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
   };
   const int nrows = wave_id < p.N ? (p.N - 1 - wave_id) / nwaves + 1 : 0;  // rows of this wave
   const int nbt = (nrows + R - 1) / R;
-  // activations of long rows (J >= 3 pieces per lane): the first kXRegs pieces per thread
+  // activations of long rows (J >= 3 pieces per lane): the first kXRegs chunks per thread
   // are requested before the codes, so the staging below waits for them only, not for the
   // codes in flight behind them (short rows keep the registers for occupancy instead)
   constexpr int kXRegs = J >= 3 ? 6 : 0;
-  const int x16 = M * (K / 8);
-  // LDS chunk of activation chunk q (row-major order of x)
-  auto xpos = [&](int q) {
-    const int m = q / (K / 8), c = q - m * (K / 8);
-    return (m * CH + c % CH) * PS + c / CH;
-  };
-  i32x4 xr[kXRegs > 0 ? kXRegs : 1];
+  // staging unit: one 16-byte chunk (int3) or one 16-code word's 32 bytes (int2)
+  constexpr int U = BITS == 2 ? 2 : 1;
+  constexpr int kXU = kXRegs / U;
+  const int upr = K / (8 * U);  // units per activation row
+  const int xu = M * upr;
+  auto uload = [&](int q, i32x4* v) {
+    const int m = q / upr, c = q - m * upr;
 #pragma unroll
-  for (int i = 0; i < kXRegs; ++i) {
-    int q = tid + i * kValuThreads;
-    q = q < x16 ? q : 0;
-    const int m = q / (K / 8), c = q - m * (K / 8);
-    xr[i] = *reinterpret_cast<const i32x4*>(p.x + (int64_t)m * p.ldx + c * 8);
+    for (int h = 0; h < U; ++h)
+      v[h] = *reinterpret_cast<const i32x4*>(p.x + (int64_t)m * p.ldx + (int64_t)(c * U + h) * 8);
+  };
+  auto ustore = [&](int q, const i32x4* v) {
+    const int m = q / upr, c = q - m * upr;
+    i32x4* xc = reinterpret_cast<i32x4*>(xs);
+    if constexpr (U == 1) {
+      xc[(m * CH + c % CH) * PS + c / CH] = v[0];
+    } else {
+      // word w of piece pc: even-indexed x -> chunk 2w, odd-indexed x -> chunk 2w + 1
+      const int pc = c / 4, w = c % 4;
+      i32x4 ev, od;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t a = static_cast<uint32_t>(v[k / 2][(2 * k) % 4]);
+        const uint32_t b2 = static_cast<uint32_t>(v[k / 2][(2 * k + 1) % 4]);
+        ev[k] = static_cast<int>(__builtin_amdgcn_perm(b2, a, 0x05040100u));
+        od[k] = static_cast<int>(__builtin_amdgcn_perm(b2, a, 0x07060302u));
+      }
+      xc[(m * CH + 2 * w) * PS + pc] = ev;
+      xc[(m * CH + 2 * w + 1) * PS + pc] = od;
+    }
+  };
+  i32x4 xr[kXU > 0 ? kXU : 1][U];
+#pragma unroll
+  for (int i = 0; i < kXU; ++i) {
+    const int q = tid + i * kValuThreads;
+    uload(q < xu ? q : 0, xr[i]);
   }
   if (nbt > 0) gload(0, 0);  // the first rows' codes are in flight during the staging
 
   // activations -> LDS, per-piece sums -> LDS
 #pragma unroll
-  for (int i = 0; i < kXRegs; ++i) {
+  for (int i = 0; i < kXU; ++i) {
     const int q = tid + i * kValuThreads;
-    if (q < x16) reinterpret_cast<i32x4*>(xs)[xpos(q)] = xr[i];
+    if (q < xu) ustore(q, xr[i]);
   }
-  for (int q = tid + kXRegs * kValuThreads; q < x16; q += kValuThreads) {
-    const int m = q / (K / 8), c = q - (q / (K / 8)) * (K / 8);
-    reinterpret_cast<i32x4*>(xs)[xpos(q)] = *reinterpret_cast<const i32x4*>(p.x + (int64_t)m * p.ldx + c * 8);
+  for (int q = tid + kXU * kValuThreads; q < xu; q += kValuThreads) {
+    i32x4 v[U];
+    uload(q, v);
+    ustore(q, v);
   }
   __syncthreads();
   for (int q = tid; q < M * npc; q += kValuThreads) {
@@ -529,6 +560,34 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
         float r[MB];
 #pragma unroll
         for (int m = 0; m < MB; ++m) r[m] = 0.f;
+        if constexpr (BITS == 2) {
+#pragma unroll
+          for (int w = 0; w < C::NW; ++w) {  // 16 codes per word: 8 bf16 pairs
+            const uint32_t lo = cw[b][i][j][w] & 0x33333333u;
+            const uint32_t hi = (cw[b][i][j][w] >> 2) & 0x33333333u;
+            const bf16x2 pl[4] = {__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(lo, 2.f, 0),
+                                  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(lo, 2.f, 1),
+                                  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(lo, 2.f, 2),
+                                  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(lo, 2.f, 3)};
+            const bf16x2 ph[4] = {__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(hi, 2.f, 0),
+                                  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(hi, 2.f, 1),
+                                  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(hi, 2.f, 2),
+                                  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(hi, 2.f, 3)};
+#pragma unroll
+            for (int m = 0; m < MB; ++m) {
+              if (m < M) {
+                const i32x4* xc = reinterpret_cast<const i32x4*>(xs) + (m * CH + 2 * w) * PS + ppc[j];
+                const i32x4 xe = xc[0], xo = xc[PS];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                  const uint32_t e0 = static_cast<uint32_t>(xe[k]), o0 = static_cast<uint32_t>(xo[k]);
+                  r[m] = __builtin_amdgcn_fdot2_f32_bf16(pl[k], __builtin_bit_cast(bf16x2, e0), r[m], false);
+                  r[m] = __builtin_amdgcn_fdot2_f32_bf16(ph[k], __builtin_bit_cast(bf16x2, o0), r[m], false);
+                }
+              }
+            }
+          }
+        } else
 #pragma unroll
         for (int v = 0; v < C::CPL / 8; ++v) {  // 8 codes per step: 4 bf16 pairs
           uint32_t bw[4];

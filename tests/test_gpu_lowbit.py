@@ -59,7 +59,7 @@ def test_dequant_asym_bit_exact(dev, bits):
 
 @pytest.mark.parametrize("bits", [2, 3])
 @pytest.mark.parametrize("N,K", [(11008, 4096), (4096, 11008), (40, 384)])
-@pytest.mark.parametrize("m", [1, 8])
+@pytest.mark.parametrize("m", [1, 2, 8])
 def test_gemv_asym_g64_bf16_config5(dev, bits, N, K, m):
     """G=64 asymmetric fp16 scale/zero, bf16 activations [1..8, K]."""
     rng = np.random.default_rng(bits + N + m)
@@ -86,11 +86,12 @@ def test_gemv_reference_layout(dev, bits, xdt, m):
     assert oq.rel_l2(y.cpu().numpy(), ref) <= F32_TOL
 
 
-@pytest.mark.parametrize("bits,K", [(3, 320), (2, 320), (3, 64), (2, 8192)])
-@pytest.mark.parametrize("m", [1, 5])
+@pytest.mark.parametrize("bits,K", [(3, 320), (2, 320), (3, 64), (2, 8192), (2, 16384), (2, 24576), (3, 12288)])
+@pytest.mark.parametrize("m", [1, 2, 5])
 def test_gemv_odd_layouts(dev, bits, K, m):
     """Rows that are not 16-byte multiples (int3 K=320: 120-byte rows) take the unstaged
-    kernel; the rest exercise partial chunks and K splits of the staged kernel."""
+    kernel; the rest exercise partial chunks and K splits of the staged kernel, and at
+    M <= 2 the decode kernel's 1, 2, 4 and 6 pieces per lane."""
     rng = np.random.default_rng(bits * K + m)
     packed, s, z = _asym(rng, 77, K, bits)
     x = oq.round_bf16(rng.standard_normal((m, K)).astype(np.float32))
