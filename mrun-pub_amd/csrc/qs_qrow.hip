@@ -723,6 +723,154 @@ __device__ __forceinline__ bool gemv_wave_rows(const QrowParams& p, int rows, ui
   return true;
 }
 
+// valu_words with the activations in registers: xw holds the 2 * NW packed bf16/f16 words
+// matching weight words 0..NW-1 (the same products and order as valu_words).
+template <int XT, int NW>
+__device__ __forceinline__ void valu_words_r(const int (&w)[4], float sc, const uint32_t* xw, float& acc) {
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    const int d = w[j];
+    if constexpr (XT == QS_BF16) {
+      bf16x2 a, b;
+      a[0] = static_cast<__bf16>(sbyte_f32<0>(d) * sc);
+      a[1] = static_cast<__bf16>(sbyte_f32<1>(d) * sc);
+      b[0] = static_cast<__bf16>(sbyte_f32<2>(d) * sc);
+      b[1] = static_cast<__bf16>(sbyte_f32<3>(d) * sc);
+      acc = __builtin_amdgcn_fdot2_f32_bf16(a, __builtin_bit_cast(bf16x2, xw[2 * j]), acc, false);
+      acc = __builtin_amdgcn_fdot2_f32_bf16(b, __builtin_bit_cast(bf16x2, xw[2 * j + 1]), acc, false);
+    } else {
+      f16x2 a, b;
+      a[0] = static_cast<_Float16>(sbyte_f32<0>(d) * sc);
+      a[1] = static_cast<_Float16>(sbyte_f32<1>(d) * sc);
+      b[0] = static_cast<_Float16>(sbyte_f32<2>(d) * sc);
+      b[1] = static_cast<_Float16>(sbyte_f32<3>(d) * sc);
+      acc = __builtin_amdgcn_fdot2(a, __builtin_bit_cast(f16x2, xw[2 * j]), acc, false);
+      acc = __builtin_amdgcn_fdot2(b, __builtin_bit_cast(f16x2, xw[2 * j + 1]), acc, false);
+    }
+  }
+}
+
+// One bf16/f16 activation row and short rows (K < 3072: at most 2 full 1 KiB chunks): the
+// activations a lane needs are only those of its own weight bytes -- 16 per chunk at
+// c * 1024 + 16 * lane, TB at the tail -- so each lane loads them straight into registers
+// (after the first wave of a CU they come from its L1), ahead of the weights.  No LDS
+// copy and no workgroup barrier: every wave runs on its own.  Same products, order and
+// wave sum as gemv_wave_rows.
+template <int XT, int U, int TB, bool SWI>
+__device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, float (&acc)[SWI ? 2 : 1], int& n_out,
+                                             int& li_out) {
+  constexpr int WPB = GemvShape<SWI, 1>::waves;
+  constexpr int P = SWI ? 2 : 1;
+  static_assert(U <= 2, "register activations cover at most two chunks");
+  const int lane = threadIdx.x & 63;
+  const int K = p.K;
+  const int F = K >> 10;
+  const int r0 = (int)blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (r0 >= rows) return false;
+  int li = 0;
+  if (!SWI) {
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      if (j < p.n_lin && r0 >= p.lin[j].tile_begin) li = j;
+  }
+  const int n = r0 - p.lin[li].tile_begin;
+  const uint8_t* xg = static_cast<const uint8_t*>(p.x);
+  const int rem = K - (F << 10);
+  // activations: chunk c -> 32 bytes at 2 * (c * 1024 + 16 * lane); tail -> 2 * TB bytes
+  uint32_t xc[U][8];
+#pragma unroll
+  for (int c = 0; c < U; ++c) {
+    const uint8_t* a = c < F ? xg + 2 * (c * 1024 + 16 * lane) : xg;
+    const i32x4 v0 = *reinterpret_cast<const i32x4*>(a);
+    const i32x4 v1 = *reinterpret_cast<const i32x4*>(a + 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xc[c][e] = static_cast<uint32_t>(v0[e]);
+      xc[c][4 + e] = static_cast<uint32_t>(v1[e]);
+    }
+  }
+  constexpr int XTW = TB / 2 > 0 ? TB / 2 : 1;  // tail activation words
+  uint32_t xt[XTW];
+  if constexpr (TB != 0) {
+    const bool tl = TB != 16 || 16 * lane < rem;
+    const uint8_t* a = tl ? xg + 2 * ((F << 10) + TB * lane) : xg;
+#pragma unroll
+    for (int e = 0; e < TB / 4; ++e) {
+      const u32x2 v = *reinterpret_cast<const u32x2*>(a + 8 * e);
+      xt[2 * e] = v[0];
+      xt[2 * e + 1] = v[1];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int8_t* wrow[P];
+  float sc[P];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) {
+    const QrowLin& L = p.lin[SWI ? pl : li];
+    wrow[pl] = L.codes + (int64_t)n * K;
+    sc[pl] = L.scales[n];
+  }
+  int tw[P][4];
+  if constexpr (TB != 0) {
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl) {
+      const int8_t* t = wrow[pl] + (F << 10);
+      if constexpr (TB == 16) {
+        const i32x4 v = __builtin_nontemporal_load(
+            reinterpret_cast<const i32x4*>(16 * lane < rem ? t + 16 * lane : wrow[pl]));
+        tw[pl][0] = v[0]; tw[pl][1] = v[1]; tw[pl][2] = v[2]; tw[pl][3] = v[3];
+      } else if constexpr (TB == 12) {
+        const u32x3 v = __builtin_nontemporal_load(reinterpret_cast<const u32x3*>(t + 12 * lane));
+        tw[pl][0] = v[0]; tw[pl][1] = v[1]; tw[pl][2] = v[2]; tw[pl][3] = 0;
+      } else if constexpr (TB == 8) {
+        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(t + 8 * lane));
+        tw[pl][0] = v[0]; tw[pl][1] = v[1]; tw[pl][2] = 0; tw[pl][3] = 0;
+      } else {
+        const unsigned v = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(t + 4 * lane));
+        tw[pl][0] = v; tw[pl][1] = 0; tw[pl][2] = 0; tw[pl][3] = 0;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  int wv[P][U][4];
+#pragma unroll
+  for (int c = 0; c < U; ++c)
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl) {
+      const int8_t* a = c < F ? wrow[pl] + c * 1024 + 16 * lane : wrow[pl];
+      const i32x4 v = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a));
+      wv[pl][c][0] = v[0]; wv[pl][c][1] = v[1]; wv[pl][c][2] = v[2]; wv[pl][c][3] = v[3];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  n_out = n;
+  li_out = li;
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) acc[pl] = 0.f;
+  if constexpr (TB == 16) {
+    if (16 * lane < rem) {
+#pragma unroll
+      for (int pl = 0; pl < P; ++pl) valu_words_r<XT, 4>(tw[pl], sc[pl], xt, acc[pl]);
+    }
+  } else if constexpr (TB != 0) {
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl) valu_words_r<XT, TB / 4>(tw[pl], sc[pl], xt, acc[pl]);
+  }
+#pragma unroll
+  for (int c = 0; c < U; ++c) {
+    if (c < F) {
+#pragma unroll
+      for (int pl = 0; pl < P; ++pl) valu_words_r<XT, 4>(wv[pl][c], sc[pl], xc[c], acc[pl]);
+    }
+  }
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) acc[pl] = wave_sum_dpp(acc[pl]);
+  return true;
+}
+
+// Whether k_gemv_valu takes gemv_wave_xg (no LDS activations).
+template <int XT, int MB, int U>
+constexpr bool kGemvXg = MB == 1 && U <= 2 && XT != QS_F32;
+
 template <int XT, int MB, int U, int TB, bool SWI>
 __global__ __launch_bounds__((GemvShape<SWI, MB>::waves * 64)) void k_gemv_valu(QrowParams p, int rows) {
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
@@ -730,7 +878,14 @@ __global__ __launch_bounds__((GemvShape<SWI, MB>::waves * 64)) void k_gemv_valu(
   const int M = p.M;
   float acc[SWI ? 2 : 1][MB];
   int n, li;
-  if (!gemv_wave_rows<XT, MB, U, TB, SWI>(p, rows, xs, acc, n, li, (int)blockIdx.x, true)) return;
+  if constexpr (kGemvXg<XT, MB, U>) {
+    float a1[SWI ? 2 : 1];
+    if (!gemv_wave_xg<XT, U, TB, SWI>(p, rows, a1, n, li)) return;
+#pragma unroll
+    for (int pl = 0; pl < (SWI ? 2 : 1); ++pl) acc[pl][0] = a1[pl];
+  } else {
+    if (!gemv_wave_rows<XT, MB, U, TB, SWI>(p, rows, xs, acc, n, li, (int)blockIdx.x, true)) return;
+  }
   if (lane != 0) return;
   const QrowLin& L = p.lin[li];
 #pragma unroll
@@ -1191,10 +1346,12 @@ void launch_valu_tb(const QrowParams& q, int rows, size_t lds, hipStream_t s) {
   constexpr int WPB = GemvShape<SWI, MB>::waves;
   const dim3 grid((unsigned)cdiv(rows, WPB)), block(WPB * 64);
   const int F = q.K >> 10;
+  constexpr bool xg1 = kGemvXg<XT, MB, 1>, xg2 = kGemvXg<XT, MB, 2>;  // no LDS activations
+  const size_t lds1 = xg1 ? 0 : lds, lds2 = xg2 ? 0 : lds;
   if (F <= 1)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 1, TB, SWI>), grid, block, lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 1, TB, SWI>), grid, block, lds1, s, q, rows);
   else if (F <= 2)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 2, TB, SWI>), grid, block, lds, s, q, rows);
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 2, TB, SWI>), grid, block, lds2, s, q, rows);
   else if (F <= 4)
     hipLaunchKernelGGL((k_gemv_valu<XT, MB, 4, TB, SWI>), grid, block, lds, s, q, rows);
   else if (F <= 8)
