@@ -588,6 +588,7 @@ struct GemvShape {
   static constexpr int waves = SWI ? (MB == 1 ? 2 : 4) : 8;
 };
 constexpr int kGemvWindow = 4;
+constexpr int kGemvXgWindow = 4;  // chunks (weights + activations) in flight
 
 // The row work of one wave, shared by the store and top-2 launches: every thread of the
 // workgroup calls it (it stages the activations and passes one barrier).  On return the
@@ -723,6 +724,19 @@ __device__ __forceinline__ bool gemv_wave_rows(const QrowParams& p, int rows, ui
   return true;
 }
 
+// k_gemv_valu takes gemv_wave_xg (activations in registers, no LDS) for one bf16/f16 row.
+template <int XT, int MB, int U>
+constexpr bool kGemvXg = MB == 1 && XT != QS_F32;
+
+// Waves per workgroup of k_gemv_valu.  Without the shared activation copy a workgroup is
+// only a dispatch unit: long rows (K >= 3072, few of them) spread over more CUs in small
+// workgroups, short rows keep 8.
+#ifndef QS_GEMV_WG_LONG
+#define QS_GEMV_WG_LONG 2
+#endif
+template <int XT, int MB, int U, bool SWI>
+constexpr int kGemvWaves = kGemvXg<XT, MB, U> && !SWI && U > 2 ? QS_GEMV_WG_LONG : GemvShape<SWI, MB>::waves;
+
 // valu_words with the activations in registers: xw holds the 2 * NW packed bf16/f16 words
 // matching weight words 0..NW-1 (the same products and order as valu_words).
 template <int XT, int NW>
@@ -759,9 +773,9 @@ __device__ __forceinline__ void valu_words_r(const int (&w)[4], float sc, const 
 template <int XT, int U, int TB, bool SWI>
 __device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, float (&acc)[SWI ? 2 : 1], int& n_out,
                                              int& li_out) {
-  constexpr int WPB = GemvShape<SWI, 1>::waves;
+  constexpr int WPB = kGemvWaves<XT, 1, U, SWI>;
   constexpr int P = SWI ? 2 : 1;
-  static_assert(U <= 2, "register activations cover at most two chunks");
+  constexpr int W = U < kGemvXgWindow ? U : kGemvXgWindow;  // chunks in flight
   const int lane = threadIdx.x & 63;
   const int K = p.K;
   const int F = K >> 10;
@@ -776,19 +790,9 @@ __device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, floa
   const int n = r0 - p.lin[li].tile_begin;
   const uint8_t* xg = static_cast<const uint8_t*>(p.x);
   const int rem = K - (F << 10);
-  // activations: chunk c -> 32 bytes at 2 * (c * 1024 + 16 * lane); tail -> 2 * TB bytes
+  // activations: chunk c -> 32 bytes at 2 * (c * 1024 + 16 * lane), requested with the
+  // chunk's weights; tail -> 2 * TB bytes, first
   uint32_t xc[U][8];
-#pragma unroll
-  for (int c = 0; c < U; ++c) {
-    const uint8_t* a = c < F ? xg + 2 * (c * 1024 + 16 * lane) : xg;
-    const i32x4 v0 = *reinterpret_cast<const i32x4*>(a);
-    const i32x4 v1 = *reinterpret_cast<const i32x4*>(a + 16);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xc[c][e] = static_cast<uint32_t>(v0[e]);
-      xc[c][4 + e] = static_cast<uint32_t>(v1[e]);
-    }
-  }
   constexpr int XTW = TB / 2 > 0 ? TB / 2 : 1;  // tail activation words
   uint32_t xt[XTW];
   if constexpr (TB != 0) {
@@ -833,15 +837,25 @@ __device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, floa
     }
   }
   int wv[P][U][4];
+  auto load_chunk = [&](int c) {
+    const uint8_t* xa = c < F ? xg + 2 * (c * 1024 + 16 * lane) : xg;
+    const i32x4 v0 = *reinterpret_cast<const i32x4*>(xa);
+    const i32x4 v1 = *reinterpret_cast<const i32x4*>(xa + 16);
 #pragma unroll
-  for (int c = 0; c < U; ++c)
+    for (int e = 0; e < 4; ++e) {
+      xc[c][e] = static_cast<uint32_t>(v0[e]);
+      xc[c][4 + e] = static_cast<uint32_t>(v1[e]);
+    }
 #pragma unroll
     for (int pl = 0; pl < P; ++pl) {
       const int8_t* a = c < F ? wrow[pl] + c * 1024 + 16 * lane : wrow[pl];
       const i32x4 v = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a));
       wv[pl][c][0] = v[0]; wv[pl][c][1] = v[1]; wv[pl][c][2] = v[2]; wv[pl][c][3] = v[3];
-      __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma unroll
+  for (int c = 0; c < W; ++c) load_chunk(c);
   n_out = n;
   li_out = li;
 #pragma unroll
@@ -861,18 +875,16 @@ __device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, floa
 #pragma unroll
       for (int pl = 0; pl < P; ++pl) valu_words_r<XT, 4>(wv[pl][c], sc[pl], xc[c], acc[pl]);
     }
+    if (c + W < U) load_chunk(c + W);
   }
 #pragma unroll
   for (int pl = 0; pl < P; ++pl) acc[pl] = wave_sum_dpp(acc[pl]);
   return true;
 }
 
-// Whether k_gemv_valu takes gemv_wave_xg (no LDS activations).
-template <int XT, int MB, int U>
-constexpr bool kGemvXg = MB == 1 && U <= 2 && XT != QS_F32;
 
 template <int XT, int MB, int U, int TB, bool SWI>
-__global__ __launch_bounds__((GemvShape<SWI, MB>::waves * 64)) void k_gemv_valu(QrowParams p, int rows) {
+__global__ __launch_bounds__((kGemvWaves<XT, MB, U, SWI> * 64)) void k_gemv_valu(QrowParams p, int rows) {
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
   const int lane = threadIdx.x & 63;
   const int M = p.M;
@@ -1341,23 +1353,22 @@ int gemv_tail(int64_t K) {
   return 16;
 }
 
+template <int XT, int MB, int U, int TB, bool SWI>
+void launch_valu_u(const QrowParams& q, int rows, size_t lds, hipStream_t s) {
+  constexpr int WPB = kGemvWaves<XT, MB, U, SWI>;
+  const dim3 grid((unsigned)cdiv(rows, WPB)), block(WPB * 64);
+  const size_t l = kGemvXg<XT, MB, U> ? 0 : lds;  // no LDS activations on the register path
+  hipLaunchKernelGGL((k_gemv_valu<XT, MB, U, TB, SWI>), grid, block, l, s, q, rows);
+}
+
 template <int XT, int MB, int TB, bool SWI>
 void launch_valu_tb(const QrowParams& q, int rows, size_t lds, hipStream_t s) {
-  constexpr int WPB = GemvShape<SWI, MB>::waves;
-  const dim3 grid((unsigned)cdiv(rows, WPB)), block(WPB * 64);
   const int F = q.K >> 10;
-  constexpr bool xg1 = kGemvXg<XT, MB, 1>, xg2 = kGemvXg<XT, MB, 2>;  // no LDS activations
-  const size_t lds1 = xg1 ? 0 : lds, lds2 = xg2 ? 0 : lds;
-  if (F <= 1)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 1, TB, SWI>), grid, block, lds1, s, q, rows);
-  else if (F <= 2)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 2, TB, SWI>), grid, block, lds2, s, q, rows);
-  else if (F <= 4)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 4, TB, SWI>), grid, block, lds, s, q, rows);
-  else if (F <= 8)
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 8, TB, SWI>), grid, block, lds, s, q, rows);
-  else
-    hipLaunchKernelGGL((k_gemv_valu<XT, MB, 12, TB, SWI>), grid, block, lds, s, q, rows);
+  if (F <= 1) launch_valu_u<XT, MB, 1, TB, SWI>(q, rows, lds, s);
+  else if (F <= 2) launch_valu_u<XT, MB, 2, TB, SWI>(q, rows, lds, s);
+  else if (F <= 4) launch_valu_u<XT, MB, 4, TB, SWI>(q, rows, lds, s);
+  else if (F <= 8) launch_valu_u<XT, MB, 8, TB, SWI>(q, rows, lds, s);
+  else launch_valu_u<XT, MB, 12, TB, SWI>(q, rows, lds, s);
 }
 
 template <int XT, int MB, bool SWI>
