@@ -928,16 +928,18 @@ __device__ __forceinline__ bool top2_better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
+// Value selects rather than branches: branching on which reference to update made the
+// compiler keep the four values in scratch memory, whose accesses share the vector-memory
+// wait counter with the weight loads.
 __device__ __forceinline__ void top2_push(float v, int i, float& v1, int& i1, float& v2, int& i2) {
-  if (top2_better(v, i, v1, i1)) {
-    v2 = v1;
-    i2 = i1;
-    v1 = v;
-    i1 = i;
-  } else if (top2_better(v, i, v2, i2)) {
-    v2 = v;
-    i2 = i;
-  }
+  const bool b1 = top2_better(v, i, v1, i1);
+  const bool b2 = top2_better(v, i, v2, i2);
+  const float nv2 = b1 ? v1 : (b2 ? v : v2);
+  const int ni2 = b1 ? i1 : (b2 ? i : i2);
+  v1 = b1 ? v : v1;
+  i1 = b1 ? i : i1;
+  v2 = nv2;
+  i2 = ni2;
 }
 
 // Workgroup epilogue: each wave's running first/second per activation row -> this
@@ -1003,6 +1005,103 @@ __global__ __launch_bounds__((GemvShape<false, MB>::waves * 64)) void k_gemv_top
     stage = false;
   }
   block_top2<WPB, MB>(v1, i1, v2, i2, p.M, part_v, part_i);
+}
+
+// The same launch for one bf16/f16 activation row and K / 1024 = U (1 or 2) full chunks:
+// each wave loads the activations of its own weight bytes into registers once (as
+// gemv_wave_xg does per row) and walks its rows blk * 8 + wave, blk = g, g + G, ... with
+// the next row's weights in flight while the current row is reduced.  Every load is
+// unconditional (a row past the end re-reads the wave's current row), so the waits stay
+// per buffer.  Same products, order, wave sum and candidates as k_gemv_top2.
+template <int XT, int U, int TB>
+__global__ __launch_bounds__(512) void k_gemv_top2_xg(QrowParams p, int rows, int start_row, float* part_v,
+                                                      int* part_i) {
+  constexpr int WPB = 8;
+  static_assert(U <= 2, "register activations cover at most two chunks");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int K = p.K;
+  constexpr int F = U;  // full chunks (the host checks K >> 10 == U)
+  const int rem = K - (F << 10);
+  const uint8_t* xg = static_cast<const uint8_t*>(p.x);
+  uint32_t xc[U][8];
+#pragma unroll
+  for (int c = 0; c < U; ++c) {
+    const uint8_t* a = xg + 2 * (c * 1024 + 16 * lane);
+    const i32x4 v0 = *reinterpret_cast<const i32x4*>(a);
+    const i32x4 v1 = *reinterpret_cast<const i32x4*>(a + 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xc[c][e] = static_cast<uint32_t>(v0[e]);
+      xc[c][4 + e] = static_cast<uint32_t>(v1[e]);
+    }
+  }
+  constexpr int XTW = TB / 2 > 0 ? TB / 2 : 1;
+  uint32_t xt[XTW];
+  const bool tl = TB != 16 || 16 * lane < rem;
+  if constexpr (TB != 0) {
+    const uint8_t* a = tl ? xg + 2 * ((F << 10) + TB * lane) : xg;
+#pragma unroll
+    for (int e = 0; e < TB / 4; ++e) {
+      const u32x2 v = *reinterpret_cast<const u32x2*>(a + 8 * e);
+      xt[2 * e] = v[0];
+      xt[2 * e + 1] = v[1];
+    }
+  }
+  const int8_t* codes = p.lin[0].codes;
+  const float* scales = p.lin[0].scales;
+  int tw[2][4], wv[2][U][4];
+  float sc[2];
+  auto load = [&](int b, int row) {
+    const int8_t* wrow = codes + (int64_t)row * K;
+    sc[b] = scales[row];
+    if constexpr (TB != 0) {
+      const int8_t* t = wrow + (F << 10);
+      if constexpr (TB == 16) {
+        const i32x4 v = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(tl ? t + 16 * lane : wrow));
+        tw[b][0] = v[0]; tw[b][1] = v[1]; tw[b][2] = v[2]; tw[b][3] = v[3];
+      } else if constexpr (TB == 12) {
+        const u32x3 v = __builtin_nontemporal_load(reinterpret_cast<const u32x3*>(t + 12 * lane));
+        tw[b][0] = v[0]; tw[b][1] = v[1]; tw[b][2] = v[2]; tw[b][3] = 0;
+      } else if constexpr (TB == 8) {
+        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(t + 8 * lane));
+        tw[b][0] = v[0]; tw[b][1] = v[1]; tw[b][2] = 0; tw[b][3] = 0;
+      } else {
+        const unsigned v = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(t + 4 * lane));
+        tw[b][0] = v; tw[b][1] = 0; tw[b][2] = 0; tw[b][3] = 0;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < U; ++c) {
+      const i32x4 v = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wrow + c * 1024 + 16 * lane));
+      wv[b][c][0] = v[0]; wv[b][c][1] = v[1]; wv[b][c][2] = v[2]; wv[b][c][3] = v[3];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  float v1[1] = {-INFINITY}, v2[1] = {-INFINITY};
+  int i1[1] = {INT_MAX}, i2[1] = {INT_MAX};
+  auto reduce = [&](int b, int row) {
+    float acc = 0.f;
+    if constexpr (TB == 16) {
+      if (tl) valu_words_r<XT, 4>(tw[b], sc[b], xt, acc);
+    } else if constexpr (TB != 0) {
+      valu_words_r<XT, TB / 4>(tw[b], sc[b], xt, acc);
+    }
+#pragma unroll
+    for (int c = 0; c < U; ++c) valu_words_r<XT, 4>(wv[b][c], sc[b], xc[c], acc);
+    acc = wave_sum_dpp(acc);
+    if (row < rows) top2_push(acc, start_row + row, v1[0], i1[0], v2[0], i2[0]);
+  };
+  const int stride = (int)gridDim.x * WPB;
+  int r = (int)blockIdx.x * WPB + wave;
+  load(0, r < rows ? r : rows - 1);
+  for (; r < rows; r += 2 * stride) {
+    load(1, r + stride < rows ? r + stride : r);
+    reduce(0, r);
+    load(0, r + 2 * stride < rows ? r + 2 * stride : r);
+    reduce(1, r + stride);
+  }
+  block_top2<WPB, 1>(v1, i1, v2, i2, 1, part_v, part_i);
 }
 
 // Any K / alignment: one wave per row, one activation row per launch (x points at it),
@@ -1432,8 +1531,19 @@ template <int XT, int MB, int TB>
 void launch_top2_tb(const QrowParams& q, int rows, int start_row, float* pv, int* pi, size_t lds,
                     hipStream_t s) {
   constexpr int WPB = GemvShape<false, MB>::waves;
+  static_assert(GemvShape<false, 1>::waves == 8, "k_gemv_top2_xg takes the 8-row blocks of top2_grid");
   const dim3 grid((unsigned)top2_grid(rows)), block(WPB * 64);
   const int F = q.K >> 10;
+  if constexpr (MB == 1 && XT != QS_F32) {  // one bf16/f16 row: register activations
+    if (F == 1) {
+      hipLaunchKernelGGL((k_gemv_top2_xg<XT, 1, TB>), grid, block, 0, s, q, rows, start_row, pv, pi);
+      return;
+    }
+    if (F == 2) {
+      hipLaunchKernelGGL((k_gemv_top2_xg<XT, 2, TB>), grid, block, 0, s, q, rows, start_row, pv, pi);
+      return;
+    }
+  }
   if (F <= 1)
     hipLaunchKernelGGL((k_gemv_top2<XT, MB, 1, TB>), grid, block, lds, s, q, rows, start_row, pv, pi);
   else if (F <= 2)
