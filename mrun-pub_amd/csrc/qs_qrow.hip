@@ -21,9 +21,13 @@
 //                                 fp32-activation call: one wave per weight row, 1 KiB
 //                                 contiguous row segments per instruction issued in row
 //                                 order through a 4-chunk window, exact-width tail,
-//                                 activations in LDS, VALU dequant + fma / v_dot2,
-//                                 fixed-order DPP wave sum.  Also the row-stable (batch
-//                                 invariant) lane.
+//                                 VALU dequant + fma / v_dot2, fixed-order DPP wave sum.
+//                                 One bf16/f16 row: each lane loads the activations of
+//                                 its own weight bytes into registers; otherwise the
+//                                 activations are staged in LDS.  Also the row-stable
+//                                 (batch invariant) lane.
+//   k_gemv_top2_xg / k_gemv_top2: the same row work with a running top-2 per wave
+//                                 instead of stores (fused head + top-2), persistent.
 //   k_generic                   : any shape / alignment, one wave per output row.
 //
 // MFMA operand mapping (16x16x32, wave64): lane l supplies row (l & 15) of A and
