@@ -728,9 +728,10 @@ __device__ __forceinline__ bool gemv_wave_rows(const QrowParams& p, int rows, ui
   return true;
 }
 
-// k_gemv_valu takes gemv_wave_xg (activations in registers, no LDS) for one bf16/f16 row.
+// k_gemv_valu takes gemv_wave_xg (activations in registers, no LDS) for up to 4 bf16/f16
+// rows.
 template <int XT, int MB, int U>
-constexpr bool kGemvXg = MB == 1 && XT != QS_F32;
+constexpr bool kGemvXg = MB <= 4 && XT != QS_F32;
 
 // Waves per workgroup of k_gemv_valu.  Without the shared activation copy a workgroup is
 // only a dispatch unit: long rows (K >= 3072, few of them) spread over more CUs in small
@@ -768,16 +769,52 @@ __device__ __forceinline__ void valu_words_r(const int (&w)[4], float sc, const 
   }
 }
 
-// One bf16/f16 activation row and short rows (K < 3072: at most 2 full 1 KiB chunks): the
-// activations a lane needs are only those of its own weight bytes -- 16 per chunk at
-// c * 1024 + 16 * lane, TB at the tail -- so each lane loads them straight into registers
-// (after the first wave of a CU they come from its L1), ahead of the weights.  No LDS
-// copy and no workgroup barrier: every wave runs on its own.  Same products, order and
-// wave sum as gemv_wave_rows.
-template <int XT, int U, int TB, bool SWI>
-__device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, float (&acc)[SWI ? 2 : 1], int& n_out,
-                                             int& li_out) {
-  constexpr int WPB = kGemvWaves<XT, 1, U, SWI>;
+// One weight word (4 codes) -> two packed bf16/f16 pairs, exact (the W8A16 contract).
+template <int XT>
+__device__ __forceinline__ void deq_word(int d, float sc, uint32_t& a, uint32_t& b) {
+  if constexpr (XT == QS_BF16) {
+    bf16x2 u, v;
+    u[0] = static_cast<__bf16>(sbyte_f32<0>(d) * sc);
+    u[1] = static_cast<__bf16>(sbyte_f32<1>(d) * sc);
+    v[0] = static_cast<__bf16>(sbyte_f32<2>(d) * sc);
+    v[1] = static_cast<__bf16>(sbyte_f32<3>(d) * sc);
+    a = __builtin_bit_cast(uint32_t, u);
+    b = __builtin_bit_cast(uint32_t, v);
+  } else {
+    f16x2 u, v;
+    u[0] = static_cast<_Float16>(sbyte_f32<0>(d) * sc);
+    u[1] = static_cast<_Float16>(sbyte_f32<1>(d) * sc);
+    v[0] = static_cast<_Float16>(sbyte_f32<2>(d) * sc);
+    v[1] = static_cast<_Float16>(sbyte_f32<3>(d) * sc);
+    a = __builtin_bit_cast(uint32_t, u);
+    b = __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+// acc += a . x0 + b . x1 in the order of valu_words (two v_dot2 with fp32 accumulation).
+template <int XT>
+__device__ __forceinline__ float dot_word(uint32_t a, uint32_t b, uint32_t x0, uint32_t x1, float acc) {
+  if constexpr (XT == QS_BF16) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, x0), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, b), __builtin_bit_cast(bf16x2, x1), acc, false);
+  } else {
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, x0), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, b), __builtin_bit_cast(f16x2, x1), acc, false);
+  }
+  return acc;
+}
+
+// Up to MB = 4 bf16/f16 activation rows: a lane only ever multiplies the activations of
+// its own weight bytes -- 16 per 1 KiB chunk at c * 1024 + 16 * lane, TB at the tail --
+// so it loads exactly those straight into registers (after the first wave of a CU they
+// come from its L1), each chunk's with the chunk's weights.  No LDS copy and no workgroup
+// barrier: every wave runs on its own.  Each weight word is dequantized once and meets
+// every row; each row sees the products and order of gemv_wave_rows, whatever MB is.
+// Rows m >= M read row M - 1 and are never stored.
+template <int XT, int MB, int U, int TB, bool SWI>
+__device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, float (&acc)[SWI ? 2 : 1][MB],
+                                             int& n_out, int& li_out) {
+  constexpr int WPB = kGemvWaves<XT, MB, U, SWI>;
   constexpr int P = SWI ? 2 : 1;
   constexpr int W = U < kGemvXgWindow ? U : kGemvXgWindow;  // chunks in flight
   const int lane = threadIdx.x & 63;
@@ -792,21 +829,27 @@ __device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, floa
       if (j < p.n_lin && r0 >= p.lin[j].tile_begin) li = j;
   }
   const int n = r0 - p.lin[li].tile_begin;
-  const uint8_t* xg = static_cast<const uint8_t*>(p.x);
-  const int rem = K - (F << 10);
-  // activations: chunk c -> 32 bytes at 2 * (c * 1024 + 16 * lane), requested with the
-  // chunk's weights; tail -> 2 * TB bytes, first
-  uint32_t xc[U][8];
-  constexpr int XTW = TB / 2 > 0 ? TB / 2 : 1;  // tail activation words
-  uint32_t xt[XTW];
-  if constexpr (TB != 0) {
-    const bool tl = TB != 16 || 16 * lane < rem;
-    const uint8_t* a = tl ? xg + 2 * ((F << 10) + TB * lane) : xg;
+  const uint8_t* xrow[MB];
 #pragma unroll
-    for (int e = 0; e < TB / 4; ++e) {
-      const u32x2 v = *reinterpret_cast<const u32x2*>(a + 8 * e);
-      xt[2 * e] = v[0];
-      xt[2 * e + 1] = v[1];
+  for (int m = 0; m < MB; ++m)
+    xrow[m] = static_cast<const uint8_t*>(p.x) + (int64_t)(m < p.M ? m : p.M - 1) * p.ldx * 2;
+  const int rem = K - (F << 10);
+  // activations: chunk c -> 32 bytes at 2 * (c * 1024 + 16 * lane) of each row, requested
+  // with the chunk's weights; tail -> 2 * TB bytes per row, first
+  uint32_t xc[U][MB][8];
+  constexpr int XTW = TB / 2 > 0 ? TB / 2 : 1;  // tail activation words
+  uint32_t xt[MB][XTW];
+  const bool tl = TB != 16 || 16 * lane < rem;
+  if constexpr (TB != 0) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const uint8_t* a = tl ? xrow[m] + 2 * ((F << 10) + TB * lane) : xrow[m];
+#pragma unroll
+      for (int e = 0; e < TB / 4; ++e) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(a + 8 * e);
+        xt[m][2 * e] = v[0];
+        xt[m][2 * e + 1] = v[1];
+      }
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -842,13 +885,16 @@ __device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, floa
   }
   int wv[P][U][4];
   auto load_chunk = [&](int c) {
-    const uint8_t* xa = c < F ? xg + 2 * (c * 1024 + 16 * lane) : xg;
-    const i32x4 v0 = *reinterpret_cast<const i32x4*>(xa);
-    const i32x4 v1 = *reinterpret_cast<const i32x4*>(xa + 16);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xc[c][e] = static_cast<uint32_t>(v0[e]);
-      xc[c][4 + e] = static_cast<uint32_t>(v1[e]);
+    for (int m = 0; m < MB; ++m) {
+      const uint8_t* xa = c < F ? xrow[m] + 2 * (c * 1024 + 16 * lane) : xrow[m];
+      const i32x4 v0 = *reinterpret_cast<const i32x4*>(xa);
+      const i32x4 v1 = *reinterpret_cast<const i32x4*>(xa + 16);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xc[c][m][e] = static_cast<uint32_t>(v0[e]);
+        xc[c][m][4 + e] = static_cast<uint32_t>(v1[e]);
+      }
     }
 #pragma unroll
     for (int pl = 0; pl < P; ++pl) {
@@ -863,26 +909,42 @@ __device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, floa
   n_out = n;
   li_out = li;
 #pragma unroll
-  for (int pl = 0; pl < P; ++pl) acc[pl] = 0.f;
-  if constexpr (TB == 16) {
-    if (16 * lane < rem) {
+  for (int pl = 0; pl < P; ++pl)
 #pragma unroll
-      for (int pl = 0; pl < P; ++pl) valu_words_r<XT, 4>(tw[pl], sc[pl], xt, acc[pl]);
+    for (int m = 0; m < MB; ++m) acc[pl][m] = 0.f;
+  if constexpr (TB != 0) {
+    if (tl) {
+#pragma unroll
+      for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+        for (int j = 0; j < TB / 4; ++j) {
+          uint32_t a, b;
+          deq_word<XT>(tw[pl][j], sc[pl], a, b);
+#pragma unroll
+          for (int m = 0; m < MB; ++m) acc[pl][m] = dot_word<XT>(a, b, xt[m][2 * j], xt[m][2 * j + 1], acc[pl][m]);
+        }
     }
-  } else if constexpr (TB != 0) {
-#pragma unroll
-    for (int pl = 0; pl < P; ++pl) valu_words_r<XT, TB / 4>(tw[pl], sc[pl], xt, acc[pl]);
   }
 #pragma unroll
   for (int c = 0; c < U; ++c) {
     if (c < F) {
 #pragma unroll
-      for (int pl = 0; pl < P; ++pl) valu_words_r<XT, 4>(wv[pl][c], sc[pl], xc[c], acc[pl]);
+      for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint32_t a, b;
+          deq_word<XT>(wv[pl][c][j], sc[pl], a, b);
+#pragma unroll
+          for (int m = 0; m < MB; ++m)
+            acc[pl][m] = dot_word<XT>(a, b, xc[c][m][2 * j], xc[c][m][2 * j + 1], acc[pl][m]);
+        }
     }
     if (c + W < U) load_chunk(c + W);
   }
 #pragma unroll
-  for (int pl = 0; pl < P; ++pl) acc[pl] = wave_sum_dpp(acc[pl]);
+  for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[pl][m] = wave_sum_dpp(acc[pl][m]);
   return true;
 }
 
@@ -895,10 +957,7 @@ __global__ __launch_bounds__((kGemvWaves<XT, MB, U, SWI> * 64)) void k_gemv_valu
   float acc[SWI ? 2 : 1][MB];
   int n, li;
   if constexpr (kGemvXg<XT, MB, U>) {
-    float a1[SWI ? 2 : 1];
-    if (!gemv_wave_xg<XT, U, TB, SWI>(p, rows, a1, n, li)) return;
-#pragma unroll
-    for (int pl = 0; pl < (SWI ? 2 : 1); ++pl) acc[pl][0] = a1[pl];
+    if (!gemv_wave_xg<XT, MB, U, TB, SWI>(p, rows, acc, n, li)) return;
   } else {
     if (!gemv_wave_rows<XT, MB, U, TB, SWI>(p, rows, xs, acc, n, li, (int)blockIdx.x, true)) return;
   }
@@ -1485,11 +1544,20 @@ void launch_valu_mb(const QrowParams& q, int rows, size_t lds, hipStream_t s) {
   }
 }
 
+// Activation rows up to which bf16/f16 calls take the VALU (register-activation) kernel
+// rather than the MFMA tiles: the weights are read once either way, and at M <= 4 the
+// VALU dot work still hides under the weight stream.
+#ifndef QS_VALU_ROWS
+#define QS_VALU_ROWS 4
+#endif
+constexpr int64_t kValuRows = QS_VALU_ROWS;
+
 // VALU path: rows of x in batches of MB (each batch one launch).  Every row is reduced
 // in the same order whatever M is.
 int run_valu(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool swiglu) {
   const int es = x_dtype == QS_F32 ? 4 : 2;
-  const int mb = valu_mb(x_dtype, p.K, M);
+  // bf16/f16 rows take the register-activation kernel in batches of up to 4
+  const int mb = x_dtype == QS_F32 ? valu_mb(x_dtype, p.K, M) : (M <= 1 ? 1 : M <= 2 ? 2 : 4);
   int rows = 0;
   if (swiglu) {
     rows = p.lin[0].N;
@@ -1507,17 +1575,20 @@ int run_valu(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool swiglu) {
       if (p.lin[i].y) q.lin[i].y = static_cast<char*>(p.lin[i].y) + m0 * p.lin[i].ldy * es;
     const size_t lds = (size_t)q.M * q.K * es;
     if (swiglu) {
-      if (mb == 2) launch_valu_mb<QS_BF16, 2, true>(q, rows, lds, s);
+      if (mb == 4) launch_valu_mb<QS_BF16, 4, true>(q, rows, lds, s);
+      else if (mb == 2) launch_valu_mb<QS_BF16, 2, true>(q, rows, lds, s);
       else launch_valu_mb<QS_BF16, 1, true>(q, rows, lds, s);
     } else if (x_dtype == QS_F32) {
       if (mb == 4) launch_valu_mb<QS_F32, 4, false>(q, rows, lds, s);
       else if (mb == 2) launch_valu_mb<QS_F32, 2, false>(q, rows, lds, s);
       else launch_valu_mb<QS_F32, 1, false>(q, rows, lds, s);
     } else if (x_dtype == QS_BF16) {
-      if (mb == 2) launch_valu_mb<QS_BF16, 2, false>(q, rows, lds, s);
+      if (mb == 4) launch_valu_mb<QS_BF16, 4, false>(q, rows, lds, s);
+      else if (mb == 2) launch_valu_mb<QS_BF16, 2, false>(q, rows, lds, s);
       else launch_valu_mb<QS_BF16, 1, false>(q, rows, lds, s);
     } else {
-      if (mb == 2) launch_valu_mb<QS_F16, 2, false>(q, rows, lds, s);
+      if (mb == 4) launch_valu_mb<QS_F16, 4, false>(q, rows, lds, s);
+      else if (mb == 2) launch_valu_mb<QS_F16, 2, false>(q, rows, lds, s);
       else launch_valu_mb<QS_F16, 1, false>(q, rows, lds, s);
     }
   }
@@ -1581,7 +1652,7 @@ int run_linears(QrowParams p, int x_dtype, int64_t M, hipStream_t s, bool row_st
   if (M == 0) return QS_OK;
   const int esz = x_dtype == QS_F32 ? 4 : 2;
   // decode-sized batches (and the row-stable contract) take the VALU path
-  if ((row_stable || M <= 2 || x_dtype == QS_F32) && valu_eligible(p, x_dtype))
+  if ((row_stable || M <= kValuRows || x_dtype == QS_F32) && valu_eligible(p, x_dtype))
     return run_valu(p, x_dtype, M, s, false);
   if (!row_stable && mfma_eligible(p, x_dtype)) {
     for (int64_t m0 = 0; m0 < M; m0 += 32) {
@@ -1739,7 +1810,7 @@ extern "C" int qs_qrow_swiglu(const void* x, int64_t ldx, const int8_t* gate_cod
   p.n_lin = 2;
   p.lin[0] = QrowLin{gate_codes, gate_scales, y, ldy, (int)N, 0};
   p.lin[1] = QrowLin{up_codes, up_scales, nullptr, 0, (int)N, 0};
-  if (M <= 2 && valu_eligible(p, QS_BF16)) return run_valu(p, QS_BF16, M, s, true);
+  if (M <= kValuRows && valu_eligible(p, QS_BF16)) return run_valu(p, QS_BF16, M, s, true);
   if (mfma_eligible(p, QS_BF16)) {
     for (int64_t m0 = 0; m0 < M; m0 += 32) {
       QrowParams q = p;
