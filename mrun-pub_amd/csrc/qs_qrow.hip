@@ -11,13 +11,13 @@
 //                                 multiply-add, so the VALU only pays for the dequant
 //                                 (cvt_sdwa + mul + half a cvt_pk per weight byte).
 //                                 K is split across the waves of a workgroup and reduced
-//                                 through LDS in a fixed order.  Used for 3 <= M.
+//                                 through LDS in a fixed order.  Used for 5 <= M.
 //   k_w8a16_s<...>              : the same contract as a streaming kernel -- one wave per
 //                                 (tile, K slice) with a sliding window of chunks in
 //                                 flight, SwiGLU planes sharing a wave, activations in LDS
-//                                 when they are small.  Used for SwiGLU at 3 <= M and for
+//                                 when they are small.  Used for SwiGLU at 5 <= M and for
 //                                 long rows (K >= 4096) while the activations fit in LDS.
-//   k_gemv_valu<...>            : M <= 2 decode rows (any activation dtype) and every
+//   k_gemv_valu<...>            : M <= 4 decode rows (M <= 2 for other dtypes) and every
 //                                 fp32-activation call: one wave per weight row, 1 KiB
 //                                 contiguous row segments per instruction issued in row
 //                                 order through a 4-chunk window, exact-width tail,
