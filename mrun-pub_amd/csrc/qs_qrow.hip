@@ -17,8 +17,8 @@
 //                                 flight, SwiGLU planes sharing a wave, activations in LDS
 //                                 when they are small.  Used for SwiGLU at 5 <= M and for
 //                                 long rows (K >= 4096) while the activations fit in LDS.
-//   k_gemv_valu<...>            : M <= 4 decode rows (M <= 2 for other dtypes) and every
-//                                 fp32-activation call: one wave per weight row, 1 KiB
+//   k_gemv_valu<...>            : M <= 4 bf16/f16 decode rows and every fp32-activation
+//                                 call: one wave per weight row, 1 KiB
 //                                 contiguous row segments per instruction issued in row
 //                                 order through a 4-chunk window, exact-width tail,
 //                                 VALU dequant + fma / v_dot2, fixed-order DPP wave sum.
