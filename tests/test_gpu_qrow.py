@@ -66,7 +66,7 @@ def test_matmul_fp32(dev, m, n, k):
     assert err <= F32_TOL, err
 
 
-@pytest.mark.parametrize("m", [1, 4, 16, 32, 37])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 16, 32, 37])
 @pytest.mark.parametrize(
     "n,k", [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (1000, 4096), (100, 192), (24, 40)]
 )
@@ -107,9 +107,31 @@ def test_row_stable_batch_invariance(dev, dtype, n, k):
     assert oq.rel_l2(full.float().cpu().numpy(), ref) <= 3 * tol
 
 
-@pytest.mark.parametrize("m", [3, 16, 32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,k", [(1536, 1536), (300, 8960), (64, 1000)])
+def test_register_rows_match_single_row(dev, dtype, n, k):
+    """Up to 4 bf16/f16 rows share one register-activation launch: every row is
+    bit-identical to its own M=1 call, including the padded rows of M=3 (SwiGLU too)."""
+    rng, codes, scales = _case(n, k, seed=17)
+    _, codes2, scales2 = _case(n, k, seed=18)
+    x = torch.from_numpy(rng.standard_normal((4, k)).astype(np.float32)).to(dev).to(dtype)
+    c, s = _dev(codes, dev), _dev(scales, dev)
+    for m in (2, 3, 4):
+        full = _qrow().qrow_matmul(c, s, x[:m])
+        for r in range(m):
+            assert torch.equal(_qrow().qrow_matmul(c, s, x[r : r + 1])[0], full[r])
+    if dtype == torch.bfloat16 and k % 16 == 0:
+        gate = _qrow().CompactQRowPage("g", 0, n, k, c, s)
+        up = _qrow().CompactQRowPage("u", 0, n, k, _dev(codes2, dev), _dev(scales2, dev))
+        for m in (2, 3, 4):
+            full = _qrow().fused_qrow_swiglu(gate, up, x[:m])[0]
+            for r in range(m):
+                assert torch.equal(_qrow().fused_qrow_swiglu(gate, up, x[r : r + 1])[0][0], full[r])
+
+
+@pytest.mark.parametrize("m", [5, 16, 32])
 def test_mfma_path_rows_independent_of_batch(dev, m):
-    """Within the MFMA path (M >= 3) a row does not depend on the other rows."""
+    """Within the MFMA path (M >= 5) a row does not depend on the other rows."""
     rng, codes, scales = _case(1536, 1536, seed=13)
     x = torch.from_numpy(rng.standard_normal((m, 1536)).astype(np.float32)).to(dev).to(torch.bfloat16)
     c, s = _dev(codes, dev), _dev(scales, dev)
@@ -138,7 +160,7 @@ def test_multi_linear_equals_individual(dev):
         assert torch.allclose(o.float(), single.float(), rtol=1e-2, atol=1e-2)
 
 
-@pytest.mark.parametrize("m", [1, 4, 16, 32])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 16, 32])
 @pytest.mark.parametrize("n,k", [(8960, 1536), (1000, 1536), (200, 128), (96, 64), (5, 4)])
 def test_swiglu(dev, m, n, k):
     rng = np.random.default_rng(m + n)
