@@ -440,51 +440,86 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
 }
 
 // Small k (kk <= 16): the same 64-bit keys as k_topk_radix ((value bits << 32) | ~column:
-// larger value first, lower column on ties; keys are unique).  Each wave selects its own
-// top kk by kk rounds of a wave-wide maximum (the winning key is cleared in its lane),
-// then wave 0 selects the final kk from the 16 waves' candidates the same way: two
-// barriers instead of the radix select's eight passes.  Emits idx in descending key order
-// and the keep mask.
+// larger value first, lower column on ties; keys are unique, and real keys are > 0).
+// Filter: the 16 wave maxima are 16 distinct keys, so with kk <= 16 every top-kk key is
+// >= T, the smallest wave maximum.  The keys >= T (a few dozen for ordinary data) are
+// compacted into LDS and wave 0 selects from them by kk rounds of a wave-wide maximum.
+// When more than 256 pass (ties across many columns), each wave first takes its own top
+// kk the same way and wave 0 selects from those 16 * kk candidates.  Emits idx in
+// descending key order and the keep mask.
 template <int VPT>
 __global__ __launch_bounds__(1024) void k_topk_small(const float* __restrict__ vals, int K, int kk,
                                                      int64_t* __restrict__ idx, float* __restrict__ keep) {
-  __shared__ unsigned long long cand[16 * 16];
+  constexpr int kCand = 256;
+  __shared__ unsigned long long cand[kCand];
   __shared__ unsigned long long sel[16];
+  __shared__ unsigned long long wmax[16];
+  __shared__ int ncand;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) ncand = 0;
   unsigned long long key[VPT];
+  unsigned long long mine = 0ull;
 #pragma unroll
   for (int e = 0; e < VPT; ++e) {
     const int k = tid + 1024 * e;
     key[e] = k < K ? (((unsigned long long)__float_as_uint(vals[k]) << 32) | (unsigned)(~(unsigned)k)) : 0ull;
     if (k < K) keep[k] = 1.f;
+    mine = key[e] > mine ? key[e] : mine;
   }
-  auto wave_top = [&](unsigned long long* keys, int n, int r) {
+  auto wave_top = [&](unsigned long long* keys, int n) {
     unsigned long long best = 0ull;
     for (int e = 0; e < n; ++e) best = keys[e] > best ? keys[e] : best;
     best = wave_max_u64(best);
     for (int e = 0; e < n; ++e)
       if (keys[e] == best) keys[e] = 0ull;
-    (void)r;
     return best;
   };
-  for (int r = 0; r < kk; ++r) {
-    const unsigned long long b = wave_top(key, VPT, r);
-    if (lane == 0) cand[wave * 16 + r] = b;
-  }
-  __syncthreads();
-  if (wave == 0) {
-    unsigned long long c[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = lane + 64 * j;  // candidate (wave i / 16, rank i % 16)
-      c[j] = (i % 16) < kk ? cand[i] : 0ull;
-    }
+  // wave 0: the final kk from 4 candidates per lane
+  auto final_select = [&](unsigned long long (&c)[4]) {
     for (int r = 0; r < kk; ++r) {
-      const unsigned long long b = wave_top(c, 4, r);
+      const unsigned long long b = wave_top(c, 4);
       if (lane == 0) {
         sel[r] = b;
         idx[r] = (int64_t)(~(unsigned)(b & 0xffffffffull));
       }
+    }
+  };
+  const unsigned long long wm = wave_max_u64(mine);
+  if (lane == 0) wmax[wave] = wm;
+  __syncthreads();
+  unsigned long long T = wmax[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) T = wmax[w] < T ? wmax[w] : T;
+#pragma unroll
+  for (int e = 0; e < VPT; ++e)
+    if (key[e] != 0ull && key[e] >= T) {
+      const int pos = atomicAdd(&ncand, 1);
+      if (pos < kCand) cand[pos] = key[e];
+    }
+  __syncthreads();
+  const int n = ncand;  // the same for every thread: the branch below is uniform
+  if (n <= kCand) {
+    if (wave == 0) {
+      unsigned long long c[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = lane + 64 * j < n ? cand[lane + 64 * j] : 0ull;
+      final_select(c);
+    }
+  } else {
+    __syncthreads();  // every thread has read ncand before cand is reused
+    for (int r = 0; r < kk; ++r) {
+      const unsigned long long b = wave_top(key, VPT);
+      if (lane == 0) cand[wave * 16 + r] = b;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      unsigned long long c[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = lane + 64 * j;  // candidate (wave i / 16, rank i % 16)
+        c[j] = (i % 16) < kk ? cand[i] : 0ull;
+      }
+      final_select(c);
     }
   }
   __syncthreads();  // every keep = 1 store precedes the zeros
