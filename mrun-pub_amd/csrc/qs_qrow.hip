@@ -742,33 +742,6 @@ constexpr bool kGemvXg = MB <= 4 && XT != QS_F32;
 template <int XT, int MB, int U, bool SWI>
 constexpr int kGemvWaves = kGemvXg<XT, MB, U> && !SWI && U > 2 ? QS_GEMV_WG_LONG : GemvShape<SWI, MB>::waves;
 
-// valu_words with the activations in registers: xw holds the 2 * NW packed bf16/f16 words
-// matching weight words 0..NW-1 (the same products and order as valu_words).
-template <int XT, int NW>
-__device__ __forceinline__ void valu_words_r(const int (&w)[4], float sc, const uint32_t* xw, float& acc) {
-#pragma unroll
-  for (int j = 0; j < NW; ++j) {
-    const int d = w[j];
-    if constexpr (XT == QS_BF16) {
-      bf16x2 a, b;
-      a[0] = static_cast<__bf16>(sbyte_f32<0>(d) * sc);
-      a[1] = static_cast<__bf16>(sbyte_f32<1>(d) * sc);
-      b[0] = static_cast<__bf16>(sbyte_f32<2>(d) * sc);
-      b[1] = static_cast<__bf16>(sbyte_f32<3>(d) * sc);
-      acc = __builtin_amdgcn_fdot2_f32_bf16(a, __builtin_bit_cast(bf16x2, xw[2 * j]), acc, false);
-      acc = __builtin_amdgcn_fdot2_f32_bf16(b, __builtin_bit_cast(bf16x2, xw[2 * j + 1]), acc, false);
-    } else {
-      f16x2 a, b;
-      a[0] = static_cast<_Float16>(sbyte_f32<0>(d) * sc);
-      a[1] = static_cast<_Float16>(sbyte_f32<1>(d) * sc);
-      b[0] = static_cast<_Float16>(sbyte_f32<2>(d) * sc);
-      b[1] = static_cast<_Float16>(sbyte_f32<3>(d) * sc);
-      acc = __builtin_amdgcn_fdot2(a, __builtin_bit_cast(f16x2, xw[2 * j]), acc, false);
-      acc = __builtin_amdgcn_fdot2(b, __builtin_bit_cast(f16x2, xw[2 * j + 1]), acc, false);
-    }
-  }
-}
-
 // One weight word (4 codes) -> two packed bf16/f16 pairs, exact (the W8A16 contract).
 template <int XT>
 __device__ __forceinline__ void deq_word(int d, float sc, uint32_t& a, uint32_t& b) {
@@ -1070,13 +1043,14 @@ __global__ __launch_bounds__((GemvShape<false, MB>::waves * 64)) void k_gemv_top
   block_top2<WPB, MB>(v1, i1, v2, i2, p.M, part_v, part_i);
 }
 
-// The same launch for one bf16/f16 activation row and K / 1024 = U (1 or 2) full chunks:
-// each wave loads the activations of its own weight bytes into registers once (as
-// gemv_wave_xg does per row) and walks its rows blk * 8 + wave, blk = g, g + G, ... with
-// the next row's weights in flight while the current row is reduced.  Every load is
-// unconditional (a row past the end re-reads the wave's current row), so the waits stay
-// per buffer.  Same products, order, wave sum and candidates as k_gemv_top2.
-template <int XT, int U, int TB>
+// The same launch for MB = 1 or 2 bf16/f16 activation rows and K / 1024 = U (1 or 2) full
+// chunks: each wave loads the activations of its own weight bytes into registers once
+// (as gemv_wave_xg does per row) and walks its rows blk * 8 + wave, blk = g, g + G, ...
+// with the next row's weights in flight while the current row is reduced.  Every load is
+// unconditional (a row past the end re-reads the wave's current row; activation rows
+// m >= M read row M - 1), so the waits stay per buffer.  Same products, order, wave sum
+// and candidates as k_gemv_top2.
+template <int XT, int MB, int U, int TB>
 __global__ __launch_bounds__(512) void k_gemv_top2_xg(QrowParams p, int rows, int start_row, float* part_v,
                                                       int* part_i) {
   constexpr int WPB = 8;
@@ -1086,29 +1060,32 @@ __global__ __launch_bounds__(512) void k_gemv_top2_xg(QrowParams p, int rows, in
   const int K = p.K;
   constexpr int F = U;  // full chunks (the host checks K >> 10 == U)
   const int rem = K - (F << 10);
-  const uint8_t* xg = static_cast<const uint8_t*>(p.x);
-  uint32_t xc[U][8];
-#pragma unroll
-  for (int c = 0; c < U; ++c) {
-    const uint8_t* a = xg + 2 * (c * 1024 + 16 * lane);
-    const i32x4 v0 = *reinterpret_cast<const i32x4*>(a);
-    const i32x4 v1 = *reinterpret_cast<const i32x4*>(a + 16);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xc[c][e] = static_cast<uint32_t>(v0[e]);
-      xc[c][4 + e] = static_cast<uint32_t>(v1[e]);
-    }
-  }
+  uint32_t xc[U][MB][8];
   constexpr int XTW = TB / 2 > 0 ? TB / 2 : 1;
-  uint32_t xt[XTW];
+  uint32_t xt[MB][XTW];
   const bool tl = TB != 16 || 16 * lane < rem;
-  if constexpr (TB != 0) {
-    const uint8_t* a = tl ? xg + 2 * ((F << 10) + TB * lane) : xg;
 #pragma unroll
-    for (int e = 0; e < TB / 4; ++e) {
-      const u32x2 v = *reinterpret_cast<const u32x2*>(a + 8 * e);
-      xt[2 * e] = v[0];
-      xt[2 * e + 1] = v[1];
+  for (int m = 0; m < MB; ++m) {
+    const uint8_t* xg = static_cast<const uint8_t*>(p.x) + (int64_t)(m < p.M ? m : p.M - 1) * p.ldx * 2;
+#pragma unroll
+    for (int c = 0; c < U; ++c) {
+      const uint8_t* a = xg + 2 * (c * 1024 + 16 * lane);
+      const i32x4 v0 = *reinterpret_cast<const i32x4*>(a);
+      const i32x4 v1 = *reinterpret_cast<const i32x4*>(a + 16);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xc[c][m][e] = static_cast<uint32_t>(v0[e]);
+        xc[c][m][4 + e] = static_cast<uint32_t>(v1[e]);
+      }
+    }
+    if constexpr (TB != 0) {
+      const uint8_t* a = tl ? xg + 2 * ((F << 10) + TB * lane) : xg;
+#pragma unroll
+      for (int e = 0; e < TB / 4; ++e) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(a + 8 * e);
+        xt[m][2 * e] = v[0];
+        xt[m][2 * e + 1] = v[1];
+      }
     }
   }
   const int8_t* codes = p.lin[0].codes;
@@ -1141,19 +1118,42 @@ __global__ __launch_bounds__(512) void k_gemv_top2_xg(QrowParams p, int rows, in
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  float v1[1] = {-INFINITY}, v2[1] = {-INFINITY};
-  int i1[1] = {INT_MAX}, i2[1] = {INT_MAX};
+  float v1[MB], v2[MB];
+  int i1[MB], i2[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    v1[m] = v2[m] = -INFINITY;
+    i1[m] = i2[m] = INT_MAX;
+  }
   auto reduce = [&](int b, int row) {
-    float acc = 0.f;
-    if constexpr (TB == 16) {
-      if (tl) valu_words_r<XT, 4>(tw[b], sc[b], xt, acc);
-    } else if constexpr (TB != 0) {
-      valu_words_r<XT, TB / 4>(tw[b], sc[b], xt, acc);
+    float acc[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[m] = 0.f;
+    if constexpr (TB != 0) {
+      if (tl) {
+#pragma unroll
+        for (int j = 0; j < TB / 4; ++j) {
+          uint32_t a, c2;
+          deq_word<XT>(tw[b][j], sc[b], a, c2);
+#pragma unroll
+          for (int m = 0; m < MB; ++m) acc[m] = dot_word<XT>(a, c2, xt[m][2 * j], xt[m][2 * j + 1], acc[m]);
+        }
+      }
     }
 #pragma unroll
-    for (int c = 0; c < U; ++c) valu_words_r<XT, 4>(wv[b][c], sc[b], xc[c], acc);
-    acc = wave_sum_dpp(acc);
-    if (row < rows) top2_push(acc, start_row + row, v1[0], i1[0], v2[0], i2[0]);
+    for (int c = 0; c < U; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t a, c2;
+        deq_word<XT>(wv[b][c][j], sc[b], a, c2);
+#pragma unroll
+        for (int m = 0; m < MB; ++m) acc[m] = dot_word<XT>(a, c2, xc[c][m][2 * j], xc[c][m][2 * j + 1], acc[m]);
+      }
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      acc[m] = wave_sum_dpp(acc[m]);
+      if (row < rows) top2_push(acc[m], start_row + row, v1[m], i1[m], v2[m], i2[m]);
+    }
   };
   const int stride = (int)gridDim.x * WPB;
   int r = (int)blockIdx.x * WPB + wave;
@@ -1164,7 +1164,7 @@ __global__ __launch_bounds__(512) void k_gemv_top2_xg(QrowParams p, int rows, in
     load(0, r + 2 * stride < rows ? r + 2 * stride : r);
     reduce(1, r + stride);
   }
-  block_top2<WPB, 1>(v1, i1, v2, i2, 1, part_v, part_i);
+  block_top2<WPB, MB>(v1, i1, v2, i2, p.M, part_v, part_i);
 }
 
 // Any K / alignment: one wave per row, one activation row per launch (x points at it),
@@ -1609,13 +1609,13 @@ void launch_top2_tb(const QrowParams& q, int rows, int start_row, float* pv, int
   static_assert(GemvShape<false, 1>::waves == 8, "k_gemv_top2_xg takes the 8-row blocks of top2_grid");
   const dim3 grid((unsigned)top2_grid(rows)), block(WPB * 64);
   const int F = q.K >> 10;
-  if constexpr (MB == 1 && XT != QS_F32) {  // one bf16/f16 row: register activations
+  if constexpr (MB <= 2 && XT != QS_F32) {  // one or two bf16/f16 rows: register activations
     if (F == 1) {
-      hipLaunchKernelGGL((k_gemv_top2_xg<XT, 1, TB>), grid, block, 0, s, q, rows, start_row, pv, pi);
+      hipLaunchKernelGGL((k_gemv_top2_xg<XT, MB, 1, TB>), grid, block, 0, s, q, rows, start_row, pv, pi);
       return;
     }
     if (F == 2) {
-      hipLaunchKernelGGL((k_gemv_top2_xg<XT, 2, TB>), grid, block, 0, s, q, rows, start_row, pv, pi);
+      hipLaunchKernelGGL((k_gemv_top2_xg<XT, MB, 2, TB>), grid, block, 0, s, q, rows, start_row, pv, pi);
       return;
     }
   }
