@@ -187,6 +187,72 @@ def paged_measurement(torch, dev, pages, x_h, x_i, passes: int = 6) -> dict:
     }
 
 
+def paged_moe_measurement(torch, dev, E: int, topk: int, H: int, I: int, layers: int = 2,
+                          steps: int = 4) -> dict:
+    """Config 4's expert layers served from the packed expert store through the HBM slot
+    cache (``ExpertPageCache``), timed by wall clock with a device sync per step (host
+    bookkeeping and H2D fills are not capturable in a graph).
+
+    * ``slots_all``: slots for every page of ``layers`` layers; after one warm-up step
+      every acquire is a hit, so the step costs the resident GEMM plus slot lookups.
+    * ``slots_one_layer_tier``: slots for one layer only and every page in the pinned host
+      tier, so each layer change refills most slots over PCIe (``h2d_GB/s``).
+    """
+    import tempfile
+
+    import numpy as np
+    from mrun_pub_amd import expert_cache, moe
+
+    rng = np.random.default_rng(11)
+    gu = rng.integers(-127, 128, size=(layers, E, 2 * I, H), dtype=np.int8)
+    gus = (rng.uniform(0.5, 1.5, size=(layers, E, 2 * I)) / 127).astype(np.float32)
+    dn = rng.integers(-127, 128, size=(layers, E, H, I), dtype=np.int8)
+    dns = (rng.uniform(0.5, 1.5, size=(layers, E, H)) / 127).astype(np.float32)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    res = {}
+    with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
+        store = expert_cache.PackedInt8ExpertStore(expert_cache.write_int8_expert_store(tmp, gu, gus, dn, dns))
+        del gu, gus, dn, dns
+        stride = store.layout.page_stride
+        total_mb = layers * E * stride / 1e6 + 1
+        tier = expert_cache.HostPageTier(store, host_cache_mb=total_mb)
+        tier.warm()
+        cases = (("slots_all", dict(cache_mb=total_mb, host_tier=None)),
+                 ("slots_one_layer_tier", dict(cache_mb=0, host_tier=tier)))
+        for T in (64, 512):
+            routes = []
+            for _ in range(steps + 1):
+                for layer in range(layers):
+                    w, idx = moe.route_topk(torch.randn(T, E, device=dev, generator=gen), topk)
+                    routes.append((layer, torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16), idx, w))
+            for name, kw in cases:
+                cache = expert_cache.ExpertPageCache(store, device=dev, max_active_pages=E, **kw)
+                backend = moe.Int8ExpertBackend(page_cache=cache)
+                for r in routes[:layers]:
+                    backend.moe(*r)
+                torch.cuda.synchronize()
+                s0 = cache.stats.as_dict()
+                t0 = time.perf_counter()
+                for r in routes[layers:]:
+                    backend.moe(*r)
+                torch.cuda.synchronize()
+                dt = time.perf_counter() - t0
+                s1 = cache.stats.as_dict()
+                n = len(routes) - layers
+                h2d = s1["host_to_device_bytes"] - s0["host_to_device_bytes"]
+                req = s1["page_requests"] - s0["page_requests"]
+                res[f"config4_moe_paged_t{T}_{name}"] = {
+                    "ms_per_layer": round(dt / n * 1e3, 3), "slots": cache.capacity,
+                    "hit_rate": round((s1["page_hits"] - s0["page_hits"]) / max(1, req), 4),
+                    "h2d_MB_per_layer": round(h2d / n / 1e6, 1), "h2d_GB/s": round(h2d / dt / 1e9, 1),
+                }
+                cache.close()
+                del backend, cache
+        store.release()
+    return res
+
+
 def secondary_measurements(torch, dev, stream) -> dict:
     """Configs 1, 3, 4, 5 of BASELINE.json, measured with HIP graphs on one stream."""
     from mrun_pub_amd import lowbit, moe, qrow, w8a8
@@ -274,6 +340,7 @@ def secondary_measurements(torch, dev, stream) -> dict:
                                     "hbm_frac": round(byts / tt / 1e9 / HBM_PEAK_GBS, 4),
                                     "TOPS": round(ops / tt / 1e12, 2), "active_experts": active}
     del layer, backend
+    res.update(paged_moe_measurement(torch, dev, E, topk, H, I))
 
     # config 5: packed int3/int2 GEMV, G=64 fp16 scale+zero, [11008,4096] and [4096,11008]
     for bits in (3, 2):

@@ -254,6 +254,12 @@ int qs_pager_submit(qs_pager* pager, int slot, const void* host, size_t bytes, s
 int qs_pager_seal(qs_pager* pager, int slot);
 int qs_pager_acquire(qs_pager* pager, int slot, void* compute_stream);
 int qs_pager_release(qs_pager* pager, int slot, void* compute_stream);
+/* acquire/release for slots[0..n) in one call (an expert layer's active set).
+ * acquire_many enqueues no wait for a slot whose copies have already landed.
+ * Replace the per-page event ordering of the MoE page cache,
+ * src/mrun/engine/qwen3_moe_cuda.py:1490-1614 (_acquire_resident, acquire_slot_binding). */
+int qs_pager_acquire_many(qs_pager* pager, const int* slots, int n, void* compute_stream);
+int qs_pager_release_many(qs_pager* pager, const int* slots, int n, void* compute_stream);
 /* Block the host until every queued copy has landed. */
 int qs_pager_sync(qs_pager* pager);
 

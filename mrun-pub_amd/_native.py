@@ -74,6 +74,8 @@ SIGNATURES: dict[str, tuple] = {
     "qs_pager_seal": (_I, [_P, _I]),
     "qs_pager_acquire": (_I, [_P, _I, _P]),
     "qs_pager_release": (_I, [_P, _I, _P]),
+    "qs_pager_acquire_many": (_I, [_P, _P, _I, _P]),
+    "qs_pager_release_many": (_I, [_P, _P, _I, _P]),
     "qs_pager_sync": (_I, [_P]),
 }
 

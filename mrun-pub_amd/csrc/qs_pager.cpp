@@ -124,6 +124,36 @@ extern "C" int qs_pager_release(qs_pager* p, int slot, void* compute_stream) {
                    "hipEventRecord(free)");
 }
 
+// Batched forms for an expert layer's whole active set (about 128 slots per acquire).
+// A slot whose ready event has already fired needs no stream wait: a wait on a completed
+// event orders nothing, so skipping it keeps the same ordering with one packet fewer.
+extern "C" int qs_pager_acquire_many(qs_pager* p, const int* slots, int n, void* compute_stream) {
+  if (!p || n < 0 || (n > 0 && !slots)) return fail(QS_ERR_INVALID, "pager_acquire_many: bad arguments");
+  for (int i = 0; i < n; ++i)
+    if (slots[i] < 0 || slots[i] >= p->slots) return fail(QS_ERR_INVALID, "pager_acquire_many: slot out of range");
+  auto stream = static_cast<hipStream_t>(compute_stream);
+  for (int i = 0; i < n; ++i) {
+    hipEvent_t ev = p->ready[slots[i]];
+    hipError_t q = hipEventQuery(ev);
+    if (q == hipSuccess) continue;
+    if (q != hipErrorNotReady) return hip_check(q, "hipEventQuery(ready)");
+    int st = hip_check(hipStreamWaitEvent(stream, ev, 0), "hipStreamWaitEvent(ready)");
+    if (st) return st;
+  }
+  return QS_OK;
+}
+
+extern "C" int qs_pager_release_many(qs_pager* p, const int* slots, int n, void* compute_stream) {
+  if (!p || n < 0 || (n > 0 && !slots)) return fail(QS_ERR_INVALID, "pager_release_many: bad arguments");
+  for (int i = 0; i < n; ++i)
+    if (slots[i] < 0 || slots[i] >= p->slots) return fail(QS_ERR_INVALID, "pager_release_many: slot out of range");
+  for (int i = 0; i < n; ++i) {
+    int st = qs_pager_release(p, slots[i], compute_stream);
+    if (st) return st;
+  }
+  return QS_OK;
+}
+
 extern "C" int qs_pager_sync(qs_pager* p) {
   if (!p) return fail(QS_ERR_INVALID, "pager_sync: null pager");
   return hip_check(hipStreamSynchronize(p->copy), "hipStreamSynchronize(copy)");

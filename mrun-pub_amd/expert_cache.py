@@ -407,9 +407,10 @@ class ExpertPageCache:
     def release(self) -> None:
         """Mark the pages of the last acquire free once the work queued so far on the current
         stream is done (also done implicitly by the next acquire)."""
-        stream = nat.stream_of(self.device)
-        for slot in self._pending_release:
-            nat.call("qs_pager_release", self._pager, slot, stream)
+        if self._pending_release:
+            slots = (ctypes.c_int * len(self._pending_release))(*self._pending_release)
+            nat.call("qs_pager_release_many", self._pager, slots, len(self._pending_release),
+                     nat.stream_of(self.device))
         self._pending_release = []
 
     def synchronize(self) -> None:
@@ -455,7 +456,7 @@ class ExpertPageCache:
 
     def _acquire_resident(self, layer: int, top_indices: torch.Tensor, *, protect: bool):
         self.release()  # the previous acquire's kernels are queued: its slots may be refilled after them
-        routed = [int(v) for v in top_indices.detach().cpu().reshape(-1)]
+        routed = top_indices.detach().reshape(-1).cpu().tolist()
         frequencies = Counter(routed)
         expert_ids = sorted(frequencies)
         if len(expert_ids) > self.max_active_pages:
@@ -474,9 +475,9 @@ class ExpertPageCache:
         if misses:
             self._fill(int(layer), misses)
         slot_list = [self.policy.entries[k] for k in keys]
-        stream = nat.stream_of(self.device)
-        for slot in slot_list:
-            nat.call("qs_pager_acquire", self._pager, slot, stream)
+        if slot_list:
+            nat.call("qs_pager_acquire_many", self._pager, (ctypes.c_int * len(slot_list))(*slot_list),
+                     len(slot_list), nat.stream_of(self.device))
         self._pending_release = list(slot_list)
         self.stats.page_requests += len(keys)
         self.stats.page_misses += len(misses)
