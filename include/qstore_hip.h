@@ -98,6 +98,21 @@ int qs_qrow_top2(const void* x, int x_dtype, int64_t ldx, const int8_t* codes, c
                  int64_t M, int64_t row_count, int64_t K, int64_t start_row, void* workspace,
                  size_t workspace_bytes, int32_t* out_indices, float* out_values, void* stream);
 
+/* No counterpart in the reference.  qs_qrow_top2 without the workspace argument, for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight decode
+ * serving loops, harnesses that forbid hipMalloc).  Same contract and results as
+ * qs_qrow_top2; the candidates live in a per-device scratch array of
+ * QS_TOP2_SCRATCH_BYTES bytes held by the library until the process ends, so the call
+ * allocates nothing.  Sizes whose qs_qrow_top2_workspace_bytes(M, row_count) exceeds
+ * that array are rejected with QS_ERR_LIMIT (about 6 activation rows of a 151,936-row
+ * head).  Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams, two threads) race and must be serialised by the caller. */
+#define QS_TOP2_SCRATCH_BYTES (4 << 20)
+int qs_qrow_top2_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
+                         const float* scales, int64_t M, int64_t row_count, int64_t K,
+                         int64_t start_row, int32_t* out_indices, float* out_values,
+                         void* stream);
+
 /* Replaces _rerank_qrow_candidates_fp32 (dense_qstore_cuda.py:1189-1236): candidates[m][c]
  * (int64 global rows, 1 <= C <= 16) scored as sum_k float(x[m][k]) * (float(code) * scale)
  * in fp32; out_indices[m] (int64) is the best candidate (lowest index on ties) and

@@ -51,6 +51,7 @@ SIGNATURES: dict[str, tuple] = {
     "qs_qrow_swiglu": (_I, [_P, _L, _P, _P, _P, _P, _P, _L, _L, _L, _L, _P]),
     "qs_qrow_top2_workspace_bytes": (ctypes.c_size_t, [_L, _L]),
     "qs_qrow_top2": (_I, [_P, _I, _L, _P, _P, _L, _L, _L, _L, _P, ctypes.c_size_t, _P, _P, _P]),
+    "qs_qrow_top2_noalloc": (_I, [_P, _I, _L, _P, _P, _L, _L, _L, _L, _P, _P, _P]),
     "qs_qrow_rerank_fp32": (_I, [_P, _I, _L, _P, _P, _L, _L, _L, _P, _I, _L, _P, _P, _P]),
     "qs_quant_rows_int8": (_I, [_P, _L, _L, _L, _P, _L, _P, _P]),
     "qs_quant_rows_lowbit": (_I, [_P, _L, _L, _L, _I, _I, _P, _L, _P, _P, _P]),

@@ -38,6 +38,8 @@
 // lane l holds D[4*(l>>4) + q][l & 15], q = 0..3.
 #include "qs_common.h"
 
+#include <mutex>
+
 namespace qs {
 
 struct QrowLin {
@@ -1845,20 +1847,30 @@ extern "C" size_t qs_qrow_top2_workspace_bytes(int64_t M, int64_t row_count) {
   return (size_t)(M * top2_blocks(row_count) * 2) * (sizeof(float) + sizeof(int));
 }
 
-extern "C" int qs_qrow_top2(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
-                            const float* scales, int64_t M, int64_t row_count, int64_t K,
-                            int64_t start_row, void* workspace, size_t workspace_bytes,
-                            int32_t* out_indices, float* out_values, void* stream) {
+namespace qs {
+namespace {
+
+// Argument checks shared by the two top-2 entry points (everything but the workspace).
+int top2_validate(const void* x, int x_dtype, int64_t ldx, const int8_t* codes, const float* scales,
+                  int64_t M, int64_t row_count, int64_t K, int64_t start_row,
+                  const int32_t* out_indices, const float* out_values) {
   if (!codes || !scales || !out_indices || !out_values) return fail(QS_ERR_INVALID, "qrow_top2: null pointer");
   int st = validate_common(x, x_dtype, ldx, M, K);
   if (st) return st;
   if (row_count < 2 || row_count > INT_MAX - 1) return fail(QS_ERR_INVALID, "qrow_top2: row_count must be >= 2");
   if (start_row < 0 || start_row + row_count > INT_MAX) return fail(QS_ERR_LIMIT, "qrow_top2: indices exceed int32");
-  if (M == 0) return QS_OK;
   if (M > 65535) return fail(QS_ERR_LIMIT, "qrow_top2: at most 65535 activation rows");
-  if (!workspace || workspace_bytes < qs_qrow_top2_workspace_bytes(M, row_count))
-    return fail(QS_ERR_INVALID, "qrow_top2: workspace smaller than qs_qrow_top2_workspace_bytes()");
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  return QS_OK;
+}
+
+// Launches of the top-2 search for validated arguments, M >= 1, with the per-block
+// candidates in `workspace` (at least qs_qrow_top2_workspace_bytes(M, row_count) bytes).
+// Every candidate slot the reduce reads is written by the search first, so the workspace
+// needs no clearing between calls.
+int top2_launch(const void* x, int x_dtype, int64_t ldx, const int8_t* codes, const float* scales,
+                int64_t M, int64_t row_count, int64_t K, int64_t start_row, void* workspace,
+                int32_t* out_indices, float* out_values, hipStream_t s) {
+  int st;
   const int es = x_dtype == QS_F32 ? 4 : 2;
   const int64_t nblk_max = top2_blocks(row_count);
   float* pv = static_cast<float*>(workspace);
@@ -1908,6 +1920,85 @@ extern "C" int qs_qrow_top2(const void* x, int x_dtype, int64_t ldx, const int8_
   if (st) return st;
   hipLaunchKernelGGL(k_top2_reduce, dim3((unsigned)M), dim3(256), 0, s, pv, pi, C, out_indices, out_values);
   return hip_check(hipGetLastError(), "k_top2_reduce launch");
+}
+
+}  // namespace
+}  // namespace qs
+
+extern "C" int qs_qrow_top2(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
+                            const float* scales, int64_t M, int64_t row_count, int64_t K,
+                            int64_t start_row, void* workspace, size_t workspace_bytes,
+                            int32_t* out_indices, float* out_values, void* stream) {
+  int st = top2_validate(x, x_dtype, ldx, codes, scales, M, row_count, K, start_row, out_indices,
+                         out_values);
+  if (st) return st;
+  if (M == 0) return QS_OK;
+  if (!workspace || workspace_bytes < qs_qrow_top2_workspace_bytes(M, row_count))
+    return fail(QS_ERR_INVALID, "qrow_top2: workspace smaller than qs_qrow_top2_workspace_bytes()");
+  return top2_launch(x, x_dtype, ldx, codes, scales, M, row_count, K, start_row, workspace,
+                     out_indices, out_values, static_cast<hipStream_t>(stream));
+}
+
+// ---- allocation-free top-2 -------------------------------------------------------------
+// The candidates live in a file-scope device array, one copy per GPU.  Host code never
+// passes `scratch` itself to a kernel: its host-side name is a stand-in, not a device
+// address.  The device address comes from hipGetSymbolAddress, taken once per device
+// with that device current, and kept in g_scratch_ptr.
+static __device__ __align__(256) unsigned char scratch[QS_TOP2_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `dev`, resolved on first use.
+int scratch_ptr(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxDevices) return fail(QS_ERR_UNSUPPORTED, "qrow_top2_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int prev = 0;
+    hipError_t e = hipGetDevice(&prev);
+    if (e != hipSuccess) return hip_check(e, "qrow_top2_noalloc: hipGetDevice");
+    if (prev != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return hip_check(e, "qrow_top2_noalloc: hipSetDevice");
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (prev != dev) {
+      hipError_t r = hipSetDevice(prev);
+      if (e == hipSuccess) e = r;
+    }
+    if (e != hipSuccess) return hip_check(e, "qrow_top2_noalloc: hipGetSymbolAddress(scratch)");
+    if (!p) return fail(QS_ERR_HIP, "qrow_top2_noalloc: scratch has no device address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return QS_OK;
+}
+}  // namespace
+
+extern "C" int qs_qrow_top2_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
+                                    const float* scales, int64_t M, int64_t row_count, int64_t K,
+                                    int64_t start_row, int32_t* out_indices, float* out_values,
+                                    void* stream) {
+  int st = top2_validate(x, x_dtype, ldx, codes, scales, M, row_count, K, start_row, out_indices,
+                         out_values);
+  if (st) return st;
+  if (M == 0) return QS_OK;
+  if (qs_qrow_top2_workspace_bytes(M, row_count) > (size_t)QS_TOP2_SCRATCH_BYTES)
+    return fail(QS_ERR_LIMIT,
+                "qrow_top2_noalloc: M=%lld x %lld rows needs %zu scratch bytes, more than the %d "
+                "bytes of the per-device scratch array",
+                (long long)M, (long long)row_count, qs_qrow_top2_workspace_bytes(M, row_count),
+                QS_TOP2_SCRATCH_BYTES);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int dev = -1;
+  hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_check(e, "qrow_top2_noalloc: stream device");
+  void* ws = nullptr;
+  st = scratch_ptr(dev, &ws);
+  if (st) return st;
+  return top2_launch(x, x_dtype, ldx, codes, scales, M, row_count, K, start_row, ws, out_indices,
+                     out_values, s);
 }
 
 extern "C" int qs_qrow_rerank_fp32(const void* x, int x_dtype, int64_t ldx, const int8_t* codes,
