@@ -48,6 +48,12 @@ const char* qs_last_error(void);
 int qs_qrow_dequant(const int8_t* codes, const float* scales, void* out, int out_dtype,
                     int64_t N, int64_t K, int64_t ld_out, void* stream);
 
+/* Replaces the qrow branch of QStore.embed_rows (src/mrun/engine/kernels/qstore.py:1099-1128):
+ * out[i, k] = float(codes[rows[i], k]) * scales[rows[i]] in fp32 for i < n_rows; rows int64
+ * device indices in [0, N) (an index outside that range yields a zero row, never a read). */
+int qs_qrow_dequant_rows(const int8_t* codes, const float* scales, int64_t N, int64_t K,
+                         const int64_t* rows, int64_t n_rows, float* out, void* stream);
+
 /* Replaces QStore.matmul (qstore.py:1082-1092), fused_qrow_matmul +
  * _qrow_w8a16_kernel (src/mrun/engine/kernels/dense_qstore_cuda.py:1105-1153, 467-512)
  * and dequantized_reference_matmul (dense_qstore_cuda.py:1003-1013):
@@ -168,7 +174,10 @@ int qs_moe_router(const void* logits, int logit_dtype, int64_t T, int E, int k, 
  * (src/mrun/engine/olmoe_cuda.py:989-1135, 131-182): expert-major queue of the T*k
  * assignments in STABLE order (identical to the reference's CPU stable argsort):
  * token_ids[q] = a / k, coef[q] = float(top_w[a]), counts[e], starts[e] (exclusive
- * prefix), inverse[a] = q (nullable).  Expert ids must lie in [0, E); E <= 512. */
+ * prefix), inverse[a] = q (nullable).  Expert ids must lie in [0, E); E <= 512.  An
+ * assignment whose expert lies outside [0, E) is left out of the queue: it counts for no
+ * expert, its inverse entry is -1, and the queue rows past sum(counts) hold token 0 with
+ * coefficient 0, so no consumer reads an unwritten index. */
 int qs_moe_route(const void* top_idx, int idx_dtype, const void* top_w, int w_dtype, int64_t T,
                  int k, int E, int64_t* token_ids, float* coef, int32_t* starts, int32_t* counts,
                  int64_t* inverse, void* stream);
@@ -197,7 +206,8 @@ int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* 
 
 /* Replaces stable_route_reduce / _stable_route_reduce_kernel (qwen3_moe_cuda.py:2561-2664,
  * 2160-2182): out[t, h] = sum over rank r = 0..k-1 (in order) of
- * float(y[inverse[t*k+r], h]) * coef[inverse[t*k+r]], each product rounded to fp32. */
+ * float(y[inverse[t*k+r], h]) * coef[inverse[t*k+r]], each product rounded to fp32.  A
+ * negative inverse entry (a rank qs_moe_route dropped) contributes 0. */
 int qs_moe_route_reduce(const void* expert_out, int y_dtype, const float* coef,
                         const int64_t* inverse, int64_t T, int k, int64_t H, float* out,
                         void* stream);

@@ -45,6 +45,7 @@ SIGNATURES: dict[str, tuple] = {
     "qs_version": (_I, []),
     "qs_last_error": (ctypes.c_char_p, []),
     "qs_qrow_dequant": (_I, [_P, _P, _P, _I, _L, _L, _L, _P]),
+    "qs_qrow_dequant_rows": (_I, [_P, _P, _L, _L, _P, _L, _P, _P]),
     "qs_qrow_matmul": (_I, [_P, _I, _L, _P, _P, _P, _L, _L, _L, _L, _P]),
     "qs_qrow_matmul_row_stable": (_I, [_P, _I, _L, _P, _P, _P, _L, _L, _L, _L, _P]),
     "qs_qrow_matmul_multi": (_I, [_P, _I, _L, _I, _P, _P, _P, _P, _P, _L, _L, _P]),

@@ -127,6 +127,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(const void* __restrict__ top
                                                     int64_t* __restrict__ inverse) {
   __shared__ int cnt[kRouteWaves][kRouteMaxE];
   __shared__ int base[kRouteMaxE];
+  __shared__ int total;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -162,6 +163,7 @@ __global__ __launch_bounds__(1024) void k_moe_route(const void* __restrict__ top
       base[e] = run;
       run += c;
     }
+    total = run;
   }
   __syncthreads();
   if (tid < E) {
@@ -202,7 +204,16 @@ __global__ __launch_bounds__(1024) void k_moe_route(const void* __restrict__ top
       else cw = bf16_bits_to_f32(static_cast<const uint16_t*>(top_w)[i]);
       coef[dest] = cw;
       if (inverse) inverse[i] = dest;
+    } else if (valid && inverse) {
+      inverse[i] = -1;  // expert outside [0, E): no queue row
     }
+  }
+  // Assignments with an expert outside [0, E) are left out of the queue.  The rows they
+  // leave free at its end get token 0 and coefficient 0, so a consumer that walks all A
+  // rows never reads an unwritten index.
+  for (int q = total + tid; q < A; q += 1024) {
+    token_ids[q] = 0;
+    coef[q] = 0.f;
   }
 }
 
@@ -542,8 +553,8 @@ __global__ __launch_bounds__(256) void k_moe_reduce(const void* __restrict__ y,
   float acc = 0.f;
   for (int r = 0; r < k; ++r) {
     const int64_t a = inv[t * k + r];
-    const float v = ld<YT>(y, a * H + h);
-    const float c = mul_rn(v, coef[a]);
+    // a < 0: the route compiler dropped this rank (expert out of range); it adds nothing
+    const float c = a < 0 ? 0.f : mul_rn(ld<YT>(y, a * H + h), coef[a]);
     acc = r == 0 ? c : add_rn(acc, c);
   }
   out[t * H + h] = acc;

@@ -153,6 +153,28 @@ class DenseQStore:
                 self.compact_cache_bytes -= ev.compact_bytes
         return page
 
+    def block_kind(self, name: str) -> str | None:
+        """``"qrow"`` / ``"fp32"`` of a block after alias resolution."""
+        return self.reader.block_kind(name)
+
+    def embed_rows(self, name: str, ids) -> torch.Tensor:
+        """fp32 rows ``ids`` of a qrow block, shape ``[*ids.shape, in]``, on the store's device
+        (qstore.py:1099-1128).  Reads only those rows from the host file unless the block is
+        already on the device."""
+        key = self._physical(name)
+        page = self._resident.get(key) or self.compact_cache.get(key)
+        if page is not None:
+            return _qrow.qrow_embed_rows(page.codes, page.scales, ids)
+        if self.reader.blocks[key].get("kind") != "qrow":
+            raise ValueError(f"{name} is not a qrow block")
+        out = int(self.reader.blocks[key]["shape"][0])
+        flat, shape = _qrow.normalize_row_ids(ids, out)
+        uniq, inverse = np.unique(flat.reshape(-1), return_inverse=True)
+        codes, scales = self.reader.qrow_rows(key, uniq)
+        c = torch.from_numpy(np.ascontiguousarray(codes)).to(self.device)
+        s = torch.from_numpy(np.ascontiguousarray(scales)).to(self.device)
+        return _qrow.qrow_embed_rows(c, s, inverse.reshape(shape))
+
     def weight(self, name: str) -> torch.Tensor:
         """Materialized ``[out, in]`` weight in the compute dtype (qstore.py:1026-1080)."""
         page = self.compact_page(name)

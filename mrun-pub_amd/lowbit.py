@@ -174,6 +174,35 @@ class DeviceLowbitQStore:
     def weight(self, name: str) -> torch.Tensor:
         return lowbit_dequant(self.page(name))
 
+    def has(self, name: str) -> bool:
+        return str(name) in self.blocks
+
+    def block_kind(self, name: str) -> str | None:
+        return self._resolve(name)[1].get("kind")
+
+    def embed_rows(self, name: str, ids) -> torch.Tensor:
+        """fp32 rows ``ids`` of a packed block, ``[*ids.shape, in]`` (qstore.py:1382-1395,
+        1513-1526).  Only the selected rows are read from the host file."""
+        from .qrow import normalize_row_ids
+
+        key, b = self._resolve(name)
+        if b.get("kind") not in self._KIND_BITS:
+            raise ValueError(f"{name} is not a packed low-bit block")
+        out, inn = (int(v) for v in b["shape"])
+        rb, ng = int(b["row_bytes"]), int(b["n_groups"])
+        G = int(b.get("group_size", self.G))
+        flat, shape = normalize_row_ids(ids, out)
+        flat = flat.reshape(-1)
+        if flat.size == 0:
+            return torch.empty((*shape, inn), dtype=torch.float32, device=self.device)
+        packed = np.asarray(self.w[b["w_off"] : b["w_off"] + out * rb], dtype=np.uint8).reshape(out, rb)
+        so = int(b["s_off"]) // 4
+        scales = np.asarray(self.s[so : so + out * ng], dtype=np.float32).reshape(out, ng)
+        sel = LowbitPage(key, self._KIND_BITS[b["kind"]], G, inn,
+                         torch.from_numpy(np.ascontiguousarray(packed[flat])).to(self.device),
+                         torch.from_numpy(np.ascontiguousarray(scales[flat])).to(self.device))
+        return lowbit_dequant(sel).reshape(*shape, inn)
+
     def matmul(self, name: str, x: torch.Tensor) -> torch.Tensor:
         return lowbit_matmul(self.page(name), x)
 

@@ -72,6 +72,12 @@ def _route_impl(top_indices, top_weights, num_experts: int, include_inverse: boo
         raise ValueError("top_indices must be int32 or int64")
     if top_weights.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("top_weights must be float32 or bfloat16")
+    if top_indices.device.type == "cpu" and top_indices.numel():
+        # host tensors are checked here; on the device the route kernel drops such
+        # assignments instead (no sync in the hot path), see qs_moe_route
+        lo, hi = int(top_indices.min()), int(top_indices.max())
+        if lo < 0 or hi >= num_experts:
+            raise ValueError(f"top_indices must lie in [0, {num_experts}); found [{lo}, {hi}]")
     device = nat.require_device(top_indices, top_weights)
     rows, top_k = map(int, top_indices.shape)
     A = rows * top_k

@@ -370,6 +370,23 @@ class PagedQStore:
             raise KeyError(f"QStore has no fp32 block {name!r}")
         return torch.from_numpy(self.reader.fp32(name)).to(self.device)
 
+    def block_kind(self, name: str) -> str | None:
+        """``"qrow"`` / ``"fp32"`` of a block after alias resolution."""
+        if self.reader is not None:
+            return self.reader.block_kind(name)
+        return "qrow" if str(name) in self.tier.blocks else None
+
+    def embed_rows(self, name: str, ids) -> torch.Tensor:
+        """fp32 rows ``ids`` of a qrow block, ``[*ids.shape, in]`` (qstore.py:1099-1128).  Only
+        the selected rows leave the pinned host tier; the ring is not involved."""
+        key = self._physical(name)
+        codes, scales = self.tier.codes(key), self.tier.scales(key)
+        flat, shape = _qrow.normalize_row_ids(ids, int(codes.shape[0]))
+        uniq, inverse = np.unique(flat.reshape(-1), return_inverse=True)
+        c = torch.from_numpy(np.ascontiguousarray(codes[uniq])).to(self.device)
+        sc = torch.from_numpy(np.ascontiguousarray(scales[uniq])).to(self.device)
+        return _qrow.qrow_embed_rows(c, sc, inverse.reshape(shape))
+
     def _acquire(self, name: str) -> CompactQRowPage:
         key = self._physical(name)
         page = self.ring.take(key) if self.prefetch else None

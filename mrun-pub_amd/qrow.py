@@ -99,6 +99,35 @@ def qrow_dequant(
     return out
 
 
+def normalize_row_ids(ids, n_rows: int):
+    """Host row indices of an embedding lookup: any integer array, negative values count
+    from the end as numpy indexing does; IndexError outside ``[-n_rows, n_rows)``."""
+    import numpy as np
+
+    idx = np.asarray(ids)
+    if idx.dtype.kind not in "iu":
+        raise TypeError("embedding row ids must be integers")
+    idx = idx.astype(np.int64)
+    if idx.size and (int(idx.min()) < -n_rows or int(idx.max()) >= n_rows):
+        raise IndexError(f"embedding row id out of range for {n_rows} rows")
+    return np.where(idx < 0, idx + n_rows, idx), idx.shape
+
+
+@torch.inference_mode()
+def qrow_embed_rows(codes: torch.Tensor, scales: torch.Tensor, ids) -> torch.Tensor:
+    """fp32 rows ``float(codes[ids]) * scales[ids]`` with shape ``[*ids.shape, in]``
+    (the qrow branch of ``QStore.embed_rows``, qstore.py:1099-1128)."""
+    n, k = _check_codes(codes, scales)
+    flat, shape = normalize_row_ids(ids, n)
+    device = nat.require_device(codes, scales)
+    rows = torch.from_numpy(flat.reshape(-1)).to(device)
+    out = torch.empty((rows.numel(), k), dtype=torch.float32, device=device)
+    if rows.numel():
+        nat.call("qs_qrow_dequant_rows", nat.ptr(codes), nat.ptr(scales), n, k, nat.ptr(rows),
+                 int(rows.numel()), nat.ptr(out), nat.stream_of(device))
+    return out.reshape(*shape, k)
+
+
 @torch.inference_mode()
 def qrow_matmul(
     codes: torch.Tensor, scales: torch.Tensor, x: torch.Tensor, *, row_stable: bool = False

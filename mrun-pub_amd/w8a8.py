@@ -13,13 +13,12 @@ The whole contract runs on the device through ``csrc/qs_w8a8.hip``:
    ``y = side + (float(acc) * act_scale) * sc_w`` (``qs_w8a8_gemm``), fp32 or bf16 out.
 
 ``_int8_gemm`` exposes the raw int32 accumulators (``qs_gemm_i8i8_i32``); they equal the
-exact integer product.  ``enable_w8a8`` / ``disable_w8a8`` rebind ``store.matmul`` of a
-``DenseQStore`` exactly like the reference (w8a8.py:145-187).
+exact integer product.  ``enable_w8a8`` / ``disable_w8a8`` keep the reference's public
+names and keywords (w8a8.py:145-187) over a binding object of this module's own design.
 """
 
 from __future__ import annotations
 
-import types
 from typing import Any
 
 import torch
@@ -166,26 +165,37 @@ def w8a8_matmul(
     return y.reshape(*x.shape[:-1], out)
 
 
-# ---- opt-in store hook (w8a8.py:130-187) -----------------------------------------------
+# ---- opt-in store hook (public names and keywords of w8a8.py:130-187) ----------------
+#
+# ``enable_w8a8`` attaches one ``_W8A8Binding`` to the store instance.  The binding owns
+# the settings and the matmul the store had before; the store's ``matmul`` attribute is a
+# small callable that routes qrow blocks through ``w8a8_matmul`` and everything else to
+# that saved matmul.  A second ``enable_w8a8`` only replaces the settings (the saved
+# matmul stays the one from before the first call), and ``disable_w8a8`` puts back exactly
+# the attribute state the store had.  Any store that exposes ``compact_page(name)`` (int8
+# codes + fp32 scales on the device) and ``block_kind(name)`` can be switched.
 
-_ORIG_MATMUL: dict[int, Any] = {}
 
+class _W8A8Binding:
+    __slots__ = ("store", "previous", "had_instance_attr", "protect_k", "protect_lists", "use_int_mm")
 
-def _raw_qrow(store: Any, name: str) -> tuple[torch.Tensor, torch.Tensor]:
-    """``(int8 [out,in], fp32 [out])`` of a qrow block without dequantization."""
-    page = store.compact_page(name)
-    return page.codes, page.scales
+    def __init__(self, store: Any, protect_k: int, protect_lists: dict[str, Any], use_int_mm: bool):
+        self.store = store
+        self.had_instance_attr = "matmul" in vars(store)
+        self.previous = store.matmul
+        self.configure(protect_k, protect_lists, use_int_mm)
 
+    def configure(self, protect_k: int, protect_lists: dict[str, Any], use_int_mm: bool) -> None:
+        self.protect_k = int(protect_k)
+        self.protect_lists = dict(protect_lists)
+        self.use_int_mm = bool(use_int_mm)
 
-def _w8a8_matmul_method(self: Any, name: str, x: torch.Tensor) -> torch.Tensor:
-    blk = self.reader._resolve(name) if hasattr(self, "reader") else self._resolve(name)
-    if blk.get("kind") != "qrow":
-        return _ORIG_MATMUL[id(self)](name, x)
-    cfg = self._w8a8
-    q_w, sc_w = _raw_qrow(self, name)
-    return w8a8_matmul(
-        q_w, sc_w, x, protect_idx=cfg["lists"].get(name), protect_k=cfg["k"], use_int_mm=cfg["use_int_mm"]
-    )
+    def __call__(self, name: str, x: torch.Tensor) -> torch.Tensor:
+        if self.store.block_kind(name) != "qrow":
+            return self.previous(name, x)
+        page = self.store.compact_page(name)
+        return w8a8_matmul(page.codes, page.scales, x, protect_idx=self.protect_lists.get(name),
+                           protect_k=self.protect_k, use_int_mm=self.use_int_mm)
 
 
 def enable_w8a8(
@@ -195,18 +205,30 @@ def enable_w8a8(
     protect_lists: dict[str, Any] | None = None,
     use_int_mm: bool = True,
 ) -> Any:
-    """Flip one store into W8A8 mode by rebinding ``matmul`` (reversible)."""
-    _ORIG_MATMUL[id(store)] = store.matmul
-    store._w8a8 = {"k": int(protect_k), "lists": protect_lists or {}, "use_int_mm": bool(use_int_mm)}
-    store.matmul = types.MethodType(_w8a8_matmul_method, store)
+    """Route the qrow projections of one store through W8A8 (reversible, idempotent).
+
+    ``protect_k`` outlier columns per call stay in fp32; ``protect_lists`` maps block names
+    to fixed column lists, which take the place of the per-call top-k for those blocks.
+    """
+    for attr in ("compact_page", "block_kind"):
+        if not callable(getattr(store, attr, None)):
+            raise TypeError(f"enable_w8a8 needs a store with {attr}(name)")
+    binding = vars(store).get("_w8a8_binding")
+    if binding is None:
+        binding = _W8A8Binding(store, protect_k, protect_lists or {}, use_int_mm)
+        store._w8a8_binding = binding
+        store.matmul = binding
+    else:
+        binding.configure(protect_k, protect_lists or {}, use_int_mm)
     return store
 
 
 def disable_w8a8(store: Any) -> Any:
-    """Restore the matmul of a store flipped by :func:`enable_w8a8`."""
-    orig = _ORIG_MATMUL.pop(id(store), None)
-    if orig is not None:
-        store.matmul = orig
-    if hasattr(store, "_w8a8"):
-        del store._w8a8
+    """Give the store back the matmul it had before :func:`enable_w8a8` (no-op if not enabled)."""
+    binding = vars(store).pop("_w8a8_binding", None)
+    if binding is not None:
+        if binding.had_instance_attr:
+            store.matmul = binding.previous
+        else:
+            del store.matmul
     return store

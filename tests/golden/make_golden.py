@@ -8,6 +8,13 @@ plain ``.npz`` fixtures (arrays only, loaded with ``allow_pickle=False``) plus
 ``golden_manifest.json`` (SHA-256 per file).  Nothing here runs at test time and the
 reference never travels with the fixtures.
 
+Sections (pass their names after the reference root to write only those; default: all):
+* ``core``     -- w8a8.npz, codecs.npz, moe.npz
+* ``refstore`` -- refstore/legacy (a store in the reference's own test layout,
+  tests/test_qstore_cache.py:19-46) and refstore/v3 (a v3 store sealed by the reference's
+  provenance functions), with refstore.npz / refstore.json holding what the reference's
+  ``QStore`` returns for them (weight, embed_rows, matmul, identity digests)
+
 Functions covered (reference file:line):
 * w8a8_matmul, _int8_gemm              src/mrun/engine/kernels/w8a8.py:33-125
 * _quant_row_int3                      src/mrun/engine/kernels/qstore_int3.py:42-56
@@ -15,6 +22,10 @@ Functions covered (reference file:line):
 * _quant_row_int8                      src/mrun/engine/kernels/qstore_build.py:496-501
 * grouped_route_tensors_with_inverse   src/mrun/engine/olmoe_cuda.py:1108-1135 (CPU branch)
 * stable_route_reduce                  src/mrun/engine/qwen3_moe_cuda.py:2561-2664 (CPU branch)
+* QStore.weight / embed_rows / matmul, _load_qstore_manifest
+                                       src/mrun/engine/kernels/qstore.py:326-373, 1026-1128
+* build_source/builder/derived_provenance
+                                       src/mrun/store_provenance.py:86-275, 390-412
 """
 
 from __future__ import annotations
@@ -29,8 +40,129 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 
 
-def main(ref_root: str) -> None:
+def _write_legacy_store(d: Path, shapes: dict, seed: int) -> None:
+    """A qrow-only store in the reference's test layout (no dtype, no schema version, an
+    unreferenced 4-byte extras file), written with this script's own code."""
+    rng = np.random.default_rng(seed)
+    blocks, w_parts, s_parts = {}, [], []
+    w_off = s_off = 0
+    for name, (out, inn) in shapes.items():
+        q = rng.integers(-128, 128, size=(out, inn), dtype=np.int8)
+        sc = (rng.random(out) + 0.1).astype(np.float32)
+        blocks[name] = {"kind": "qrow", "shape": [out, inn], "w_off": w_off, "w_len": out * inn,
+                        "s_off": s_off, "s_len": out * 4}
+        w_parts.append(q.reshape(-1))
+        s_parts.append(sc)
+        w_off += out * inn
+        s_off += out * 4
+    d.mkdir(parents=True)
+    np.concatenate(w_parts).tofile(d / "weights.i8")
+    np.concatenate(s_parts).tofile(d / "scales.f32")
+    np.zeros(1, np.float32).tofile(d / "extras.f32")
+    (d / "manifest.json").write_text(json.dumps({"arch": "qwen2", "config": {"hidden_size": 8}, "blocks": blocks}))
+
+
+def refstore_section(files: dict) -> None:
+    import shutil
+    import tempfile
+
+    import torch
+
+    from mrun import store_provenance as sp
+    from mrun.engine.kernels import qstore_build as qb
+    from mrun.engine.kernels.qstore import QStore
+
+    root = HERE / "refstore"
+    if root.exists():
+        shutil.rmtree(root)
+    root.mkdir()
+    arrays: dict = {}
+    info: dict = {}
+
+    # legacy store: reference test layout, opened by the reference without validation
+    _write_legacy_store(root / "legacy", {"L0.q": (32, 16), "L0.up": (48, 16)}, seed=0)
+    st = QStore("legacy", root=root)
+    ids = np.array([[3, 0, 31], [7, 7, 1]], dtype=np.int64)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 16)).astype(np.float32)
+    arrays["legacy_ids"] = ids
+    arrays["legacy_x"] = x
+    for name in ("L0.q", "L0.up"):
+        arrays[f"legacy_weight_{name}"] = st.weight(name).numpy()
+        arrays[f"legacy_embed_{name}"] = st.embed_rows(name, ids).numpy()
+        arrays[f"legacy_matmul_{name}"] = st.matmul(name, torch.from_numpy(x)).numpy()
+    stb = QStore("legacy", root=root, compute_dtype="bf16")
+    arrays["legacy_weight_bf16_L0.up"] = stb.weight("L0.up").float().numpy()
+    info["legacy"] = {"identity_status": st.identity_status,
+                      "content_identity_verified": bool(st.content_identity_verified)}
+
+    # v3 store: blocks written here, provenance records built by the reference's own
+    # functions over a tiny stand-in checkpoint directory, opened (and so verified) by the
+    # reference's QStore
+    d = root / "v3"
+    d.mkdir()
+    rng = np.random.default_rng(1)
+    blocks = {}
+    q0 = rng.integers(-127, 128, size=(24, 32), dtype=np.int8)
+    s0 = (rng.uniform(0.5, 1.5, 24) / 127).astype(np.float32)
+    q1 = rng.integers(-127, 128, size=(16, 24), dtype=np.int8)
+    s1 = (rng.uniform(0.5, 1.5, 16) / 127).astype(np.float32)
+    n0 = rng.standard_normal(32).astype(np.float32)
+    (d / "weights.i8").write_bytes(q0.tobytes() + q1.tobytes())
+    (d / "scales.f32").write_bytes(s0.tobytes() + s1.tobytes())
+    (d / "extras.f32").write_bytes(n0.tobytes())
+    blocks["L0.gate"] = {"kind": "qrow", "shape": [24, 32], "w_off": 0, "w_len": 768, "s_off": 0, "s_len": 96}
+    blocks["L0.down"] = {"kind": "qrow", "shape": [16, 24], "w_off": 768, "w_len": 384, "s_off": 96, "s_len": 64}
+    blocks["L0.norm"] = {"kind": "fp32", "shape": [32], "e_off": 0, "e_len": 128}
+    blocks["lm_head"] = {"alias": "L0.gate"}
+    with tempfile.TemporaryDirectory() as tmp:
+        ck = Path(tmp) / "ckpt"
+        ck.mkdir()
+        (ck / "config.json").write_text(json.dumps({"hidden_size": 32}))
+        (ck / "model.safetensors").write_bytes(b"stand-in checkpoint shard")
+        source = sp.build_source_provenance(ck, [ck / "model.safetensors"], model_name="tiny-v3",
+                                            hf_id="local/tiny-v3", revision="0" * 40)
+    builder = sp.build_builder_provenance([Path(qb.__file__)], name="qstore_build",
+                                          schema_version=qb.QSTORE_SCHEMA,
+                                          quantization=qb.QSTORE_QUANTIZATION)
+    manifest = {"schema_version": qb.QSTORE_SCHEMA, "model_name": "tiny-v3", "arch": "qwen2",
+                "dtype": "int8", "tie_word_embeddings": False, "config": {"hidden_size": 32},
+                "source": source, "builder": builder, "blocks": blocks}
+    manifest["derived"] = sp.build_derived_provenance(d, qb.QSTORE_FILES, semantic_manifest=manifest)
+    (d / "manifest.json").write_text(json.dumps(manifest, indent=2, sort_keys=True) + "\n")
+    st3 = QStore("v3", root=root)
+    assert st3.content_identity_verified, st3.identity_status
+    info["v3"] = {k: st3.store_identity.get(k) for k in
+                  ("identity_status", "content_identity_verified", "source_checkpoint_sha256",
+                   "derived_store_sha256", "manifest_semantic_sha256")}
+    x3 = np.random.default_rng(9).standard_normal((2, 32)).astype(np.float32)
+    arrays["v3_x"] = x3
+    arrays["v3_weight_lm_head"] = st3.weight("lm_head").numpy()
+    arrays["v3_matmul_L0.gate"] = st3.matmul("L0.gate", torch.from_numpy(x3)).numpy()
+    arrays["v3_weight_L0.down"] = st3.weight("L0.down").numpy()
+    arrays["v3_fp32_L0.norm"] = st3.fp32("L0.norm").numpy()
+    files["refstore.npz"] = arrays
+    (HERE / "refstore.json").write_text(json.dumps(info, indent=1, sort_keys=True) + "\n")
+
+
+def main(ref_root: str, sections: list[str]) -> None:
     sys.path.insert(0, str(Path(ref_root) / "src"))
+    files: dict = {}
+    if "refstore" in sections:
+        refstore_section(files)
+    if "core" in sections:
+        core_section(files)
+    manifest_path = HERE / "golden_manifest.json"
+    manifest = json.loads(manifest_path.read_text()) if manifest_path.exists() else {}
+    for name, arrs in files.items():
+        path = HERE / name
+        np.savez(path, **arrs)
+        manifest[name] = hashlib.sha256(path.read_bytes()).hexdigest()
+    manifest_path.write_text(json.dumps(manifest, indent=1, sort_keys=True) + "\n")
+    print(json.dumps(manifest, indent=1))
+
+
+def core_section(files: dict) -> None:
     import torch
 
     from mrun.engine.kernels.qstore_build import _quant_row_int8
@@ -102,14 +234,9 @@ def main(ref_root: str) -> None:
     arrays["red_bf16"] = stable_route_reduce(eob, coef.to(torch.bfloat16), tok, counts, ti, sel).numpy()
     files["moe.npz"] = arrays
 
-    manifest = {}
-    for name, arrs in files.items():
-        path = HERE / name
-        np.savez(path, **arrs)
-        manifest[name] = hashlib.sha256(path.read_bytes()).hexdigest()
-    (HERE / "golden_manifest.json").write_text(json.dumps(manifest, indent=1) + "\n")
-    print(json.dumps(manifest, indent=1))
 
+SECTIONS = ("core", "refstore")
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    main(root, sys.argv[2:] or list(SECTIONS))

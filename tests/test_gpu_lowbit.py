@@ -136,4 +136,12 @@ def test_reference_store_reader(dev, tmp_path):
     x = rng.standard_normal((3, 256)).astype(np.float32)
     y = store.matmul("W2", torch.from_numpy(x).to(dev))
     assert oq.rel_l2(y.cpu().numpy(), ol.lowbit_matmul(packed, scales, x, 256, 3, 128)) <= F32_TOL
-    assert np.array_equal(store.weight("W").cpu().numpy(), ol.dequant(packed, scales, 256, 3, 128))
+    full = ol.dequant(packed, scales, 256, 3, 128)
+    assert np.array_equal(store.weight("W").cpu().numpy(), full)
+    # embed_rows (qstore.py:1382-1395): any id shape, negative ids from the end
+    ids = np.array([[0, 69, -1], [5, 5, 33]])
+    e = store.embed_rows("W2", ids)
+    assert e.shape == (2, 3, 256) and e.dtype == torch.float32
+    assert np.array_equal(e.cpu().numpy(), full[ids])
+    with pytest.raises(IndexError):
+        store.embed_rows("W", np.array([70]))

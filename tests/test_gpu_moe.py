@@ -52,6 +52,41 @@ def test_route_equals_stable_argsort(dev, T, E, k, wdt):
     assert coef.dtype == wdt
 
 
+def test_route_drops_out_of_range_experts(dev):
+    """Device indices outside [0, E) leave the queue (no host sync): the valid assignments
+    keep the stable order, inverse is -1 for the dropped ones, the spare queue rows hold
+    token 0 / coefficient 0, and the reduce adds nothing for a dropped rank."""
+    E, k = 6, 3
+    top = np.array([[0, 5, 2], [-1, 1, 6], [2, 3, 99]], dtype=np.int64)
+    w = np.arange(1, 10, dtype=np.float32).reshape(3, 3) / 10
+    tok, coef, starts, counts, inv, _ = _moe().grouped_route_tensors_with_inverse(
+        _t(top, dev), _t(w, dev), num_experts=E)
+    keep = (top >= 0) & (top < E)
+    r_tok, r_coef, r_starts, r_counts, r_inv = om.route_stable(np.where(keep, top, 0)[keep][None, :], w[keep][None, :], E)
+    n = int(keep.sum())
+    assert counts.cpu().numpy().tolist() == np.bincount(top[keep], minlength=E).tolist()
+    assert starts.cpu().numpy().tolist() == r_starts.tolist()
+    flat_tok = (np.arange(9) // 3)[keep.reshape(-1)]
+    assert tok.cpu().numpy()[:n].tolist() == flat_tok[np.argsort(top[keep], kind="stable")].tolist()
+    assert tok.cpu().numpy()[n:].tolist() == [0] * (9 - n)
+    assert coef.cpu().numpy()[n:].tolist() == [0.0] * (9 - n)
+    inv_h = inv.cpu().numpy()
+    assert (inv_h[~keep.reshape(-1)] == -1).all() and sorted(inv_h[keep.reshape(-1)].tolist()) == list(range(n))
+    H = 8
+    eo = np.random.default_rng(0).standard_normal((9, H)).astype(np.float32)
+    red = _moe().stable_route_reduce(_t(eo, dev), coef, tok, counts, _t(top, dev), torch.arange(E, device=dev),
+                                     inverse_assignments=inv)
+    ref = np.zeros((3, H), np.float32)
+    for t in range(3):
+        acc = None
+        for r in range(3):
+            q = inv_h[t * 3 + r]
+            c = np.float32(0) * eo[0] if q < 0 else (eo[q] * coef.cpu().numpy()[q]).astype(np.float32)
+            acc = c if acc is None else (acc + c).astype(np.float32)
+        ref[t] = acc
+    assert np.array_equal(red.float().cpu().numpy(), ref)
+
+
 def test_router_against_oracle(dev):
     rng = np.random.default_rng(4)
     logits = rng.standard_normal((512, 128)).astype(np.float32)

@@ -203,3 +203,27 @@ def test_enable_w8a8_on_dense_store(dev, tmp_path):
     assert oq.rel_l2(yq.cpu().numpy(), ow.w8a8_matmul(q_w, sc_w, x, protect_k=8)) <= F32_TOL
     disable_w8a8(store)
     assert torch.equal(store.matmul("L0.q", torch.from_numpy(x).to(dev)), base)
+
+
+def test_enable_w8a8_twice_then_disable(dev, tmp_path):
+    """A second enable only changes the settings; disable restores the original matmul, and
+    non-qrow blocks keep going to it while enabled."""
+    from mrun_pub_amd.dense_store import DenseQStore
+    from mrun_pub_amd.store import write_qstore
+    from mrun_pub_amd.w8a8 import disable_w8a8, enable_w8a8
+
+    rng, q_w, sc_w = _weights(96, 128, 22)
+    d = write_qstore(tmp_path / "s", {"L0.q": (q_w, sc_w)}, {"L0.norm": np.ones(128, np.float32)})
+    store = DenseQStore(d, device=dev, compute_dtype="fp32")
+    x = torch.from_numpy(rng.standard_normal((3, 128)).astype(np.float32)).to(dev)
+    base = store.matmul("L0.q", x)
+    enable_w8a8(store, protect_k=8)
+    enable_w8a8(store, protect_k=4)
+    y4 = store.matmul("L0.q", x)
+    assert oq.rel_l2(y4.cpu().numpy(), ow.w8a8_matmul(q_w, sc_w, x.cpu().numpy(), protect_k=4)) <= F32_TOL
+    with pytest.raises(ValueError, match="not a qrow block"):
+        store.matmul("L0.norm", x)  # routed to the original matmul, which refuses fp32 blocks
+    disable_w8a8(store)
+    assert "matmul" not in vars(store)
+    assert torch.equal(store.matmul("L0.q", x), base)
+    disable_w8a8(store)  # no-op
