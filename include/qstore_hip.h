@@ -182,6 +182,40 @@ int qs_moe_route(const void* top_idx, int idx_dtype, const void* top_w, int w_dt
                  int k, int E, int64_t* token_ids, float* coef, int32_t* starts, int32_t* counts,
                  int64_t* inverse, void* stream);
 
+/* Replaces build_expert_queue / build_expert_queue_flat / build_expert_queue_device
+ * (src/mrun/engine/kernels/expert_queue.py:242-470): compiles A router packets into
+ * expert-major ranges in STABLE order (equal to the reference's CPU argsort(stable=True)).
+ * Dense form (tokens = slots = nullptr, A = rows * top_k): packet a is route slot a % top_k of
+ * row a / top_k.  Flat form: tokens[a], slots[a] given.  experts I32/I64 [A], weights
+ * F32/BF16/F16 [A] (stored as fp32 coefficients), row_epochs / row_deadlines int64 [rows].
+ * Outputs (queue order): token_ids, expert_ids, route_slots, coefficients, epochs and
+ * deadlines (of the packet's row) [A]; starts / counts [E] as I32 or I64 (count_dtype).  A
+ * packet whose expert lies outside [0, E) is left out (the host validates first where the
+ * reference does); the rows it frees at the end hold token 0, expert -1, slot -1, epoch
+ * INT64_MIN.  E <= 512. */
+int qs_expert_queue_build(const void* experts, int expert_dtype, const int64_t* tokens,
+                          const int64_t* slots, const void* weights, int weight_dtype,
+                          const int64_t* row_epochs, const int64_t* row_deadlines, int64_t A,
+                          int top_k, int64_t rows, int E, int64_t* token_ids, int64_t* expert_ids,
+                          int64_t* route_slots, float* coefficients, int64_t* epochs,
+                          int64_t* deadlines, void* starts, void* counts, int count_dtype,
+                          void* stream);
+
+/* Replaces scatter_committed / scatter_committed_device (expert_queue.py:487-560):
+ * valid[q] = (epochs[q] == active_epochs[token_ids[q]]) (uint8), and for every row t
+ * reduced[t, h] = sum over its valid packets q in ascending queue order of
+ * fp32(float(expert_out[q, h]) * coefficients[q]), accumulated from 0 in that order (the
+ * roundings of the reference's index_add_; no atomics, same bits on every call).  Packets
+ * are identified per row by their route slot (< top_k <= 64).  workspace:
+ * qs_expert_queue_scatter_workspace_bytes(rows, top_k) bytes.  rows <= 65535. */
+size_t qs_expert_queue_scatter_workspace_bytes(int64_t rows, int top_k);
+int qs_expert_queue_scatter(const int64_t* token_ids, const int64_t* route_slots,
+                            const float* coefficients, const int64_t* epochs,
+                            const int64_t* active_epochs, const void* expert_out, int out_dtype,
+                            int64_t ld_out, int64_t A, int64_t rows, int top_k, int64_t H,
+                            void* workspace, size_t workspace_bytes, float* reduced,
+                            uint8_t* valid, void* stream);
+
 /* Routed-row quantization (int8 analogue of quantize_fp8_activation,
  * olmoe_cuda.py:1173-1176, with the W8A8 recipe of w8a8.py:118-121):
  * row a of the output is source[rows[a]] (rows nullable = identity). */

@@ -10,6 +10,7 @@ reference never travels with the fixtures.
 
 Sections (pass their names after the reference root to write only those; default: all):
 * ``core``     -- w8a8.npz, codecs.npz, moe.npz
+* ``queue``    -- queue.npz: build_expert_queue / build_expert_queue_flat / scatter_committed
 * ``refstore`` -- refstore/legacy (a store in the reference's own test layout,
   tests/test_qstore_cache.py:19-46) and refstore/v3 (a v3 store sealed by the reference's
   provenance functions), with refstore.npz / refstore.json holding what the reference's
@@ -22,6 +23,8 @@ Functions covered (reference file:line):
 * _quant_row_int8                      src/mrun/engine/kernels/qstore_build.py:496-501
 * grouped_route_tensors_with_inverse   src/mrun/engine/olmoe_cuda.py:1108-1135 (CPU branch)
 * stable_route_reduce                  src/mrun/engine/qwen3_moe_cuda.py:2561-2664 (CPU branch)
+* build_expert_queue(_flat), scatter_committed
+                                       src/mrun/engine/kernels/expert_queue.py:242-398, 487-514
 * QStore.weight / embed_rows / matmul, _load_qstore_manifest
                                        src/mrun/engine/kernels/qstore.py:326-373, 1026-1128
 * build_source/builder/derived_provenance
@@ -152,6 +155,8 @@ def main(ref_root: str, sections: list[str]) -> None:
         refstore_section(files)
     if "core" in sections:
         core_section(files)
+    if "queue" in sections:
+        queue_section(files)
     manifest_path = HERE / "golden_manifest.json"
     manifest = json.loads(manifest_path.read_text()) if manifest_path.exists() else {}
     for name, arrs in files.items():
@@ -235,7 +240,51 @@ def core_section(files: dict) -> None:
     files["moe.npz"] = arrays
 
 
-SECTIONS = ("core", "refstore")
+def queue_section(files: dict) -> None:
+    import torch
+
+    from mrun.engine.kernels.expert_queue import build_expert_queue, build_expert_queue_flat, scatter_committed
+
+    rng = np.random.default_rng(31)
+    arrays: dict = {}
+    rows, E, k, H = 40, 24, 6, 20
+    top = np.stack([rng.permutation(E)[:k] for _ in range(rows)]).astype(np.int64)
+    w = rng.random((rows, k)).astype(np.float32)
+    ep = rng.integers(0, 5, size=rows).astype(np.int64)
+    dl = rng.integers(100, 200, size=rows).astype(np.int64)
+    arrays.update(d_top=top, d_w=w, d_ep=ep, d_dl=dl)
+    for tag, tw in (("f32", torch.from_numpy(w)), ("bf16", torch.from_numpy(w).to(torch.bfloat16))):
+        plan = build_expert_queue(torch.from_numpy(top), tw, num_experts=E, epochs=torch.from_numpy(ep),
+                                  deadlines=torch.from_numpy(dl))
+        for f in ("token_ids", "expert_ids", "route_slots", "coefficients", "epochs", "deadlines", "starts", "counts"):
+            arrays[f"d_{tag}_{f}"] = getattr(plan, f).numpy()
+        out = rng.standard_normal((plan.assignments, H)).astype(np.float32)
+        active = np.where(rng.random(rows) < 0.7, ep, ep + 1).astype(np.int64)
+        red, valid = scatter_committed(plan, torch.from_numpy(out), active_epochs=torch.from_numpy(active))
+        arrays[f"d_{tag}_out"], arrays[f"d_{tag}_active"] = out, active
+        arrays[f"d_{tag}_reduced"], arrays[f"d_{tag}_valid"] = red.numpy(), valid.numpy()
+    # pruned packets: a random subset of the dense (row, slot) pairs, in a shuffled order
+    keep = rng.random(rows * k) < 0.6
+    tok = np.repeat(np.arange(rows), k)[keep]
+    slot = np.tile(np.arange(k), rows)[keep]
+    exp = top.reshape(-1)[keep]
+    cf = w.reshape(-1)[keep]
+    perm = rng.permutation(tok.size)
+    tok, slot, exp, cf = tok[perm], slot[perm], exp[perm], cf[perm]
+    plan = build_expert_queue_flat(torch.from_numpy(tok), torch.from_numpy(exp), torch.from_numpy(slot),
+                                   torch.from_numpy(cf), num_rows=rows, num_experts=E, top_k=k,
+                                   epochs=torch.from_numpy(ep), deadlines=torch.from_numpy(dl))
+    arrays.update(f_tok=tok, f_slot=slot, f_exp=exp, f_cf=cf)
+    for f in ("token_ids", "expert_ids", "route_slots", "coefficients", "epochs", "deadlines", "starts", "counts"):
+        arrays[f"f_{f}"] = getattr(plan, f).numpy()
+    out = rng.standard_normal((plan.assignments, H)).astype(np.float32) * 3
+    active = np.where(rng.random(rows) < 0.5, ep, ep - 1).astype(np.int64)
+    red, valid = scatter_committed(plan, torch.from_numpy(out), active_epochs=torch.from_numpy(active))
+    arrays.update(f_out=out, f_active=active, f_reduced=red.numpy(), f_valid=valid.numpy())
+    files["queue.npz"] = arrays
+
+
+SECTIONS = ("core", "refstore", "queue")
 
 if __name__ == "__main__":
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
