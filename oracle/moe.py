@@ -14,13 +14,17 @@ Restates (reference paths relative to /root/reference):
                            (olmoe_cuda.py:1308-1420) with the stable reducer
                            (qwen3_moe_cuda.py:2911-2920) and bf16 boundaries
 * ``moe_dense_reference`` -- per-expert float math of streamed_moe_forward
-                           (moe_safetensors.py:603-627), weights dequantized to fp32
+                           (moe_safetensors.py:603-627), weights dequantized to fp32, in float64
+* ``moe_streamed_reference`` -- the same in the model dtype (bf16 / fp32 roundings)
 
 Pinned by (tests/test_oracle_moe.py): the reference KATs test_olmoe_cuda.py:73-112 and
 test_qwen3_moe_cuda.py:1140-1241 (counts/starts/token ids/coefficients, inverse bijection,
 reduce == index_add and invariance under within-group permutation); numpy/torch library
 routines for the router; exact integer brute force for the grouped GEMM; the dense fp32
-per-expert formulation for the whole layer (tolerance).
+per-expert formulation for the whole layer (tolerance).  ``moe_dense_reference`` and
+``moe_streamed_reference`` are pinned by tests/golden/moe_forward.npz, written by the
+reference's own streamed_moe_forward on a tiny Qwen3-MoE layer: fp32 within 1e-6, and the
+bf16 restatement reproduces the reference's residual bit for bit.
 """
 
 from __future__ import annotations
@@ -110,6 +114,37 @@ def moe_forward(source, top_indices, top_weights, gate_up, gate_up_scales, down,
     q2, s2 = quantize_rows(act)
     y = grouped_int8_mm(q2, s2, down, down_scales, starts, counts)
     return round_bf16(stable_route_reduce(y, coef, inverse, rows, k))
+
+
+def moe_streamed_reference(y, top_indices, top_weights, gate_up, gate_up_scales, down, down_scales,
+                           dtype: str = "bf16", round_act: bool = True):
+    """Per-expert math of streamed_moe_forward (moe_safetensors.py:603-627) in the model dtype.
+
+    Weights are ``dtype(float(code) * scale)``; every torch op's result is rounded to
+    ``dtype`` as the reference's eager ops round it: the fused gate/up GEMM, silu, the
+    product, the down GEMM, ``w_e * ye`` and the running ``moe[tok] += ...``.  GEMMs sum in
+    float64 and round once (the reference's BLAS order is not fixed).  ``round_act=False``
+    drops the rounding of ``silu(g) * u`` (a planted mistake for the tests).  Returns the
+    ``moe`` tensor as fp32 values."""
+    rnd = round_bf16 if dtype == "bf16" else (lambda a: np.asarray(a, dtype=np.float32))
+    y = rnd(np.asarray(y, dtype=np.float32))
+    T, H = y.shape
+    out = np.zeros((T, H), dtype=np.float32)
+    I = gate_up.shape[1] // 2
+    w_all = rnd(np.asarray(top_weights, dtype=np.float32))
+    for e in np.unique(top_indices):
+        sel = top_indices == e
+        tok = sel.any(-1)
+        w_e = rnd((w_all * sel).sum(-1))[tok]
+        Wgu = rnd(gate_up[e].astype(np.float32) * gate_up_scales[e][:, None]).astype(np.float64)
+        Wd = rnd(down[e].astype(np.float32) * down_scales[e][:, None]).astype(np.float64)
+        gu = rnd(y[tok].astype(np.float64) @ Wgu.T)
+        g, u = gu[:, :I], gu[:, I:]
+        act = rnd(silu_f32(g)) * u
+        act = rnd(act) if round_act else act.astype(np.float32)
+        ye = rnd(act.astype(np.float64) @ Wd.T)
+        out[tok] = rnd(out[tok] + rnd(w_e[:, None] * ye))
+    return out
 
 
 def moe_dense_reference(source, top_indices, top_weights, gate_up, gate_up_scales, down, down_scales):

@@ -10,6 +10,7 @@ reference never travels with the fixtures.
 
 Sections (pass their names after the reference root to write only those; default: all):
 * ``core``     -- w8a8.npz, codecs.npz, moe.npz
+* ``moe_forward`` -- moe_forward.npz: streamed_moe_forward's expert math on a tiny layer
 * ``queue``    -- queue.npz: build_expert_queue / build_expert_queue_flat / scatter_committed
 * ``refstore`` -- refstore/legacy (a store in the reference's own test layout,
   tests/test_qstore_cache.py:19-46) and refstore/v3 (a v3 store sealed by the reference's
@@ -25,6 +26,7 @@ Functions covered (reference file:line):
 * stable_route_reduce                  src/mrun/engine/qwen3_moe_cuda.py:2561-2664 (CPU branch)
 * build_expert_queue(_flat), scatter_committed
                                        src/mrun/engine/kernels/expert_queue.py:242-398, 487-514
+* streamed_moe_forward (per-expert math) src/mrun/engine/moe_safetensors.py:404, 585-627
 * QStore.weight / embed_rows / matmul, _load_qstore_manifest
                                        src/mrun/engine/kernels/qstore.py:326-373, 1026-1128
 * build_source/builder/derived_provenance
@@ -157,6 +159,8 @@ def main(ref_root: str, sections: list[str]) -> None:
         core_section(files)
     if "queue" in sections:
         queue_section(files)
+    if "moe_forward" in sections:
+        moe_forward_section(files)
     manifest_path = HERE / "golden_manifest.json"
     manifest = json.loads(manifest_path.read_text()) if manifest_path.exists() else {}
     for name, arrs in files.items():
@@ -284,7 +288,61 @@ def queue_section(files: dict) -> None:
     files["queue.npz"] = arrays
 
 
-SECTIONS = ("core", "refstore", "queue")
+def moe_forward_section(files: dict) -> None:
+    """streamed_moe_forward on a tiny 2-layer Qwen3-MoE whose layer-0 experts hold int8
+    codes x row scales exactly; layer 0's attention is ablated (an exact zero contribution),
+    so the residual after layer 0 is h0 + moe(rmsnorm(h0))."""
+    import tempfile
+
+    import torch
+    import transformers
+
+    from mrun.engine.moe_safetensors import PagedSafetensors, _rmsnorm, streamed_moe_forward
+
+    rng = np.random.default_rng(41)
+    E, k, H, I, T = 8, 3, 32, 24, 12
+    cfg = transformers.Qwen3MoeConfig(
+        vocab_size=99, hidden_size=H, intermediate_size=48, moe_intermediate_size=I, num_hidden_layers=2,
+        num_attention_heads=4, num_key_value_heads=2, head_dim=8, num_experts=E, num_experts_per_tok=k,
+        norm_topk_prob=True, decoder_sparse_step=1, max_position_embeddings=64, attn_implementation="eager",
+        tie_word_embeddings=False)
+    torch.manual_seed(0)
+    model = transformers.Qwen3MoeForCausalLM(cfg).eval().float()
+    gu_q = rng.integers(-127, 128, size=(E, 2 * I, H), dtype=np.int8)
+    gu_s = (rng.uniform(0.5, 1.5, size=(E, 2 * I)) / 127 / np.sqrt(H)).astype(np.float32)
+    dn_q = rng.integers(-127, 128, size=(E, H, I), dtype=np.int8)
+    dn_s = (rng.uniform(0.5, 1.5, size=(E, H)) / 127 / np.sqrt(I)).astype(np.float32)
+    router = rng.standard_normal((E, H)).astype(np.float32)
+    ln = rng.uniform(0.5, 1.5, size=H).astype(np.float32)
+    layer = model.model.layers[0]
+    with torch.no_grad():
+        layer.mlp.experts.gate_up_proj.copy_(torch.from_numpy(gu_q.astype(np.float32) * gu_s[..., None]))
+        layer.mlp.experts.down_proj.copy_(torch.from_numpy(dn_q.astype(np.float32) * dn_s[..., None]))
+        layer.mlp.gate.weight.copy_(torch.from_numpy(router))
+        layer.post_attention_layernorm.weight.copy_(torch.from_numpy(ln))
+        model.model.embed_tokens.weight.copy_(torch.from_numpy(rng.standard_normal((99, H)).astype(np.float32)))
+    ids = rng.integers(1, 99, size=T)
+    arrays = dict(gu_q=gu_q, gu_s=gu_s, dn_q=dn_q, dn_s=dn_s, router=router, ln=ln, ids=ids)
+    eps = float(cfg.rms_norm_eps)
+    with tempfile.TemporaryDirectory() as tmp:
+        d = Path(tmp) / "m"
+        model.save_pretrained(str(d), safe_serialization=True)
+        cfg.save_pretrained(str(d))
+        ps = PagedSafetensors(d)
+        for tag, dt in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+            got = streamed_moe_forward(ps, torch.from_numpy(ids), dtype=dt, capture_hidden_states=True,
+                                       ablate_component=(0, "attn"), skip_lm_head=True)
+            h0, h1 = got["hidden_states"][0], got["hidden_states"][1]
+            y = _rmsnorm(h0.to(dt), torch.from_numpy(ln).to(dt), eps)
+            arrays[f"{tag}_h0"] = h0.float().numpy()
+            arrays[f"{tag}_h1"] = h1.float().numpy()
+            arrays[f"{tag}_y"] = y.float().numpy()
+            arrays[f"{tag}_top_idx"] = got["topk_idx"][0].astype(np.int64)
+            arrays[f"{tag}_top_w"] = got["topk_w"][0].astype(np.float32)
+    files["moe_forward.npz"] = arrays
+
+
+SECTIONS = ("core", "refstore", "queue", "moe_forward")
 
 if __name__ == "__main__":
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
