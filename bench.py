@@ -82,40 +82,134 @@ def build_stack(torch, dev, seed: int = 0):
     return arena, pages
 
 
-def cpu_baseline(seconds: float = 12.0, m: int = 1) -> dict:
-    """Reference CPU path (QStore.matmul, bf16 compute) over a bounded sample of the stack."""
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def _timed_loop(fn, seconds: float, min_calls: int = 1) -> tuple[int, float]:
+    done, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        done += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds and done >= min_calls:
+            return done, dt
+
+
+def cpu_baseline(seconds: float = 6.0, m: int = 1, threads: int | None = None) -> dict:
+    """Reference CPU path (QStore.matmul, bf16 compute) over a bounded sample of the config-2
+    stack: whole decoder layers, every linear dequantised then multiplied."""
     import numpy as np
     import torch
 
     from oracle import cpu_path
 
-    rng = np.random.default_rng(0)
-    layer = [
-        (rng.integers(-127, 128, size=s, dtype=np.int8), (rng.uniform(0.5, 1.5, size=s[0]) / 127).astype(np.float32))
-        for s in SHAPES.values()
-    ]
-    xs = {inn: torch.randn(m, inn).to(torch.bfloat16) for _, inn in SHAPES.values()}
-    layer_bytes = algorithmic_bytes_per_pass(m) // LAYERS
-    done, t0 = 0, time.perf_counter()
-    while True:
-        for q, s in layer:
-            cpu_path.qstore_matmul(q, s, xs[q.shape[1]])
-        done += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = time.perf_counter() - t0
-    return {
-        "value": round(done * layer_bytes / dt / 1e9, 3),
-        "unit": "GB/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": f"{done} decoder layers (7 qrow linears each, M={m}, bf16 compute) of the same "
-        f"stack through the reference CPU path (oracle/cpu_path.py), {dt:.1f} s",
-    }
+    prev = torch.get_num_threads()
+    if threads:
+        torch.set_num_threads(threads)
+    try:
+        rng = np.random.default_rng(0)
+        layer = [
+            (rng.integers(-127, 128, size=s, dtype=np.int8), (rng.uniform(0.5, 1.5, size=s[0]) / 127).astype(np.float32))
+            for s in SHAPES.values()
+        ]
+        xs = {inn: torch.randn(m, inn).to(torch.bfloat16) for _, inn in SHAPES.values()}
+        layer_bytes = algorithmic_bytes_per_pass(m) // LAYERS
+
+        def one_layer():
+            for q, sc in layer:
+                cpu_path.qstore_matmul(q, sc, xs[q.shape[1]])
+
+        done, dt = _timed_loop(one_layer, seconds)
+        return {
+            "value": round(done * layer_bytes / dt / 1e9, 3),
+            "unit": "GB/s",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{done} decoder layers (7 qrow linears each, M={m}, bf16 compute) of the config-2 stack "
+            f"through the reference CPU path restated in oracle/cpu_path.py, {dt:.1f} s",
+        }
+    finally:
+        torch.set_num_threads(prev)
 
 
-def _graph_time(torch, stream, fn, calls: int, reps: int = 5) -> float:
-    """Seconds per call of ``fn`` (one launch sequence), captured ``calls`` times in a graph."""
+def cpu_baselines_per_config(seconds: float = 2.0) -> dict:
+    """The reference's CPU paths for configs 1, 3, 4 and 5 (oracle/cpu_path.py) on bounded
+    samples, at all torch threads and at one thread, in the metric's unit."""
+    import numpy as np
+    import torch
+
+    from oracle import cpu_path
+
+    rng = np.random.default_rng(7)
+    all_threads = torch.get_num_threads()
+    out: dict = {"cpu_model": _cpu_model(), "threads_all": all_threads}
+
+    def both(name, fn, unit_per_call, unit, sample):
+        res = {"unit": unit, "sample": sample}
+        for tag, th in (("all_threads", all_threads), ("one_thread", 1)):
+            torch.set_num_threads(th)
+            try:
+                done, dt = _timed_loop(fn, seconds)
+            finally:
+                torch.set_num_threads(all_threads)
+            res[tag] = round(done * unit_per_call / dt, 3)
+        out[name] = res
+
+    # config 1: fp32 GEMV [1,1024] x [4096,1024]
+    q1 = rng.integers(-127, 128, size=(4096, 1024), dtype=np.int8)
+    s1 = (rng.uniform(0.5, 1.5, 4096) / 127).astype(np.float32)
+    x1 = torch.randn(1, 1024)
+    both("config1_fp32_gemv", lambda: cpu_path.qstore_matmul(q1, s1, x1, torch.float32), 4231168 / 1e9, "GB/s",
+         "QStore.matmul fp32 (dequant + GEMV) of the config-1 block")
+    # config 3: W8A8 over one GPU share of the weight rows (1792 of 14336), M = 512
+    N3, K3 = 1792, 4096
+    qw = torch.from_numpy(rng.integers(-127, 128, size=(N3, K3), dtype=np.int8))
+    sw = torch.from_numpy((rng.uniform(0.5, 1.5, N3) / 127).astype(np.float32))
+    x3 = torch.randn(512, K3)
+    x3[:, :4] *= 20
+    both("config3_w8a8_m512", lambda: cpu_path.w8a8_matmul(qw, sw, x3, protect_k=8), 2 * 512 * N3 * K3 / 1e12,
+         "TOPS", "w8a8_matmul CPU path (fp32 side path top-8, torch._int_mm) on M=512 x 1792 of the 14336 weight "
+         "rows (one eighth of config 3's N)")
+    # config 4: routed MoE, H 2048, I 768, T = 64, top-8 over 128 experts; sample = 8 experts
+    E, k, H, I, T = 128, 8, 2048, 768, 64
+    ex = list(range(8))
+    gu_q = rng.integers(-127, 128, size=(8, 2 * I, H), dtype=np.int8)
+    gu_s = (rng.uniform(0.5, 1.5, size=(8, 2 * I)) / 127).astype(np.float32)
+    dn_q = rng.integers(-127, 128, size=(8, H, I), dtype=np.int8)
+    dn_s = (rng.uniform(0.5, 1.5, size=(8, H)) / 127).astype(np.float32)
+    logits = torch.randn(T, E)
+    w4, i4 = torch.softmax(logits, -1).topk(k, -1)
+    i4 = i4 % 8  # routes that land in the sampled experts
+    w4 = (w4 / w4.sum(-1, keepdim=True)).to(torch.bfloat16)
+    src = torch.randn(T, H).to(torch.bfloat16)
+    page = 2 * I * H + 2 * I * 4 + H * I + H * 4
+    both("config4_moe_t64", lambda: cpu_path.moe_layer(src, i4, w4, gu_q, gu_s, dn_q, dn_s, experts=ex),
+         8 * page / 1e9, "GB/s", "streamed_moe_forward expert math (bf16, int8 experts dequantised per active "
+         "expert) over 8 of the 128 experts, T=64 routed onto them")
+    # config 5: int3 G64 fp16 scale/zero [11008, 4096] M = 1, 2048 of the rows
+    N5, K5 = 2048, 4096
+    packed = rng.integers(0, 256, size=(N5, K5 * 3 // 8), dtype=np.uint8)
+    sc5 = ((rng.uniform(0.5, 1.5, size=(N5, K5 // 64))) / 7).astype(np.float16)
+    z5 = (rng.uniform(0, 7, size=(N5, K5 // 64))).astype(np.float16)
+    x5 = torch.randn(1, K5)
+    b5 = N5 * (K5 * 3 // 8) + 2 * 2 * N5 * (K5 // 64) + 2 * K5 + 4 * N5
+    both("config5_int3_m1", lambda: cpu_path.lowbit_matmul(packed, sc5, z5, x5, K5, 3, 64, 0.0), b5 / 1e9, "GB/s",
+         "QStoreInt3.matmul CPU path (chunked np.unpackbits dequant + sgemm) on 2048 of the 11008 rows")
+    return out
+
+
+def _graph_time(torch, stream, fn, calls: int, reps: int = 20) -> float:
+    """Median seconds per call of ``fn`` (one launch sequence), captured ``calls`` times in
+    a graph; each replay is timed with its own pair of HIP events on ``stream``."""
     with torch.cuda.stream(stream):
         fn(0)
         torch.cuda.synchronize()
@@ -123,15 +217,30 @@ def _graph_time(torch, stream, fn, calls: int, reps: int = 5) -> float:
         with torch.cuda.graph(g, stream=stream):
             for i in range(calls):
                 fn(i)
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            g.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e-3 / (reps * calls)
+        per = _replay_times(torch, stream, g, reps, warmup=2)
+    return _median(per) / calls
+
+
+def _median(v: list[float]) -> float:
+    v = sorted(v)
+    n = len(v)
+    return v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
+
+
+def _replay_times(torch, stream, graph, reps: int, warmup: int) -> list[float]:
+    """Seconds of each of ``reps`` replays (after ``warmup`` untimed ones), HIP events on the
+    replay stream around every replay."""
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    with torch.cuda.stream(stream):
+        ev[0].record(stream)
+        for r in range(reps):
+            graph.replay()
+            ev[r + 1].record(stream)
+    torch.cuda.synchronize()
+    return [ev[r].elapsed_time(ev[r + 1]) * 1e-3 for r in range(reps)]
 
 
 def paged_measurement(torch, dev, pages, x_h, x_i, passes: int = 6) -> dict:
@@ -363,6 +472,40 @@ def secondary_measurements(torch, dev, stream) -> dict:
     return res
 
 
+class DecodeChain:
+    """One decoder pass as a decoder orders its linears: the layer input feeds the fused
+    q/k/v launch, q's output feeds o, o's output feeds the paired gate/up + SwiGLU, whose
+    output feeds down, and down's output is the next layer's input.  (Attention, norms and
+    residuals sit between these in a real decoder; they are not on this path.)  Every
+    launch therefore depends on the one before it, as in a real decode step."""
+
+    def __init__(self, torch, dev, pages, m: int, gen):
+        self.pages = pages
+        self.m = m
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.x0 = torch.randn(m, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
+        self.q = torch.empty(m, HIDDEN, **bf)
+        self.k = torch.empty(m, KV, **bf)
+        self.v = torch.empty(m, KV, **bf)
+        self.o = torch.empty(m, HIDDEN, **bf)
+        self.h = torch.empty(m, INTER, **bf)
+        self.d = [torch.empty(m, HIDDEN, **bf) for _ in range(2)]
+
+    def per_linear(self, _i=0):
+        from mrun_pub_amd import qrow
+
+        x = self.x0
+        for li, L in enumerate(self.pages):
+            qrow.qrow_matmul_multi([(L[n].codes, L[n].scales) for n in ("q", "k", "v")], x,
+                                   out=[self.q, self.k, self.v])
+            qrow.qrow_matmul(L["o"].codes, L["o"].scales, self.q, out=self.o)
+            qrow.qrow_swiglu_into(L["gate"], L["up"], self.o, self.h)
+            nxt = self.d[li % 2]
+            qrow.qrow_matmul(L["down"].codes, L["down"].scales, self.h, out=nxt)
+            x = nxt
+        return x
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -370,11 +513,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--m", type=int, default=1, help="decode tokens per pass (1, 4, 16, 32)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-secondary", action="store_true", help="skip configs 1/3/4/5")
     ap.add_argument("--profile", choices=("swiglu", "stack", "copy"),
-                    help="eager launches only, for rocprofv3 counter runs: 28 paired gate/up+SwiGLU "
-                    "launches, one stack pass, or a plain 256 MiB device copy (counter calibration); x5")
+                    help="for rocprofv3 runs: replay exactly the timed graph of the roofline kernel (28 "
+                    "paired gate/up+SwiGLU launches) or of the headline pass, --steps times after "
+                    "--warmup replays; or a plain 256 MiB device copy x5 (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -406,60 +550,54 @@ def main() -> int:
     arena, pages = build_stack(torch, dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
-    x_h = torch.randn(m, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
-    x_i = torch.randn(m, INTER, device=dev, generator=gen).to(torch.bfloat16)
+    chain = DecodeChain(torch, dev, pages, m, gen)
+    stream = torch.cuda.Stream(device=dev)
 
-    def one_pass():
+    def capture(fn):
+        with torch.cuda.stream(stream):
+            fn()  # eager warm-up (also loads the library)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                fn()
+        return g
+
+    graph = capture(chain.per_linear)
+
+    # the dominant kernel: the paired gate/up + SwiGLU launch, 28 distinct layers per replay
+    # (input: the chain's own o-projection output buffer)
+    def swiglu_28():
         for L in pages:
-            qrow.qrow_matmul_multi([(L[n].codes, L[n].scales) for n in ("q", "k", "v")], x_h)
-            qrow.fused_qrow_matmul(L["o"], x_h)
-            qrow.fused_qrow_swiglu(L["gate"], L["up"], x_h)
-            qrow.fused_qrow_matmul(L["down"], x_i)
+            qrow.qrow_swiglu_into(L["gate"], L["up"], chain.o, chain.h)
 
+    sw_graph = capture(swiglu_28)
     if args.profile:
-        for _ in range(5):
-            if args.profile == "stack":
-                one_pass()
-            else:
-                for L in pages:
-                    qrow.fused_qrow_swiglu(L["gate"], L["up"], x_h)
-        torch.cuda.synchronize()
-        print(json.dumps({"profile": args.profile, "m": m, "swiglu_launch_bytes": swiglu_launch_bytes(m)}), flush=True)
+        g = sw_graph if args.profile == "swiglu" else graph
+        times = _replay_times(torch, stream, g, args.steps, args.warmup)
+        per_launch = _median(times) / (LAYERS if args.profile == "swiglu" else 1)
+        print(json.dumps({"profile": args.profile, "m": m, "replays": args.steps, "median_us": round(per_launch * 1e6, 3),
+                          "swiglu_launch_bytes": swiglu_launch_bytes(m)}), flush=True)
         return 0
 
-    stream = torch.cuda.Stream(device=dev)
+    # timed region: exactly --steps replays of the pass, synchronised on both sides; each
+    # replay is also bracketed by its own events on the replay stream (median reported)
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    t0 = time.perf_counter()
     with torch.cuda.stream(stream):
-        one_pass()  # eager warm-up (also loads the library)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            one_pass()
-        for _ in range(args.warmup):
+        ev[0].record(stream)
+        for r in range(args.steps):
             graph.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            graph.replay()
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
+            ev[r + 1].record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    per_replay = [ev[r].elapsed_time(ev[r + 1]) * 1e-3 for r in range(args.steps)]
+    per_pass = _median(per_replay)
+    sw_times = _replay_times(torch, stream, sw_graph, max(50, args.steps), 5)
+    sw_s = _median(sw_times) / LAYERS
 
-        # dominant kernel: the paired gate/up + SwiGLU launch, 28 distinct layers per replay
-        sw_graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(sw_graph, stream=stream):
-            for L in pages:
-                qrow.fused_qrow_swiglu(L["gate"], L["up"], x_h)
-        sw_graph.replay()
-        torch.cuda.synchronize()
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 20
-        ev0.record(stream)
-        for _ in range(reps):
-            sw_graph.replay()
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        sw_s = ev0.elapsed_time(ev1) * 1e-3 / (reps * LAYERS)
-
-    per_pass = elapsed / args.steps
     value = algorithmic_bytes_per_pass(m) / per_pass / 1e9
     sw_gbs = swiglu_launch_bytes(m) / sw_s / 1e9
     traffic = None
@@ -480,7 +618,8 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "dense decoder int8 qrow linear stack (BASELINE configs[1]), decode pass",
+            "workload": "dense decoder int8 qrow linear stack (BASELINE configs[1]), one decode pass with "
+            "each linear's input the previous linear's output",
             "layers": LAYERS,
             "hidden": HIDDEN,
             "intermediate": INTER,
@@ -489,48 +628,50 @@ def main() -> int:
             "pass_bytes": algorithmic_bytes_per_pass(m),
             "launches_per_pass": 4 * LAYERS,
             "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+            "timing": f"median of {args.steps} graph replays (HIP events per replay) after {args.warmup} "
+            f"warm-up replays; mean {sum(per_replay) / len(per_replay) * 1e3:.4f} ms, wall "
+            f"{elapsed / args.steps * 1e3:.4f} ms per replay",
         },
         "roofline": {
-            "kernel": "paired gate/up W8A16 + SwiGLU (qs_qrow_swiglu)",
+            "kernel": "paired gate/up W8A16 + SwiGLU (qs_qrow_swiglu, k_gemv_valu)",
             "bound": "hbm",
             "achieved": round(sw_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(sw_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": "committed figure: profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE and "
+            "WRITE_SIZE runs of bench.py --profile swiglu, scaled by a 256 MiB copy)",
             "launch_us": round(sw_s * 1e6, 3),
             "bytes_per_launch": swiglu_launch_bytes(m),
+            "timing": f"median of {len(sw_times)} replays of a graph of the 28 launches, / 28",
         },
     }
     if not args.no_secondary:
-        # config 2's other batch sizes (M = 4, 16, 32): the same resident stack and graph
-        # protocol; M >= 3 runs the MFMA W8A16 kernels
+        # config 2's other batch sizes (M = 4, 16, 32): the same chained pass and protocol
         batches = {}
         for mm in (4, 16, 32):
             if mm == m:
                 continue
-            xb_h = torch.randn(mm, HIDDEN, device=dev, generator=gen).to(torch.bfloat16)
-            xb_i = torch.randn(mm, INTER, device=dev, generator=gen).to(torch.bfloat16)
-
-            def pass_m(_i, xh=xb_h, xi=xb_i):
-                for L in pages:
-                    qrow.qrow_matmul_multi([(L[nm].codes, L[nm].scales) for nm in ("q", "k", "v")], xh)
-                    qrow.fused_qrow_matmul(L["o"], xh)
-                    qrow.fused_qrow_swiglu(L["gate"], L["up"], xh)
-                    qrow.fused_qrow_matmul(L["down"], xi)
-
-            tp = _graph_time(torch, stream, pass_m, 1, reps=10)
+            cm = DecodeChain(torch, dev, pages, mm, gen)
+            tp = _graph_time(torch, stream, lambda _i, c=cm: c.per_linear(), 1, reps=20)
             batches[f"config2_stack_m{mm}"] = {
                 "ms_per_pass": round(tp * 1e3, 4),
                 "GB/s": round(algorithmic_bytes_per_pass(mm) / tp / 1e9, 1),
                 "hbm_frac": round(algorithmic_bytes_per_pass(mm) / tp / 1e9 / HBM_PEAK_GBS, 4),
             }
+        x_h = chain.x0
+        x_i = torch.randn(m, INTER, device=dev, generator=gen).to(torch.bfloat16)
         paged = paged_measurement(torch, dev, pages, x_h, x_i)
-        del arena, pages, graph, sw_graph
+        del arena, pages, graph, sw_graph, chain
         out["secondary"] = {**batches, "config2_paged_pinned_host": paged,
                             **secondary_measurements(torch, dev, stream)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds, m)
+        out["cpu_baseline"]["one_thread"] = cpu_baseline(args.cpu_seconds / 2, m, threads=1)["value"]
+        out["cpu_baseline"]["cpu_model"] = _cpu_model()
+        if not args.no_secondary:
+            out["cpu_baselines_per_config"] = cpu_baselines_per_config()
     print(json.dumps(out), flush=True)
     return 0
 

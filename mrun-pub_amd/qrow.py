@@ -128,9 +128,20 @@ def qrow_embed_rows(codes: torch.Tensor, scales: torch.Tensor, ids) -> torch.Ten
     return out.reshape(*shape, k)
 
 
+def _out_buffer(out: torch.Tensor | None, m: int, n: int, dtype: torch.dtype, device) -> torch.Tensor:
+    """A caller's output buffer (contiguous ``[m, n]`` of ``dtype`` on ``device``, any leading
+    shape) or a fresh one."""
+    if out is None:
+        return torch.empty((m, n), dtype=dtype, device=device)
+    if out.dtype != dtype or out.device != device or not out.is_contiguous() or out.numel() != m * n:
+        raise ValueError(f"out must be a contiguous {dtype} tensor of {m}x{n} elements on {device}")
+    return out.view(m, n)
+
+
 @torch.inference_mode()
 def qrow_matmul(
-    codes: torch.Tensor, scales: torch.Tensor, x: torch.Tensor, *, row_stable: bool = False
+    codes: torch.Tensor, scales: torch.Tensor, x: torch.Tensor, *, row_stable: bool = False,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """``x[..., K] @ W^T`` with the dtype contract of ``qs_qrow_matmul``.
 
@@ -138,7 +149,8 @@ def qrow_matmul(
     bf16 / fp16 activations: weights rounded per element to the activation dtype, fp32
     accumulation, output in the activation dtype (W8A16, dense_qstore_cuda.py:467-512).
     ``row_stable=True`` selects the batch-invariant lane (``matmul_row_stable``,
-    qstore.py:49-76): every row equals its own ``M = 1`` result bit for bit.
+    qstore.py:49-76): every row equals its own ``M = 1`` result bit for bit.  ``out``: an
+    optional preallocated output (it must not overlap ``x``).
     """
     n, k = _check_codes(codes, scales)
     if x.dtype not in _ACT_DTYPES:
@@ -150,7 +162,7 @@ def qrow_matmul(
     if not flat.is_contiguous():
         flat = flat.contiguous()
     m = int(flat.shape[0])
-    y = torch.empty((m, n), dtype=x.dtype, device=device)
+    y = _out_buffer(out, m, n, x.dtype, device)
     if m:
         nat.call(
             "qs_qrow_matmul_row_stable" if row_stable else "qs_qrow_matmul",
@@ -171,9 +183,11 @@ def qrow_matmul(
 
 @torch.inference_mode()
 def qrow_matmul_multi(
-    pages: list[tuple[torch.Tensor, torch.Tensor]], x: torch.Tensor
+    pages: list[tuple[torch.Tensor, torch.Tensor]], x: torch.Tensor,
+    out: list[torch.Tensor] | None = None,
 ) -> list[torch.Tensor]:
-    """Several linears over one activation in a single launch (q/k/v)."""
+    """Several linears over one activation in a single launch (q/k/v); ``out``: optional
+    preallocated outputs, one per linear."""
     if not 1 <= len(pages) <= 4:
         raise ValueError("qrow_matmul_multi takes 1..4 linears")
     k = int(x.shape[-1])
@@ -185,7 +199,9 @@ def qrow_matmul_multi(
     device = nat.require_device(x, *[t for p in pages for t in p])
     flat = x.reshape(-1, k).contiguous()
     m = int(flat.shape[0])
-    outs = [torch.empty((m, n), dtype=x.dtype, device=device) for n, _ in shapes]
+    if out is not None and len(out) != len(pages):
+        raise ValueError("one output buffer per linear")
+    outs = [_out_buffer(None if out is None else out[i], m, n, x.dtype, device) for i, (n, _) in enumerate(shapes)]
     if m:
         nat.call(
             "qs_qrow_matmul_multi",
@@ -265,14 +281,22 @@ def fused_qrow_swiglu(
 ) -> tuple[torch.Tensor, str]:
     """Drop-in for ``fused_qrow_swiglu`` (dense_qstore_cuda.py:1053-1102)."""
     del require_triton
-    _validate_paired_qrow_pages(gate_page, up_page, activations)
     _validate_block_m(block_m)
+    return qrow_swiglu_into(gate_page, up_page, activations), IMPL_SWIGLU
+
+
+@torch.inference_mode()
+def qrow_swiglu_into(gate_page: CompactQRowPage, up_page: CompactQRowPage, activations: torch.Tensor,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """The paired SwiGLU of :func:`fused_qrow_swiglu`, optionally into a preallocated bf16
+    ``out`` (which must not overlap the activations)."""
+    _validate_paired_qrow_pages(gate_page, up_page, activations)
     n, k = _check_codes(gate_page.codes, gate_page.scales)
     _check_codes(up_page.codes, up_page.scales)
     device = nat.require_device(activations, gate_page.codes)
     flat = activations.reshape(-1, k).contiguous()
     m = int(flat.shape[0])
-    y = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    y = _out_buffer(out, m, n, torch.bfloat16, device)
     if m:
         nat.call(
             "qs_qrow_swiglu",
@@ -289,7 +313,7 @@ def fused_qrow_swiglu(
             k,
             nat.stream_of(device),
         )
-    return y.reshape(*activations.shape[:-1], n), IMPL_SWIGLU
+    return y.reshape(*activations.shape[:-1], n)
 
 
 # ---- head: fused top-2 and fp32 candidate rerank ----------------------------------------------
