@@ -82,6 +82,33 @@ int qs_qrow_matmul_multi(const void* x, int x_dtype, int64_t ldx, int n_linear,
                          void* const* y, const int64_t* ldy, const int64_t* N, int64_t M,
                          int64_t K, void* stream);
 
+/* Batched decode (M rows of bf16/f16 activations, 1 <= M <= 32), same contracts as
+ * qs_qrow_matmul_multi (W8A16, y in the activation dtype) and qs_qrow_swiglu (x, y BF16),
+ * for the reference's batched decode through fused_qrow_matmul / fused_qrow_swiglu
+ * (dense_qstore_cuda.py:1105-1153, 1053-1102).  K % 128 == 0, K <= 16384 (SwiGLU:
+ * K <= 2048), otherwise QS_ERR_UNSUPPORTED; weight and activation rows 16-byte aligned.  K is split into slices chosen from (N, K) only, and the slices' fp32
+ * partial sums are added in slice order, so every row equals the same row computed alone
+ * (M = 1 through this entry point) bit for bit.
+ *   workspace: qs_qrow_batched_workspace_bytes(M, n_linear, N, K, swiglu) bytes (may be 0),
+ *              contents clobbered;
+ *   counters:  at least qs_qrow_batched_counters(n_linear, N, swiglu) int32 that are zero
+ *              on entry; every call leaves them zero when it completes, so one array serves
+ *              all calls on one stream.  Calls that run concurrently (other streams) need
+ *              their own counters and workspace. */
+size_t qs_qrow_batched_workspace_bytes(int64_t M, int n_linear, const int64_t* N, int64_t K,
+                                       int swiglu);
+int64_t qs_qrow_batched_counters(int n_linear, const int64_t* N, int swiglu);
+int qs_qrow_matmul_batched(const void* x, int x_dtype, int64_t ldx, int n_linear,
+                           const int8_t* const* codes, const float* const* scales,
+                           void* const* y, const int64_t* ldy, const int64_t* N, int64_t M,
+                           int64_t K, void* workspace, size_t workspace_bytes, int32_t* counters,
+                           int64_t n_counters, void* stream);
+int qs_qrow_swiglu_batched(const void* x, int64_t ldx, const int8_t* gate_codes,
+                           const float* gate_scales, const int8_t* up_codes,
+                           const float* up_scales, void* y, int64_t ldy, int64_t M, int64_t N,
+                           int64_t K, void* workspace, size_t workspace_bytes, int32_t* counters,
+                           int64_t n_counters, void* stream);
+
 /* Replaces fused_qrow_swiglu + _qrow_w8a16_paired_swiglu_kernel
  * (dense_qstore_cuda.py:1053-1102, 515-575); reference contract
  * fused_qrow_swiglu_reference (dense_qstore_cuda.py:1037-1050):

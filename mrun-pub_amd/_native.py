@@ -49,6 +49,10 @@ SIGNATURES: dict[str, tuple] = {
     "qs_qrow_matmul": (_I, [_P, _I, _L, _P, _P, _P, _L, _L, _L, _L, _P]),
     "qs_qrow_matmul_row_stable": (_I, [_P, _I, _L, _P, _P, _P, _L, _L, _L, _L, _P]),
     "qs_qrow_matmul_multi": (_I, [_P, _I, _L, _I, _P, _P, _P, _P, _P, _L, _L, _P]),
+    "qs_qrow_batched_workspace_bytes": (ctypes.c_size_t, [_L, _I, _P, _L, _I]),
+    "qs_qrow_batched_counters": (_L, [_I, _P, _I]),
+    "qs_qrow_matmul_batched": (_I, [_P, _I, _L, _I, _P, _P, _P, _P, _P, _L, _L, _P, ctypes.c_size_t, _P, _L, _P]),
+    "qs_qrow_swiglu_batched": (_I, [_P, _L, _P, _P, _P, _P, _P, _L, _L, _L, _L, _P, ctypes.c_size_t, _P, _L, _P]),
     "qs_qrow_swiglu": (_I, [_P, _L, _P, _P, _P, _P, _P, _L, _L, _L, _L, _P]),
     "qs_qrow_top2_workspace_bytes": (ctypes.c_size_t, [_L, _L]),
     "qs_qrow_top2": (_I, [_P, _I, _L, _P, _P, _L, _L, _L, _L, _P, ctypes.c_size_t, _P, _P, _P]),

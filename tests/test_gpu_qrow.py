@@ -142,6 +142,33 @@ def test_mfma_path_rows_independent_of_batch(dev, m):
     assert torch.equal(perm[0], full[0])
 
 
+@pytest.mark.parametrize("n,k,swiglu", [(1536, 1536, False), (256, 1536, False), (1536, 8960, False),
+                                        (8960, 1536, True), (200, 384, True), (70, 1024, False)])
+@pytest.mark.parametrize("m", [5, 16, 23, 32])
+def test_batched_rows_equal_rows_alone(dev, n, k, swiglu, m):
+    """qs_qrow_matmul_batched / qs_qrow_swiglu_batched: every row of an M-row call is bit for
+    bit the row computed alone through the same entry point, and the batch matches the
+    oracle to the bf16 tolerance."""
+    q = _qrow()
+    rng, codes, scales = _case(n, k, seed=m + n + k)
+    _, codes2, scales2 = _case(n, k, seed=m + n + k + 1)
+    x = oq.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
+    xd = _dev(x, dev, torch.bfloat16)
+    pages = [(_dev(codes, dev), _dev(scales, dev))]
+    if swiglu:
+        pages.append((_dev(codes2, dev), _dev(scales2, dev)))
+    full = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    q._run_batched(xd, pages, [full], swiglu=swiglu)
+    for r in (0, m // 2, m - 1):
+        one = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+        q._run_batched(xd[r:r + 1].contiguous(), pages, [one], swiglu=swiglu)
+        assert torch.equal(one[0], full[r]), r
+    ref = oq.qrow_swiglu(codes, scales, codes2, scales2, x) if swiglu else oq.qrow_matmul_w8a16(codes, scales, x)
+    assert oq.rel_l2(full.float().cpu().numpy(), ref) <= BF16_TOL
+    if not swiglu and m >= q.BATCHED_MIN_M and k >= q.BATCHED_MIN_K:  # the public wrapper's path
+        assert torch.equal(q.qrow_matmul(pages[0][0], pages[0][1], xd), full)
+
+
 def test_multi_linear_equals_individual(dev):
     rng = np.random.default_rng(12)
     k = 1536
