@@ -362,6 +362,46 @@ def paged_moe_measurement(torch, dev, E: int, topk: int, H: int, I: int, layers:
     return res
 
 
+def profile_mfma_kernels(torch, dev, which: str, calls: int) -> dict:
+    """Eager launches of config 3's fused W8A8 GEMM or config 4's MoE layer, for counter runs
+    (MFMA utilisation, HBM bytes); prints the algorithmic figures to compare against."""
+    from mrun_pub_amd import _native as nat
+    from mrun_pub_amd import moe, w8a8
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    out: dict = {"profile": which, "calls": calls}
+    if which == "w8a8":
+        N, K = 14336, 4096
+        qw = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen)
+        sw = (torch.rand(N, device=dev, generator=gen) + 0.5) / 127
+        for M in (512, 2048):
+            xb = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+            qx, asc = w8a8.quantize_activation(xb)
+            y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            for _ in range(calls):
+                nat.call("qs_w8a8_gemm", nat.ptr(qx), nat.ptr(asc), nat.ptr(qw), nat.ptr(sw), None, None, 0,
+                         nat.ptr(y), nat.QS_BF16, M, N, K, nat.stream_of(dev))
+            out[f"m{M}_ops_per_call"] = 2 * M * N * K
+    else:
+        E, topk, H, I = 128, 8, 2048, 768
+        layer = moe.Int8ExpertLayer.from_arrays(
+            torch.randint(-127, 128, (E, 2 * I, H), dtype=torch.int8, device=dev, generator=gen),
+            (torch.rand(E, 2 * I, device=dev, generator=gen) + 0.5) / 127,
+            torch.randint(-127, 128, (E, H, I), dtype=torch.int8, device=dev, generator=gen),
+            (torch.rand(E, H, device=dev, generator=gen) + 0.5) / 127, dev)
+        backend = moe.Int8ExpertBackend([layer])
+        for T in (64, 512):
+            tw, ti = moe.route_topk(torch.randn(T, E, device=dev, generator=gen), topk)
+            xs = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16)
+            for _ in range(calls):
+                backend.moe(0, xs, ti, tw)
+            out[f"t{T}_active_experts"] = int(torch.unique(ti).numel())
+            out[f"t{T}_ops_per_layer"] = 2 * T * topk * (2 * I * H + H * I)
+    torch.cuda.synchronize()
+    return out
+
+
 def secondary_measurements(torch, dev, stream) -> dict:
     """Configs 1, 3, 4, 5 of BASELINE.json, measured with HIP graphs on one stream."""
     from mrun_pub_amd import lowbit, moe, qrow, w8a8
@@ -515,10 +555,14 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-secondary", action="store_true", help="skip configs 1/3/4/5")
-    ap.add_argument("--profile", choices=("swiglu", "stack", "copy"),
+    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "moe"),
                     help="for rocprofv3 runs: replay exactly the timed graph of the roofline kernel (28 "
                     "paired gate/up+SwiGLU launches) or of the headline pass, --steps times after "
-                    "--warmup replays; or a plain 256 MiB device copy x5 (counter calibration)")
+                    "--warmup replays; a plain 256 MiB device copy x5 (counter calibration); or config 3's "
+                    "fused W8A8 GEMM (M=512 and 2048) / config 4's MoE layer (T=64 and 512), --steps calls each")
+    ap.add_argument("--eager", action="store_true",
+                    help="with --profile swiglu/stack: launch the same sequence eagerly instead of replaying "
+                    "the graph (counter collection needs eager dispatches)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -547,6 +591,9 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"profile": "copy", "launches": 5, "read_bytes": n, "write_bytes": n}), flush=True)
         return 0
+    if args.profile in ("w8a8", "moe"):
+        print(json.dumps(profile_mfma_kernels(torch, dev, args.profile, args.steps)), flush=True)
+        return 0
     arena, pages = build_stack(torch, dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
@@ -571,6 +618,15 @@ def main() -> int:
             qrow.qrow_swiglu_into(L["gate"], L["up"], chain.o, chain.h)
 
     sw_graph = capture(swiglu_28)
+    if args.profile and args.eager:
+        with torch.cuda.stream(stream):
+            for _ in range(args.warmup + args.steps):
+                swiglu_28() if args.profile == "swiglu" else chain.per_linear()
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": args.profile, "m": m, "eager_passes": args.warmup + args.steps,
+                          "swiglu_launch_bytes": swiglu_launch_bytes(m), "pass_bytes": algorithmic_bytes_per_pass(m)}),
+              flush=True)
+        return 0
     if args.profile:
         g = sw_graph if args.profile == "swiglu" else graph
         times = _replay_times(torch, stream, g, args.steps, args.warmup)
