@@ -697,7 +697,8 @@ def main() -> int:
             "frac": round(sw_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": "committed figure: profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE and "
-            "WRITE_SIZE runs of bench.py --profile swiglu, scaled by a 256 MiB copy)",
+            "WRITE_SIZE runs of bench.py --profile stack --eager, scaled by a 256 MiB copy; "
+            "profiles/decode_gemv_m1.md)",
             "launch_us": round(sw_s * 1e6, 3),
             "bytes_per_launch": swiglu_launch_bytes(m),
             "timing": f"median of {len(sw_times)} replays of a graph of the 28 launches, / 28",
