@@ -273,6 +273,13 @@ int qs_moe_route_reduce(const void* expert_out, int y_dtype, const float* coef,
                         const int64_t* inverse, int64_t T, int k, int64_t H, float* out,
                         void* stream);
 
+/* qs_moe_route_reduce with the output in out_dtype (QS_F32 or QS_BF16): BF16 rounds each
+ * fp32 sum once (RNE), the value of the reference's fp32 reduce followed by its cast to
+ * the model dtype (qwen3_moe_cuda.py:2910-2918 then :2936, output.to(self.dtype)). */
+int qs_moe_route_reduce_to(const void* expert_out, int y_dtype, const float* coef,
+                           const int64_t* inverse, int64_t T, int k, int64_t H, void* out,
+                           int out_dtype, void* stream);
+
 /* ---- packed int3 / int2 ("qrow3" / "qrow2") --------------------------------------------
  * packed: uint8 [N, row_bytes], each row an LSB-first bitstream of K codes of `bits` bits
  * (code k at bits [bits*k, bits*k + bits)); scales [N, K/G] (F32 or F16); zeros [N, K/G]

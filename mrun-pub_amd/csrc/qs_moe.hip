@@ -5,16 +5,21 @@
 // Kernels
 //   k_moe_router      : one wave per token: fp32 softmax over E logits, top-k (ties ->
 //                       lower expert id), optional renormalisation, weights as fp32/bf16.
+//   k_moe_route_par   : one workgroup per expert (moderate A * E): ballot counts of the
+//                       lower experts give its start, then its assignments in index order.
 //   k_moe_route       : one workgroup; expert histogram, exclusive prefix and a STABLE
 //                       expert-major scatter (wave ballots give each assignment its rank
 //                       among earlier same-expert assignments), so the queue order equals
 //                       the reference's stable argsort and is identical on every call.
 //   k_moe_gather_quant: per routed row, int8 per-token quantization of source[token_ids[a]]
-//                       (the W8A8 recipe: s = max|x|/127, 0 -> 1; rint; clamp +-127).
-//   k_moe_stream<...> : one workgroup per (group, 8 or 4 waves of output rows).  The group's
+//                       (the W8A8 recipe: s = max|x|/127, 0 -> 1; rint; clamp +-127);
+//                       k_moe_gather_quant8 is the same with a wave per row and 16-byte
+//                       loads (H % 8 == 0, aligned rows).
+//   k_moe_stream<...> : one workgroup per (group, 4 or 8 waves of output rows), the row
+//                       blocks of a group kept on one XCD.  The group's
 //                       routed rows (up to 16*MT at a time) are staged once in LDS; each
 //                       wave streams its weight rows (16 rows of gate and up for SwiGLU,
-//                       16-64 rows otherwise) over the full K through a window of 64-byte
+//                       16-64 rows otherwise) over the full K through a window of 128-byte
 //                       chunks in flight and multiplies them with v_mfma_i32_16x16x64_i8
 //                       against every 16-row tile of the staged rows; epilogue (float(acc) * a_scale[row]) * w_scale[n] ->
 //                       bf16/fp32, or the paired SwiGLU of gate row n and up row n + N.
@@ -22,8 +27,12 @@
 //                       tile); its waves split K, hold their weight slice in VGPRs and
 //                       walk the group's rows 16 at a time, LDS reduction over the split.
 //   k_moe_reduce      : out[t, :] = sum over rank r of float(y[inv[t*k + r], :]) *
-//                       coef[inv[t*k + r]], each product rounded, summed in rank order.
+//                       coef[inv[t*k + r]], each product rounded, summed in rank order;
+//                       fp32 out, or bf16 (the fp32 sum rounded once).  k_moe_reduce8 is
+//                       the same with 8 consecutive h per thread.
 #include "qs_common.h"
+
+#include <type_traits>
 
 namespace qs {
 
@@ -36,18 +45,19 @@ __device__ __forceinline__ float ld(const void* p, int64_t i) {
   else return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
 }
 
-// E <= 1024 (16 per lane), k <= 16.
-template <int XT>
+// E <= 64 * J logits per wave (J per lane), k <= 16.  Rank r is kept by lane r (no
+// dynamically indexed arrays, which would live in scratch memory).
+template <int XT, int J>
 __global__ __launch_bounds__(256) void k_moe_router(const void* __restrict__ logits, int T, int E,
                                                     int k, int norm, int64_t* __restrict__ idx,
                                                     void* __restrict__ w, int w_dtype) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  float v[16];
+  float v[J];
   float mx = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < J; ++j) {
     const int e = lane + 64 * j;
     v[j] = e < E ? ld<XT>(logits, (int64_t)t * E + e) : -INFINITY;
     mx = fmaxf(mx, v[j]);
@@ -55,22 +65,22 @@ __global__ __launch_bounds__(256) void k_moe_router(const void* __restrict__ log
   mx = wave_max(mx);
   float sum = 0.f;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < J; ++j) {
     const int e = lane + 64 * j;
     v[j] = e < E ? expf(v[j] - mx) : 0.f;
     sum += v[j];
   }
   sum = wave_sum(sum);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = v[j] / sum;
-  float picked[16];
-  int pidx[16];
-  float tot = 0.f;
+  for (int j = 0; j < J; ++j) v[j] = v[j] / sum;
+  float mine = 0.f;  // lane r: the weight of rank r
+  int mine_idx = 0;
+  float tot = 0.f;   // fp32 sum of the kept weights in rank order
   for (int r = 0; r < k; ++r) {
     float best = -1.f;
     int bi = 0x7fffffff;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < J; ++j) {
       const int e = lane + 64 * j;
       if (e < E && (v[j] > best || (v[j] == best && e < bi))) {
         best = v[j];
@@ -86,27 +96,24 @@ __global__ __launch_bounds__(256) void k_moe_router(const void* __restrict__ log
         bi = oi;
       }
     }
-    picked[r] = best;
-    pidx[r] = bi;
+    if (lane == r) {
+      mine = best;
+      mine_idx = bi;
+    }
     tot += best;
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
+    for (int j = 0; j < J; ++j)
       if (lane + 64 * j == bi) v[j] = -2.f;  // exclude
   }
-  if (lane == 0) {
-    // renormalisation divides by the fp32 sum of the kept weights, summed in rank order
-    float s = 0.f;
-    for (int r = 0; r < k; ++r) s += picked[r];
-    for (int r = 0; r < k; ++r) {
-      const float wr = norm ? picked[r] / s : picked[r];
-      idx[(int64_t)t * k + r] = pidx[r];
-      if (w_dtype == QS_F32)
-        static_cast<float*>(w)[(int64_t)t * k + r] = wr;
-      else
-        static_cast<uint16_t*>(w)[(int64_t)t * k + r] = f32_to_bf16_bits(wr);
-    }
+  // renormalisation divides by the fp32 sum of the kept weights, summed in rank order
+  if (lane < k) {
+    const float wr = norm ? mine / tot : mine;
+    idx[(int64_t)t * k + lane] = mine_idx;
+    if (w_dtype == QS_F32)
+      static_cast<float*>(w)[(int64_t)t * k + lane] = wr;
+    else
+      static_cast<uint16_t*>(w)[(int64_t)t * k + lane] = f32_to_bf16_bits(wr);
   }
-  (void)tot;
 }
 
 // ----------------------------------------------------------------------------------
@@ -114,6 +121,8 @@ __global__ __launch_bounds__(256) void k_moe_router(const void* __restrict__ log
 // ----------------------------------------------------------------------------------
 constexpr int kRouteWaves = 16;
 constexpr int kRouteMaxE = 512;
+constexpr int kRouteBatch = 8;  // 64-assignment segments a wave loads before using them
+constexpr int kRouteStage = 8192;  // assignments staged in LDS (64 KB)
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 
@@ -127,7 +136,13 @@ __global__ __launch_bounds__(1024) void k_moe_route(const void* __restrict__ top
                                                     int64_t* __restrict__ inverse) {
   __shared__ int cnt[kRouteWaves][kRouteMaxE];
   __shared__ int base[kRouteMaxE];
+  __shared__ int wave_tot[kRouteMaxE / 64];
   __shared__ int total;
+  // queues of up to kRouteStage assignments are built in LDS and written out coalesced
+  // (one workgroup's scattered 64-lane stores are what limits this kernel otherwise)
+  __shared__ int st_tok[kRouteStage];
+  __shared__ float st_coef[kRouteStage];
+  const bool staged = A <= kRouteStage;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -142,27 +157,41 @@ __global__ __launch_bounds__(1024) void k_moe_route(const void* __restrict__ top
   const int per = (segs + kRouteWaves - 1) / kRouteWaves;
   const int lo = wave * per * 64;
   const int hi = min(A, (wave + 1) * per * 64);
-  for (int i = lo + lane; i < hi; i += 64) {
-    const int e = expert_of(i);
-    if (e >= 0 && e < E) atomicAdd(&cnt[wave][e], 1);
+  // the wave's expert ids, 8 loads in flight per lane (one memory round trip per 512)
+  for (int b0 = lo; b0 < hi; b0 += 64 * kRouteBatch) {
+    int eb[kRouteBatch];
+#pragma unroll
+    for (int j = 0; j < kRouteBatch; ++j) {
+      const int i = b0 + 64 * j + lane;
+      eb[j] = i < hi ? expert_of(i) : -1;
+    }
+    for (int j = 0; j < kRouteBatch; ++j)
+      if (eb[j] >= 0 && eb[j] < E) atomicAdd(&cnt[wave][eb[j]], 1);
   }
   __syncthreads();
-  // per expert: total count, exclusive prefix over experts, per-wave bases
+  // per expert: total count, then the exclusive prefix over experts as a wave scan
+  // (threads 0 .. E-1, at most 8 waves) plus the totals of the lower waves
+  int c_e = 0;
+  if (tid < E)
+    for (int w = 0; w < kRouteWaves; ++w) c_e += cnt[w][tid];
+  int incl = c_e;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63 && wave < kRouteMaxE / 64) wave_tot[wave] = incl;
+  __syncthreads();
   if (tid < E) {
-    int c = 0;
-    for (int w = 0; w < kRouteWaves; ++w) c += cnt[w][tid];
-    base[tid] = c;
+    int excl = incl - c_e;
+    for (int w = 0; w < wave; ++w) excl += wave_tot[w];
+    counts[tid] = c_e;
+    starts[tid] = excl;
+    base[tid] = excl;
   }
-  __syncthreads();
   if (tid == 0) {
     int run = 0;
-    for (int e = 0; e < E; ++e) {
-      const int c = base[e];
-      counts[e] = c;
-      starts[e] = run;
-      base[e] = run;
-      run += c;
-    }
+    for (int w = 0; w < (E + 63) / 64; ++w) run += wave_tot[w];
     total = run;
   }
   __syncthreads();
@@ -177,44 +206,155 @@ __global__ __launch_bounds__(1024) void k_moe_route(const void* __restrict__ top
   __syncthreads();
   int nbits = 1;
   while ((1 << nbits) < E) ++nbits;
-  for (int s0 = lo; s0 < hi; s0 += 64) {
-    const int i = s0 + lane;
-    const bool valid = i < hi;
-    const int e = valid ? expert_of(i) : -1;
-    const bool ok = valid && e >= 0 && e < E;
-    uint64_t match = ballot64(ok);
-    for (int b = 0; b < nbits; ++b) {
-      const uint64_t bb = ballot64(ok && ((e >> b) & 1));
-      match &= ((e >> b) & 1) ? bb : ~bb;
+  for (int b0 = lo; b0 < hi; b0 += 64 * kRouteBatch) {
+    int eb[kRouteBatch];
+    float wb[kRouteBatch];
+#pragma unroll
+    for (int j = 0; j < kRouteBatch; ++j) {
+      const int i = b0 + 64 * j + lane;
+      eb[j] = i < hi ? expert_of(i) : -1;
+      if constexpr (WT == QS_F32) wb[j] = i < hi ? static_cast<const float*>(top_w)[i] : 0.f;
+      else wb[j] = i < hi ? bf16_bits_to_f32(static_cast<const uint16_t*>(top_w)[i]) : 0.f;
     }
-    // match: lanes with the same expert (valid ones); my rank among lower lanes
-    const uint64_t lower = lane ? (~0ull >> (64 - lane)) : 0ull;
-    const int rank = __popcll(match & lower);
-    const int n_same = __popcll(match);
-    int dest = 0;
-    if (ok) dest = cnt[wave][e] + rank;
-    // the highest lane of each expert group advances the cursor (after everyone read it)
-    __builtin_amdgcn_wave_barrier();
-    if (ok && rank == n_same - 1) cnt[wave][e] += n_same;
-    __builtin_amdgcn_wave_barrier();
-    if (ok) {
-      token_ids[dest] = i / k;
-      float cw;
-      if constexpr (WT == QS_F32) cw = static_cast<const float*>(top_w)[i];
-      else cw = bf16_bits_to_f32(static_cast<const uint16_t*>(top_w)[i]);
-      coef[dest] = cw;
-      if (inverse) inverse[i] = dest;
-    } else if (valid && inverse) {
-      inverse[i] = -1;  // expert outside [0, E): no queue row
+    for (int j = 0; j < kRouteBatch; ++j) {
+      if (b0 + 64 * j >= hi) break;  // wave-uniform: no segment left
+      const int i = b0 + 64 * j + lane;
+      const bool valid = i < hi;
+      const int e = eb[j];
+      const bool ok = valid && e >= 0 && e < E;
+      uint64_t match = ballot64(ok);
+      for (int b = 0; b < nbits; ++b) {
+        const uint64_t bb = ballot64(ok && ((e >> b) & 1));
+        match &= ((e >> b) & 1) ? bb : ~bb;
+      }
+      // match: lanes with the same expert (valid ones); my rank among lower lanes
+      const uint64_t lower = lane ? (~0ull >> (64 - lane)) : 0ull;
+      const int rank = __popcll(match & lower);
+      const int n_same = __popcll(match);
+      int dest = 0;
+      if (ok) dest = cnt[wave][e] + rank;
+      // the highest lane of each expert group advances the cursor (after everyone read it)
+      __builtin_amdgcn_wave_barrier();
+      if (ok && rank == n_same - 1) cnt[wave][e] += n_same;
+      __builtin_amdgcn_wave_barrier();
+      if (ok) {
+        if (staged) {
+          st_tok[dest] = i / k;
+          st_coef[dest] = wb[j];
+        } else {
+          token_ids[dest] = i / k;
+          coef[dest] = wb[j];
+        }
+        if (inverse) inverse[i] = dest;
+      } else if (valid && inverse) {
+        inverse[i] = -1;  // expert outside [0, E): no queue row
+      }
     }
   }
   // Assignments with an expert outside [0, E) are left out of the queue.  The rows they
   // leave free at its end get token 0 and coefficient 0, so a consumer that walks all A
   // rows never reads an unwritten index.
-  for (int q = total + tid; q < A; q += 1024) {
-    token_ids[q] = 0;
-    coef[q] = 0.f;
+  if (staged) {
+    __syncthreads();
+    for (int q = tid; q < A; q += 1024) {
+      token_ids[q] = q < total ? st_tok[q] : 0;
+      coef[q] = q < total ? st_coef[q] : 0.f;
+    }
+  } else {
+    for (int q = total + tid; q < A; q += 1024) {
+      token_ids[q] = 0;
+      coef[q] = 0.f;
+    }
   }
+}
+
+// Route compiler for moderate A * E: one workgroup per expert e, 8 waves, each wave owning
+// a contiguous range of 64-assignment segments.  Pass 1 counts, with ballots, the valid
+// assignments of a lower expert (their sum over the waves is starts[e]) and those of e;
+// pass 2 writes e's assignments in index order at starts[e] + (rank among them), which is
+// the stable expert-major order of k_moe_route.  No workgroup waits for another.  Ranges
+// of at most kParSegs segments per wave stay in registers between the passes.
+constexpr int kParWaves = 8;
+constexpr int kParSegs = 8;
+
+template <int IT, int WT>
+__global__ __launch_bounds__(kParWaves * 64) void k_moe_route_par(
+    const void* __restrict__ top_idx, const void* __restrict__ top_w, int A, int k, int E,
+    int64_t* __restrict__ token_ids, float* __restrict__ coef, int32_t* __restrict__ starts,
+    int32_t* __restrict__ counts, int64_t* __restrict__ inverse) {
+  const int e = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  auto expert_of = [&](int i) -> int {
+    if constexpr (IT == QS_I64) return (int)static_cast<const int64_t*>(top_idx)[i];
+    else return static_cast<const int32_t*>(top_idx)[i];
+  };
+  const int nseg = (A + 63) / 64;
+  const int per = (nseg + kParWaves - 1) / kParWaves;
+  const int s_lo = wave * per, s_hi = min(nseg, s_lo + per);
+  const bool resident = per <= kParSegs;
+  int ev[kParSegs];  // expert of assignment (seg * 64 + lane); -1: none or out of range
+  auto load = [&](int s0) {
+#pragma unroll
+    for (int j = 0; j < kParSegs; ++j) {
+      const int i = (s0 + j) * 64 + lane;
+      const int x = (s0 + j < s_hi && i < A) ? expert_of(i) : -1;
+      ev[j] = x >= 0 && x < E ? x : -1;
+    }
+  };
+  int lt = 0, eq = 0;
+  for (int s0 = s_lo; s0 < s_hi; s0 += kParSegs) {
+    load(s0);
+#pragma unroll
+    for (int j = 0; j < kParSegs; ++j) {
+      lt += __popcll(ballot64(ev[j] >= 0 && ev[j] < e));
+      eq += __popcll(ballot64(ev[j] == e));
+    }
+  }
+  __shared__ int s_lt[kParWaves], s_eq[kParWaves];
+  if (lane == 0) {
+    s_lt[wave] = lt;
+    s_eq[wave] = eq;
+  }
+  __syncthreads();
+  int start = 0, cnt = 0, run = 0;
+#pragma unroll
+  for (int w = 0; w < kParWaves; ++w) {
+    start += s_lt[w];
+    cnt += s_eq[w];
+    run += w < wave ? s_eq[w] : 0;
+  }
+  run += start;
+  if (threadIdx.x == 0) {
+    starts[e] = start;
+    counts[e] = cnt;
+  }
+  const uint64_t lower = lane ? (~0ull >> (64 - lane)) : 0ull;
+  for (int s0 = s_lo; s0 < s_hi; s0 += kParSegs) {
+    if (!resident) load(s0);
+#pragma unroll
+    for (int j = 0; j < kParSegs; ++j) {
+      if (s0 + j >= s_hi) break;  // wave-uniform
+      const int i = (s0 + j) * 64 + lane;
+      const uint64_t m = ballot64(ev[j] == e);
+      if (ev[j] == e) {
+        const int dest = run + __popcll(m & lower);
+        token_ids[dest] = i / k;
+        if constexpr (WT == QS_F32) coef[dest] = static_cast<const float*>(top_w)[i];
+        else coef[dest] = bf16_bits_to_f32(static_cast<const uint16_t*>(top_w)[i]);
+        if (inverse) inverse[i] = dest;
+      } else if (e == 0 && inverse && i < A && ev[j] < 0) {
+        inverse[i] = -1;  // expert outside [0, E): no queue row
+      }
+      run += __popcll(m);
+    }
+  }
+  // rows past the valid assignments: token 0, coefficient 0 (the last expert's workgroup
+  // knows their number, start + cnt)
+  if (e == E - 1)
+    for (int q = start + cnt + (int)threadIdx.x; q < A; q += kParWaves * 64) {
+      token_ids[q] = 0;
+      coef[q] = 0.f;
+    }
 }
 
 // ----------------------------------------------------------------------------------
@@ -243,6 +383,94 @@ __global__ __launch_bounds__(256) void k_moe_gather_quant(const void* __restrict
     v = fminf(fmaxf(v, -127.f), 127.f);
     q[a * H + h] = static_cast<int8_t>(v);
   }
+}
+
+// One wave per routed row, 8 elements (one 16- or 32-byte piece) per lane and piece; the
+// row stays in registers between the absmax and the quantization when it has at most
+// 512 pieces (H <= 4096), otherwise it is read twice.  Same recipe and results as
+// k_moe_gather_quant (max is order-free; x / s is the correctly rounded quotient).
+template <int XT>
+struct Piece8 {
+  static constexpr int kBytes = XT == QS_F32 ? 32 : 16;
+  i32x4 v[XT == QS_F32 ? 2 : 1];
+  __device__ __forceinline__ void load(const char* p) {
+    v[0] = *reinterpret_cast<const i32x4*>(p);
+    if constexpr (XT == QS_F32) v[1] = *reinterpret_cast<const i32x4*>(p + 16);
+  }
+  __device__ __forceinline__ float at(int e) const {
+    if constexpr (XT == QS_F32) return __int_as_float(v[e >> 2][e & 3]);
+    else return bf16_bits_to_f32((static_cast<uint32_t>(v[0][e >> 1]) >> (16 * (e & 1))) & 0xffffu);
+  }
+};
+
+constexpr int kQuantPieces = 8;  // pieces per lane kept in registers
+
+// x / s for a bf16 x, |x| <= 127 s, with r = RN(1 / s): Markstein's corrected quotient
+// (y0 = RN(x r), rem = fma(-y0, s, x), RN(rem r + y0); P. Markstein, IBM J. Res. Dev.
+// 34(1), 1990).  For every bf16 amax with s = amax / 127 >= 2^-120 and every bf16 x with
+// |x| <= amax, clamp(rint(.)) of it equals that of the correctly rounded x / s (checked
+// exhaustively over all 1.07e9 such pairs by tests/quant_division_check.c); 3 VALU
+// operations instead of a full division.
+__device__ __forceinline__ float quot_markstein(float x, float s, float r) {
+  const float y0 = mul_rn(x, r);
+  return __builtin_fmaf(__builtin_fmaf(-y0, s, x), r, y0);
+}
+
+template <int XT>
+__global__ __launch_bounds__(256) void k_moe_gather_quant8(const void* __restrict__ src, int64_t ld_src,
+                                                           const int64_t* __restrict__ rows, int64_t A,
+                                                           int H, int8_t* __restrict__ q,
+                                                           float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t a = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (a >= A) return;
+  const int64_t r = rows ? rows[a] : a;
+  const char* xr = static_cast<const char*>(src) + r * ld_src * (XT == QS_F32 ? 4 : 2);
+  const int np = H >> 3;
+  Piece8<XT> pc[kQuantPieces];
+  float amax = 0.f;
+  for (int p0 = 0; p0 < np; p0 += 64 * kQuantPieces) {
+#pragma unroll
+    for (int j = 0; j < kQuantPieces; ++j) {
+      const int pi = p0 + 64 * j + lane;
+      if (pi < np) {
+        pc[j].load(xr + (int64_t)pi * Piece8<XT>::kBytes);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(pc[j].at(e)));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  float s = amax / 127.0f;
+  if (s == 0.f) s = 1.f;
+  if (lane == 0) scale[a] = s;
+  const bool resident = np <= 64 * kQuantPieces;
+  int8_t* qr = q + a * H;
+  const float rs = 1.0f / s;  // correctly rounded
+  // wave-uniform: bf16 rows with s >= 2^-120 take the corrected product, others divide
+  const bool fast = XT == QS_BF16 && s >= 0x1p-120f;
+  auto quantize = [&](auto fast_tag) {
+    for (int p0 = 0; p0 < np; p0 += 64 * kQuantPieces) {
+#pragma unroll
+      for (int j = 0; j < kQuantPieces; ++j) {
+        const int pi = p0 + 64 * j + lane;
+        if (pi < np) {
+          if (!resident) pc[j].load(xr + (int64_t)pi * Piece8<XT>::kBytes);
+          uint32_t w[2] = {0u, 0u};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = pc[j].at(e);
+            float v = rintf(decltype(fast_tag)::value ? quot_markstein(x, s, rs) : x / s);
+            v = fminf(fmaxf(v, -127.f), 127.f);
+            w[e >> 2] |= (static_cast<uint32_t>(static_cast<int>(v)) & 0xffu) << (8 * (e & 3));
+          }
+          *reinterpret_cast<uint2*>(qr + (int64_t)pi * 8) = make_uint2(w[0], w[1]);
+        }
+      }
+    }
+  };
+  if (fast) quantize(std::true_type{});
+  else quantize(std::false_type{});
 }
 
 // ----------------------------------------------------------------------------------
@@ -382,48 +610,54 @@ __global__ __launch_bounds__(P * KW * 64) void k_moe_gemm(MoeGemmParams p) {
 // Streaming grouped GEMM.  Each wave owns RW output rows over the full K: SwiGLU
 // (P = 2): 16 rows n0 .. n0 + 15 of gate and the same rows + N of up; plain (P = 1):
 // NB consecutive 16-row tiles.  Its NB weight tiles are the B operands of
-// v_mfma_i32_16x16x64_i8: lane l loads bytes 64c + 16(l >> 4) .. +16 of tile row l & 15
-// for k-chunk c (column l & 15, k-block l >> 4).  The A operand is the same k range of
-// staged row (l & 15) of a 16-row tile of the group, read once from LDS per chunk and
+// v_mfma_i32_16x16x64_i8.  K is walked in chunks of CB bytes: with PAIR (K % 128 == 0)
+// a chunk is 128 bytes and lane l loads the 32 contiguous bytes 32(l >> 4) .. +32 of
+// tile row l & 15 as two 16-byte pieces, so each 128-byte line of a weight row is asked
+// for whole by two back-to-back loads (without PAIR, 64-byte chunks, 16 bytes per lane).
+// Piece j of a chunk is the k-block l >> 4 of one MFMA; the A operand is the same bytes
+// of staged row (l & 15) of a 16-row tile of the group, read from LDS per piece and
 // shared by the NB tiles (rows padded by 16 bytes, so the 16 rows of a read fall in
-// distinct banks).  The chunk loads run W chunks ahead of the MFMAs, issued in k order;
-// slots past the last chunk reload it (static wait counts).  Staged rows past the
-// group's count hold stale LDS data: their MFMA columns are never stored.
-// waves per workgroup: 8 for SwiGLU (gate/up), 4 for plain products (more workgroups per
-// CU; the T=512 down projection 80 -> 74 us, while gate/up is fastest at 8)
-template <int P>
-constexpr int kMoeWaves = P == 2 ? 8 : 4;
-
+// distinct banks).  Any assignment of bytes to k-blocks that A and B share gives the
+// same exact int32 sum.  The chunk loads run W chunks ahead of the MFMAs, issued in k
+// order; slots past the last chunk reload it (static wait counts).  Staged rows past the
+// group's count hold stale LDS data: their MFMA columns are never stored.  Weights are
+// read with ordinary cached loads: nontemporal loads measured 20-30% slower here.
 template <int P, int NB>
 struct MoeStreamCfg {
   static constexpr int RW = P == 2 ? 16 : 16 * NB;  // output rows per wave
 };
 
-template <int P, int NB, int MT>
-__global__ __launch_bounds__(kMoeWaves<P> * 64) void k_moe_stream(MoeGemmParams p) {
+template <int P, int NB, int MT, int W, int WAVES, int PAIR>
+__global__ __launch_bounds__(WAVES * 64) void k_moe_stream(MoeGemmParams p) {
   static_assert(P == 1 || NB == 2, "SwiGLU streams the gate and up tiles of one row block");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int MC = 16 * MT;
-  constexpr int NT = kMoeWaves<P> * 64;
-  // chunks in flight: 4 weight loads per wave for one row tile, 8 for more (a small
-  // window keeps the kernel at 110-160 VGPRs, 3-4 waves per SIMD; 16 loads measured
-  // 3-13% slower at 2 waves per SIMD)
-  constexpr int W = (MT == 1 ? 4 : 8) / NB > 0 ? (MT == 1 ? 4 : 8) / NB : 1;
+  constexpr int NT = WAVES * 64;
   constexpr int RW = MoeStreamCfg<P, NB>::RW;
+  constexpr int CB = PAIR ? 128 : 64;  // bytes of a weight row per chunk
+  constexpr int PL = PAIR ? 2 : 1;     // 16-byte pieces per lane per chunk
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, q = lane >> 4;
-  const int g = blockIdx.y;
+  // Workgroup i runs on XCD i % 8.  The row blocks of one group share its staged routed
+  // rows, so consecutive logical indices (group-major) go to one XCD and its L2 serves
+  // the repeats: the first 8 * floor(total / 8) workgroups are dealt out XCD-major, the
+  // remainder keeps its index (a bijection on [0, total)).
+  const int total = gridDim.x * gridDim.y, lin = blockIdx.y * gridDim.x + blockIdx.x;
+  const int per_xcd = total / 8;
+  const int logical = lin < 8 * per_xcd ? (lin % 8) * per_xcd + lin / 8 : lin;
+  const int g = logical / gridDim.x, bx = logical - g * gridDim.x;
   const int count = p.counts[g];
   if (count == 0) return;
   const int start = p.starts[g];
   const int slot = p.slots ? p.slots[g] : g;
-  const int K = p.K, C = K >> 6;
+  const int K = p.K, C = K / CB;
   const int xstride = K + 16;
   int8_t* xs = reinterpret_cast<int8_t*>(lds);                 // [MC][K + 16]
   float* asl = reinterpret_cast<float*>(lds + MC * xstride);   // [MC]
-  const int n0 = (blockIdx.x * kMoeWaves<P> + wave) * RW;
+  const int n0 = (bx * WAVES + wave) * RW;
   const bool live = n0 < p.N;
+  const int lo = PAIR ? 32 * q : 16 * q;  // the lane's byte offset within a chunk
   const int8_t* wexp = p.w + (int64_t)slot * p.w_stride;
   const int8_t* wr[NB];
   float wsc[NB];
@@ -431,19 +665,21 @@ __global__ __launch_bounds__(kMoeWaves<P> * 64) void k_moe_stream(MoeGemmParams 
   for (int b = 0; b < NB; ++b) {
     // weight row of tile b for this lane's column
     const int nb = P == 2 ? min(n0 + col, p.N - 1) + b * p.N : min(n0 + 16 * b + col, p.N - 1);
-    wr[b] = wexp + (int64_t)nb * K + 16 * q;
+    wr[b] = wexp + (int64_t)nb * K + lo;
     wsc[b] = p.ws[(int64_t)slot * p.ws_stride + nb];
   }
   const int ppr = K >> 4;  // 16-byte pieces per row
 
   for (int m0 = 0; m0 < count; m0 += MC) {
     const int mc = min(MC, count - m0);
-    i32x4 wv[W][NB];
+    i32x4 wv[W][NB][PL];
 #pragma unroll
     for (int u = 0; u < W; ++u) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        wv[u][b] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wr[b] + (int64_t)min(u, C - 1) * 64));
+#pragma unroll
+        for (int j = 0; j < PL; ++j)
+          wv[u][b][j] = *reinterpret_cast<const i32x4*>(wr[b] + (int64_t)min(u, C - 1) * CB + 16 * j);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -484,17 +720,21 @@ __global__ __launch_bounds__(kMoeWaves<P> * 64) void k_moe_stream(MoeGemmParams 
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             if (mt * 16 < mc) {
-              const i32x4 av = *reinterpret_cast<const i32x4*>(xs + (mt * 16 + col) * xstride + c * 64 + 16 * q);
 #pragma unroll
-              for (int b = 0; b < NB; ++b)
-                acc[mt][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, wv[u][b], acc[mt][b], 0, 0, 0);
+              for (int j = 0; j < PL; ++j) {
+                const i32x4 av = *reinterpret_cast<const i32x4*>(xs + (mt * 16 + col) * xstride + c * CB + lo + 16 * j);
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                  acc[mt][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, wv[u][b][j], acc[mt][b], 0, 0, 0);
+              }
             }
           }
         }
         const int cn = min(c + W, C - 1);
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-          wv[u][b] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wr[b] + (int64_t)cn * 64));
+#pragma unroll
+          for (int j = 0; j < PL; ++j) wv[u][b][j] = *reinterpret_cast<const i32x4*>(wr[b] + (int64_t)cn * CB + 16 * j);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -542,13 +782,13 @@ __global__ __launch_bounds__(kMoeWaves<P> * 64) void k_moe_stream(MoeGemmParams 
 // ----------------------------------------------------------------------------------
 // stable rank-order reduce
 // ----------------------------------------------------------------------------------
-template <int YT>
+template <int YT, int OT>
 __global__ __launch_bounds__(256) void k_moe_reduce(const void* __restrict__ y,
                                                     const float* __restrict__ coef,
                                                     const int64_t* __restrict__ inv, int k,
-                                                    int H, float* __restrict__ out) {
-  const int64_t t = blockIdx.y;
-  const int h = blockIdx.x * 256 + threadIdx.x;
+                                                    int H, void* __restrict__ out) {
+  const int64_t t = blockIdx.x;
+  const int h = blockIdx.y * 256 + threadIdx.x;
   if (h >= H) return;
   float acc = 0.f;
   for (int r = 0; r < k; ++r) {
@@ -557,7 +797,60 @@ __global__ __launch_bounds__(256) void k_moe_reduce(const void* __restrict__ y,
     const float c = a < 0 ? 0.f : mul_rn(ld<YT>(y, a * H + h), coef[a]);
     acc = r == 0 ? c : add_rn(acc, c);
   }
-  out[t * H + h] = acc;
+  if constexpr (OT == QS_F32) static_cast<float*>(out)[t * H + h] = acc;
+  else static_cast<uint16_t*>(out)[t * H + h] = f32_to_bf16_bits(acc);
+}
+
+// Eight consecutive h per thread (16- or 32-byte loads of y), one token per blockIdx.x;
+// the same products, sums and order as k_moe_reduce.  OT = BF16 rounds the fp32 sum once
+// (RNE), which is the fp32 reduce followed by a cast to bf16.
+template <int YT, int OT>
+__global__ __launch_bounds__(256) void k_moe_reduce8(const void* __restrict__ y,
+                                                     const float* __restrict__ coef,
+                                                     const int64_t* __restrict__ inv, int k,
+                                                     int H, void* __restrict__ out) {
+  const int64_t t = blockIdx.x;
+  const int h0 = (blockIdx.y * 256 + threadIdx.x) * 8;
+  if (h0 >= H) return;
+  float acc[8];
+  // ranks in batches of 8: every row of a batch is requested before the first is used
+  constexpr int RB = 8;
+  for (int r0 = 0; r0 < k; r0 += RB) {
+    int64_t a[RB];
+    float cf[RB];
+    Piece8<YT> pc[RB];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) a[j] = r0 + j < k ? inv[t * k + r0 + j] : -1;
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      if (a[j] >= 0) {
+        cf[j] = coef[a[j]];
+        pc[j].load(static_cast<const char*>(y) + (a[j] * H + h0) * (YT == QS_F32 ? 4 : 2));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      if (r0 + j >= k) break;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // a negative inverse entry: the route compiler dropped this rank, it adds 0
+        const float c = a[j] < 0 ? 0.f : mul_rn(pc[j].at(e), cf[j]);
+        acc[e] = r0 + j == 0 ? c : add_rn(acc[e], c);
+      }
+    }
+  }
+  if constexpr (OT == QS_F32) {
+    float* o = static_cast<float*>(out) + t * H + h0;
+    *reinterpret_cast<f32x4*>(o) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = static_cast<uint32_t>(f32_to_bf16_bits(acc[2 * e])) | (static_cast<uint32_t>(f32_to_bf16_bits(acc[2 * e + 1])) << 16);
+    *reinterpret_cast<i32x4*>(static_cast<uint16_t*>(out) + t * H + h0) =
+        i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+  }
 }
 
 }  // namespace qs
@@ -572,14 +865,25 @@ extern "C" int qs_moe_router(const void* logits, int logit_dtype, int64_t T, int
     return fail(QS_ERR_LIMIT, "moe_router: need 1 <= E <= 1024, 1 <= k <= min(16, E)");
   if (w_dtype != QS_F32 && w_dtype != QS_BF16) return fail(QS_ERR_INVALID, "moe_router: weight dtype F32 or BF16");
   if (T == 0) return QS_OK;
+  if (logit_dtype != QS_F32 && logit_dtype != QS_BF16) return fail(QS_ERR_INVALID, "moe_router: logits F32 or BF16");
+  if (T > (int64_t)INT32_MAX) return fail(QS_ERR_LIMIT, "moe_router: too many tokens");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const unsigned blocks = (unsigned)cdiv(T, 4);
-  if (logit_dtype == QS_F32)
-    hipLaunchKernelGGL(k_moe_router<QS_F32>, dim3(blocks), dim3(256), 0, s, logits, (int)T, E, k, norm_topk, top_idx, top_w, w_dtype);
-  else if (logit_dtype == QS_BF16)
-    hipLaunchKernelGGL(k_moe_router<QS_BF16>, dim3(blocks), dim3(256), 0, s, logits, (int)T, E, k, norm_topk, top_idx, top_w, w_dtype);
-  else
-    return fail(QS_ERR_INVALID, "moe_router: logits F32 or BF16");
+#define QS_ROUTER(J)                                                                                        \
+  do {                                                                                                      \
+    if (logit_dtype == QS_F32)                                                                              \
+      hipLaunchKernelGGL((k_moe_router<QS_F32, J>), dim3(blocks), dim3(256), 0, s, logits, (int)T, E, k,    \
+                         norm_topk, top_idx, top_w, w_dtype);                                               \
+    else                                                                                                    \
+      hipLaunchKernelGGL((k_moe_router<QS_BF16, J>), dim3(blocks), dim3(256), 0, s, logits, (int)T, E, k,   \
+                         norm_topk, top_idx, top_w, w_dtype);                                               \
+  } while (0)
+  if (E <= 64) QS_ROUTER(1);
+  else if (E <= 128) QS_ROUTER(2);
+  else if (E <= 256) QS_ROUTER(4);
+  else if (E <= 512) QS_ROUTER(8);
+  else QS_ROUTER(16);
+#undef QS_ROUTER
   return hip_check(hipGetLastError(), "k_moe_router launch");
 }
 
@@ -593,8 +897,18 @@ extern "C" int qs_moe_route(const void* top_idx, int idx_dtype, const void* top_
   if (T * k > (int64_t)1 << 28) return fail(QS_ERR_LIMIT, "moe_route: too many assignments");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int A = (int)(T * k);
-#define QS_ROUTE(IT, WT) \
-  hipLaunchKernelGGL((k_moe_route<IT, WT>), dim3(1), dim3(1024), 0, s, top_idx, top_w, A, k, E, token_ids, coef, starts, counts, inverse)
+  // one workgroup per expert while the E re-reads of the A expert ids stay small (they
+  // come from L2); a single workgroup otherwise
+  const bool par = (int64_t)A * E <= ((int64_t)1 << 22);
+#define QS_ROUTE(IT, WT)                                                                              \
+  do {                                                                                                \
+    if (par)                                                                                          \
+      hipLaunchKernelGGL((k_moe_route_par<IT, WT>), dim3(E), dim3(kParWaves * 64), 0, s, top_idx, top_w, \
+                         A, k, E, token_ids, coef, starts, counts, inverse);                          \
+    else                                                                                              \
+      hipLaunchKernelGGL((k_moe_route<IT, WT>), dim3(1), dim3(1024), 0, s, top_idx, top_w, A, k, E,   \
+                         token_ids, coef, starts, counts, inverse);                                   \
+  } while (0)
   if (idx_dtype == QS_I64 && w_dtype == QS_F32) QS_ROUTE(QS_I64, QS_F32);
   else if (idx_dtype == QS_I64 && w_dtype == QS_BF16) QS_ROUTE(QS_I64, QS_BF16);
   else if (idx_dtype == QS_I32 && w_dtype == QS_F32) QS_ROUTE(QS_I32, QS_F32);
@@ -610,13 +924,23 @@ extern "C" int qs_moe_gather_quant(const void* source, int src_dtype, int64_t ld
   if (!source || !q || !scale) return fail(QS_ERR_INVALID, "moe_gather_quant: null pointer");
   if (A < 0 || H <= 0 || ld_src < H) return fail(QS_ERR_INVALID, "moe_gather_quant: bad shape");
   if (A == 0) return QS_OK;
+  if (src_dtype != QS_BF16 && src_dtype != QS_F32) return fail(QS_ERR_INVALID, "moe_gather_quant: source F32 or BF16");
+  if (H > INT32_MAX) return fail(QS_ERR_LIMIT, "moe_gather_quant: H too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t esize = src_dtype == QS_F32 ? 4 : 2;
+  if (H % 8 == 0 && aligned(source, 16) && (ld_src * esize) % 16 == 0 && aligned(q, 8)) {
+    const dim3 grid((unsigned)cdiv(A, 4));
+    if (src_dtype == QS_BF16)
+      hipLaunchKernelGGL(k_moe_gather_quant8<QS_BF16>, grid, dim3(256), 0, s, source, ld_src, rows, A, (int)H, q, scale);
+    else
+      hipLaunchKernelGGL(k_moe_gather_quant8<QS_F32>, grid, dim3(256), 0, s, source, ld_src, rows, A, (int)H, q, scale);
+    return hip_check(hipGetLastError(), "k_moe_gather_quant8 launch");
+  }
+  if (A > INT32_MAX) return fail(QS_ERR_LIMIT, "moe_gather_quant: too many rows for the unaligned path");
   if (src_dtype == QS_BF16)
     hipLaunchKernelGGL(k_moe_gather_quant<QS_BF16>, dim3((unsigned)A), dim3(256), 0, s, source, ld_src, rows, (int)H, q, scale);
-  else if (src_dtype == QS_F32)
-    hipLaunchKernelGGL(k_moe_gather_quant<QS_F32>, dim3((unsigned)A), dim3(256), 0, s, source, ld_src, rows, (int)H, q, scale);
   else
-    return fail(QS_ERR_INVALID, "moe_gather_quant: source F32 or BF16");
+    hipLaunchKernelGGL(k_moe_gather_quant<QS_F32>, dim3((unsigned)A), dim3(256), 0, s, source, ld_src, rows, (int)H, q, scale);
   return hip_check(hipGetLastError(), "k_moe_gather_quant launch");
 }
 
@@ -642,14 +966,31 @@ size_t moe_stream_lds(int MT, int64_t K) {
   return b <= kMoeStreamLds ? b : 0;
 }
 
+// Launch shapes measured on config-4 shapes (E 128, H 2048, I 768, T 64 / 512):
+// SwiGLU streams with 4 waves when one row tile is staged (T = 64: 70 us vs 76 us with 8)
+// and 8 waves for more; two 128-byte chunks in flight.  Plain products keep 128 bytes
+// of each weight row in flight for NB >= 2 tiles per wave, 256 for one.
+template <int P, int NB, int MT, int PAIR>
+void launch_moe_stream_mt(const MoeGemmParams& p, int G, hipStream_t s) {
+  constexpr int WAVES = P == 2 ? (MT == 1 ? 4 : 8) : 4;
+  constexpr int WP = P == 2 ? 2 : (NB >= 2 ? 1 : 2);  // 128-byte chunks in flight
+  constexpr int W = PAIR ? WP : 2 * WP;
+  constexpr int RW = MoeStreamCfg<P, NB>::RW;
+  const dim3 grid((unsigned)cdiv(p.N, RW * WAVES), (unsigned)G), block(WAVES * 64);
+  hipLaunchKernelGGL((k_moe_stream<P, NB, MT, W, WAVES, PAIR>), grid, block, moe_stream_lds(MT, p.K), s, p);
+}
+
 template <int P, int NB>
 void launch_moe_stream(const MoeGemmParams& p, int G, int MT, hipStream_t s) {
-  constexpr int RW = MoeStreamCfg<P, NB>::RW;
-  const dim3 grid((unsigned)cdiv(p.N, RW * kMoeWaves<P>), (unsigned)G), block(kMoeWaves<P> * 64);
-  const size_t lds = moe_stream_lds(MT, p.K);
-  if (MT == 4) hipLaunchKernelGGL((k_moe_stream<P, NB, 4>), grid, block, lds, s, p);
-  else if (MT == 2) hipLaunchKernelGGL((k_moe_stream<P, NB, 2>), grid, block, lds, s, p);
-  else hipLaunchKernelGGL((k_moe_stream<P, NB, 1>), grid, block, lds, s, p);
+  if (p.K % 128 == 0) {
+    if (MT == 4) launch_moe_stream_mt<P, NB, 4, 1>(p, G, s);
+    else if (MT == 2) launch_moe_stream_mt<P, NB, 2, 1>(p, G, s);
+    else launch_moe_stream_mt<P, NB, 1, 1>(p, G, s);
+  } else {
+    if (MT == 4) launch_moe_stream_mt<P, NB, 4, 0>(p, G, s);
+    else if (MT == 2) launch_moe_stream_mt<P, NB, 2, 0>(p, G, s);
+    else launch_moe_stream_mt<P, NB, 1, 0>(p, G, s);
+  }
 }
 }  // namespace
 
@@ -676,9 +1017,9 @@ extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, con
   const int64_t mean = max_rows > 0 ? cdiv(max_rows, G) : 16;
   int MT = 2 * mean <= 16 ? 1 : (2 * mean <= 32 ? 2 : 4);
   while (MT > 1 && !moe_stream_lds(MT, K)) MT /= 2;
-  // Plain products over short groups (one 16-row tile) read faster as many small
-  // workgroups that each take whole rows (the K-split kernel) than as long streams.
-  if (moe_stream_lds(MT, K) && (swiglu || MT > 1)) {
+  // The K-split kernel only takes K beyond what the staged row tile fits in LDS (with
+  // 128-byte chunk loads the stream also beats it on short groups: T = 64 down 50 -> 42 us).
+  if (moe_stream_lds(MT, K)) {
     // plain: row tiles per wave so that a wave streams about 48 KB or more
     if (swiglu) launch_moe_stream<2, 2>(p, G, MT, s);
     else if (K <= 1024) launch_moe_stream<1, 4>(p, G, MT, s);
@@ -699,19 +1040,38 @@ extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, con
   return hip_check(hipGetLastError(), "k_moe_gemm launch");
 }
 
+extern "C" int qs_moe_route_reduce_to(const void* expert_out, int y_dtype, const float* coef,
+                                      const int64_t* inverse, int64_t T, int k, int64_t H,
+                                      void* out, int out_dtype, void* stream) {
+  if (!expert_out || !coef || !inverse || !out) return fail(QS_ERR_INVALID, "moe_route_reduce: null pointer");
+  if (T < 0 || k < 1 || H <= 0) return fail(QS_ERR_INVALID, "moe_route_reduce: bad shape");
+  if (T > INT32_MAX || H > 65535 * 256) return fail(QS_ERR_LIMIT, "moe_route_reduce: T or H too large");
+  if (y_dtype != QS_BF16 && y_dtype != QS_F32) return fail(QS_ERR_INVALID, "moe_route_reduce: expert output F32 or BF16");
+  if (out_dtype != QS_BF16 && out_dtype != QS_F32) return fail(QS_ERR_INVALID, "moe_route_reduce: out F32 or BF16");
+  if (T == 0) return QS_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (H % 8 == 0 && aligned(expert_out, 16) && aligned(out, 16)) {
+    const dim3 grid((unsigned)T, (unsigned)cdiv(H, 2048));
+#define QS_RED8(YT, OT) hipLaunchKernelGGL((k_moe_reduce8<YT, OT>), grid, dim3(256), 0, s, expert_out, coef, inverse, k, (int)H, out)
+    if (y_dtype == QS_BF16 && out_dtype == QS_F32) QS_RED8(QS_BF16, QS_F32);
+    else if (y_dtype == QS_BF16) QS_RED8(QS_BF16, QS_BF16);
+    else if (out_dtype == QS_F32) QS_RED8(QS_F32, QS_F32);
+    else QS_RED8(QS_F32, QS_BF16);
+#undef QS_RED8
+    return hip_check(hipGetLastError(), "k_moe_reduce8 launch");
+  }
+  const dim3 grid((unsigned)T, (unsigned)cdiv(H, 256));
+#define QS_RED(YT, OT) hipLaunchKernelGGL((k_moe_reduce<YT, OT>), grid, dim3(256), 0, s, expert_out, coef, inverse, k, (int)H, out)
+  if (y_dtype == QS_BF16 && out_dtype == QS_F32) QS_RED(QS_BF16, QS_F32);
+  else if (y_dtype == QS_BF16) QS_RED(QS_BF16, QS_BF16);
+  else if (out_dtype == QS_F32) QS_RED(QS_F32, QS_F32);
+  else QS_RED(QS_F32, QS_BF16);
+#undef QS_RED
+  return hip_check(hipGetLastError(), "k_moe_reduce launch");
+}
+
 extern "C" int qs_moe_route_reduce(const void* expert_out, int y_dtype, const float* coef,
                                    const int64_t* inverse, int64_t T, int k, int64_t H,
                                    float* out, void* stream) {
-  if (!expert_out || !coef || !inverse || !out) return fail(QS_ERR_INVALID, "moe_route_reduce: null pointer");
-  if (T < 0 || k < 1 || H <= 0 || T > 65535 * 1024) return fail(QS_ERR_INVALID, "moe_route_reduce: bad shape");
-  if (T == 0) return QS_OK;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid((unsigned)cdiv(H, 256), (unsigned)T);
-  if (y_dtype == QS_BF16)
-    hipLaunchKernelGGL(k_moe_reduce<QS_BF16>, grid, dim3(256), 0, s, expert_out, coef, inverse, k, (int)H, out);
-  else if (y_dtype == QS_F32)
-    hipLaunchKernelGGL(k_moe_reduce<QS_F32>, grid, dim3(256), 0, s, expert_out, coef, inverse, k, (int)H, out);
-  else
-    return fail(QS_ERR_INVALID, "moe_route_reduce: expert output F32 or BF16");
-  return hip_check(hipGetLastError(), "k_moe_reduce launch");
+  return qs_moe_route_reduce_to(expert_out, y_dtype, coef, inverse, T, k, H, out, QS_F32, stream);
 }

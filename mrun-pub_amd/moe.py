@@ -137,9 +137,12 @@ def stable_route_reduce(
     selected_experts: torch.Tensor,
     *,
     inverse_assignments: torch.Tensor | None = None,
+    out_dtype: torch.dtype = torch.float32,
 ) -> torch.Tensor:
     """``out[t] = sum_rank float(expert_out[inv[t*k+rank]]) * float(coef[...])`` in fixed rank
-    order, fp32 ``[T, H]`` (qwen3_moe_cuda.py:2561-2664)."""
+    order, fp32 ``[T, H]`` (qwen3_moe_cuda.py:2561-2664).  ``out_dtype=torch.bfloat16``
+    returns the fp32 sums rounded once, what the caller's ``output.to(self.dtype)``
+    (qwen3_moe_cuda.py:2936) makes of them, from the same kernel."""
     if top_indices.ndim != 2:
         raise ValueError("stable route reduction requires [rows, top_k] indices")
     rows, top_k = map(int, top_indices.shape)
@@ -176,10 +179,12 @@ def stable_route_reduce(
     if y.dtype not in (torch.float32, torch.bfloat16):
         y = y.float()
     coef = coefficients.float().contiguous()
-    out = torch.empty((rows, H), dtype=torch.float32, device=device)
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("stable route reduction output must be float32 or bfloat16")
+    out = torch.empty((rows, H), dtype=out_dtype, device=device)
     nat.call(
-        "qs_moe_route_reduce", nat.ptr(y), nat.dtype_code(y.dtype), nat.ptr(coef), nat.ptr(inverse.contiguous()),
-        rows, top_k, H, nat.ptr(out), nat.stream_of(device),
+        "qs_moe_route_reduce_to", nat.ptr(y), nat.dtype_code(y.dtype), nat.ptr(coef), nat.ptr(inverse.contiguous()),
+        rows, top_k, H, nat.ptr(out), nat.dtype_code(out_dtype), nat.stream_of(device),
     )
     return out
 
@@ -367,6 +372,11 @@ class Int8ExpertBackend:
         self.stats = {"grouped_kernel_calls": 0, "route_compiler_calls": 0, "expert_assignments": 0}
         self._experts: dict[tuple[torch.device, int], torch.Tensor] = {}
 
+    def _reduce_dtype(self) -> torch.dtype:
+        # the reduce kernel rounds its fp32 sums to bf16 itself; other model dtypes are
+        # cast from the fp32 result
+        return self.dtype if self.dtype in (torch.float32, torch.bfloat16) else torch.float32
+
     def _expert_ids(self, device: torch.device, E: int) -> torch.Tensor:
         key = (device, E)
         ids = self._experts.get(key)
@@ -401,7 +411,7 @@ class Int8ExpertBackend:
         )
         out = stable_route_reduce(
             expert_output, coef, token_ids, counts, top_indices,
-            self._expert_ids(source.device, E), inverse_assignments=inverse,
+            self._expert_ids(source.device, E), inverse_assignments=inverse, out_dtype=self._reduce_dtype(),
         )
         self.stats["grouped_kernel_calls"] += 2
         self.stats["route_compiler_calls"] += 1
@@ -428,6 +438,7 @@ class Int8ExpertBackend:
         )
         out = stable_route_reduce(
             expert_output, coef, token_ids, counts, top_indices, selected, inverse_assignments=inverse,
+            out_dtype=self._reduce_dtype(),
         )
         cache.release()
         self.stats["grouped_kernel_calls"] += 2

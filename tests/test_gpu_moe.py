@@ -35,7 +35,9 @@ def test_route_reference_kat(dev):
     assert sorted(inv.tolist()) == list(range(6))
 
 
-@pytest.mark.parametrize("T,E,k", [(64, 128, 8), (512, 128, 8), (7, 5, 3), (1, 128, 8), (3000, 64, 4)])
+# A * E <= 2^22: one workgroup per expert; (16384, 64, 4) and (9000, 512, 1): one workgroup
+@pytest.mark.parametrize("T,E,k", [(64, 128, 8), (512, 128, 8), (7, 5, 3), (1, 128, 8), (3000, 64, 4),
+                                   (200, 512, 8), (100, 300, 6), (16384, 64, 4), (9000, 512, 1)])
 @pytest.mark.parametrize("wdt", [torch.float32, torch.bfloat16])
 def test_route_equals_stable_argsort(dev, T, E, k, wdt):
     rng = np.random.default_rng(T + E + k)
@@ -87,6 +89,28 @@ def test_route_drops_out_of_range_experts(dev):
     assert np.array_equal(red.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("T,E,k", [(300, 64, 4), (16384, 64, 4)])  # per-expert / one workgroup
+def test_route_drops_out_of_range_both_kernels(dev, T, E, k):
+    rng = np.random.default_rng(T)
+    top = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
+    bad = rng.random((T, k)) < 0.01
+    top[bad] = rng.choice([-3, -1, E, E + 7], size=int(bad.sum()))
+    w = rng.random((T, k)).astype(np.float32)
+    tok, coef, starts, counts, inv, _ = _moe().grouped_route_tensors_with_inverse(_t(top, dev), _t(w, dev), num_experts=E)
+    keep = ~bad
+    flat = top.reshape(-1)
+    fk = keep.reshape(-1)
+    order = np.argsort(np.where(fk, flat, E), kind="stable")[: int(fk.sum())]
+    n = int(fk.sum())
+    assert counts.cpu().numpy().tolist() == np.bincount(flat[fk], minlength=E).tolist()
+    assert tok.cpu().numpy()[:n].tolist() == (order // k).tolist()
+    assert np.array_equal(coef.cpu().numpy()[:n], w.reshape(-1)[order])
+    assert not tok.cpu().numpy()[n:].any() and not coef.cpu().numpy()[n:].any()
+    exp_inv = np.full(T * k, -1, np.int64)
+    exp_inv[order] = np.arange(n)
+    assert np.array_equal(inv.cpu().numpy(), exp_inv)
+
+
 def test_router_against_oracle(dev):
     rng = np.random.default_rng(4)
     logits = rng.standard_normal((512, 128)).astype(np.float32)
@@ -94,6 +118,19 @@ def test_router_against_oracle(dev):
     rw, ridx = om.router(logits, 8)
     assert np.array_equal(idx.cpu().numpy(), ridx)
     assert oq.rel_l2(w.float().cpu().numpy(), rw) < 2e-3
+
+
+# expert counts for each logits-per-lane width (1, 2, 4, 8, 16 per lane), k up to 16
+@pytest.mark.parametrize("T,E,k", [(33, 5, 3), (64, 64, 16), (70, 200, 8), (40, 300, 6), (20, 1024, 16), (9, 700, 1)])
+@pytest.mark.parametrize("norm", [True, False])
+def test_router_widths_fp32(dev, T, E, k, norm):
+    rng = np.random.default_rng(E + k)
+    logits = (rng.standard_normal((T, E)) * 3).astype(np.float32)
+    w, idx = _moe().route_topk(_t(logits, dev), k, norm_topk=norm, out_dtype=torch.float32)
+    rw, ridx = om.router(logits, k, norm_topk=norm, bf16=False)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    # expf and numpy's exp may differ in the last place
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6, atol=0)
 
 
 def test_stable_reduce_reference_kat(dev):
@@ -127,6 +164,47 @@ def test_stable_reduce_bit_exact(dev, T, k, H):
     assert np.array_equal(got.cpu().numpy(), om.stable_route_reduce(eo, coef, inv, T, k))
 
 
+@pytest.mark.parametrize("T,k,H", [(64, 8, 2048), (5, 3, 100)])  # 8-wide kernel, scalar kernel
+def test_stable_reduce_bf16_out_is_cast_of_fp32(dev, T, k, H):
+    rng = np.random.default_rng(T + 1)
+    A = T * k
+    eo = _t(oq.round_bf16(rng.standard_normal((A, H)).astype(np.float32)), dev, torch.bfloat16)
+    coef = _t(rng.random(A).astype(np.float32), dev)
+    inv = rng.permutation(A).astype(np.int64)
+    tok = _t((np.argsort(inv) // k).astype(np.int64), dev)
+    args = (eo, coef, tok, torch.tensor([A], dtype=torch.int32, device=dev),
+            torch.zeros((T, k), dtype=torch.long, device=dev), torch.zeros(1, dtype=torch.long, device=dev))
+    f32 = _moe().stable_route_reduce(*args, inverse_assignments=_t(inv, dev))
+    b16 = _moe().stable_route_reduce(*args, inverse_assignments=_t(inv, dev), out_dtype=torch.bfloat16)
+    assert b16.dtype == torch.bfloat16
+    assert torch.equal(b16, f32.to(torch.bfloat16))
+
+
+# H = 2048 / 768: one wave per row, row kept in registers; 8192: row read twice;
+# 100: scalar kernel (H % 8 != 0)
+@pytest.mark.parametrize("H", [2048, 768, 8192, 100])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_quantize_rows_matches_oracle(dev, H, dtype):
+    rng = np.random.default_rng(H)
+    T, A = 37, 150
+    x = rng.standard_normal((T, H)).astype(np.float32) * rng.uniform(0.1, 10, size=(T, 1)).astype(np.float32)
+    x[3] = 0.0  # all-zero row: scale 1, codes 0
+    x[5, 7] = 40.0  # an outlier sets the scale
+    x[6] *= np.float32(1e-37)  # scale below 2^-120: the division path
+    x[7] *= np.float32(1e-30)  # denormal elements in a row with a normal scale
+    if dtype == torch.bfloat16:
+        x = oq.round_bf16(x)
+    rows = rng.integers(0, T, size=A).astype(np.int64)
+    rows[:6] = [3, 5, 3, 0, 6, 7]
+    q, s = _moe().quantize_rows(_t(x, dev, dtype), _t(rows, dev))
+    q_r, s_r = om.quantize_rows(x[rows])
+    assert np.array_equal(s.cpu().numpy(), s_r)
+    assert np.array_equal(q.cpu().numpy(), q_r)
+    q2, s2 = _moe().quantize_rows(_t(x, dev, dtype))  # no gather: row a is source row a
+    q2_r, s2_r = om.quantize_rows(x)
+    assert np.array_equal(s2.cpu().numpy(), s2_r) and np.array_equal(q2.cpu().numpy(), q2_r)
+
+
 def _layer(rng, E, H, I):
     gu = rng.integers(-127, 128, size=(E, 2 * I, H), dtype=np.int8)
     gus = (rng.uniform(0.5, 1.5, size=(E, 2 * I)) / 127).astype(np.float32)
@@ -136,7 +214,8 @@ def _layer(rng, E, H, I):
 
 
 @pytest.mark.parametrize("swiglu", [False, True])
-@pytest.mark.parametrize("H", [256, 4096, 12288])  # K = H: streamed (256, 4096), K-split (12288)
+# K = H: streamed with 128-byte chunks (256, 4096) or 64-byte chunks (320), K-split (12288)
+@pytest.mark.parametrize("H", [256, 320, 4096, 12288])
 def test_grouped_gemm_matches_oracle(dev, swiglu, H):
     if swiglu and H > 8192:
         pytest.skip("the SwiGLU kernel takes K <= 8192 (its K splits stop at 8 waves)")
