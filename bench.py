@@ -299,11 +299,14 @@ def paged_measurement(torch, dev, pages, x_h, x_i, passes: int = 6) -> dict:
 def paged_moe_measurement(torch, dev, E: int, topk: int, H: int, I: int, layers: int = 2,
                           steps: int = 4) -> dict:
     """Config 4's expert layers served from the packed expert store through the HBM slot
-    cache (``ExpertPageCache``), timed by wall clock with a device sync per step (host
-    bookkeeping and H2D fills are not capturable in a graph).
+    cache (``ExpertPageCache``), timed by wall clock around the whole sequence of layer
+    calls with one device sync at its end (host bookkeeping and H2D fills are not
+    capturable in a graph).  A layer whose pages are not all resident reads its routes
+    on the host (one sync in that call); a fully resident layer binds its slots through
+    the device slot table without one.
 
-    * ``slots_all``: slots for every page of ``layers`` layers; after one warm-up step
-      every acquire is a hit, so the step costs the resident GEMM plus slot lookups.
+    * ``slots_all``: slots for every page of ``layers`` layers, all preloaded: every layer
+      is fully resident, so a call costs the resident kernels plus the slot-table binding.
     * ``slots_one_layer_tier``: slots for one layer only and every page in the pinned host
       tier, so each layer change refills most slots over PCIe (``h2d_GB/s``).
     """
@@ -337,6 +340,8 @@ def paged_moe_measurement(torch, dev, E: int, topk: int, H: int, I: int, layers:
                     routes.append((layer, torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16), idx, w))
             for name, kw in cases:
                 cache = expert_cache.ExpertPageCache(store, device=dev, max_active_pages=E, **kw)
+                if name == "slots_all":
+                    cache.preload()  # every page resident: the device slot-table binding
                 backend = moe.Int8ExpertBackend(page_cache=cache)
                 for r in routes[:layers]:
                     backend.moe(*r)
@@ -355,6 +360,7 @@ def paged_moe_measurement(torch, dev, E: int, topk: int, H: int, I: int, layers:
                     "ms_per_layer": round(dt / n * 1e3, 3), "slots": cache.capacity,
                     "hit_rate": round((s1["page_hits"] - s0["page_hits"]) / max(1, req), 4),
                     "h2d_MB_per_layer": round(h2d / n / 1e6, 1), "h2d_GB/s": round(h2d / dt / 1e9, 1),
+                    "device_table_layers": cache.device_table_stats["device_table_layers"],
                 }
                 cache.close()
                 del backend, cache

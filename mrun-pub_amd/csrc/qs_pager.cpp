@@ -32,9 +32,40 @@ struct qs_pager {
   int slots = 0;
   char* arena = nullptr;  // caller-owned, slot_bytes * slots bytes
   hipStream_t copy = nullptr;
-  std::vector<hipEvent_t> ready, freed;
-  std::vector<int> used;  // a free event has been recorded at least once
+  std::vector<hipEvent_t> ready;
+  std::vector<char> ready_done;  // ready has been seen complete since the last seal
+  // "free" events: one event per release batch, shared by the batch's slots and reference
+  // counted, so a 128-slot release is one hipEventRecord; an event goes back to the pool
+  // once no slot refers to it (it is never re-recorded while a slot still waits on it)
+  std::vector<int> freed;  // slot -> event index, -1: never released or already waited on
+  std::vector<hipEvent_t> events;
+  std::vector<int> refs;
+  std::vector<int> pool;
 };
+
+namespace {
+int take_event(qs_pager* p, int* out) {
+  if (p->pool.empty()) {
+    hipEvent_t e = nullptr;
+    int st = hip_check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+    if (st) return st;
+    p->events.push_back(e);
+    p->refs.push_back(0);
+    *out = (int)p->events.size() - 1;
+  } else {
+    *out = p->pool.back();
+    p->pool.pop_back();
+  }
+  return QS_OK;
+}
+
+void drop_free_ref(qs_pager* p, int slot) {
+  const int e = p->freed[slot];
+  if (e < 0) return;
+  if (--p->refs[e] == 0) p->pool.push_back(e);
+  p->freed[slot] = -1;
+}
+}  // namespace
 
 extern "C" int qs_pager_create(void* device_arena, size_t slot_bytes, int slots,
                                size_t max_transfer, qs_pager** out) {
@@ -49,12 +80,10 @@ extern "C" int qs_pager_create(void* device_arena, size_t slot_bytes, int slots,
   p->arena = static_cast<char*>(device_arena);
   int st = hip_check(hipStreamCreateWithFlags(&p->copy, hipStreamNonBlocking), "hipStreamCreate");
   p->ready.assign(slots, nullptr);
-  p->freed.assign(slots, nullptr);
-  p->used.assign(slots, 0);
-  for (int i = 0; !st && i < slots; ++i) {
+  p->ready_done.assign(slots, 1);  // never sealed: nothing to wait for
+  p->freed.assign(slots, -1);
+  for (int i = 0; !st && i < slots; ++i)
     st = hip_check(hipEventCreateWithFlags(&p->ready[i], hipEventDisableTiming), "hipEventCreate");
-    if (!st) st = hip_check(hipEventCreateWithFlags(&p->freed[i], hipEventDisableTiming), "hipEventCreate");
-  }
   if (st) {
     qs_pager_destroy(p);
     return st;
@@ -68,7 +97,7 @@ extern "C" int qs_pager_destroy(qs_pager* p) {
   if (p->copy) hipStreamSynchronize(p->copy);
   for (auto e : p->ready)
     if (e) hipEventDestroy(e);
-  for (auto e : p->freed)
+  for (auto e : p->events)
     if (e) hipEventDestroy(e);
   if (p->copy) hipStreamDestroy(p->copy);
   delete p;
@@ -85,16 +114,18 @@ extern "C" int qs_pager_submit(qs_pager* p, int slot, const void* host, size_t b
   if (!p || !host || slot < 0 || slot >= p->slots)
     return fail(QS_ERR_INVALID, "pager_submit: bad arguments");
   if (dst_offset + bytes > p->slot_bytes) return fail(QS_ERR_LIMIT, "pager_submit: range exceeds the slot");
-  if (p->used[slot]) {
+  if (p->freed[slot] >= 0) {
     // The slot's last consumer must be done before the copy overwrites it.  The wait is
     // taken on the host (a query, and a block only when the host is a whole ring ahead of
     // the GPU): a copy stream made to wait on a compute-stream event can stall the host
     // inside the following hipMemcpyAsync until that event fires, and the link then
     // idles between blocks.
-    hipError_t q = hipEventQuery(p->freed[slot]);
-    if (q == hipErrorNotReady) q = hipEventSynchronize(p->freed[slot]);
+    hipEvent_t ev = p->events[p->freed[slot]];
+    hipError_t q = hipEventQuery(ev);
+    if (q == hipErrorNotReady) q = hipEventSynchronize(ev);
     int st = hip_check(q, "slot free event");
     if (st) return st;
+    drop_free_ref(p, slot);
   }
   char* dst = p->arena + p->slot_bytes * (size_t)slot + dst_offset;
   const char* src = static_cast<const char*>(host);
@@ -108,34 +139,28 @@ extern "C" int qs_pager_submit(qs_pager* p, int slot, const void* host, size_t b
 
 extern "C" int qs_pager_seal(qs_pager* p, int slot) {
   if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_seal: bad arguments");
+  p->ready_done[slot] = 0;
   return hip_check(hipEventRecord(p->ready[slot], p->copy), "hipEventRecord(ready)");
-}
-
-extern "C" int qs_pager_acquire(qs_pager* p, int slot, void* compute_stream) {
-  if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_acquire: bad arguments");
-  return hip_check(hipStreamWaitEvent(static_cast<hipStream_t>(compute_stream), p->ready[slot], 0),
-                   "hipStreamWaitEvent(ready)");
-}
-
-extern "C" int qs_pager_release(qs_pager* p, int slot, void* compute_stream) {
-  if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_release: bad arguments");
-  p->used[slot] = 1;
-  return hip_check(hipEventRecord(p->freed[slot], static_cast<hipStream_t>(compute_stream)),
-                   "hipEventRecord(free)");
 }
 
 // Batched forms for an expert layer's whole active set (about 128 slots per acquire).
 // A slot whose ready event has already fired needs no stream wait: a wait on a completed
-// event orders nothing, so skipping it keeps the same ordering with one packet fewer.
+// event orders nothing, so skipping it keeps the same ordering with one packet fewer.  A
+// slot seen complete once stays so until its next seal, so it costs no further query.
 extern "C" int qs_pager_acquire_many(qs_pager* p, const int* slots, int n, void* compute_stream) {
   if (!p || n < 0 || (n > 0 && !slots)) return fail(QS_ERR_INVALID, "pager_acquire_many: bad arguments");
   for (int i = 0; i < n; ++i)
     if (slots[i] < 0 || slots[i] >= p->slots) return fail(QS_ERR_INVALID, "pager_acquire_many: slot out of range");
   auto stream = static_cast<hipStream_t>(compute_stream);
   for (int i = 0; i < n; ++i) {
-    hipEvent_t ev = p->ready[slots[i]];
+    const int sl = slots[i];
+    if (p->ready_done[sl]) continue;
+    hipEvent_t ev = p->ready[sl];
     hipError_t q = hipEventQuery(ev);
-    if (q == hipSuccess) continue;
+    if (q == hipSuccess) {
+      p->ready_done[sl] = 1;
+      continue;
+    }
     if (q != hipErrorNotReady) return hip_check(q, "hipEventQuery(ready)");
     int st = hip_check(hipStreamWaitEvent(stream, ev, 0), "hipStreamWaitEvent(ready)");
     if (st) return st;
@@ -143,15 +168,36 @@ extern "C" int qs_pager_acquire_many(qs_pager* p, const int* slots, int n, void*
   return QS_OK;
 }
 
+// One "free" event recorded for the whole batch; each slot drops its previous event.
 extern "C" int qs_pager_release_many(qs_pager* p, const int* slots, int n, void* compute_stream) {
   if (!p || n < 0 || (n > 0 && !slots)) return fail(QS_ERR_INVALID, "pager_release_many: bad arguments");
   for (int i = 0; i < n; ++i)
     if (slots[i] < 0 || slots[i] >= p->slots) return fail(QS_ERR_INVALID, "pager_release_many: slot out of range");
+  if (n == 0) return QS_OK;
+  int e = -1;
+  int st = take_event(p, &e);
+  if (st) return st;
+  st = hip_check(hipEventRecord(p->events[e], static_cast<hipStream_t>(compute_stream)), "hipEventRecord(free)");
+  if (st) {
+    p->pool.push_back(e);
+    return st;
+  }
   for (int i = 0; i < n; ++i) {
-    int st = qs_pager_release(p, slots[i], compute_stream);
-    if (st) return st;
+    drop_free_ref(p, slots[i]);
+    p->freed[slots[i]] = e;
+    ++p->refs[e];
   }
   return QS_OK;
+}
+
+extern "C" int qs_pager_acquire(qs_pager* p, int slot, void* compute_stream) {
+  if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_acquire: bad arguments");
+  return qs_pager_acquire_many(p, &slot, 1, compute_stream);
+}
+
+extern "C" int qs_pager_release(qs_pager* p, int slot, void* compute_stream) {
+  if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_release: bad arguments");
+  return qs_pager_release_many(p, &slot, 1, compute_stream);
 }
 
 extern "C" int qs_pager_sync(qs_pager* p) {

@@ -252,7 +252,7 @@ class SlotPolicy:
     evicted; decode-protected pages lose protection when evicted.
     """
 
-    def __init__(self, capacity: int, layers: int, policy: str, stats: PageCacheStats):
+    def __init__(self, capacity: int, layers: int, policy: str, stats: PageCacheStats, on_change=None):
         if policy not in SUPPORTED_CACHE_POLICIES:
             raise ValueError(f"unsupported expert cache policy {policy!r}; "
                              f"expected one of {sorted(SUPPORTED_CACHE_POLICIES)}")
@@ -265,8 +265,13 @@ class SlotPolicy:
         quota, remainder = divmod(capacity, layers)
         self.layer_quotas = tuple(quota + (1 if layer < remainder else 0) for layer in range(layers))
         self.layer_entry_counts = [0] * layers
+        # on_change(key, slot): key now lives in slot (-1: key left the cache)
+        self.on_change = on_change
 
     def reset(self) -> None:
+        if self.on_change is not None:
+            for key in self.entries:
+                self.on_change(key, -1)
         self.entries.clear()
         self.decode_protected.clear()
         self.free_slots = list(range(self.capacity - 1, -1, -1))
@@ -297,6 +302,8 @@ class SlotPolicy:
                 self.decode_protected.remove(victim)
                 self.stats.decode_protected_demotions += 1
             self.layer_entry_counts[victim[0]] -= 1
+            if self.on_change is not None:
+                self.on_change(victim, -1)
             self.stats.evictions += 1
             if reason == "same-layer":
                 self.stats.same_layer_evictions += 1
@@ -306,6 +313,8 @@ class SlotPolicy:
                 self.stats.fallback_evictions += 1
         self.entries[key] = slot
         self.layer_entry_counts[key[0]] += 1
+        if self.on_change is not None:
+            self.on_change(key, slot)
         return slot
 
 
@@ -348,8 +357,19 @@ class ExpertPageCache:
         requested = int(float(cache_mb) * 1e6) // stride
         self.capacity = min(store.layers * store.experts, max(int(max_active_pages), requested))
         self.max_active_pages = int(max_active_pages)
-        self.stats = PageCacheStats()
-        self.policy = SlotPolicy(self.capacity, store.layers, str(policy).strip().lower(), self.stats)
+        self._stats = PageCacheStats()
+        # device route -> slot table: slot_table[layer, expert] = cache slot or -1, kept equal
+        # to the policy's entries (host mirror updated on every change, dirty rows copied
+        # to the device before a kernel reads them)
+        self._slot_host = np.full((store.layers, store.experts), -1, dtype=np.int32)
+        self.slot_table = torch.full((store.layers, store.experts), -1, dtype=torch.int32, device=self.device)
+        self._dirty_layers: set[int] = set()
+        self._layer_slot_arrays: dict[int, Any] = {}
+        # routes of device-table layers whose bookkeeping has not been applied yet
+        self._deferred: list[tuple[int, torch.Tensor, bool]] = []
+        self.device_table_stats = {"device_table_layers": 0, "deferred_drains": 0}
+        self.policy = SlotPolicy(self.capacity, store.layers, str(policy).strip().lower(), self._stats,
+                                 on_change=self._slot_changed)
         self.cache_policy = self.policy.policy
         self.cache = torch.empty((self.capacity, stride), dtype=torch.uint8, device=self.device)
         # pinned staging for pages the host tier does not hold (read from the store file)
@@ -364,15 +384,23 @@ class ExpertPageCache:
         self._pending_release: list[int] = []
         self._stage_in_flight = False
         self._prev_routes: dict[int, list[int]] = {}
-        self.prefetch_stats = {"prefetched_pages": 0, "prefetch_rounds": 0}
+        self._prefetched: set[tuple[int, int]] = set()  # prefetched pages no acquire has used yet
+        self.prefetch_stats = {"prefetched_pages": 0, "prefetch_rounds": 0, "wasted_prefetches": 0}
 
     # -- reference surface ------------------------------------------------------------------
     @property
+    def stats(self) -> PageCacheStats:
+        self._drain_deferred()
+        return self._stats
+
+    @property
     def entries(self) -> OrderedDict:
+        self._drain_deferred()
         return self.policy.entries
 
     @property
     def decode_protected(self) -> set:
+        self._drain_deferred()
         return self.policy.decode_protected
 
     @property
@@ -382,9 +410,11 @@ class ExpertPageCache:
 
     def reset(self, *, clear_pages: bool) -> None:
         self.synchronize()
-        self.stats.__init__()
-        self.prefetch_stats = {"prefetched_pages": 0, "prefetch_rounds": 0}
+        self._deferred.clear()
+        self._stats.__init__()
+        self.prefetch_stats = {"prefetched_pages": 0, "prefetch_rounds": 0, "wasted_prefetches": 0}
         self._prev_routes.clear()
+        self._prefetched.clear()
         if clear_pages:
             self.policy.reset()
 
@@ -393,6 +423,37 @@ class ExpertPageCache:
         their cache slots directly (the grouped GEMM's ``group_slots``)."""
         selected, slots = self._acquire_resident(layer, top_indices, protect=protect)
         return selected, self.store.view_pages(self.cache), slots
+
+    def acquire_layer_table(self, layer: int, top_indices: torch.Tensor, *, protect: bool = False):
+        """Fast binding for a layer whose every expert page is resident: ``(page views of
+        the whole cache, slot_table[layer])``, a device int32 ``[experts]`` row that the
+        grouped GEMMs index by expert id, or ``None`` when some page of the layer is not
+        in the cache (then use ``acquire_slot_binding``).
+
+        No host synchronisation: the routes are kept on the device and their bookkeeping
+        (LRU touches in admission order, decode protection, hit statistics) is applied, in
+        call order, before the next decision that depends on it -- the next acquire that
+        may evict, or any read of ``stats`` / ``entries`` / ``decode_protected``.  With
+        every page of the layer resident nothing is filled or evicted, so the deferred
+        updates leave the cache in the state the synchronous path would have left it in.
+        Route prefetch reads the routes on the host, so it turns this binding off, and so
+        does the compact-copy binding policy."""
+        if (self.route_prefetch or self.page_binding_policy != SLOT_INDIRECT_PAGE_BINDING_POLICY
+                or self.policy.layer_entry_counts[int(layer)] != self.store.experts):
+            return None
+        layer = int(layer)
+        self.release()
+        self._push_slot_table()
+        arr = self._layer_slot_arrays.get(layer)
+        if arr is None:
+            arr = self._layer_slot_arrays[layer] = (ctypes.c_int * self.store.experts)(*self._slot_host[layer].tolist())
+        nat.call("qs_pager_acquire_many", self._pager, arr, self.store.experts, nat.stream_of(self.device))
+        self._pending_release = arr
+        self._deferred.append((layer, top_indices.detach().reshape(-1).clone(), bool(protect)))
+        self.device_table_stats["device_table_layers"] += 1
+        if len(self._deferred) >= 64:  # bound the device copies held
+            self._drain_deferred()
+        return self.store.view_pages(self.cache), self.slot_table[layer]
 
     def acquire(self, layer: int, top_indices: torch.Tensor, *, protect: bool = False):
         """``(selected_experts, page views of a compact copy)`` (the compact binding)."""
@@ -407,11 +468,39 @@ class ExpertPageCache:
     def release(self) -> None:
         """Mark the pages of the last acquire free once the work queued so far on the current
         stream is done (also done implicitly by the next acquire)."""
-        if self._pending_release:
-            slots = (ctypes.c_int * len(self._pending_release))(*self._pending_release)
-            nat.call("qs_pager_release_many", self._pager, slots, len(self._pending_release),
-                     nat.stream_of(self.device))
+        pend = self._pending_release
+        if len(pend):
+            slots = pend if isinstance(pend, ctypes.Array) else (ctypes.c_int * len(pend))(*pend)
+            nat.call("qs_pager_release_many", self._pager, slots, len(slots), nat.stream_of(self.device))
         self._pending_release = []
+
+    def preload(self, layers=None) -> int:
+        """Fill every page of ``layers`` (default: all) that is not resident, in layer order,
+        as far as the cache holds them without evicting a page of a layer preloaded here.
+        Returns the number of pages filled.  A layer whose pages are then all resident
+        takes the device slot-table binding from its next call on."""
+        self.release()
+        self._drain_deferred()
+        todo = range(self.store.layers) if layers is None else [int(l) for l in layers]
+        guard: set[tuple[int, int]] = set()
+        filled = 0
+        for layer in todo:
+            keys = [(layer, e) for e in range(self.store.experts)]
+            guard.update(keys)
+            missing = [k for k in keys if k not in self.policy.entries]
+            for i in range(0, len(missing), self.max_active_pages):
+                fills = []
+                for key in missing[i:i + self.max_active_pages]:
+                    try:
+                        fills.append((key[1], self.policy.reserve(key, guard)))
+                    except RuntimeError:
+                        break  # full: the rest stays demand-filled
+                if fills:
+                    self._fill(layer, fills)
+                    filled += len(fills)
+                if len(fills) < len(missing[i:i + self.max_active_pages]):
+                    return filled
+        return filled
 
     def synchronize(self) -> None:
         nat.call("qs_pager_sync", self._pager)
@@ -429,6 +518,60 @@ class ExpertPageCache:
             pass
 
     # -- internals ----------------------------------------------------------------------------
+    def _slot_changed(self, key, slot: int) -> None:
+        if slot < 0 and key in self._prefetched:
+            self._prefetched.discard(key)
+            self.prefetch_stats["wasted_prefetches"] += 1  # evicted before any acquire used it
+        layer, expert = key
+        self._slot_host[layer, expert] = slot
+        self._dirty_layers.add(int(layer))
+        self._layer_slot_arrays.pop(int(layer), None)
+
+    def _push_slot_table(self) -> None:
+        """Copy changed rows of the slot table to the device (ordered on the current stream
+        before the kernels that read them; the copy is taken from the host mirror at the
+        call, so later changes of the mirror do not race with it)."""
+        for layer in sorted(self._dirty_layers):
+            self.slot_table[layer].copy_(torch.from_numpy(self._slot_host[layer].copy()))
+        self._dirty_layers.clear()
+
+    def _drain_deferred(self) -> None:
+        """Apply the bookkeeping of device-table layers in call order (one host sync)."""
+        if not self._deferred:
+            return
+        pending, self._deferred = self._deferred, []
+        flat = torch.cat([r for _, r, _ in pending]).cpu().tolist()
+        self.device_table_stats["deferred_drains"] += 1
+        pos = 0
+        for layer, routes, protect in pending:
+            n = int(routes.numel())
+            self._touch(layer, flat[pos:pos + n], protect)
+            pos += n
+
+    def _admission(self, layer: int, routed: list[int]):
+        frequencies = Counter(routed)
+        expert_ids = sorted(frequencies)
+        keys = [(int(layer), e) for e in expert_ids]
+        admission = keys
+        if self.cache_policy == LAYER_FREQUENCY_CACHE_POLICY:
+            admission = sorted(keys, key=lambda k: (frequencies[k[1]], k[1]))
+        return expert_ids, keys, admission
+
+    def _touch(self, layer: int, routed: list[int], protect: bool) -> None:
+        """Bookkeeping of an acquire whose pages were all resident (no fills)."""
+        _, keys, admission = self._admission(layer, [e for e in routed if 0 <= e < self.store.experts])
+        self._prefetched.difference_update(keys)
+        for key in admission:
+            self.policy.entries.move_to_end(key)
+        self._stats.page_requests += len(keys)
+        self._stats.page_hits += len(keys)
+        self._stats.layer_acquires += 1
+        self._stats.active_experts_sum += len(keys)
+        if protect:
+            new = set(keys) - self.policy.decode_protected
+            self.policy.decode_protected.update(keys)
+            self._stats.decode_protected_promotions += len(new)
+
     def _fill(self, layer: int, misses: list[tuple[int, int]]) -> None:
         """One H2D transfer per missing page into its slot (pager copy stream)."""
         stride = self.layout.page_stride
@@ -452,20 +595,17 @@ class ExpertPageCache:
                 nat.call("qs_pager_submit", self._pager, slot, self.stage[i].data_ptr(), stride, 0)
                 nat.call("qs_pager_seal", self._pager, slot)
             self._stage_in_flight = True
-        self.stats.host_to_device_bytes += len(misses) * stride
+        self._stats.host_to_device_bytes += len(misses) * stride
 
     def _acquire_resident(self, layer: int, top_indices: torch.Tensor, *, protect: bool):
         self.release()  # the previous acquire's kernels are queued: its slots may be refilled after them
+        self._drain_deferred()  # earlier device-table layers' LRU touches precede any eviction here
         routed = top_indices.detach().reshape(-1).cpu().tolist()
-        frequencies = Counter(routed)
-        expert_ids = sorted(frequencies)
+        expert_ids, keys, admission = self._admission(layer, routed)
         if len(expert_ids) > self.max_active_pages:
             raise RuntimeError(f"active expert set {len(expert_ids)} exceeds staging limit {self.max_active_pages}")
-        keys = [(int(layer), e) for e in expert_ids]
         protected = set(keys)
-        admission = keys
-        if self.cache_policy == LAYER_FREQUENCY_CACHE_POLICY:
-            admission = sorted(keys, key=lambda k: (frequencies[k[1]], k[1]))
+        self._prefetched.difference_update(keys)
         misses: list[tuple[int, int]] = []
         for key in admission:
             if key in self.policy.entries:
@@ -479,15 +619,15 @@ class ExpertPageCache:
             nat.call("qs_pager_acquire_many", self._pager, (ctypes.c_int * len(slot_list))(*slot_list),
                      len(slot_list), nat.stream_of(self.device))
         self._pending_release = list(slot_list)
-        self.stats.page_requests += len(keys)
-        self.stats.page_misses += len(misses)
-        self.stats.page_hits += len(keys) - len(misses)
-        self.stats.layer_acquires += 1
-        self.stats.active_experts_sum += len(keys)
+        self._stats.page_requests += len(keys)
+        self._stats.page_misses += len(misses)
+        self._stats.page_hits += len(keys) - len(misses)
+        self._stats.layer_acquires += 1
+        self._stats.active_experts_sum += len(keys)
         if protect:
             new = set(keys) - self.policy.decode_protected
             self.policy.decode_protected.update(keys)
-            self.stats.decode_protected_promotions += len(new)
+            self._stats.decode_protected_promotions += len(new)
         if self.route_prefetch:
             self._prefetch_next_layer(int(layer), protected)
             self._prev_routes[int(layer)] = expert_ids
@@ -496,18 +636,27 @@ class ExpertPageCache:
         return selected, slots
 
     def _prefetch_next_layer(self, layer: int, protected: set) -> None:
-        """Stage the previous step's routes for layer + 1 (qwen3_moe_cuda.py:1778-1815)."""
+        """Stage the previous step's routes for layer + 1 (qwen3_moe_cuda.py:1778-1815).
+
+        Unlike the reference, the pages reserved in one round protect each other: the
+        reference's round can evict a page it prefetched a moment earlier (a wasted
+        transfer).  Results never depend on which pages are cached; prefetched pages that
+        are evicted before any acquire uses them are counted as ``wasted_prefetches``."""
         nxt = layer + 1
         predicted = self._prev_routes.get(nxt)
         if not predicted:
             return
         wanted = [e for e in predicted if (nxt, e) not in self.policy.entries][: self.max_active_pages]
         fills: list[tuple[int, int]] = []
+        guard = set(protected)
         for expert in wanted:
+            key = (nxt, expert)
             try:
-                fills.append((expert, self.policy.reserve((nxt, expert), protected)))
+                fills.append((expert, self.policy.reserve(key, guard)))
             except RuntimeError:
                 break  # the cache is saturated by the active set
+            guard.add(key)
+            self._prefetched.add(key)
         if not fills:
             return
         self._fill(nxt, fills)

@@ -423,11 +423,20 @@ class Int8ExpertBackend:
         expert (a compact group id) to its cache slot, and the grouped GEMMs read the pages
         in place through ``group_slots``."""
         cache = self.page_cache
-        selected, page, slots = cache.acquire_slot_binding(layer, top_indices, protect=not prefill)
-        compact = torch.searchsorted(selected, top_indices)
-        token_ids, coef, starts, counts, inverse, _ = _route_impl(
-            compact, top_weights, int(selected.numel()), True, coef_f32=True
-        )
+        table = cache.acquire_layer_table(layer, top_indices, protect=not prefill)
+        if table is not None:
+            # every page of the layer is resident: groups are the expert ids themselves and
+            # the device slot table binds them, with no host synchronisation
+            page, slots = table
+            E = int(slots.numel())
+            selected = self._expert_ids(source.device, E)
+            token_ids, coef, starts, counts, inverse, _ = _route_impl(top_indices, top_weights, E, True, coef_f32=True)
+        else:
+            selected, page, slots = cache.acquire_slot_binding(layer, top_indices, protect=not prefill)
+            compact = torch.searchsorted(selected, top_indices)
+            token_ids, coef, starts, counts, inverse, _ = _route_impl(
+                compact, top_weights, int(selected.numel()), True, coef_f32=True
+            )
         rows_q, rows_s = quantize_rows(source, token_ids)
         activated, _ = grouped_int8_mm(
             rows_q, rows_s, page.gate_up, page.gate_up_scales, starts, counts, group_slots=slots, swiglu=True

@@ -96,3 +96,61 @@ def test_cache_holds_everything_after_one_pass(dev, tmp_path):
     assert cache.stats.page_misses == 16 and cache.stats.evictions == 0
     assert cache.stats.host_to_device_bytes == 16 * store.layout.page_stride
     cache.close()
+
+
+def _state(cache):
+    st = cache.stats.as_dict()
+    return list(cache.entries.items()), sorted(cache.decode_protected), st
+
+
+@pytest.mark.parametrize("slots", [48, 40])  # every page resident / some layers paged
+@pytest.mark.parametrize("policy", ["global-lru-v1", "layer-frequency-lru-v1"])
+def test_device_slot_table_matches_host_binding(dev, tmp_path, slots, policy):
+    """Layers whose pages are all resident bind their slots through the device table with
+    no host sync; outputs and the cache's LRU order, protection set and statistics equal
+    those of the host-side binding on the same sequence."""
+    ec, moe = _mods()
+    store, resident = _setup(tmp_path, dev)
+    runs = []
+    for use_table in (True, False):
+        cache = ec.ExpertPageCache(store, device=dev, cache_mb=slots * store.layout.page_stride / 1e6,
+                                   max_active_pages=16, cache_policy=policy)
+        if not use_table:
+            cache.acquire_layer_table = lambda *a, **k: None
+        paged = moe.Int8ExpertBackend(page_cache=cache)
+        outs = []
+        steps = _steps(dev, 3, 16, T=24, k=4, steps=4)
+        for i, (layer, x, idx, w) in enumerate(steps):
+            outs.append(paged.moe(layer, x, idx, w, prefill=(i % 5 == 0)))
+        torch.cuda.synchronize()
+        runs.append((outs, _state(cache), dict(cache.device_table_stats)))
+        cache.close()
+    (o1, s1, d1), (o2, s2, d2) = runs
+    assert all(torch.equal(a, b) for a, b in zip(o1, o2))
+    assert s1 == s2
+    if slots == 48:
+        assert d1["device_table_layers"] > 0  # the fast binding was taken
+    ref = [resident.moe(layer, x, idx, w) for layer, x, idx, w in _steps(dev, 3, 16, T=24, k=4, steps=4)]
+    assert all(torch.equal(a, b) for a, b in zip(o1, ref))
+
+
+def test_preload_makes_layers_use_the_device_table(dev, tmp_path):
+    ec, moe = _mods()
+    store, resident = _setup(tmp_path, dev, L=2, E=8)
+    cache = ec.ExpertPageCache(store, device=dev, cache_mb=1e4, max_active_pages=4)
+    assert cache.preload() == 16
+    assert cache.stats.host_to_device_bytes == 16 * store.layout.page_stride
+    paged = moe.Int8ExpertBackend(page_cache=cache)
+    steps = _steps(dev, 2, 8, k=2, steps=2)
+    for layer, x, idx, w in steps:
+        assert torch.equal(paged.moe(layer, x, idx, w), resident.moe(layer, x, idx, w))
+    assert cache.device_table_stats["device_table_layers"] == len(steps)
+    assert cache.stats.page_misses == 0 and cache.stats.page_hits == cache.stats.page_requests > 0
+    cache.close()
+    # a cache smaller than the model preloads what fits and demand-fills the rest
+    small = ec.ExpertPageCache(store, device=dev, cache_mb=10 * store.layout.page_stride / 1e6, max_active_pages=8)
+    assert small.preload() == 10
+    paged = moe.Int8ExpertBackend(page_cache=small)
+    for layer, x, idx, w in steps:
+        assert torch.equal(paged.moe(layer, x, idx, w), resident.moe(layer, x, idx, w))
+    small.close()
