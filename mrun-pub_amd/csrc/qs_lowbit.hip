@@ -16,7 +16,9 @@
 // and y += scale * (R - (OFF + z) * S0).  fp32 activations are split exactly into three
 // bf16 terms (x = h + m + l) that run as three activation rows and are summed at the end.
 //   k_lowbit_valu  decode (M <= 2 bf16 rows): one wave per weight row, v_dot2_f32_bf16
-//   k_lowbit_slot  M <= 16 rows: v_mfma_f32_16x16x32_bf16, one whole group per lane
+//   k_lowbit_gk    3..16 bf16 rows, one launch: v_mfma_f32_16x16x32_bf16 per group, a
+//                  quarter group per lane, K split over the waves of a workgroup
+//   k_lowbit_slot  M <= 16 fp32 rows (split into bf16 terms): one whole group per lane
 //   k_lowbit_mfma  any aligned-to-4 layout (fallback), four lanes per group
 #include "qs_common.h"
 
@@ -54,32 +56,40 @@ inline void pair_consts(LowbitParams& p, int bits) {
 
 // Lane code extraction: the lane's G/4 codes (BITS*G/4 bits, at a 2- or 4-byte aligned
 // offset) are returned as a 64/96-bit little-endian field.
-template <int BITS, int G>
+// Weight-stream load: nontemporal (the M <= 2 decode kernels, measured faster so) or plain
+// (the multi-row kernels, measured faster so).
+template <bool NT, typename T>
+__device__ __forceinline__ T ldw(const T* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
+template <int BITS, int G, bool NT = true>
 __device__ __forceinline__ void load_codes(const uint8_t* p, uint32_t (&f)[3]) {
   constexpr int NB = BITS * G / 4;  // bits per lane: 48, 96, 32, 64
   if constexpr (NB == 96) {
     const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    f[0] = __builtin_nontemporal_load(q);
-    f[1] = __builtin_nontemporal_load(q + 1);
-    f[2] = __builtin_nontemporal_load(q + 2);
+    f[0] = ldw<NT>(q);
+    f[1] = ldw<NT>(q + 1);
+    f[2] = ldw<NT>(q + 2);
   } else if constexpr (NB == 64) {
     const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    f[0] = __builtin_nontemporal_load(q);
-    f[1] = __builtin_nontemporal_load(q + 1);
+    f[0] = ldw<NT>(q);
+    f[1] = ldw<NT>(q + 1);
     f[2] = 0;
   } else if constexpr (NB == 32) {
-    f[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+    f[0] = ldw<NT>(reinterpret_cast<const uint32_t*>(p));
     f[1] = f[2] = 0;
   } else {  // 48 bits at a 2-byte aligned offset; never reads outside [p, p + 6)
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
     if (a & 2) {
-      const uint16_t h0 = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
-      const uint32_t d1 = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p + 2));
+      const uint16_t h0 = ldw<NT>(reinterpret_cast<const uint16_t*>(p));
+      const uint32_t d1 = ldw<NT>(reinterpret_cast<const uint32_t*>(p + 2));
       f[0] = (uint32_t)h0 | (d1 << 16);
       f[1] = d1 >> 16;
     } else {
-      f[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
-      f[1] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p + 4));
+      f[0] = ldw<NT>(reinterpret_cast<const uint32_t*>(p));
+      f[1] = ldw<NT>(reinterpret_cast<const uint16_t*>(p + 4));
     }
     f[2] = 0;
   }
@@ -207,13 +217,13 @@ struct SlotCfg {
 // 1 = fp16 zero points, 2 = fp32.  Compile-time so that every load in the main loop is
 // unconditional (addresses clamped into range, invalid data zeroed by selects) and the
 // compiler can keep whole batches in flight.
-template <int SM, int ZM>
+template <int SM, int ZM, bool NT = true>
 __device__ __forceinline__ void load_sz(const LowbitParams& p, int64_t i, float& sc, float& z) {
-  if constexpr (SM == 1) sc = f16_bits_to_f32(__builtin_nontemporal_load(static_cast<const uint16_t*>(p.scales) + i));
-  else sc = __builtin_nontemporal_load(static_cast<const float*>(p.scales) + i);
+  if constexpr (SM == 1) sc = f16_bits_to_f32(ldw<NT>(static_cast<const uint16_t*>(p.scales) + i));
+  else sc = ldw<NT>(static_cast<const float*>(p.scales) + i);
   if constexpr (ZM == 0) z = p.offset;
-  else if constexpr (ZM == 1) z = f16_bits_to_f32(__builtin_nontemporal_load(static_cast<const uint16_t*>(p.zeros) + i));
-  else z = __builtin_nontemporal_load(static_cast<const float*>(p.zeros) + i);
+  else if constexpr (ZM == 1) z = f16_bits_to_f32(ldw<NT>(static_cast<const uint16_t*>(p.zeros) + i));
+  else z = ldw<NT>(static_cast<const float*>(p.zeros) + i);
 }
 
 template <int BITS, int G, int MP, int SM, int ZM>
@@ -374,6 +384,227 @@ __global__ __launch_bounds__(256) void k_lowbit_slot(LowbitParams p, int gps, fl
     else
       p.y[(int64_t)m * p.ldy + nrow] = v;
   }
+}
+
+// ----------------------------------------------------------------------------------
+// GEMM for 3..16 bf16 activation rows in one launch (k_lowbit_gk): one workgroup per
+// RT x 16 weight rows; its W waves split the groups (NGR consecutive groups each) and
+// their partial results meet in a fixed-order LDS reduction.
+//  * Codes, scales and zero points of the wave's groups for the workgroup's rows are read
+//    as contiguous row ranges (16-byte code pieces and 4-byte scale words, 64 lanes per
+//    load) and staged in the wave's LDS area.  The activations of the wave's k range go
+//    to VGPRs (PF groups in flight) and serve all RT row tiles.
+//  * Per group and row tile, lane l takes quarter q = l >> 4 (G/4 codes) of weight row
+//    n = l & 15 and the same k range of activation row m = l & 15:
+//    v_mfma_f32_16x16x32_bf16 with A = x and B = (OFF + code) pairs, G/32 MFMAs from zero,
+//    so D[m][n] = R = sum_k x (OFF + c), and
+//      y[m][n] += scale * (R - (OFF + zero) * S0[m, g]),
+//    S0 the group's activation sum: a second MFMA of the same A with an all-ones B, which
+//    lands in the D layout (m = 4 (l >> 4) + r) and serves every row tile.
+// Rows m >= M read as 0 and issue no activation loads.
+// ----------------------------------------------------------------------------------
+constexpr int kGkMaxWaves = 16;
+template <int G>
+constexpr int kGkGroupsShort = G == 64 ? 8 : 4;  // two row tiles, every activation in VGPRs
+template <int G>
+constexpr int kGkGroupsLong = G == 64 ? 12 : 6;  // one row tile, activations streamed
+template <int G, int NGR>
+constexpr int kGkPrefetch = NGR == kGkGroupsShort<G> ? NGR : (G == 64 ? 8 : 4);
+
+template <int BITS, int G, int SM, int ZM, int NGR, int RT>
+struct GkLds {
+  static constexpr int CB = BITS * G / 8;
+  static constexpr int RB = NGR * CB;         // code bytes per row in a wave's range
+  static constexpr int RBP = RB + 16;         // 16-byte rows for ds_write_b128, 4 banks apart
+  static constexpr int ES = SM == 1 ? 2 : 4;  // bytes per scale
+  static constexpr int EZ = ZM == 0 ? 0 : (ZM == 1 ? 2 : 4);
+  static constexpr int SWR = NGR * ES / 4;    // scale words per row (NGR even)
+  static constexpr int ZWR = NGR * EZ / 4;
+  static constexpr int CODE = RT * 16 * RBP;
+  static constexpr int WORDS = RT * 16 * (SWR + ZWR);
+  static constexpr int WAVE = CODE + 4 * WORDS;       // bytes of LDS per wave
+  static_assert(WAVE >= 64 * 16 * RT, "the partials reuse the staging area");
+};
+
+template <int BITS, int G, int SM, int ZM, int NGR, int RT>
+__global__ __launch_bounds__(kGkMaxWaves * 64) void k_lowbit_gk(LowbitParams p) {
+  using L = GkLds<BITS, G, SM, ZM, NGR, RT>;
+  constexpr float OFF = BITS == 3 ? 8.f : 4.f;
+  constexpr int CB = L::CB;
+  constexpr int QB = CB / 4;        // code bytes of a lane quarter
+  constexpr int QC = G / 4;         // codes of a lane quarter
+  constexpr int NJ = G / 32;        // MFMAs per group
+  constexpr int PF = kGkPrefetch<G, NGR>;
+  static_assert(RT == 1 || PF == NGR, "row tiles share the wave's activations");
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int W = blockDim.x >> 6;
+  const int col = lane & 15, q = lane >> 4;
+  const int n0 = blockIdx.x * 16 * RT;
+  const int gb = wave * NGR;
+  const int M = p.M;
+  const bool mval = col < M;
+  const uint16_t* xr = p.x + (int64_t)min(col, M - 1) * p.ldx + q * QC;
+  uint8_t* area = lds + (size_t)wave * L::WAVE;
+  uint32_t* lc = reinterpret_cast<uint32_t*>(area);                     // codes [RT*16][RBP]
+  uint32_t* lw = reinterpret_cast<uint32_t*>(area + L::CODE);           // scales, then zeros
+
+  // codes: 16-byte pieces of each row's range (pieces past the row's last group read its
+  // last 16 bytes again; pieces past the range are loaded but not stored)
+  constexpr int PPR = L::RB / 16;
+  constexpr int TOT = RT * 16 * PPR;
+  constexpr int NPL = (TOT + 63) / 64;
+  const int vb = p.ng * CB;
+  i32x4 cp[NPL];
+#pragma unroll
+  for (int u = 0; u < NPL; ++u) {
+    const int t = min(lane + 64 * u, TOT - 1), r = t / PPR;
+    const int o = min(gb * CB + (t - r * PPR) * 16, vb - 16);
+    cp[u] = *reinterpret_cast<const i32x4*>(p.packed + (int64_t)min(n0 + r, p.N - 1) * p.row_bytes + o);
+  }
+  // scale / zero words of each row's range (words past the row's last group repeat its
+  // last word: those groups get scale 0 below)
+  constexpr int SWT = RT * 16 * L::SWR, TWT = L::WORDS;
+  constexpr int NWL = (TWT + 63) / 64;
+  uint32_t sw[NWL];
+#pragma unroll
+  for (int u = 0; u < NWL; ++u) {
+    const int t = min(lane + 64 * u, TWT - 1);
+    const bool isz = t >= SWT;
+    const int tt = isz ? t - SWT : t;
+    const int wr = isz ? L::ZWR : L::SWR, eb = isz ? L::EZ : L::ES;
+    const int r = tt / wr, wi = tt - r * wr;
+    const int64_t row = min(n0 + r, p.N - 1);
+    const int64_t rw = (int64_t)p.ng * eb / 4;  // words per row of the array
+    const int64_t w = min((int64_t)gb * eb / 4 + wi, rw - 1);
+    const uint32_t* src = static_cast<const uint32_t*>(isz ? p.zeros : p.scales);
+    sw[u] = src[row * rw + w];
+  }
+  i32x4 xv[PF][NJ];
+  auto xload = [&](int b, int i) {
+    const int g = min(gb + i, p.ng - 1);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      i32x4 v = {0, 0, 0, 0};
+      if (mval) v = *reinterpret_cast<const i32x4*>(xr + (int64_t)g * G + 8 * j);
+      xv[b][j] = v;
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < PF; ++i) xload(i, i);
+#pragma unroll
+  for (int u = 0; u < NPL; ++u) {
+    const int t = lane + 64 * u, r = t / PPR;
+    if (t < TOT) *reinterpret_cast<i32x4*>(lc + (r * L::RBP + (t - r * PPR) * 16) / 4) = cp[u];
+  }
+#pragma unroll
+  for (int u = 0; u < NWL; ++u) {
+    const int t = lane + 64 * u;
+    if (t < TWT) lw[t] = sw[u];
+  }
+  __syncthreads();
+
+  // the lane's quarter field of group i in row tile rt: QB bytes at i * CB + q * QB of its
+  // row (2- or 4-byte aligned), as a little-endian bit field
+  auto field = [&](int rt, int i, uint32_t (&f)[3]) {
+    const int o = (rt * 16 + col) * L::RBP + i * CB + q * QB;
+    const uint32_t* w = lc + (o >> 2);
+    if constexpr (QB == 6) {
+      const uint32_t d0 = w[0], d1 = w[1];
+      const int sh = (o & 3) * 8;
+      f[0] = __builtin_amdgcn_alignbit(d1, d0, sh);
+      f[1] = d1 >> sh;
+      f[2] = 0;
+    } else {
+      f[0] = w[0];
+      f[1] = QB >= 8 ? w[1] : 0u;
+      f[2] = QB >= 12 ? w[2] : 0u;
+    }
+  };
+  auto scale_zero = [&](int rt, int i, float& sc, float& cz) {
+    const int e = (rt * 16 + col) * NGR + i;
+    if constexpr (SM == 1) sc = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(lw)[e]);
+    else sc = __uint_as_float(lw[e]);
+    float z;
+    if constexpr (ZM == 0) z = p.offset;
+    else if constexpr (ZM == 1) z = f16_bits_to_f32(reinterpret_cast<const uint16_t*>(lw + SWT)[e]);
+    else z = __uint_as_float(lw[SWT + e]);
+    sc = gb + i < p.ng ? sc : 0.f;
+    cz = OFF + z;
+  };
+
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+  f32x4 y[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) y[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NGR; ++i) {
+    const int b = i % PF;
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[b][j]), ones, s0, 0, 0, 0);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      uint32_t cf[3];
+      field(rt, i, cf);
+      f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        u32x4 bw;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bw[e] = code_pair<BITS>(cf, BITS * (8 * j + 2 * e), p.pair_mask, p.pair_base);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[b][j]),
+                                                    __builtin_bit_cast(bf16x8, bw), d, 0, 0, 0);
+      }
+      float sc, cz;
+      scale_zero(rt, i, sc, cz);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) y[rt][r] = fmaf(sc, fmaf(-cz, s0[r], d[r]), y[rt][r]);
+    }
+    if (i + PF < NGR) xload(b, i + PF);
+  }
+
+  __syncthreads();  // every wave is done with its staging area: it now holds the partials
+  f32x4* red = reinterpret_cast<f32x4*>(lds);  // [W][RT][64]
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) red[(wave * RT + rt) * 64 + lane] = y[rt];
+  __syncthreads();
+  // row tile rt is summed over the waves in order by wave rt % W
+  for (int rt = wave; rt < RT; rt += W) {
+    const int nn = n0 + rt * 16 + col;
+    f32x4 t = red[rt * 64 + lane];
+    for (int w = 1; w < W; ++w) t += red[(w * RT + rt) * 64 + lane];
+    if (nn < p.N) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * q + r;
+        if (m < M) p.y[(int64_t)m * p.ldy + nn] = t[r];
+      }
+    }
+  }
+}
+
+template <int BITS, int G, int NGR, int RT>
+void launch_gk_n(const LowbitParams& p, hipStream_t s) {
+  const int waves = (int)cdiv(p.ng, NGR);
+  const dim3 grid((unsigned)cdiv(p.N, 16 * RT)), block(waves * 64);
+  if (p.scale_f16) {
+    const size_t lds = (size_t)waves * GkLds<BITS, G, 1, 1, NGR, RT>::WAVE;
+    hipLaunchKernelGGL((k_lowbit_gk<BITS, G, 1, 1, NGR, RT>), grid, block, lds, s, p);
+  } else {
+    const size_t lds = (size_t)waves * GkLds<BITS, G, 0, 0, NGR, RT>::WAVE;
+    hipLaunchKernelGGL((k_lowbit_gk<BITS, G, 0, 0, NGR, RT>), grid, block, lds, s, p);
+  }
+}
+
+// the short form (two row tiles) while its waves fit a workgroup
+template <int BITS, int G>
+void launch_gk(const LowbitParams& p, hipStream_t s) {
+  if (p.ng <= kGkMaxWaves * kGkGroupsShort<G>) launch_gk_n<BITS, G, kGkGroupsShort<G>, 2>(p, s);
+  else launch_gk_n<BITS, G, kGkGroupsLong<G>, 1>(p, s);
 }
 
 // ----------------------------------------------------------------------------------
@@ -865,6 +1096,42 @@ extern "C" int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uin
         else launch_valu<2>(J, mbv, group_size, grid, lds, s, q);
       }
       return hip_check(hipGetLastError(), "k_lowbit_valu launch");
+    }
+  }
+  {
+    // 3..16 bf16 rows (and any bf16 M in chunks of 16): the single-launch group-MFMA kernel
+    const bool layout = (scale_dtype == QS_F16 && zeros && zero_dtype == QS_F16) || (scale_dtype == QS_F32 && !zeros);
+    const int ngr = group_size == 64 ? kGkGroupsLong<64> : kGkGroupsLong<128>;
+    const int waves = (int)cdiv(ng, ngr);  // the long form's count bounds both
+    const int64_t vb = K * bits / 8;  // code bytes of a row (the kernel reads 16-byte pieces)
+    // scale / zero rows are read as 4-byte words: fp16 arrays need an even group count
+    const bool words = aligned(scales, 4) && (!zeros || aligned(zeros, 4)) && (scale_dtype == QS_F32 || ng % 2 == 0);
+    if (x_dtype == QS_BF16 && layout && words && waves <= kGkMaxWaves && aligned(x, 16) && ldx % 8 == 0 &&
+        vb % 16 == 0 && row_bytes % 16 == 0 && aligned(packed, 16)) {
+      LowbitParams p{};
+      p.ldx = ldx;
+      p.packed = packed;
+      p.row_bytes = row_bytes;
+      p.scales = scales;
+      p.zeros = zeros;
+      p.scale_f16 = scale_dtype == QS_F16;
+      p.zero_f16 = zero_dtype == QS_F16;
+      p.offset = offset;
+      p.ldy = ldy;
+      p.N = (int)N;
+      p.K = (int)K;
+      p.ng = ng;
+      pair_consts(p, bits);
+      for (int64_t m0 = 0; m0 < M; m0 += 16) {
+        p.x = static_cast<const uint16_t*>(x) + m0 * ldx;
+        p.y = y + m0 * ldy;
+        p.M = (int)(M - m0 < 16 ? M - m0 : 16);
+        if (bits == 3 && group_size == 64) launch_gk<3, 64>(p, s);
+        else if (bits == 3) launch_gk<3, 128>(p, s);
+        else if (group_size == 64) launch_gk<2, 64>(p, s);
+        else launch_gk<2, 128>(p, s);
+      }
+      return hip_check(hipGetLastError(), "k_lowbit_gk launch");
     }
   }
   for (int64_t m0 = 0; m0 < M; m0 += mb) {

@@ -145,3 +145,31 @@ def test_reference_store_reader(dev, tmp_path):
     assert np.array_equal(e.cpu().numpy(), full[ids])
     with pytest.raises(IndexError):
         store.embed_rows("W", np.array([70]))
+
+
+# the single-launch multi-row kernel: one wave per workgroup (K = 256), both group-count
+# forms (K = 4096 / 11008), M from 3 to 16 and M > 16 (chunks of 16 rows), N not a
+# multiple of the 32-row tile; K = 320 (odd group count) takes the other kernels
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("N,K", [(80, 256), (100, 4096), (72, 11008), (40, 320)])
+@pytest.mark.parametrize("m", [3, 16, 21])
+def test_gemv_multirow_bf16(dev, bits, N, K, m):
+    rng = np.random.default_rng(bits * 7 + N + m)
+    packed, s, z = _asym(rng, N, K, bits)
+    x = oq.round_bf16(rng.standard_normal((m, K)).astype(np.float32))
+    y = _lb().lowbit_matmul(_page(dev, packed, s, K, bits, 64, z), torch.from_numpy(x).to(dev).to(torch.bfloat16))
+    ref = ol.lowbit_matmul(packed, s, x, K, bits, 64, zeros=z)
+    assert oq.rel_l2(y.cpu().numpy(), ref) <= F32_TOL
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("m", [4, 9])
+def test_gemv_multirow_reference_layout_g128(dev, bits, m):
+    """fp32 scales with the fixed offset, G = 128 (both row-tile forms: K = 1024 / 16384)."""
+    for K in (1024, 16384):
+        rng = np.random.default_rng(bits * 11 + m + K)
+        packed, scales = _sym(rng, 96, K, bits)
+        x = oq.round_bf16(rng.standard_normal((m, K)).astype(np.float32))
+        y = _lb().lowbit_matmul(_page(dev, packed, scales, K, bits, 128), torch.from_numpy(x).to(dev).to(torch.bfloat16))
+        ref = ol.lowbit_matmul(packed, scales, x, K, bits, 128)
+        assert oq.rel_l2(y.cpu().numpy(), ref) <= F32_TOL
