@@ -277,44 +277,61 @@ class SlotPolicy:
         self.free_slots = list(range(self.capacity - 1, -1, -1))
         self.layer_entry_counts = [0] * len(self.layer_entry_counts)
 
-    def eviction_candidate(self, key, protected) -> tuple[tuple[int, int] | None, str]:
-        if self.policy == GLOBAL_LRU_CACHE_POLICY:
-            return next((c for c in self.entries if c not in protected), None), "fallback"
-        layer = key[0]
-        same_layer = next((c for c in self.entries if c[0] == layer and c not in protected), None)
-        if same_layer is not None and self.layer_entry_counts[layer] >= self.layer_quotas[layer]:
-            return same_layer, "same-layer"
-        over = next((c for c in self.entries if c not in protected
-                     and self.layer_entry_counts[c[0]] > self.layer_quotas[c[0]]), None)
+    def victim(self, incoming_layer: int, protected) -> tuple[tuple[int, int] | None, str]:
+        """The page to evict for a page of ``incoming_layer`` and the statistics counter it
+        counts under, from one scan of the pages in LRU order (oldest first), skipping
+        ``protected`` (the current acquire's pages):
+
+        * global LRU: the oldest page (``fallback_evictions``);
+        * layer-frequency LRU: the oldest page of the incoming layer when that layer holds
+          at least its quota (``same_layer_evictions``), else the oldest page of any layer
+          above its quota (``over_quota_evictions``), else the oldest page
+          (``fallback_evictions``).
+
+        ``None`` when every cached page is protected."""
+        counts, quotas = self.layer_entry_counts, self.layer_quotas
+        layer_full = counts[incoming_layer] >= quotas[incoming_layer]
+        oldest = over = None
+        for key in self.entries:
+            if key in protected:
+                continue
+            if self.policy == GLOBAL_LRU_CACHE_POLICY:
+                return key, "fallback_evictions"
+            if layer_full and key[0] == incoming_layer:
+                return key, "same_layer_evictions"  # the rule that ranks first decides at once
+            if oldest is None:
+                oldest = key
+            if over is None and counts[key[0]] > quotas[key[0]]:
+                over = key
         if over is not None:
-            return over, "over-quota"
-        return next((c for c in self.entries if c not in protected), None), "fallback"
+            return over, "over_quota_evictions"
+        return oldest, "fallback_evictions"
 
     def reserve(self, key, protected) -> int:
+        """A slot for ``key`` (a free one, else the victim's), recorded as most recently used."""
         if self.free_slots:
             slot = self.free_slots.pop()
         else:
-            victim, reason = self.eviction_candidate(key, protected)
+            victim, counter = self.victim(key[0], protected)
             if victim is None:
-                raise RuntimeError("expert cache cannot evict a page from the active set")
-            slot = self.entries.pop(victim)
-            if victim in self.decode_protected:
-                self.decode_protected.remove(victim)
-                self.stats.decode_protected_demotions += 1
-            self.layer_entry_counts[victim[0]] -= 1
-            if self.on_change is not None:
-                self.on_change(victim, -1)
-            self.stats.evictions += 1
-            if reason == "same-layer":
-                self.stats.same_layer_evictions += 1
-            elif reason == "over-quota":
-                self.stats.over_quota_evictions += 1
-            else:
-                self.stats.fallback_evictions += 1
+                raise RuntimeError("no expert page can be evicted: every cached page belongs to the active set")
+            slot = self._evict(victim, counter)
         self.entries[key] = slot
         self.layer_entry_counts[key[0]] += 1
         if self.on_change is not None:
             self.on_change(key, slot)
+        return slot
+
+    def _evict(self, victim, counter: str) -> int:
+        slot = self.entries.pop(victim)
+        self.layer_entry_counts[victim[0]] -= 1
+        if victim in self.decode_protected:  # a protected page loses protection with its slot
+            self.decode_protected.discard(victim)
+            self.stats.decode_protected_demotions += 1
+        self.stats.evictions += 1
+        setattr(self.stats, counter, getattr(self.stats, counter) + 1)
+        if self.on_change is not None:
+            self.on_change(victim, -1)
         return slot
 
 

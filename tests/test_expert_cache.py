@@ -106,3 +106,41 @@ def test_protected_pages_lose_protection_when_evicted():
     assert stats.decode_protected_demotions == 1 and not pol.decode_protected
     with pytest.raises(ValueError, match="cache policy"):
         ec.SlotPolicy(1, 1, "mru", stats)
+
+
+def test_victim_follows_the_rules_on_random_states():
+    """The one-scan victim choice against the rules written as three filters (oldest
+    first): same layer when the incoming layer is at its quota, then any layer above its
+    quota, then the oldest unprotected page; global LRU takes the oldest."""
+    import random
+
+    ec = _ec()
+    rng = random.Random(5)
+    for trial in range(400):
+        layers, cap = rng.randint(1, 4), rng.randint(2, 12)
+        policy = rng.choice(["global-lru-v1", "layer-frequency-lru-v1"])
+        pol = ec.SlotPolicy(cap, layers, policy, ec.PageCacheStats())
+        keys = [(l, e) for l in range(layers) for e in range(6)]
+        rng.shuffle(keys)
+        for i, k in enumerate(keys[:cap]):
+            pol.entries[k] = i
+            pol.layer_entry_counts[k[0]] += 1
+        order = list(pol.entries)
+        protected = set(rng.sample(order, rng.randint(0, len(order))))
+        incoming = rng.randrange(layers)
+        free = [k for k in order if k not in protected]
+        counts, quotas = pol.layer_entry_counts, pol.layer_quotas
+        if not free:
+            want = (None, "fallback_evictions")
+        elif policy == "global-lru-v1":
+            want = (free[0], "fallback_evictions")
+        else:
+            same = [k for k in free if k[0] == incoming]
+            over = [k for k in free if counts[k[0]] > quotas[k[0]]]
+            if same and counts[incoming] >= quotas[incoming]:
+                want = (same[0], "same_layer_evictions")
+            elif over:
+                want = (over[0], "over_quota_evictions")
+            else:
+                want = (free[0], "fallback_evictions")
+        assert pol.victim(incoming, protected) == want, (trial, policy, order, protected, incoming)
