@@ -653,20 +653,31 @@ enum { EPI_I32 = 0, EPI_F32 = 1, EPI_BF16 = 2 };
 
 constexpr int kBK = 64;        // default k bytes per step; LDS rows padded by 16 bytes
 constexpr int kSideLds = 16;   // side-path columns per LDS staging in the epilogue
+// Epilogue operands fetched by the DMA GEMM ahead of its epilogue ("tail", floats):
+// act scales [256], weight scales [256], side activations [BM][P] and weights [BN][P]
+// for P <= kTailSide.
+constexpr int kTailSide = 8;
+constexpr int kTailAs = 0, kTailBs = 256, kTailXp = 512;
+template <int BM, int BN>
+constexpr int tail_floats() { return kTailXp + (BM + BN) * kTailSide; }
 
 // Epilogue shared by the GEMM kernels: scales, the optional fp32 side path and the store.
 // `ws0` is the workgroup's LDS (at least (BM + BN) * (kSideLds + 1) floats), free once the
-// main loop's last barrier has passed.
-template <int BM, int BN, int WM, int WN, int EPI, int NT>
+// main loop's last barrier has passed.  PRE: the scales, and the side operands when
+// P <= kTailSide, already sit in LDS at `tail` (layout above), visible to every wave.
+template <int BM, int BN, int WM, int WN, int EPI, int NT, int PRE = 0>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, i32x16 (&acc)[WM / 32][WN / 32], float* ws0,
-                                              int bm, int bn, int wm, int wn, int tid, int lane) {
+                                              int bm, int bn, int wm, int wn, int tid, int lane,
+                                              const float* tail = nullptr) {
   constexpr int FM = WM / 32, FN = WN / 32;
+  static_assert(!PRE || (EPI != EPI_I32 && BM <= 256 && BN <= 256), "tail layout");
+  const bool tside = PRE && p.P > 0 && p.P <= kTailSide;
   // Epilogue.  The side path (P protected columns, fp32) runs on the matrix cores:
   // side[32x32 tile] = xs[rows][P] . ws[P][cols] with v_mfma_f32_32x32x2_f32, whose
   // accumulator layout is the int32 one, so each lane adds side[r] to its own outputs.
   // Operands go through LDS in chunks of kSideLds columns (zero padded); with
   // P <= kSideLds one staging serves every tile.
-  const int nsc = (EPI != EPI_I32 && p.P > 0) ? (p.P + kSideLds - 1) / kSideLds : 0;
+  const int nsc = (EPI != EPI_I32 && p.P > 0 && !tside) ? (p.P + kSideLds - 1) / kSideLds : 0;
   float* xs = ws0;  // [BM][kSideLds]
   float* ws = xs + BM * kSideLds;                     // [kSideLds][BN]
   auto stage_side = [&](int q0) {
@@ -681,14 +692,15 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, i32x16 (&acc)
   };
   // the block's activation and weight scales, staged once: read per output from LDS
   // instead of one dependent L2 round trip per output row
-  float* asl = ws + kSideLds * BN;  // [BM]
-  float* bsl = asl + BM;            // [BN]
-  if constexpr (EPI != EPI_I32) {
-    for (int t = tid; t < BM; t += NT) asl[t] = bm + t < p.M ? p.as[bm + t] : 0.f;
-    for (int t = tid; t < BN; t += NT) bsl[t] = bn + t < p.N ? p.bs[bn + t] : 0.f;
+  const float* asl = PRE ? tail + kTailAs : ws + kSideLds * BN;  // [BM]
+  const float* bsl = PRE ? tail + kTailBs : ws + kSideLds * BN + BM;  // [BN]
+  if constexpr (EPI != EPI_I32 && !PRE) {
+    float* as_st = ws + kSideLds * BN;
+    for (int t = tid; t < BM; t += NT) as_st[t] = bm + t < p.M ? p.as[bm + t] : 0.f;
+    for (int t = tid; t < BN; t += NT) as_st[BM + t] = bn + t < p.N ? p.bs[bn + t] : 0.f;
   }
   if (nsc == 1) stage_side(0);
-  if (EPI != EPI_I32) __syncthreads();
+  if ((EPI != EPI_I32 && !PRE) || nsc == 1) __syncthreads();
   typedef float f32x16 __attribute__((ext_vector_type(16)));
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -697,6 +709,17 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, i32x16 (&acc)
       const int lr = wm * WM + 32 * i;  // tile row / column offsets within the block
       const int lc = wn * WN + 32 * j;
       f32x16 side = {};
+      if (tside) {
+        // the same MFMAs, in the same order, as the staged path below
+        const float* txp = tail + kTailXp;             // [BM][P]
+        const float* twp = tail + kTailXp + BM * kTailSide;  // [BN][P]
+        for (int s2 = 0; s2 < p.P; s2 += 2) {
+          const int q = s2 + (lane >> 5);
+          const float xa = q < p.P ? txp[(lr + (lane & 31)) * p.P + q] : 0.f;
+          const float wb = q < p.P ? twp[(lc + (lane & 31)) * p.P + q] : 0.f;
+          side = __builtin_amdgcn_mfma_f32_32x32x2f32(xa, wb, side, 0, 0, 0);
+        }
+      }
       for (int c = 0; c < nsc; ++c) {
         if (nsc > 1) {
           __syncthreads();
@@ -723,7 +746,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, i32x16 (&acc)
           } else {
             // reference order: (float(acc) * act_scale) * w_scale, added to the side path
             float v = mul_rn(mul_rn(static_cast<float>(acc[i][j][r]), asl[lrow]), bsc);
-            if (nsc) v = add_rn(side[r], v);
+            if (nsc || tside) v = add_rn(side[r], v);
             if constexpr (EPI == EPI_F32)
               static_cast<float*>(p.c)[(int64_t)row * p.ldc + col] = v;
             else
@@ -862,7 +885,7 @@ __device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, int8_t* dst
 // wave waits for its own copies of tile kt (vmcnt), then the barrier makes every wave's
 // copies visible and retires the stage read in step kt - 1, which the next copy reuses.
 // Needs K % 64 == 0, 16-byte aligned rows and 256 * ld < 2^31.
-template <int BM, int BN, int WM, int WN, int EPI>
+template <int BM, int BN, int WM, int WN, int EPI, int PRE = 0>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(GemmParams p) {
   constexpr int BK = 64, S = 4;
   constexpr int WAVES_M = BM / WM, NW = WAVES_M * (BN / WN), NT = NW * 64;
@@ -872,7 +895,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
   constexpr int JA = BM / 16 / NW, JB = BN / 16 / NW;  // 1 KiB copies per wave per stage
   static_assert(JA >= 1 && JB >= 1 && JA * 16 * NW == BM && JB * 16 * NW == BN, "whole copies per wave");
   static_assert(S * STAGE >= (BM + BN) * (kSideLds + 1) * 4, "epilogue staging needs the tile LDS");
-  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE];
+  constexpr int TAIL = PRE ? 4 * tail_floats<BM, BN>() : 0;  // bytes
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE + TAIL];
+  int8_t* const tail = lds + S * STAGE;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -906,12 +931,51 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
     boff[j] = r * (int)p.ldb + 16 * ((lane & 3) ^ dma_swz(r));
   }
   const int KT = p.K / BK;
+  // PRE: the copy slots of step KT, which loads nothing otherwise, fetch the epilogue's
+  // operands into the tail instead -- act / weight scales (1 KiB each) and, for
+  // P <= kTailSide, the side operands' row slices (BM * P and BN * P floats, 1 KiB per
+  // copy, zero past M / N).  Every wave still issues JA + JB copies per step, so the wait
+  // counts hold; the step is waited for only by the loop's final vmcnt(0), and the copies
+  // land while the last steps multiply.
+  auto tail_copies = [&](int8_t* st) {
+    const int tp = p.P > 0 && p.P <= kTailSide ? p.P : 0;
+    const int ncx = (BM * tp + 255) / 256, ncw = (BN * tp + 255) / 256;
+    auto rs = [](const float* base, int64_t n) {  // n floats readable from base
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0,
+                                               (int)(4 * n < INT_MAX ? 4 * n : INT_MAX), 0x00020000);
+    };
+    static_assert(2 + (BM + BN) * kTailSide / 256 <= (JA + JB) * NW, "tail copies fit the step's slots");
+#pragma unroll
+    for (int j = 0; j < JA + JB; ++j) {
+      const int c = j * NW + wave;  // wave-uniform
+      if (c == 0)
+        lds_copy16(rs(p.as + bm, p.M - bm), tail + 4 * kTailAs, 16 * lane, 0);
+      else if (c == 1)
+        lds_copy16(rs(p.bs + bn, p.N - bn), tail + 4 * kTailBs, 16 * lane, 0);
+      else if (c < 2 + ncx)
+        lds_copy16(rs(p.xp + (int64_t)bm * tp, (int64_t)(p.M - bm) * tp), tail + 4 * kTailXp + 1024 * (c - 2),
+                   16 * lane + 1024 * (c - 2), 0);
+      else if (c < 2 + ncx + ncw)
+        lds_copy16(rs(p.wp + (int64_t)bn * tp, (int64_t)(p.N - bn) * tp),
+                   tail + 4 * (kTailXp + BM * kTailSide) + 1024 * (c - 2 - ncx), 16 * lane + 1024 * (c - 2 - ncx), 0);
+      else
+        lds_copy16(rsa, st + 1024 * c, alim, 0);  // nothing to fetch: out of range, no access
+    }
+  };
   // rows past M / N read as zero; steps past K load out of the buffer's range (zero, no
   // memory access) into a stage that is not read again
-  auto dma = [&](int kt) {
+  // chk: this step's copies may be step KT's (false in the main loop, so that its body
+  // stays one straight block)
+  auto dma = [&](int kt, bool chk) {
     const bool live = kt < KT;
     const int ko = live ? kt * BK : 0;
     int8_t* st = lds + (kt & (S - 1)) * STAGE;
+    if constexpr (PRE) {
+      if (chk && kt == KT) {
+        tail_copies(st);
+        return;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < JA; ++j) lds_copy16(rsa, st + 1024 * (JA * wave + j), live ? aoff[j] : alim, ko);
 #pragma unroll
@@ -951,9 +1015,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
   // reads of slice 0 of tile kt + 1, and the MFMAs of slice 1 of tile kt, which cover the
   // barrier and those reads.
   i32x4 fa[FM + FN], fb[FM + FN];
-  dma(0);
-  dma(1);
-  dma(2);
+  dma(0, true);
+  dma(1, true);
+  dma(2, true);
   constexpr int NEWER = 2 * (JA + JB);  // this wave's copies of the two newer stages
   static_assert(NEWER == 8 || NEWER == 6 || NEWER == 4, "wait counts below");
   if constexpr (NEWER == 8)
@@ -962,9 +1026,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
     asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
   else
     asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
-  dma(3);
+  dma(3, true);
+  // The prologue's copies may take the tail path (K <= 3 * BK), whose kernel-argument
+  // loads count in lgkmcnt; settle them here, visibly to the compiler, so that the loop
+  // keeps its partial LDS waits.
+  if constexpr (PRE) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt unconstrained
   frag(fa, 0, 0);
-  for (int kt = 0; kt < KT; ++kt) {
+  auto step = [&](int kt, bool chk) {
     frag(fb, kt, 1);
     mma(fa);
     if (kt + 1 < KT) {
@@ -974,14 +1042,20 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
         asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       else
         asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      dma(kt + 4);
+      dma(kt + 4, chk);
       frag(fa, kt + 1, 0);
     }
     mma(fb);
-  }
+  };
+  // PRE: the last four steps, whose copies may be step KT's, run in a loop of their own
+  const int kmain = !PRE ? KT : (KT > 4 ? KT - 4 : 0);
+  int kt = 0;
+  for (; kt < kmain; ++kt) step(kt, false);
+  for (; kt < KT; ++kt) step(kt, true);
   // every copy (including the ones past K) has landed before the epilogue reuses LDS
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  gemm_epilogue<BM, BN, WM, WN, EPI, NT>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn, tid, lane);
+  gemm_epilogue<BM, BN, WM, WN, EPI, NT, PRE>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn, tid, lane,
+                                              reinterpret_cast<const float*>(tail));
 }
 
 // Any shape: one thread per output, exact int32 accumulation.
@@ -1039,12 +1113,20 @@ void launch_gemm(const GemmParams& p, hipStream_t s) {
   const bool dma_ok = p.K % 64 == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned(p.a, 16) &&
                       aligned(p.b, 16) && 256 * p.lda < INT_MAX && 256 * p.ldb < INT_MAX;
   if (kGemmDma && dma_ok) {
+    // epilogue operands by DMA (PRE) when their row slices are whole 16-byte chunks and
+    // 16-byte aligned: a copy's range check then never splits a chunk
+    const bool side_tail = p.P > 0 && p.P <= kTailSide;
+    const bool pre = EPI != EPI_I32 && p.M % 4 == 0 && p.N % 4 == 0 && aligned(p.as, 16) && aligned(p.bs, 16) &&
+                     (!side_tail || (aligned(p.xp, 16) && aligned(p.wp, 16) && ((int64_t)p.M * p.P) % 4 == 0 &&
+                                     ((int64_t)p.N * p.P) % 4 == 0));
     if (big) {
       const int G = (int)(cdiv(p.M, 256) * cdiv(p.N, 256));
-      hipLaunchKernelGGL((k_gemm_i8_dma<256, 256, 128, 64, EPI>), dim3(G), dim3(512), 0, s, p);
+      if (pre) hipLaunchKernelGGL((k_gemm_i8_dma<256, 256, 128, 64, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(512), 0, s, p);
+      else hipLaunchKernelGGL((k_gemm_i8_dma<256, 256, 128, 64, EPI>), dim3(G), dim3(512), 0, s, p);
     } else {
       const int G = (int)(cdiv(p.M, 256) * cdiv(p.N, 128));
-      hipLaunchKernelGGL((k_gemm_i8_dma<256, 128, 64, 64, EPI>), dim3(G), dim3(512), 0, s, p);
+      if (pre) hipLaunchKernelGGL((k_gemm_i8_dma<256, 128, 64, 64, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(512), 0, s, p);
+      else hipLaunchKernelGGL((k_gemm_i8_dma<256, 128, 64, 64, EPI>), dim3(G), dim3(512), 0, s, p);
     }
     return;
   }

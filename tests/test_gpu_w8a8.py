@@ -143,6 +143,55 @@ def test_w8a8_bf16_out_bit_exact(dev, t, n):
     assert torch.equal(y.cpu(), ref)
 
 
+@pytest.mark.parametrize(
+    "t,n,p,ydt",
+    [(300, 1000, 0, "f32"), (300, 1000, 1, "bf16"), (300, 1000, 3, "f32"), (64, 640, 8, "f32"),
+     (1028, 8200, 8, "bf16"), (1028, 8200, 5, "f32"), (256, 384, 12, "f32")],
+)
+def test_gemm_dma_epilogue_operands_match_staged(dev, t, n, p, ydt):
+    """The DMA GEMM fetches its epilogue operands (act / weight scales, and the side
+    operands for P <= 8) into LDS with the main loop's copies when their row slices are
+    16-byte aligned whole chunks; the same values at a 4-byte offset take the staged
+    epilogue.  Both agree bit for bit, over ragged M / N edges of both tile shapes."""
+    from mrun_pub_amd import _native as nat
+
+    K = 512
+    g = torch.Generator(device=dev)
+    g.manual_seed(t * 31 + n + p)
+    qx = torch.randint(-127, 128, (t, K), dtype=torch.int8, device=dev, generator=g)
+    qw = torch.randint(-127, 128, (n, K), dtype=torch.int8, device=dev, generator=g)
+    a_s = torch.rand(t, device=dev, generator=g) / 100 + 1e-3
+    b_s = torch.rand(n, device=dev, generator=g) / 100 + 1e-3
+    xp = torch.randn(t, max(p, 1), device=dev, generator=g)[:, :p].contiguous()
+    wp = torch.randn(n, max(p, 1), device=dev, generator=g)[:, :p].contiguous()
+
+    def shifted(a):  # same values, 4 bytes past a 16-byte boundary
+        buf = torch.zeros(a.numel() + 4, dtype=a.dtype, device=dev)
+        buf[1 : 1 + a.numel()] = a.reshape(-1)
+        return buf[1 : 1 + a.numel()]
+
+    code = nat.QS_F32 if ydt == "f32" else nat.QS_BF16
+    dt = torch.float32 if ydt == "f32" else torch.bfloat16
+    outs = []
+    for ops in ((a_s, b_s, xp, wp), tuple(shifted(x) for x in (a_s, b_s, xp, wp))):
+        y = torch.full((t, n), float("nan"), dtype=dt, device=dev)
+        nat.call("qs_w8a8_gemm", nat.ptr(qx), nat.ptr(ops[0]), nat.ptr(qw), nat.ptr(ops[1]),
+                 nat.ptr(ops[2]) if p else None, nat.ptr(ops[3]) if p else None, p, nat.ptr(y), code, t, n, K,
+                 nat.stream_of(dev))
+        outs.append(y)
+    torch.cuda.synchronize()
+    assert not torch.isnan(outs[0].float()).any()
+    assert torch.equal(outs[0].view(torch.int16 if ydt == "bf16" else torch.int32),
+                       outs[1].view(torch.int16 if ydt == "bf16" else torch.int32))
+    # and the fp32 result is the reference formula: side + (float(acc) * a_s) * b_s
+    rows = torch.arange(0, t, 37, device=dev)
+    acc = (qx[rows].double() @ qw.double().T)
+    ref = (acc.float() * a_s[rows, None]) * b_s[None, :]
+    if p:
+        ref = ref + (xp[rows].double() @ wp.double().T).float()
+    assert torch.allclose(outs[0][rows].float(), ref.to(dt).float(), rtol=1e-2 if ydt == "bf16" else 1e-5, atol=1e-5)
+
+
 @pytest.mark.parametrize("protect_k", [4, 8, 16, 24])
 def test_w8a8_outlier_protection(dev, protect_k):
     rng, q_w, sc_w = _weights(640, 4096, protect_k)
