@@ -757,6 +757,158 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, i32x16 (&acc)
     }
 }
 
+// Epilogue of the DMA GEMM, whose MFMAs take the weight fragment as A and the activation
+// fragment as B: accumulator register r of lane l then holds
+// C[row (l & 31)][col 8 * (r / 4) + 4 * (l >> 5) + (r % 4)] of the 32 x 32 tile, i.e. four
+// consecutive columns of one row per register group, stored with one 16-byte (int32 /
+// fp32) or 8-byte (bf16) instruction instead of four scalar ones.  The side path's
+// MFMAs swap their operands the same way and keep their order, so every value equals the
+// one gemm_epilogue computes.  PRE as in gemm_epilogue.
+template <int BM, int BN, int WM, int WN, int EPI, int NT, int PRE>
+__device__ __forceinline__ void gemm_epilogue_t(const GemmParams& p, i32x16 (&acc)[WM / 32][WN / 32], float* ws0,
+                                                int bm, int bn, int wm, int wn, int tid, int lane,
+                                                const float* tail) {
+  constexpr int FM = WM / 32, FN = WN / 32;
+  static_assert(!PRE || (EPI != EPI_I32 && BM <= 256 && BN <= 256), "tail layout");
+  const int h = lane >> 5, l32 = lane & 31;
+  const bool tside = PRE && p.P > 0 && p.P <= kTailSide;
+  const int nsc = (EPI != EPI_I32 && p.P > 0 && !tside) ? (p.P + kSideLds - 1) / kSideLds : 0;
+  float* xs = ws0;                 // [BM][kSideLds]
+  float* ws = xs + BM * kSideLds;  // [kSideLds][BN]
+  auto stage_side = [&](int q0) {
+    for (int t = tid; t < BM * kSideLds; t += NT) {
+      const int r = t / kSideLds, q = q0 + (t - (t / kSideLds) * kSideLds);
+      xs[t] = (bm + r < p.M && q < p.P) ? p.xp[(int64_t)(bm + r) * p.P + q] : 0.f;
+    }
+    for (int t = tid; t < BN * kSideLds; t += NT) {
+      const int c = t / kSideLds, qq = t - (t / kSideLds) * kSideLds, q = q0 + qq;
+      ws[qq * BN + c] = (bn + c < p.N && q < p.P) ? p.wp[(int64_t)(bn + c) * p.P + q] : 0.f;
+    }
+  };
+  const float* asl = PRE ? tail + kTailAs : ws + kSideLds * BN;       // [BM]
+  const float* bsl = PRE ? tail + kTailBs : ws + kSideLds * BN + BM;  // [BN]
+  if constexpr (EPI != EPI_I32 && !PRE) {
+    float* as_st = ws + kSideLds * BN;
+    for (int t = tid; t < BM; t += NT) as_st[t] = bm + t < p.M ? p.as[bm + t] : 0.f;
+    for (int t = tid; t < BN; t += NT) as_st[BM + t] = bn + t < p.N ? p.bs[bn + t] : 0.f;
+  }
+  if (nsc == 1) stage_side(0);
+  if ((EPI != EPI_I32 && !PRE) || nsc == 1) __syncthreads();
+  // 4-wide stores need 16-byte aligned rows (ldc % 4 == 0, y 16-byte aligned)
+  const bool vec = p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int lrow = wm * WM + 32 * i + l32;
+    const int row = bm + lrow;
+    // the side operands of this lane's row (P == 8 tail: two 16-byte LDS reads)
+    float xr[kTailSide];
+    if (tside) {
+      const float* txp = tail + kTailXp;
+      if (p.P == kTailSide) {
+        const f32x4 a0 = *reinterpret_cast<const f32x4*>(txp + lrow * kTailSide);
+        const f32x4 a1 = *reinterpret_cast<const f32x4*>(txp + lrow * kTailSide + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xr[e] = a0[e], xr[4 + e] = a1[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < kTailSide; ++e) xr[e] = e < p.P ? txp[lrow * p.P + e] : 0.f;
+      }
+    }
+    float asc = 0.f;
+    if constexpr (EPI != EPI_I32) asc = asl[lrow];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int lc = wn * WN + 32 * j;
+      f32x16 side = {};
+      if (tside) {
+        const float* twp = tail + kTailXp + BM * kTailSide;  // [BN][P]
+        const int lcol = lc + l32;
+        float wr[kTailSide];
+        if (p.P == kTailSide) {
+          const f32x4 b0 = *reinterpret_cast<const f32x4*>(twp + lcol * kTailSide);
+          const f32x4 b1 = *reinterpret_cast<const f32x4*>(twp + lcol * kTailSide + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wr[e] = b0[e], wr[4 + e] = b1[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < kTailSide; ++e) wr[e] = e < p.P ? twp[lcol * p.P + e] : 0.f;
+        }
+        // steps of two columns (2s, 2s + 1), half h of the wave supplying column 2s + h
+#pragma unroll
+        for (int s2 = 0; s2 < kTailSide; s2 += 2) {
+          if (s2 < p.P) {
+            const float xa = h ? xr[s2 + 1] : xr[s2];
+            const float wb = h ? wr[s2 + 1] : wr[s2];
+            side = __builtin_amdgcn_mfma_f32_32x32x2f32(wb, xa, side, 0, 0, 0);
+          }
+        }
+      }
+      for (int c = 0; c < nsc; ++c) {
+        if (nsc > 1) {
+          __syncthreads();
+          stage_side(c * kSideLds);
+          __syncthreads();
+        }
+        const int qn = min(kSideLds, p.P - c * kSideLds);
+        for (int s2 = 0; s2 < qn; s2 += 2) {
+          const float xa = xs[lrow * kSideLds + s2 + h];
+          const float wb = ws[(s2 + h) * BN + lc + l32];
+          side = __builtin_amdgcn_mfma_f32_32x32x2f32(wb, xa, side, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int lcol0 = lc + 8 * g + 4 * h;
+        const int col0 = bn + lcol0;
+        if (row >= p.M || col0 >= p.N) continue;
+        const int64_t o = (int64_t)row * p.ldc + col0;
+        const bool full = vec && col0 + 3 < p.N;
+        if constexpr (EPI == EPI_I32) {
+          const i32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          if (full) {
+            *reinterpret_cast<i32x4*>(static_cast<int32_t*>(p.c) + o) = v;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (col0 + e < p.N) static_cast<int32_t*>(p.c)[o + e] = v[e];
+          }
+        } else {
+          const f32x4 bsc = *reinterpret_cast<const f32x4*>(bsl + lcol0);
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            // reference order: (float(acc) * act_scale) * w_scale, added to the side path
+            v[e] = mul_rn(mul_rn(static_cast<float>(acc[i][j][4 * g + e]), asc), bsc[e]);
+            if (nsc || tside) v[e] = add_rn(side[4 * g + e], v[e]);
+          }
+          if constexpr (EPI == EPI_F32) {
+            if (full) {
+              *reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + o) = f32x4{v[0], v[1], v[2], v[3]};
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (col0 + e < p.N) static_cast<float*>(p.c)[o + e] = v[e];
+            }
+          } else {
+            uint16_t b[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) b[e] = f32_to_bf16_bits(v[e]);
+            if (full) {
+              const uint2 pk = make_uint2(b[0] | (uint32_t)b[1] << 16, b[2] | (uint32_t)b[3] << 16);
+              *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.c) + o) = pk;
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (col0 + e < p.N) static_cast<uint16_t*>(p.c)[o + e] = b[e];
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int WM, int WN, int EPI, int BK = kBK>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8(GemmParams p) {
   constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
@@ -1007,7 +1159,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[i], f[FM + j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[FM + j], f[i], acc[i][j], 0, 0, 0);  // C^T tile
   };
   // Step kt: read slice 1 of tile kt, multiply slice 0 (read one step earlier), then the
   // barrier for tile kt + 1 -- this wave's copies of kt + 1 done (vmcnt) and its reads of
@@ -1054,8 +1206,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
   for (; kt < KT; ++kt) step(kt, true);
   // every copy (including the ones past K) has landed before the epilogue reuses LDS
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  gemm_epilogue<BM, BN, WM, WN, EPI, NT, PRE>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn, tid, lane,
-                                              reinterpret_cast<const float*>(tail));
+  gemm_epilogue_t<BM, BN, WM, WN, EPI, NT, PRE>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn, tid, lane,
+                                                reinterpret_cast<const float*>(tail));
 }
 
 // Any shape: one thread per output, exact int32 accumulation.
