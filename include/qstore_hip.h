@@ -85,16 +85,16 @@ int qs_qrow_matmul_multi(const void* x, int x_dtype, int64_t ldx, int n_linear,
 /* Batched decode (M rows of bf16/f16 activations, 1 <= M <= 32), same contracts as
  * qs_qrow_matmul_multi (W8A16, y in the activation dtype) and qs_qrow_swiglu (x, y BF16),
  * for the reference's batched decode through fused_qrow_matmul / fused_qrow_swiglu
- * (dense_qstore_cuda.py:1105-1153, 1053-1102).  K % 128 == 0, K <= 16384 (SwiGLU:
- * K <= 2048), otherwise QS_ERR_UNSUPPORTED; weight and activation rows 16-byte aligned.  K is split into slices chosen from (N, K) only, and the slices' fp32
- * partial sums are added in slice order, so every row equals the same row computed alone
- * (M = 1 through this entry point) bit for bit.
- *   workspace: qs_qrow_batched_workspace_bytes(M, n_linear, N, K, swiglu) bytes (may be 0),
- *              contents clobbered;
- *   counters:  at least qs_qrow_batched_counters(n_linear, N, swiglu) int32 that are zero
- *              on entry; every call leaves them zero when it completes, so one array serves
- *              all calls on one stream.  Calls that run concurrently (other streams) need
- *              their own counters and workspace. */
+ * (dense_qstore_cuda.py:1105-1153, 1053-1102).  K % 128 == 0, K <= 16384, otherwise
+ * QS_ERR_UNSUPPORTED; weight and activation rows 16-byte aligned; a K split (rows longer
+ * than 2048) needs every N % 4 == 0.  The K order of every sum (waves per slice, slices)
+ * is chosen from (N, K) only and the slices' fp32 partial sums are added in slice order,
+ * so every row equals the same row computed alone (M = 1 through this entry point) bit
+ * for bit.
+ *   workspace: qs_qrow_batched_workspace_bytes(M, n_linear, N, K, swiglu) bytes, 16-byte
+ *              aligned (0 when K is not split), contents clobbered; calls that run
+ *              concurrently (other streams) need their own;
+ *   counters:  unused (qs_qrow_batched_counters returns 0); may be null. */
 size_t qs_qrow_batched_workspace_bytes(int64_t M, int n_linear, const int64_t* N, int64_t K,
                                        int swiglu);
 int64_t qs_qrow_batched_counters(int n_linear, const int64_t* N, int swiglu);

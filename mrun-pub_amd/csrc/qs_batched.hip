@@ -1,53 +1,24 @@
 // Batched-decode W8A16 qrow linears on gfx950 (1 <= M <= 32 bf16/f16 activation rows).
 //
-// Kernel
-//   k_bdec<P, MT, F16> : one workgroup = (64-row weight tile, K slice).  Its 4 waves own 16
-//                        weight rows each (P = 2: the same 16 rows of gate and of up) and
-//                        share ONE LDS copy of the activation slice [M, slice], so the
-//                        activations cross the memory system 2M/64 bytes per weight byte
-//                        (<= 1 at M = 32) instead of once per 16-row tile.  The activation
-//                        slice is requested first, the weights second (HBM straight to
-//                        VGPRs, nontemporal 128-bit loads), so the LDS staging waits only for
-//                        the activations while the weights stay in flight.  Weights are
-//                        dequantized in registers to the W8A16 contract bf16(float(code) *
-//                        scale) and fed to v_mfma_f32_16x16x32_{bf16,f16} with the
-//                        activations as operand A.
-//                        With one slice the epilogue is stored straight from the
-//                        accumulators.  Otherwise each slice's fp32 partial sums go to the
-//                        workspace through coherent stores, the workgroup bumps its tile's
-//                        counter, and the workgroup that brings it to S sums the S partials
-//                        of every output of the tile in slice order s = 0..S-1 (coherent
-//                        loads), stores the epilogue (bf16/f16, or the paired SwiGLU) and
-//                        resets the counter to zero for the next call.  No workgroup ever
-//                        waits for another, and there is no second launch.
-// The split S and the slice length depend on (N, K) only, never on M, and a 16x16x32 MFMA
-// sums every output element over its k in a fixed order whatever the other rows hold, so
-// a row's result does not depend on the rest of the batch.
-//
+// Kernels
+//   k_bd2<P, MT, WR, WK, F16> : one workgroup = (16 * WR weight rows of P planes, K slice);
+//                               P = 2 pairs the gate and up rows of a SwiGLU tile.  The
+//                               slice's activations reach LDS by DMA and serve all of the
+//                               workgroup's rows; the weights stream from HBM into VGPRs,
+//                               are dequantized in registers to the W8A16 contract
+//                               bf16(float(code) * scale) and fed to
+//                               v_mfma_f32_16x16x32_{bf16,f16}.
+//   k_bd2_reduce<P, F16>      : the K slices' fp32 partial sums added in slice order, and the
+//                               epilogue (bf16/f16, or the paired SwiGLU).
 // MFMA operand mapping (16x16x32, wave64): lane l supplies row (l & 15) of A and column
-// (l & 15) of B, 8 consecutive k of k-block (l >> 4).  Per 128-k chunk a lane reads the
-// 32 contiguous weight bytes at k = 128c + 32(l >> 4) of its row and the matching 32
-// activations; each 8 of them feed one MFMA.  The accumulator of lane l holds
+// (l & 15) of B, 8 consecutive k of k-block (l >> 4); the accumulator of lane l holds
 // D[4(l >> 4) + q][l & 15], q = 0..3.
 #include "qs_common.h"
 
+#include <algorithm>
+
 namespace qs {
 namespace {
-
-constexpr int kBdecRows = 64;   // weight rows per workgroup tile
-constexpr int kBdecWaves = 4;   // 16 rows per wave
-
-// 128-k chunks per slice at most: K <= 2048 takes one slice, so no workgroup hands partial
-// sums to another; the slice's activations sit in LDS
-template <int P>
-constexpr int kBdecMaxCS = 16;
-// slices at most (the fixup holds every partial of its outputs in VGPRs at once)
-template <int P>
-constexpr int kBdecMaxS = P == 2 ? 1 : 8;
-// weight chunks in flight per wave: the whole slice (a 64-row tile runs one workgroup per
-// CU, 1 wave per SIMD, so the registers are there; every byte is requested at once)
-template <int P>
-constexpr int kBdecWin = 16;
 
 struct BdecLin {
   const int8_t* codes;
@@ -55,20 +26,17 @@ struct BdecLin {
   void* y;
   int64_t ldy;
   int N;
-  int tile_begin;  // first 64-row tile of this linear
+  int tile_begin;  // first workgroup row tile of this linear
   int n_begin;     // first output column of this linear in the partial rows
 };
 
+// The checked call arguments shared by the entry points.
 struct BdecParams {
   const uint16_t* x;
   int64_t ldx;
-  int M, K, C;     // C = K / 128
-  int S, CS;       // slices and chunks per slice (the last slice may be shorter)
+  int M, K;
   int n_lin;
-  int n_total;     // columns of a partial row (sum of N over the linears)
   BdecLin lin[4];
-  float* part;     // [S][P][M][n_total]
-  int* counters;   // [tiles], zero on entry and on exit
   bool f16;
 };
 
@@ -95,18 +63,6 @@ struct Half<true> {
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf(-g))); }
 
-// LDS row stride of the staged activation slice, in bytes: 16 bytes of padding put
-// consecutive rows 4 banks apart, so the 16 rows a fragment read touches do not collide.
-template <int P>
-constexpr int kXStride = kBdecMaxCS<P> * 256 + 16;
-
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Epilogue of one output: plane sums -> bf16/f16 (P = 1) or the paired SwiGLU (P = 2).
 template <int P, bool F16>
 __device__ __forceinline__ uint16_t bdec_out(const float (&v)[P]) {
@@ -117,209 +73,6 @@ __device__ __forceinline__ uint16_t bdec_out(const float (&v)[P]) {
     return f32_to_bf16_bits(sl * ut);
   } else {
     return Half<F16>::out(v[0]);
-  }
-}
-
-template <int P, int MT, bool F16>
-__global__ __launch_bounds__(kBdecWaves * 64, 1) void k_bdec(BdecParams p) {
-  typedef Half<F16> H;
-  typedef typename H::vec hvec;
-  constexpr int CSM = kBdecMaxCS<P>;
-  constexpr int XS = kXStride<P>;
-  constexpr int XPT = 16 * MT * CSM * 16 / (kBdecWaves * 64);  // staged vectors per thread
-  __shared__ __attribute__((aligned(16))) uint8_t xs[16 * MT * XS];
-  __shared__ int last;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 15, grp = lane >> 4;
-  const int tile = (int)blockIdx.x / p.S;
-  const int s = (int)blockIdx.x - tile * p.S;
-  int li = 0;
-  if (P == 1) {
-#pragma unroll
-    for (int j = 1; j < 4; ++j)
-      if (j < p.n_lin && tile >= p.lin[j].tile_begin) li = j;
-  }
-  const BdecLin& L0 = p.lin[li];
-  const int N = L0.N;
-  const int t0 = (tile - L0.tile_begin) * kBdecRows;  // first row of the tile
-  const int n0 = t0 + 16 * wave;
-  const int n = n0 + col < N ? n0 + col : N - 1;  // clamped rows are loaded, never stored
-  const int c0 = s * p.CS;
-  const int cs = min(p.CS, p.C - c0);  // >= 1
-
-  // 1. activation slice [16*MT rows, cs*128 k] -> registers, rows >= M as zeros
-  const int vec_per_row = cs * 16;
-  const int total = 16 * MT * vec_per_row;
-  i32x4 xv[XPT];
-#pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    const int v = tid + i * kBdecWaves * 64;
-    const int m = v / vec_per_row;
-    const int e = v - m * vec_per_row;
-    xv[i] = (v < total && m < p.M)
-                ? *reinterpret_cast<const i32x4*>(p.x + (int64_t)m * p.ldx + (int64_t)c0 * 128 + 8 * e)
-                : i32x4{0, 0, 0, 0};
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  // 2. the first window of this wave's weight chunks (16 rows) -> VGPRs
-  constexpr int WW = kBdecWin<P>;
-  const int8_t* wrow[P];
-#pragma unroll
-  for (int pl = 0; pl < P; ++pl)
-    wrow[pl] = p.lin[P == 2 ? pl : li].codes + (int64_t)n * p.K + (int64_t)c0 * 128 + 32 * grp;
-  i32x4 wv[CSM][P][2];
-  auto load_chunk = [&](int c) {
-#pragma unroll
-    for (int pl = 0; pl < P; ++pl)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        wv[c][pl][h] = c < cs ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wrow[pl] + c * 128 + 16 * h))
-                              : i32x4{0, 0, 0, 0};
-  };
-#pragma unroll
-  for (int c = 0; c < WW; ++c) load_chunk(c);
-  float sc[P];
-#pragma unroll
-  for (int pl = 0; pl < P; ++pl) sc[pl] = p.lin[P == 2 ? pl : li].scales[n];
-  __builtin_amdgcn_sched_barrier(0);
-  // 3. stage the activations (waits for them only)
-#pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    const int v = tid + i * kBdecWaves * 64;
-    if (v < total) {
-      const int m = v / vec_per_row;
-      const int e = v - m * vec_per_row;
-      *reinterpret_cast<i32x4*>(xs + m * XS + 16 * e) = xv[i];
-    }
-  }
-  __syncthreads();
-
-  // 4. MFMA over the slice; chunk c + WW is requested once chunk c is consumed
-  f32x4 acc[P][MT];
-#pragma unroll
-  for (int pl = 0; pl < P; ++pl)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[pl][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int c = 0; c < CSM; ++c) {
-    if (c < cs) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        hvec a[MT][2];
-#pragma unroll
-        for (int t = 0; t < MT; ++t)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            a[t][j] = *reinterpret_cast<const hvec*>(xs + (16 * t + col) * XS + 2 * (c * 128 + 32 * grp + 16 * h + 8 * j));
-#pragma unroll
-        for (int pl = 0; pl < P; ++pl) {
-          hvec b0, b1;
-          H::deq(wv[c][pl][h], sc[pl], b0, b1);
-#pragma unroll
-          for (int t = 0; t < MT; ++t) {
-            acc[pl][t] = H::mma(a[t][0], b0, acc[pl][t]);
-            acc[pl][t] = H::mma(a[t][1], b1, acc[pl][t]);
-          }
-        }
-      }
-    }
-    if (c + WW < CSM) load_chunk(c + WW);
-  }
-
-  // lane holds D[m = 16t + 4grp + q][n0 + col]
-  const int no = n0 + col;
-  if (p.S == 1) {  // the whole K in one slice: store the epilogue directly
-    if (no >= N) return;
-    uint16_t* y = static_cast<uint16_t*>(L0.y);
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = 16 * t + 4 * grp + q;
-        float v[P];
-#pragma unroll
-        for (int pl = 0; pl < P; ++pl) v[pl] = acc[pl][t][q];
-        if (m < p.M) y[(int64_t)m * L0.ldy + no] = bdec_out<P, F16>(v);
-      }
-    return;
-  }
-
-  // 5. partial sums of this slice (coherent stores), then the tile's arrival counter
-  if (no < N) {
-    const int ncol = L0.n_begin + no;
-#pragma unroll
-    for (int pl = 0; pl < P; ++pl)
-#pragma unroll
-      for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int m = 16 * t + 4 * grp + q;
-          if (m < p.M) store_coherent(&p.part[(((int64_t)s * P + pl) * p.M + m) * p.n_total + ncol], acc[pl][t][q]);
-        }
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-  __syncthreads();
-  if (tid == 0)
-    last = __hip_atomic_fetch_add(&p.counters[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.S - 1;
-  __syncthreads();
-  if (!last) return;
-
-  // 6. the tile's last workgroup: fixed-order sum over the slices, epilogue, counter reset.
-  //    Thread tid owns column r = tid % 64 of rows m = tid / 64 + 4i; all of its partials
-  //    are requested before the first is summed, so the fixup costs one memory latency.
-  constexpr int SM = kBdecMaxS<P>;
-  constexpr int OPT = 16 * MT / kBdecWaves;  // outputs per thread
-  const int r = tid & 63;
-  const int mg = tid >> 6;
-  const bool rok = t0 + r < N;
-  const int64_t ncol = L0.n_begin + t0 + (rok ? r : 0);
-  float pv[OPT][P][SM];
-#pragma unroll
-  for (int o = 0; o < OPT; ++o) {
-    const int m = mg + kBdecWaves * o;
-#pragma unroll
-    for (int pl = 0; pl < P; ++pl)
-#pragma unroll
-      for (int k2 = 0; k2 < SM; ++k2)
-        pv[o][pl][k2] = (k2 < p.S && m < p.M && rok)
-                            ? load_coherent(&p.part[(((int64_t)k2 * P + pl) * p.M + m) * p.n_total + ncol])
-                            : 0.f;
-  }
-  uint16_t* y = static_cast<uint16_t*>(L0.y);
-#pragma unroll
-  for (int o = 0; o < OPT; ++o) {
-    const int m = mg + kBdecWaves * o;
-    float v[P];
-#pragma unroll
-    for (int pl = 0; pl < P; ++pl) {
-      float a = pv[o][pl][0];
-#pragma unroll
-      for (int k2 = 1; k2 < SM; ++k2)
-        if (k2 < p.S) a = add_rn(a, pv[o][pl][k2]);
-      v[pl] = a;
-    }
-    if (m < p.M && rok) y[(int64_t)m * L0.ldy + t0 + r] = bdec_out<P, F16>(v);
-  }
-  if (tid == 0) __hip_atomic_store(&p.counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Slices from K only: as few as hold at most kBdecMaxCS<P> chunks each, of equal length.
-void bdec_split(int64_t n_tiles, int C, int P, int& S, int& CS) {
-  (void)n_tiles;
-  const int csm = P == 2 ? kBdecMaxCS<2> : kBdecMaxCS<1>;
-  S = (C + csm - 1) / csm;  // may exceed kBdecMaxS<P>: rejected by the caller
-  CS = (C + S - 1) / S;
-  S = (C + CS - 1) / CS;
-}
-
-void bdec_shape(const int64_t* N, int n_lin, int P, int64_t& tiles, int64_t& cols) {
-  tiles = cols = 0;
-  for (int i = 0; i < n_lin; ++i) {
-    tiles += cdiv(N[i], kBdecRows);
-    cols += N[i];
-    if (P == 2) break;  // gate and up share the tiles and the columns
   }
 }
 
@@ -336,48 +89,388 @@ int bdec_prepare(BdecParams& p, const void* x, int x_dtype, int64_t ldx, int64_t
   p.ldx = ldx;
   p.M = (int)M;
   p.K = (int)K;
-  p.C = (int)(K / 128);
   p.f16 = x_dtype == QS_F16;
   return QS_OK;
 }
 
+// ---------------------------------------------------------------------------------
+// k_bd2: one workgroup = (16 * WR weight rows, K slice); its WR * WK waves own 16 rows x
+// a contiguous part of the slice each.  The slice's activations [M, slice] reach LDS by
+// DMA (buffer_load ... lds, 1 KiB per wave instruction, 16-byte chunk j of row m at slot
+// j ^ (m & 15), so the 16 rows of a fragment read fall in distinct banks); the wave's
+// weight chunks (64 k of 16 rows, 16 bytes per lane) are all requested right behind the
+// copies and land in VGPRs while the copies are waited for.  Dequantized weights are the
+// MFMA A operand, the activations B, so lane l ends up with 4 consecutive output columns
+// of one activation row.  The WK parts are summed in fixed order through LDS; with S > 1
+// slices the fp32 partial sums go to the workspace and k_bd2_reduce sums them in slice
+// order and stores the epilogue.  WK, S and the slice length -- the K order of every sum --
+// depend on (N, K) only (WR, the rows per workgroup, may follow M: it changes no sum), and
+// an MFMA sums each output over its k in a fixed order whatever the other rows hold, so a
+// row's result does not depend on the rest of the batch.
+// ---------------------------------------------------------------------------------
+constexpr int kBd2MaxPS = 8;   // 64-k chunks per wave part (all requested at once)
+constexpr int kBd2MaxCS = 20;  // 64-k chunks per slice: <= 80 KiB of activations at M = 32,
+                               // so two workgroups fit a CU's LDS
+constexpr int kBd2MaxS = 16;   // slices (k_bd2_reduce requests all of them at once)
+
+struct Bd2Params {
+  const uint16_t* x;
+  int64_t ldx;
+  int M, K, C;   // C = K / 64
+  int S, CS;     // slices and 64-k chunks per slice (even: 16-chunk LDS row groups)
+  int n_lin, n_total;
+  int vec;       // outputs and partial rows allow 4-wide stores
+  BdecLin lin[4];
+  float* part;   // [S][P][M][n_total] when S > 1
+};
+
+// One wave's 1 KiB global -> LDS copy (lane l's 16 bytes at buffer offset voff land at
+// dst + 16 l).  Not a template: in template-dependent code the host compilation pass drops
+// the kernel's launch stub over this builtin.
+__device__ __forceinline__ void bd2_copy16(__amdgpu_buffer_rsrc_t r, uint8_t* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
+}
+
+template <int P, int MT, int WR, int WK, bool F16>
+__global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
+  typedef Half<F16> H;
+  typedef typename H::vec hvec;
+  constexpr int NW = WR * WK;
+  constexpr int R = 16 * WR;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t bsm[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave % WR, wk = wave / WR;
+  const int col = lane & 15, grp = lane >> 4;
+  const int tile = (int)blockIdx.x / p.S;
+  const int s = (int)blockIdx.x - tile * p.S;
+  int li = 0;
+  if (P == 1) {
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      if (j < p.n_lin && tile >= p.lin[j].tile_begin) li = j;
+  }
+  const BdecLin& L0 = p.lin[li];
+  const int N = L0.N;
+  const int n0 = (tile - L0.tile_begin) * R + 16 * wr;  // this wave's 16 rows
+  const int c0 = s * p.CS;
+  const int cs = min(p.CS, p.C - c0);  // chunks of this slice, >= 1
+  const int kbeg = c0 * 64;
+  const int NCH = p.CS * 8;  // 16-byte chunks per staged activation row
+
+  // 1. row scales: the oldest requests, so the wait below covers them
+  const int nr = n0 + col;
+  float sc[P];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) sc[pl] = p.lin[P == 2 ? pl : li].scales[nr < N ? nr : N - 1];
+
+  // 2. the activation slice [16 MT rows][NCH chunks] -> LDS; rows >= M and chunks past the
+  //    slice read out of the buffer's range (zero, no memory access)
+  const int xlim = p.M * (int)p.ldx * 2;
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x), (short)0, xlim, 0x00020000);
+  const int total = 16 * MT * NCH;
+  for (int u0 = wave * 64; u0 < total; u0 += NW * 64) {
+    const int u = u0 + lane;
+    const int m = u / NCH, jj = u - m * NCH, j = jj ^ (m & 15);
+    const bool ok = m < p.M && j < 8 * cs;
+    bd2_copy16(xr, bsm + 16 * u0, ok ? (m * (int)p.ldx + kbeg + 8 * j) * 2 : xlim);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. this wave's part of the slice: every chunk requested at once (zero past the part
+  //    and for rows >= N, whose lane offsets lie past the buffer)
+  const int PS = (cs + WK - 1) / WK;
+  const int cb = wk * PS;
+  const int ce = min(cs, cb + PS);
+  const int wlim = N * p.K;
+  const int wlane = nr * p.K + kbeg + 16 * grp;
+  i32x4 wv[kBd2MaxPS][P];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) {
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(p.lin[P == 2 ? pl : li].codes), (short)0, wlim, 0x00020000);
+#pragma unroll
+    for (int c = 0; c < kBd2MaxPS; ++c)
+      wv[c][pl] = __builtin_bit_cast(
+          i32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, cb + c < ce ? wlane + 64 * (cb + c) : wlim, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 4. this wave's copies have landed once at most its kBd2MaxPS * P weight loads are
+  //    outstanding; the barrier then makes every wave's copies visible
+  static_assert(kBd2MaxPS * P == 8 || kBd2MaxPS * P == 16, "wait counts below");
+  if constexpr (kBd2MaxPS * P == 16)
+    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+
+  // 5. MFMA over the part
+  f32x4 acc[P][MT];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[pl][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < kBd2MaxPS; ++c) {
+    if (cb + c < ce) {
+      const int j = 8 * (cb + c) + 2 * grp;  // chunk of k = 64 (cb + c) + 16 grp in the slice
+      hvec xa[MT][2];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int m = 16 * t + col;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          xa[t][h] = *reinterpret_cast<const hvec*>(bsm + 16 * (m * NCH + ((j + h) ^ (m & 15))));
+      }
+#pragma unroll
+      for (int pl = 0; pl < P; ++pl) {
+        hvec b0, b1;
+        H::deq(wv[c][pl], sc[pl], b0, b1);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acc[pl][t] = H::mma(b0, xa[t][0], acc[pl][t]);
+          acc[pl][t] = H::mma(b1, xa[t][1], acc[pl][t]);
+        }
+      }
+    }
+  }
+
+  // 6. the WK parts summed in order wk = 0, 1, ... through LDS
+  f32x4 out[P][MT];
+  if constexpr (WK > 1) {
+    __syncthreads();  // every wave is done with the activation slice
+    f32x4* red = reinterpret_cast<f32x4*>(bsm);  // [WK][WR][P][MT][64]
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) red[(((wk * WR + wr) * P + pl) * MT + t) * 64 + lane] = acc[pl][t];
+    __syncthreads();
+    if (wk != 0) return;
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        f32x4 a = red[((wr * P + pl) * MT + t) * 64 + lane];
+#pragma unroll
+        for (int k2 = 1; k2 < WK; ++k2) a += red[(((k2 * WR + wr) * P + pl) * MT + t) * 64 + lane];
+        out[pl][t] = a;
+      }
+  } else {
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) out[pl][t] = acc[pl][t];
+  }
+
+  // 7. lane holds D[n = nb + q][m = 16 t + col]
+  const int nb = n0 + 4 * grp;
+  if (nb >= N) return;
+  const bool full = p.vec && nb + 3 < N;
+  if (p.S == 1) {
+    uint16_t* y = static_cast<uint16_t*>(L0.y);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = 16 * t + col;
+      if (m >= p.M) continue;
+      uint16_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v[P];
+#pragma unroll
+        for (int pl = 0; pl < P; ++pl) v[pl] = out[pl][t][q];
+        o[q] = bdec_out<P, F16>(v);
+      }
+      uint16_t* yr = y + (int64_t)m * L0.ldy + nb;
+      if (full) {
+        *reinterpret_cast<uint2*>(yr) = make_uint2(o[0] | (uint32_t)o[1] << 16, o[2] | (uint32_t)o[3] << 16);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (nb + q < N) yr[q] = o[q];
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = 16 * t + col;
+      if (m >= p.M) continue;
+      float* pr = p.part + (((int64_t)s * P + pl) * p.M + m) * p.n_total + L0.n_begin + nb;
+      if (full) {
+        *reinterpret_cast<f32x4*>(pr) = out[pl][t];
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (nb + q < N) pr[q] = out[pl][t][q];
+      }
+    }
+}
+
+// Slice sums of k_bd2 in slice order and the epilogue: one thread per (row m, 4 columns
+// of the partial row); every linear's N is a multiple of 4 (the host checks).
+template <int P, bool F16>
+__global__ __launch_bounds__(128) void k_bd2_reduce(Bd2Params p) {
+  const int q4 = p.n_total / 4;
+  const int i = (int)blockIdx.x * 128 + (int)threadIdx.x;
+  const int m = i / q4;
+  if (m >= p.M) return;
+  const int ncol = 4 * (i - m * q4);
+  int li = 0;
+  if (P == 1) {
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      if (j < p.n_lin && ncol >= p.lin[j].n_begin) li = j;
+  }
+  f32x4 v[kBd2MaxS][P];  // every slice requested before the first is added
+#pragma unroll
+  for (int s = 0; s < kBd2MaxS; ++s)
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl)
+      if (s < p.S) v[s][pl] = *reinterpret_cast<const f32x4*>(p.part + (((int64_t)s * P + pl) * p.M + m) * p.n_total + ncol);
+  f32x4 a[P];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) {
+    a[pl] = v[0][pl];
+#pragma unroll
+    for (int s = 1; s < kBd2MaxS; ++s)
+      if (s < p.S) a[pl] += v[s][pl];
+  }
+  const BdecLin& L = p.lin[li];
+  uint16_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float v[P];
+#pragma unroll
+    for (int pl = 0; pl < P; ++pl) v[pl] = a[pl][q];
+    o[q] = bdec_out<P, F16>(v);
+  }
+  uint16_t* yr = static_cast<uint16_t*>(L.y) + (int64_t)m * L.ldy + (ncol - L.n_begin);
+  if (p.vec) {
+    *reinterpret_cast<uint2*>(yr) = make_uint2(o[0] | (uint32_t)o[1] << 16, o[2] | (uint32_t)o[3] << 16);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) yr[q] = o[q];
+  }
+}
+
+struct Bd2Shape {
+  int WR, WK, S, CS;
+};
+
+// Split.  The K order of every sum -- WK waves per slice and S slices -- depends on (N, K)
+// only; WR (rows per workgroup, which does not change any sum) may follow M.  From
+// same-box timings of the config-2 shapes at M = 16 / 32:
+//  * rows up to 2048 k: one slice, 16-row workgroups of 8 waves along K (q/k/v 4.9 / 6.0 us,
+//    o 4.8 / 6.0 us; a K split with its reduce launch costs 2-3 us more);
+//  * the paired SwiGLU (1536 k): one slice, 4 waves along K; 16-row workgroups at M <= 16,
+//    64-row ones above (their 96 KiB activation slice allows one workgroup per CU, and 140
+//    of them still fit one round): 10.8 / 14.3 us;
+//  * longer rows: 64-row workgroups, slices of at most kBd2MaxCS chunks to about 256
+//    workgroups, 2 or 4 waves along K (1536 x 8960: 10 slices, 9.1 / 11.5 us).
+Bd2Shape bd2_shape(const int64_t* N, int n_lin, int P, int64_t K, int64_t M) {
+  const int C = (int)(K / 64);
+  if (C <= 32) {
+    if (P == 2) return Bd2Shape{M <= 16 ? 1 : 4, 4, 1, C};
+    return Bd2Shape{1, 8, 1, C};
+  }
+  Bd2Shape sh{4, 1, 1, C};
+  int64_t tiles = 0;
+  for (int i = 0; i < (P == 2 ? 1 : n_lin); ++i) tiles += cdiv(N[i], 16 * sh.WR);
+  // slices: enough for about 256 workgroups and for the LDS cap, at most kBd2MaxS; then
+  // equal even lengths
+  int S = (int)std::max<int64_t>(1, 256 / tiles);
+  S = std::max(S, (C + kBd2MaxCS - 1) / kBd2MaxCS);
+  S = std::min(S, kBd2MaxS);
+  int CS = (C + S - 1) / S;
+  CS += CS & 1;
+  sh.S = (C + CS - 1) / CS;
+  sh.CS = CS;
+  const int need = (CS + kBd2MaxPS - 1) / kBd2MaxPS;
+  sh.WK = need <= 1 ? 1 : need <= 2 ? 2 : 4;
+  return sh;
+}
+
+template <int P, int MT, bool F16>
+void bd2_launch_mt(const Bd2Params& p, const Bd2Shape& sh, int64_t tiles, hipStream_t s) {
+  const dim3 grid((unsigned)(tiles * sh.S));
+  const size_t xbytes = (size_t)16 * MT * sh.CS * 8 * 16;
+  const size_t rbytes = (size_t)sh.WK * sh.WR * P * MT * 64 * 16;
+  const size_t lds = std::max(xbytes, rbytes);
+#define QS_BD2(WR_, WK_)                                                                              \
+  if (sh.WR == WR_ && sh.WK == WK_) {                                                                 \
+    hipLaunchKernelGGL((k_bd2<P, MT, WR_, WK_, F16>), grid, dim3(WR_ * WK_ * 64), lds, s, p);         \
+    return;                                                                                           \
+  }
+  QS_BD2(4, 1) QS_BD2(4, 2) QS_BD2(4, 4) QS_BD2(1, 4) QS_BD2(1, 8)
+#undef QS_BD2
+}
+
 template <int P>
-int bdec_launch(BdecParams& p, void* workspace, size_t workspace_bytes, int* counters, int64_t n_counters,
-                hipStream_t s) {
-  int64_t N[4], tiles, cols;
-  for (int i = 0; i < p.n_lin; ++i) N[i] = p.lin[i].N;
-  bdec_shape(N, p.n_lin, P, tiles, cols);
-  int tb = 0, nb = 0;
+int bd2_launch(Bd2Params& p, const Bd2Shape& sh, void* workspace, size_t workspace_bytes, bool f16, hipStream_t s) {
+  int64_t tiles = 0;
+  int nb = 0;
   for (int i = 0; i < (P == 2 ? 1 : p.n_lin); ++i) {
-    p.lin[i].tile_begin = tb;
+    p.lin[i].tile_begin = (int)tiles;
     p.lin[i].n_begin = nb;
-    tb += (int)cdiv(p.lin[i].N, kBdecRows);
+    tiles += cdiv(p.lin[i].N, 16 * sh.WR);
     nb += p.lin[i].N;
   }
-  p.n_total = (int)cols;
-  bdec_split(tiles, p.C, P, p.S, p.CS);
-  if (p.S > kBdecMaxS<P>)
-    return fail(QS_ERR_UNSUPPORTED, "qrow batched: K = %d is longer than %d x %d x 128", p.K, kBdecMaxS<P>,
-                kBdecMaxCS<P>);
+  p.n_total = nb;
+  p.S = sh.S;
+  p.CS = sh.CS;
   if (p.S > 1) {
     const size_t need = (size_t)p.S * P * p.M * p.n_total * sizeof(float);
     if (!workspace || workspace_bytes < need)
       return fail(QS_ERR_INVALID, "qrow batched: workspace smaller than qs_qrow_batched_workspace_bytes()");
-    if (!counters || n_counters < tiles)
-      return fail(QS_ERR_INVALID, "qrow batched: fewer tile counters than qs_qrow_batched_counters()");
+    if (!aligned(workspace, 16)) return fail(QS_ERR_INVALID, "qrow batched: workspace must be 16-byte aligned");
   }
   p.part = static_cast<float*>(workspace);
-  p.counters = counters;
-  const dim3 grid((unsigned)(tiles * p.S)), block(kBdecWaves * 64);
-  const bool mt2 = p.M > 16;
-  if (p.f16) {
-    if (mt2) hipLaunchKernelGGL((k_bdec<P, 2, true>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((k_bdec<P, 1, true>), grid, block, 0, s, p);
+  if (p.M > 16) {
+    if (f16) bd2_launch_mt<P, 2, true>(p, sh, tiles, s);
+    else bd2_launch_mt<P, 2, false>(p, sh, tiles, s);
   } else {
-    if (mt2) hipLaunchKernelGGL((k_bdec<P, 2, false>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((k_bdec<P, 1, false>), grid, block, 0, s, p);
+    if (f16) bd2_launch_mt<P, 1, true>(p, sh, tiles, s);
+    else bd2_launch_mt<P, 1, false>(p, sh, tiles, s);
   }
-  return hip_check(hipGetLastError(), "k_bdec launch");
+  int st = hip_check(hipGetLastError(), "k_bd2 launch");
+  if (st || p.S == 1) return st;
+  const int64_t threads = (int64_t)p.M * (p.n_total / 4);
+  const dim3 rg((unsigned)cdiv(threads, 128));
+  if (f16) hipLaunchKernelGGL((k_bd2_reduce<P, true>), rg, dim3(128), 0, s, p);
+  else hipLaunchKernelGGL((k_bd2_reduce<P, false>), rg, dim3(128), 0, s, p);
+  return hip_check(hipGetLastError(), "k_bd2_reduce launch");
+}
+
+// The batched entry points on k_bd2: limits, the (N, K) split and the store layout.
+template <int P>
+int bd2_run(const BdecParams& b, const int64_t* N, int n_lin, void* workspace, size_t workspace_bytes,
+            hipStream_t s, const Bd2Shape* forced = nullptr) {
+  Bd2Params p{};
+  p.x = b.x;
+  p.ldx = b.ldx;
+  p.M = b.M;
+  p.K = b.K;
+  p.C = b.K / 64;
+  p.n_lin = b.n_lin;
+  for (int i = 0; i < 4; ++i) p.lin[i] = b.lin[i];
+  if ((int64_t)b.M * b.ldx * 2 >= INT_MAX) return fail(QS_ERR_LIMIT, "qrow batched: activations exceed 2^31 bytes");
+  bool vec = true;
+  for (int i = 0; i < (P == 2 ? 1 : n_lin); ++i) {
+    if ((N[i] + 64) * b.K >= INT_MAX) return fail(QS_ERR_LIMIT, "qrow batched: weights exceed 2^31 bytes");
+    vec = vec && N[i] % 4 == 0 && p.lin[i].ldy % 4 == 0 && aligned(p.lin[i].y, 8);
+  }
+  p.vec = vec;
+  const Bd2Shape sh = forced ? *forced : bd2_shape(N, n_lin, P, b.K, b.M);
+  if ((sh.CS + sh.WK - 1) / sh.WK > kBd2MaxPS || sh.S > kBd2MaxS)
+    return fail(QS_ERR_UNSUPPORTED, "qrow batched: K = %d needs more than %d slices of %d chunks", b.K, kBd2MaxS,
+                4 * kBd2MaxPS);
+  if (sh.S > 1) {
+    for (int i = 0; i < (P == 2 ? 1 : n_lin); ++i)
+      if (N[i] % 4) return fail(QS_ERR_UNSUPPORTED, "qrow batched: a K split needs N %% 4 == 0");
+  }
+  return bd2_launch<P>(p, sh, workspace, workspace_bytes, b.f16, s);
 }
 
 }  // namespace
@@ -389,18 +482,17 @@ extern "C" size_t qs_qrow_batched_workspace_bytes(int64_t M, int n_linear, const
                                                   int swiglu) {
   if (!N || n_linear < 1 || n_linear > 4 || M < 1 || K < 128) return 0;
   const int P = swiglu ? 2 : 1;
-  int64_t tiles, cols;
-  bdec_shape(N, n_linear, P, tiles, cols);
-  int S, CS;
-  bdec_split(tiles, (int)(K / 128), P, S, CS);
-  return S > 1 ? (size_t)S * P * M * cols * sizeof(float) : 0;
+  int64_t cols = 0;
+  for (int i = 0; i < (P == 2 ? 1 : n_linear); ++i) cols += N[i];
+  const Bd2Shape sh = bd2_shape(N, n_linear, P, K, std::min<int64_t>(M, 32));
+  return sh.S > 1 ? (size_t)sh.S * P * std::min<int64_t>(M, 32) * cols * sizeof(float) : 0;
 }
 
 extern "C" int64_t qs_qrow_batched_counters(int n_linear, const int64_t* N, int swiglu) {
-  if (!N || n_linear < 1 || n_linear > 4) return 0;
-  int64_t tiles, cols;
-  bdec_shape(N, n_linear, swiglu ? 2 : 1, tiles, cols);
-  return tiles;
+  (void)n_linear;
+  (void)N;
+  (void)swiglu;
+  return 0;  // the kernels need no counters (the argument stays for ABI stability)
 }
 
 extern "C" int qs_qrow_matmul_batched(const void* x, int x_dtype, int64_t ldx, int n_linear,
@@ -421,7 +513,9 @@ extern "C" int qs_qrow_matmul_batched(const void* x, int x_dtype, int64_t ldx, i
     if (!aligned(codes[i], 16)) return fail(QS_ERR_UNSUPPORTED, "qrow batched: weight rows must be 16-byte aligned");
     p.lin[i] = BdecLin{codes[i], scales[i], y[i], ldy[i], (int)N[i], 0, 0};
   }
-  return bdec_launch<1>(p, workspace, workspace_bytes, counters, n_counters, static_cast<hipStream_t>(stream));
+  (void)counters;
+  (void)n_counters;
+  return bd2_run<1>(p, N, n_linear, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int qs_qrow_swiglu_batched(const void* x, int64_t ldx, const int8_t* gate_codes,
@@ -439,5 +533,8 @@ extern "C" int qs_qrow_swiglu_batched(const void* x, int64_t ldx, const int8_t* 
   p.n_lin = 2;
   p.lin[0] = BdecLin{gate_codes, gate_scales, y, ldy, (int)N, 0, 0};
   p.lin[1] = BdecLin{up_codes, up_scales, nullptr, 0, (int)N, 0, 0};
-  return bdec_launch<2>(p, workspace, workspace_bytes, counters, n_counters, static_cast<hipStream_t>(stream));
+  (void)counters;
+  (void)n_counters;
+  const int64_t Ns[1] = {N};
+  return bd2_run<2>(p, Ns, 1, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

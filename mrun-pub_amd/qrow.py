@@ -138,39 +138,22 @@ def _out_buffer(out: torch.Tensor | None, m: int, n: int, dtype: torch.dtype, de
     return out.view(m, n)
 
 
-# The batched kernels (64-row tiles sharing one LDS activation slice, K split in slices of
-# up to 2048) win over the 16-row-tile kernels for long rows with many activation rows:
-# 1536 x 8960 at M = 16 / 32 in same-box A/B timings.  Shorter rows and fewer rows keep the
-# other kernels, which spread small matrices over more CUs.
+# The batched kernels (k_bd2: an LDS activation slice shared by a workgroup's weight rows,
+# weights streamed into VGPRs, K split only for rows longer than 2048) serve every
+# bf16/f16 call with at least 16 activation rows: in same-box A/B timings of the config-2
+# shapes they match or beat the 16-row-tile kernels at M = 16 and beat them at M = 32
+# (1536 x 8960: 25.4 -> 11.5 us, paired SwiGLU 8960 x 1536: 18.5 -> 14.3 us).
 BATCHED_MIN_M = 16
-BATCHED_MIN_K = 4096
+BATCHED_MAX_K = 16384
 
 
 def _batched_eligible(x2: torch.Tensor, codes: list[torch.Tensor], swiglu: bool = False) -> bool:
     m, k = int(x2.shape[0]), int(x2.shape[1])
-    return (not swiglu and x2.dtype in (torch.bfloat16, torch.float16) and m >= BATCHED_MIN_M
-            and k % 128 == 0 and BATCHED_MIN_K <= k <= 16384
-            and x2.data_ptr() % 16 == 0 and all(c.data_ptr() % 16 == 0 for c in codes))
-
-
-_COUNTERS: dict[int, torch.Tensor] = {}
-
-
-def _tile_counters(device: torch.device, n: int) -> torch.Tensor:
-    """Zeroed int32 tile counters for the batched kernels, one array per device: every call
-    leaves them zero, so calls that follow each other share it (also from a captured graph,
-    whose replays run in stream order).  Batched calls that run concurrently on two streams
-    of one device would share it too: serialise them.  An array first needed under graph
-    capture is zero-filled inside the graph and not kept (it lives in the graph's pool)."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    buf = _COUNTERS.get(idx)
-    if buf is not None and buf.numel() >= n:
-        return buf
-    if torch.cuda.is_current_stream_capturing():
-        return torch.zeros(max(n, 1), dtype=torch.int32, device=device)
-    buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=device)
-    _COUNTERS[idx] = buf
-    return buf
+    ns = [int(c.shape[0]) for c in codes]
+    return (x2.dtype in (torch.bfloat16, torch.float16) and (not swiglu or x2.dtype == torch.bfloat16)
+            and m >= BATCHED_MIN_M and k % 128 == 0 and k <= BATCHED_MAX_K
+            and (k <= 2048 or all(n % 4 == 0 for n in ns))
+            and x2.stride(0) == k and x2.data_ptr() % 16 == 0 and all(c.data_ptr() % 16 == 0 for c in codes))
 
 
 def _run_batched(x2: torch.Tensor, pages: list[tuple[torch.Tensor, torch.Tensor]], outs: list[torch.Tensor],
@@ -185,21 +168,18 @@ def _run_batched(x2: torch.Tensor, pages: list[tuple[torch.Tensor, torch.Tensor]
     lib = nat.load()
     ws_bytes = int(lib.qs_qrow_batched_workspace_bytes(min(32, m_all), len(ns), n_arr, k, int(swiglu)))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=device)
-    n_ctr = int(lib.qs_qrow_batched_counters(len(ns), n_arr, int(swiglu)))
-    ctr = _tile_counters(device, n_ctr)
     for m0 in range(0, m_all, 32):
         mm = min(32, m_all - m0)
         xb = x2[m0:m0 + mm]
         if swiglu:
             (gc, gs), (uc, us) = pages
             nat.call("qs_qrow_swiglu_batched", nat.ptr(xb), k, nat.ptr(gc), nat.ptr(gs), nat.ptr(uc), nat.ptr(us),
-                     nat.ptr(outs[0][m0:]), ns[0], mm, ns[0], k, nat.ptr(ws), ws_bytes, nat.ptr(ctr), ctr.numel(),
-                     stream)
+                     nat.ptr(outs[0][m0:]), ns[0], mm, ns[0], k, nat.ptr(ws), ws_bytes, None, 0, stream)
         else:
             nat.call("qs_qrow_matmul_batched", nat.ptr(xb), nat.dtype_code(x2.dtype), k, len(pages),
                      nat.pointer_array([nat.ptr(c) for c, _ in pages]), nat.pointer_array([nat.ptr(sc) for _, sc in pages]),
                      nat.pointer_array([nat.ptr(o[m0:]) for o in outs]), n_arr, n_arr, mm, k, nat.ptr(ws), ws_bytes,
-                     nat.ptr(ctr), ctr.numel(), stream)
+                     None, 0, stream)
 
 
 @torch.inference_mode()

@@ -165,8 +165,12 @@ def test_batched_rows_equal_rows_alone(dev, n, k, swiglu, m):
         assert torch.equal(one[0], full[r]), r
     ref = oq.qrow_swiglu(codes, scales, codes2, scales2, x) if swiglu else oq.qrow_matmul_w8a16(codes, scales, x)
     assert oq.rel_l2(full.float().cpu().numpy(), ref) <= BF16_TOL
-    if not swiglu and m >= q.BATCHED_MIN_M and k >= q.BATCHED_MIN_K:  # the public wrapper's path
+    if not swiglu and q._batched_eligible(xd, [pages[0][0]]):  # the public wrapper's path
         assert torch.equal(q.qrow_matmul(pages[0][0], pages[0][1], xd), full)
+    if swiglu and q._batched_eligible(xd, [p[0] for p in pages], swiglu=True):
+        g = q.CompactQRowPage("g", 0, n, k, *pages[0])
+        u = q.CompactQRowPage("u", 0, n, k, *pages[1])
+        assert torch.equal(q.fused_qrow_swiglu(g, u, xd)[0], full)
 
 
 def test_multi_linear_equals_individual(dev):
