@@ -176,6 +176,20 @@ int qs_w8a8_side_gather(const void* x, int x_dtype, int64_t ldx, const int8_t* q
                         const float* sw, const int64_t* idx, int P, int64_t M, int64_t N,
                         int64_t K, float* xp, float* wp, void* stream);
 
+/* The protect_k front end of w8a8_matmul (w8a8.py:92-121) in two launches: the column
+ * maxima of x, then one kernel in which every workgroup selects the k outlier columns
+ * exactly as qs_outlier_topk does, quantizes its rows as qs_act_quant_i8 does with those
+ * columns' keep factor 0, and writes its share of the side operands exactly as
+ * qs_w8a8_side_gather does.  Bit for bit the outputs of those three entry points.
+ * 1 <= k <= 16, k <= K; K <= 8192 with K % 8 == 0 (f32: K <= 4096, K % 4 == 0); x rows
+ * 16-byte aligned.  colmax_ws: ceil(M / 1024) * K floats of workspace, 16-byte aligned (keep too).  q [M, K] int8,
+ * act_scale [M], xp [M, k], wp [N, k]; idx [k] and keep [K] are optional (null: not
+ * written). */
+int qs_w8a8_protect_quant(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int k,
+                          const int8_t* qw, const float* sw, int64_t N, float* colmax_ws,
+                          int8_t* q, float* act_scale, float* xp, float* wp, int64_t* idx,
+                          float* keep, void* stream);
+
 /* Replaces _int8_gemm / torch._int_mm (w8a8.py:33-64): acc[M,N] = qx[M,K] . qw[N,K]^T,
  * exact int32 accumulation (v_mfma_i32_32x32x32_i8). */
 int qs_gemm_i8i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int64_t M, int64_t N,

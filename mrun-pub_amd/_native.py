@@ -63,6 +63,7 @@ SIGNATURES: dict[str, tuple] = {
     "qs_act_quant_i8": (_I, [_P, _I, _L, _P, _P, _P, _L, _L, _P]),
     "qs_outlier_topk": (_I, [_P, _I, _L, _L, _L, _I, _P, _P, _P, _P]),
     "qs_w8a8_side_gather": (_I, [_P, _I, _L, _P, _P, _P, _I, _L, _L, _L, _P, _P, _P]),
+    "qs_w8a8_protect_quant": (_I, [_P, _I, _L, _L, _L, _I, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P]),
     "qs_gemm_i8i8_i32": (_I, [_P, _P, _P, _L, _L, _L, _P]),
     "qs_w8a8_gemm": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _I, _L, _L, _L, _P]),
     "qs_moe_router": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _P]),

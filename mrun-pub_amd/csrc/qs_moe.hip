@@ -405,17 +405,6 @@ struct Piece8 {
 
 constexpr int kQuantPieces = 8;  // pieces per lane kept in registers
 
-// x / s for a bf16 x, |x| <= 127 s, with r = RN(1 / s): Markstein's corrected quotient
-// (y0 = RN(x r), rem = fma(-y0, s, x), RN(rem r + y0); P. Markstein, IBM J. Res. Dev.
-// 34(1), 1990).  For every bf16 amax with s = amax / 127 >= 2^-120 and every bf16 x with
-// |x| <= amax, clamp(rint(.)) of it equals that of the correctly rounded x / s (checked
-// exhaustively over all 1.07e9 such pairs by tests/quant_division_check.c); 3 VALU
-// operations instead of a full division.
-__device__ __forceinline__ float quot_markstein(float x, float s, float r) {
-  const float y0 = mul_rn(x, r);
-  return __builtin_fmaf(__builtin_fmaf(-y0, s, x), r, y0);
-}
-
 template <int XT>
 __global__ __launch_bounds__(256) void k_moe_gather_quant8(const void* __restrict__ src, int64_t ld_src,
                                                            const int64_t* __restrict__ rows, int64_t A,

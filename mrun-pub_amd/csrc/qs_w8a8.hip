@@ -22,6 +22,8 @@
 // C[8*(r/4) + 4*(l>>5) + (r%4)][l & 31].
 #include "qs_common.h"
 
+#include <type_traits>
+
 namespace qs {
 
 typedef int i32x16 __attribute__((ext_vector_type(16)));
@@ -69,27 +71,41 @@ __global__ __launch_bounds__(256) void k_act_quant(const void* __restrict__ x, i
   }
 }
 
-// WPR waves per row (1, or 4 for short batches) with the row held in registers between
-// the max pass and the quantize pass: lane l of the row's wave wr owns the 16-byte chunks
-// (c * WPR + wr) * 64 + l (each wave instruction reads 1 KiB contiguous); the waves'
-// maxima meet in LDS.  Same arithmetic, element by element, as k_act_quant.
-// Requires K % E == 0, 16-byte aligned rows of x and keep, 8/4-byte aligned rows of q
-// and K <= 64 * WPR * CPL * E.
 template <int XT, int CPL, int WPR>
-__global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x, int64_t ldx,
-                                                     const float* __restrict__ keep,
-                                                     int8_t* __restrict__ q, int64_t ldq,
-                                                     float* __restrict__ scale, int M, int K) {
+struct QuantRow {
+  i32x4 v[CPL];
+};
+
+// The row's chunks of this lane into registers (zero loads for rows >= M).
+template <int XT, int CPL, int WPR>
+__device__ __forceinline__ void act_quant_load(const void* __restrict__ x, int64_t ldx, int row, int M, int K,
+                                               QuantRow<XT, CPL, WPR>& qr) {
+  constexpr int ES = XT == QS_F32 ? 4 : 2;
+  constexpr int E = 16 / ES;
+  const int lane = threadIdx.x & 63, wr = (threadIdx.x >> 6) % WPR;
+  const bool live = row < M;
+  const char* xr = static_cast<const char*>(x) + (int64_t)(live ? row : 0) * ldx * ES;
+  const int nch = K / E;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = (c * WPR + wr) * 64 + lane;
+    if (live && ch < nch) qr.v[c] = *reinterpret_cast<const i32x4*>(xr + (int64_t)ch * 16);
+  }
+}
+
+// Scale and codes of the row from the loaded chunks.  keep4(ch, h) gives the keep factors
+// of elements 4h..4h+3 of chunk ch (has_keep false: no factors).  Every thread of the
+// workgroup reaches the barrier (WPR > 1).
+template <int XT, int CPL, int WPR, class KeepF>
+__device__ __forceinline__ void act_quant_compute(const QuantRow<XT, CPL, WPR>& qrow, bool has_keep, KeepF keep4,
+                                                  int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+                                                  int row, int M, int K) {
   constexpr int ES = XT == QS_F32 ? 4 : 2;
   constexpr int E = 16 / ES;  // elements per 16-byte chunk
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // WPR waves share a row: wave wr of the row takes chunks (c * WPR + wr) * 64 + lane
-  const int row = blockIdx.x * (4 / WPR) + wave / WPR, wr = wave % WPR;
+  const int wr = wave % WPR;
   const bool live = row < M;
-  if (WPR == 1 && !live) return;
-  const char* xr = static_cast<const char*>(x) + (int64_t)(live ? row : 0) * ldx * ES;
   const int nch = K / E;
-  i32x4 v[CPL];
   float amax = 0.f;
   auto widen = [&](const i32x4& c, int e) -> float {
     if constexpr (XT == QS_F32) return __int_as_float(c[e]);
@@ -98,23 +114,20 @@ __global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x,
     if constexpr (XT == QS_BF16) return bf16_bits_to_f32(h);
     return f16_bits_to_f32(static_cast<uint16_t>(h));
   };
-  // keep mask of chunk ch: E floats at keep + ch*E (16-byte aligned), read as float4s
-  auto keep4 = [&](int ch, int h) -> f32x4 { return reinterpret_cast<const f32x4*>(keep + ch * E)[h]; };
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int ch = (c * WPR + wr) * 64 + lane;
     if (live && ch < nch) {
-      v[c] = *reinterpret_cast<const i32x4*>(xr + (int64_t)ch * 16);
-      if (keep) {
+      if (has_keep) {
 #pragma unroll
         for (int h = 0; h < E / 4; ++h) {
           const f32x4 kv = keep4(ch, h);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(mul_rn(widen(v[c], 4 * h + e), kv[e])));
+          for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(mul_rn(widen(qrow.v[c], 4 * h + e), kv[e])));
         }
       } else {
 #pragma unroll
-        for (int e = 0; e < E; ++e) amax = fmaxf(amax, fabsf(widen(v[c], e)));
+        for (int e = 0; e < E; ++e) amax = fmaxf(amax, fabsf(widen(qrow.v[c], e)));
       }
     }
   }
@@ -125,36 +138,64 @@ __global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x,
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < WPR; ++j) amax = fmaxf(amax, wmax[(wave / WPR) * WPR + j]);
-    if (!live) return;
   }
+  if (!live) return;
   float s = amax / 127.0f;  // IEEE division
   if (s == 0.f) s = 1.f;
   if (lane == 0 && wr == 0) scale[row] = s;
   int8_t* qr = q + (int64_t)row * ldq;
+  const float rs = 1.0f / s;  // correctly rounded
+  // row-uniform: bf16 rows with s >= 2^-120 take the corrected quotient (the same codes as
+  // the IEEE division for every bf16 element, x * keep included), others divide
+  const bool fast = XT == QS_BF16 && s >= 0x1p-120f;
+  auto quantize = [&](auto fast_tag) {
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    const int ch = (c * WPR + wr) * 64 + lane;
-    if (ch < nch) {
-      uint32_t packed[E / 4];
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = (c * WPR + wr) * 64 + lane;
+      if (ch < nch) {
+        uint32_t packed[E / 4];
 #pragma unroll
-      for (int j = 0; j < E / 4; ++j) packed[j] = 0;
-      f32x4 kv[E / 4];
+        for (int j = 0; j < E / 4; ++j) packed[j] = 0;
+        f32x4 kv[E / 4];
 #pragma unroll
-      for (int h = 0; h < E / 4; ++h) kv[h] = keep ? keep4(ch, h) : f32x4{1.f, 1.f, 1.f, 1.f};
+        for (int h = 0; h < E / 4; ++h) kv[h] = has_keep ? keep4(ch, h) : f32x4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        float f = widen(v[c], e);
-        if (keep) f = mul_rn(f, kv[e >> 2][e & 3]);
-        float r = rintf(f / s);  // IEEE division, round half to even
-        r = fminf(fmaxf(r, -127.f), 127.f);
-        packed[e >> 2] |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xffu) << (8 * (e & 3));
+        for (int e = 0; e < E; ++e) {
+          float f = widen(qrow.v[c], e);
+          if (has_keep) f = mul_rn(f, kv[e >> 2][e & 3]);
+          float r = rintf(decltype(fast_tag)::value ? quot_markstein(f, s, rs) : f / s);  // half to even
+          r = fminf(fmaxf(r, -127.f), 127.f);
+          packed[e >> 2] |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xffu) << (8 * (e & 3));
+        }
+        if constexpr (E == 8)
+          *reinterpret_cast<uint2*>(qr + (int64_t)ch * 8) = make_uint2(packed[0], packed[1]);
+        else
+          *reinterpret_cast<uint32_t*>(qr + (int64_t)ch * 4) = packed[0];
       }
-      if constexpr (E == 8)
-        *reinterpret_cast<uint2*>(qr + (int64_t)ch * 8) = make_uint2(packed[0], packed[1]);
-      else
-        *reinterpret_cast<uint32_t*>(qr + (int64_t)ch * 4) = packed[0];
     }
-  }
+  };
+  if (fast) quantize(std::true_type{});
+  else quantize(std::false_type{});
+}
+
+// WPR waves per row (1, or 4 for short batches) with the row held in registers between
+// the max pass and the quantize pass: lane l of the row's wave wr owns the 16-byte chunks
+// (c * WPR + wr) * 64 + l (each wave instruction reads 1 KiB contiguous); the waves'
+// maxima meet in LDS.  Same arithmetic, element by element, as k_act_quant.
+// Requires K % E == 0, 16-byte aligned rows of x, 8/4-byte aligned rows of q and
+// K <= 64 * WPR * CPL * E.
+template <int XT, int CPL, int WPR>
+__global__ __launch_bounds__(256) void k_act_quant_w(const void* __restrict__ x, int64_t ldx,
+                                                     const float* __restrict__ keep,
+                                                     int8_t* __restrict__ q, int64_t ldq,
+                                                     float* __restrict__ scale, int M, int K) {
+  constexpr int E = XT == QS_F32 ? 4 : 8;
+  const int row = blockIdx.x * (4 / WPR) + (int)(threadIdx.x >> 6) / WPR;
+  // keep mask of chunk ch: E floats at keep + ch*E (16-byte aligned), read as float4s
+  auto keep4 = [&](int ch, int h) -> f32x4 { return reinterpret_cast<const f32x4*>(keep + ch * E)[h]; };
+  QuantRow<XT, CPL, WPR> qr;
+  act_quant_load<XT, CPL, WPR>(x, ldx, row, M, K, qr);
+  act_quant_compute<XT, CPL, WPR>(qr, keep != nullptr, keep4, q, ldq, scale, row, M, K);
 }
 
 // Column maxima: block (bx, by) covers 256 columns x 64 rows and folds the max over its
@@ -181,17 +222,21 @@ __global__ __launch_bounds__(256) void k_col_absmax(const void* __restrict__ x, 
   atomicMax(reinterpret_cast<unsigned int*>(part) + k, __float_as_uint(r));
 }
 
-// Column maxima in one pass for short batches: workgroup bx covers 64 columns with 16
-// row groups (rows g, g + 16, ...), combined through LDS; writes colmax[k] directly, so
-// no zero fill and no atomics.
+// Column maxima in one pass for short batches: workgroup (bx, by) covers 64 columns of
+// rows [1024 by, 1024 by + 1024) with 16 row groups (rows g, g + 16, ...), combined
+// through LDS; writes colmax[by * K + k] directly, so no zero fill and no atomics (one
+// row of partial maxima per 1024 rows).
 template <int XT>
 __global__ __launch_bounds__(1024) void k_col_absmax_rows(const void* __restrict__ x, int64_t ldx,
                                                           int M, int K, float* __restrict__ colmax) {
   __shared__ float red[16][64];
   const int c = blockIdx.x * 64 + (threadIdx.x & 63), g = threadIdx.x >> 6;
+  const int r0 = (int)blockIdx.y * 1024;
+  M = min(M, r0 + 1024);
+  colmax += (int64_t)blockIdx.y * K;
   float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (c < K) {
-    int m = g;
+    int m = r0 + g;
     for (; m + 7 * 16 < M; m += 8 * 16) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) a[j] = fmaxf(a[j], fabsf(load_x<XT>(x, (int64_t)(m + 16 * j) * ldx + c)));
@@ -207,6 +252,60 @@ __global__ __launch_bounds__(1024) void k_col_absmax_rows(const void* __restrict
 #pragma unroll
     for (int j = 1; j < 16; ++j) r = fmaxf(r, red[j][threadIdx.x]);
     colmax[c] = r;
+  }
+}
+
+// k_col_absmax_rows with 16-byte loads (rows 16-byte aligned): lane l of wave w holds
+// the E columns 64 bx + E (l % CG) of rows w RPI + l / CG + 16 RPI i, four rows' loads in
+// flight at a time; lanes of one column group meet by shuffles, the 16 waves through LDS.
+template <int XT>
+__global__ __launch_bounds__(1024) void k_col_absmax_v(const void* __restrict__ x, int64_t ldx, int M, int K,
+                                                       float* __restrict__ colmax) {
+  constexpr int ES = XT == QS_F32 ? 4 : 2, E = 16 / ES, CG = 64 / E, RPI = 64 / CG;
+  __shared__ float red[16][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int cg = lane % CG, ro = lane / CG;
+  const int c0 = (int)blockIdx.x * 64 + cg * E;
+  const int r0 = (int)blockIdx.y * 1024, r1 = min(M, r0 + 1024);
+  auto widen = [&](const i32x4& c, int e) -> float {
+    if constexpr (XT == QS_F32) return __int_as_float(c[e]);
+    const uint32_t d = static_cast<uint32_t>(c[e >> 1]);
+    const uint32_t h = (e & 1) ? (d >> 16) : (d & 0xffffu);
+    if constexpr (XT == QS_BF16) return bf16_bits_to_f32(h);
+    return f16_bits_to_f32(static_cast<uint16_t>(h));
+  };
+  float a[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) a[e] = 0.f;
+  if (c0 < K) {  // K % E == 0: a lane's E columns are all in range or all out
+    const char* xb = static_cast<const char*>(x) + (int64_t)c0 * ES;
+    for (int m = r0 + w * RPI + ro; m < r1; m += 4 * 16 * RPI) {
+      i32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int mu = m + u * 16 * RPI;
+        v[u] = mu < r1 ? *reinterpret_cast<const i32x4*>(xb + (int64_t)mu * ldx * ES) : i32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < E; ++e) a[e] = fmaxf(a[e], fabsf(widen(v[u], e)));
+    }
+  }
+#pragma unroll
+  for (int off = CG; off < 64; off <<= 1)
+#pragma unroll
+    for (int e = 0; e < E; ++e) a[e] = fmaxf(a[e], __shfl_xor(a[e], off));
+  if (ro == 0)
+#pragma unroll
+    for (int e = 0; e < E; ++e) red[w][cg * E + e] = a[e];
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int c = (int)blockIdx.x * 64 + (int)threadIdx.x;
+    float r = red[0][threadIdx.x];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) r = fmaxf(r, red[j][threadIdx.x]);
+    if (c < K) colmax[(int64_t)blockIdx.y * K + c] = r;
   }
 }
 
@@ -610,6 +709,173 @@ __global__ __launch_bounds__(1024) void k_topk_radix(const float* __restrict__ v
     const int col = (int)(~(unsigned)my);
     idx[rank] = col;
     keep[col] = 0.f;
+  }
+}
+
+// The protect_k front end of w8a8_matmul in one launch after the column maxima.  Every
+// workgroup takes the kk largest column maxima (the keys and order of k_topk_small:
+// value bits above ~column, kk rounds of a block-wide maximum over the maxima staged in
+// LDS), quantizes its activation rows with those columns' keep factor 0 (act_quant_*,
+// the factors read from an LDS bitmap), gathers its rows' side activations
+// xp[m, p] = x[m, idx[p]] and a 1 / gridDim.x slice of the side weights
+// wp[n, p] = float(qw[n, idx[p]]) * sw[n]; workgroup 0 also stores idx, keep and the
+// column maxima when asked.  Needs K <= kProtectMaxK (the maxima sit in LDS).
+constexpr int kProtectMaxK = 8192;
+constexpr int kProtectMaxP = 16;
+
+struct ProtectParams {
+  const void* x;
+  int64_t ldx;
+  int M, K, N;
+  const float* colpart;  // [R][K] partial column maxima
+  int R;
+  int kk;  // protected columns
+  const int8_t* qw;
+  const float* sw;
+  int8_t* q;
+  float* scale;
+  float* xp;  // [M][kk]
+  float* wp;  // [N][kk]
+  int64_t* idx;  // optional outputs (workgroup 0)
+  float* keep;
+  float* colmax;
+};
+
+template <int XT, int CPL, int WPR>
+__global__ __launch_bounds__(256) void k_protect_quant(ProtectParams p) {
+  constexpr int VM = kProtectMaxK / 256;  // keys per thread at most
+  __shared__ uint32_t selbits[kProtectMaxK / 32];
+  __shared__ unsigned long long gmax[16];
+  __shared__ unsigned long long cand[256];
+  __shared__ unsigned long long wbest[2][4];
+  __shared__ int sel[kProtectMaxP];
+  __shared__ int ncand;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = p.K;
+  // 0. this workgroup's activation rows into registers first: their HBM reads overlap the
+  //    column maxima's reads and the selection
+  const int row0 = (int)blockIdx.x * (4 / WPR);
+  const int row = row0 + wave / WPR;
+  QuantRow<XT, CPL, WPR> qrow;
+  act_quant_load<XT, CPL, WPR>(p.x, p.ldx, row, p.M, K, qrow);
+  if (tid == 0) ncand = 0;
+  for (int w = tid; w < (K + 31) / 32; w += 256) selbits[w] = 0u;
+  // 1. keys of the column maxima (over the R partial rows): thread tid holds columns
+  //    4 tid + 1024 j + e, read as 16-byte vectors (all of a partial row's loads in flight
+  //    at once); value bits above ~column, so larger values first, lower column on ties,
+  //    and every real key > 0
+  f32x4 cv[VM / 4];
+#pragma unroll
+  for (int j = 0; j < VM / 4; ++j) {
+    const int k0 = 4 * tid + 1024 * j;
+    cv[j] = k0 < K ? *reinterpret_cast<const f32x4*>(p.colpart + k0) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int r = 1; r < p.R; ++r) {
+    f32x4 w[VM / 4];
+#pragma unroll
+    for (int j = 0; j < VM / 4; ++j) {
+      const int k0 = 4 * tid + 1024 * j;
+      w[j] = k0 < K ? *reinterpret_cast<const f32x4*>(p.colpart + (int64_t)r * K + k0) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < VM / 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cv[j][e] = fmaxf(cv[j][e], w[j][e]);
+  }
+  unsigned long long key[VM];
+  unsigned long long mine = 0ull;
+#pragma unroll
+  for (int j = 0; j < VM / 4; ++j) {
+    const int k0 = 4 * tid + 1024 * j;
+    if (k0 < K && p.colmax && blockIdx.x == 0) *reinterpret_cast<f32x4*>(p.colmax + k0) = cv[j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = k0 + e;
+      key[4 * j + e] = k < K ? ((unsigned long long)__float_as_uint(cv[j][e]) << 32) | (unsigned)(~(unsigned)k) : 0ull;
+      mine = key[4 * j + e] > mine ? key[4 * j + e] : mine;
+    }
+  }
+  // 2. the 16 maxima of 16-lane groups are 16 distinct keys (or 0 where a group holds no
+  //    column), so each of the kk <= 16 largest keys is >= the smallest of them, T.  The
+  //    keys >= T (a few dozen for ordinary data) go to LDS, and each candidate's rank (the
+  //    candidates above it) places it: rank < kk is selected, at position rank.
+  unsigned long long g = dpp_max_u64<0x111, 0xf>(mine);
+  g = dpp_max_u64<0x112, 0xf>(g);
+  g = dpp_max_u64<0x114, 0xf>(g);
+  g = dpp_max_u64<0x118, 0xf>(g);
+  if ((lane & 15) == 15) gmax[wave * 4 + (lane >> 4)] = g;
+  __syncthreads();
+  unsigned long long T = gmax[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) T = gmax[w] < T ? gmax[w] : T;
+#pragma unroll
+  for (int j = 0; j < VM; ++j)
+    if (key[j] != 0ull && key[j] >= T) {  // rare: one LDS atomic per candidate
+      const int pos = atomicAdd(&ncand, 1);
+      if (pos < 256) cand[pos] = key[j];
+    }
+  __syncthreads();
+  const int n = ncand;  // uniform
+  if (n <= 256) {
+    if (tid < n) {  // each candidate's rank counts the larger ones
+      const unsigned long long my = cand[tid];
+      int rank = 0;
+#pragma unroll 8
+      for (int j = 0; j < n; ++j) rank += cand[j] > my;
+      if (rank < p.kk) {
+        const int col = (int)(~(unsigned)(my & 0xffffffffull));
+        sel[rank] = col;
+        atomicOr(&selbits[col >> 5], 1u << (col & 31));
+      }
+    }
+  } else {
+    // many ties across columns: kk rounds of a block-wide maximum over the keys
+    for (int r = 0; r < p.kk; ++r) {
+      unsigned long long best = 0ull;
+#pragma unroll
+      for (int j = 0; j < VM; ++j) best = key[j] > best ? key[j] : best;
+      best = wave_max_u64(best);
+      if (lane == 0) wbest[r & 1][wave] = best;
+      __syncthreads();
+      unsigned long long b = wbest[r & 1][0];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) b = wbest[r & 1][w] > b ? wbest[r & 1][w] : b;
+#pragma unroll
+      for (int j = 0; j < VM; ++j)
+        if (key[j] == b) key[j] = 0ull;
+      if (tid == 0) {
+        const int col = (int)(~(unsigned)(b & 0xffffffffull));
+        sel[r] = col;
+        selbits[col >> 5] |= 1u << (col & 31);
+      }
+    }
+  }
+  __syncthreads();
+  // 3. the workgroup's rows, quantized with keep factor 0 at the selected columns
+  constexpr int E = XT == QS_F32 ? 4 : 8;
+  auto keep4 = [&](int ch, int h) -> f32x4 {
+    const int c0 = ch * E + 4 * h;  // a multiple of 4: the 4 bits share a word
+    const uint32_t w = selbits[c0 >> 5] >> (c0 & 31);
+    return f32x4{(w & 1u) ? 0.f : 1.f, (w & 2u) ? 0.f : 1.f, (w & 4u) ? 0.f : 1.f, (w & 8u) ? 0.f : 1.f};
+  };
+  act_quant_compute<XT, CPL, WPR>(qrow, true, keep4, p.q, K, p.scale, row, p.M, K);
+  // 4. side activations of the workgroup's rows
+  if (tid < (4 / WPR) * p.kk) {
+    const int row = row0 + tid / p.kk, pp = tid % p.kk;
+    if (row < p.M) p.xp[(int64_t)row * p.kk + pp] = load_x<XT>(p.x, (int64_t)row * p.ldx + sel[pp]);
+  }
+  // 5. a slice of the side weights
+  const int nper = (p.N + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int nb = (int)blockIdx.x * nper;
+  for (int i = tid; i < nper * p.kk; i += 256) {
+    const int n = nb + i / p.kk, pp = i % p.kk;
+    if (n < p.N) p.wp[(int64_t)n * p.kk + pp] = static_cast<float>(p.qw[(int64_t)n * K + sel[pp]]) * p.sw[n];
+  }
+  // 6. the selection itself, when asked
+  if (blockIdx.x == 0) {
+    if (p.idx && tid < p.kk) p.idx[tid] = sel[tid];
+    if (p.keep)
+      for (int k = tid; k < K; k += 256) p.keep[k] = ((selbits[k >> 5] >> (k & 31)) & 1u) ? 0.f : 1.f;
   }
 }
 
@@ -1417,6 +1683,77 @@ extern "C" int qs_w8a8_side_gather(const void* x, int x_dtype, int64_t ldx, cons
   else
     return fail(QS_ERR_INVALID, "side_gather: dtype must be F32, BF16 or F16");
   return hip_check(hipGetLastError(), "k_gather_side launch");
+}
+
+extern "C" int qs_w8a8_protect_quant(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int k,
+                                     const int8_t* qw, const float* sw, int64_t N, float* colmax_ws,
+                                     int8_t* q, float* act_scale, float* xp, float* wp, int64_t* idx,
+                                     float* keep, void* stream) {
+  if (!x || !qw || !sw || !colmax_ws || !q || !act_scale || !xp || !wp)
+    return fail(QS_ERR_INVALID, "protect_quant: null pointer");
+  if (!aligned(colmax_ws, 16) || (keep && !aligned(keep, 16)))
+    return fail(QS_ERR_INVALID, "protect_quant: colmax_ws and keep must be 16-byte aligned");
+  if (M < 1 || N < 1 || K < 1 || ldx < K) return fail(QS_ERR_INVALID, "protect_quant: bad shape");
+  if (k < 1 || k > kProtectMaxP || k > K) return fail(QS_ERR_LIMIT, "protect_quant: k must be in 1..min(%d, K)", kProtectMaxP);
+  if (M > (1 << 30) || N > (1 << 30)) return fail(QS_ERR_LIMIT, "protect_quant: dimension exceeds 2^30");
+  if (x_dtype != QS_F32 && x_dtype != QS_BF16 && x_dtype != QS_F16)
+    return fail(QS_ERR_INVALID, "protect_quant: dtype must be F32, BF16 or F16");
+  const int es = x_dtype == QS_F32 ? 4 : 2;
+  const int E = 16 / es;
+  if (K > kProtectMaxK || K % E || K / E > 64 * kQuantCpl || !aligned(x, 16) || (ldx * es) % 16 ||
+      !aligned(q, E == 8 ? 8 : 4))
+    return fail(QS_ERR_UNSUPPORTED, "protect_quant: needs K <= %d, K %% %d == 0 and 16-byte aligned rows",
+                kProtectMaxK, E);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int R = (int)cdiv(M, 1024);
+  if (R > 65535) return fail(QS_ERR_LIMIT, "protect_quant: too many rows");
+  const dim3 cgrid((unsigned)cdiv(K, 64), (unsigned)R);
+  if (x_dtype == QS_F32)
+    hipLaunchKernelGGL(k_col_absmax_v<QS_F32>, cgrid, dim3(1024), 0, s, x, ldx, (int)M, (int)K, colmax_ws);
+  else if (x_dtype == QS_BF16)
+    hipLaunchKernelGGL(k_col_absmax_v<QS_BF16>, cgrid, dim3(1024), 0, s, x, ldx, (int)M, (int)K, colmax_ws);
+  else
+    hipLaunchKernelGGL(k_col_absmax_v<QS_F16>, cgrid, dim3(1024), 0, s, x, ldx, (int)M, (int)K, colmax_ws);
+  int st = hip_check(hipGetLastError(), "k_col_absmax_v launch");
+  if (st) return st;
+  ProtectParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.M = (int)M;
+  p.K = (int)K;
+  p.N = (int)N;
+  p.colpart = colmax_ws;
+  p.R = R;
+  p.kk = k;
+  p.qw = qw;
+  p.sw = sw;
+  p.q = q;
+  p.scale = act_scale;
+  p.xp = xp;
+  p.wp = wp;
+  p.idx = idx;
+  p.keep = keep;
+  const size_t lds = 0;
+  // 4 waves per row up to 1024 rows, else 4 rows per workgroup: the selection is repeated
+  // per workgroup, and the grid stays within one resident round
+  if (M <= 1024 && K / E <= 4 * 64 * (kQuantCpl / 4)) {
+    const dim3 grid((unsigned)M);
+    if (x_dtype == QS_F32)
+      hipLaunchKernelGGL((k_protect_quant<QS_F32, kQuantCpl / 4, 4>), grid, dim3(256), lds, s, p);
+    else if (x_dtype == QS_BF16)
+      hipLaunchKernelGGL((k_protect_quant<QS_BF16, kQuantCpl / 4, 4>), grid, dim3(256), lds, s, p);
+    else
+      hipLaunchKernelGGL((k_protect_quant<QS_F16, kQuantCpl / 4, 4>), grid, dim3(256), lds, s, p);
+  } else {
+    const dim3 grid((unsigned)cdiv(M, 4));
+    if (x_dtype == QS_F32)
+      hipLaunchKernelGGL((k_protect_quant<QS_F32, kQuantCpl, 1>), grid, dim3(256), lds, s, p);
+    else if (x_dtype == QS_BF16)
+      hipLaunchKernelGGL((k_protect_quant<QS_BF16, kQuantCpl, 1>), grid, dim3(256), lds, s, p);
+    else
+      hipLaunchKernelGGL((k_protect_quant<QS_F16, kQuantCpl, 1>), grid, dim3(256), lds, s, p);
+  }
+  return hip_check(hipGetLastError(), "k_protect_quant launch");
 }
 
 extern "C" int qs_gemm_i8i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int64_t M,

@@ -86,6 +86,14 @@ def quantize_activation(
     return q, s
 
 
+def _fused_front_end_ok(x2: torch.Tensor, protect_k: int, inn: int) -> bool:
+    """qs_w8a8_protect_quant's limits: at most 16 protected columns, K a multiple of the
+    16-byte element count and at most 8192 (4096 for fp32), 16-byte aligned rows."""
+    e = 4 if x2.dtype == torch.float32 else 8
+    return (min(int(protect_k), inn) <= 16 and inn % e == 0 and inn <= 64 * 16 * e and inn <= 8192
+            and x2.data_ptr() % 16 == 0)
+
+
 @torch.inference_mode()
 def w8a8_matmul(
     q_w: torch.Tensor,
@@ -121,6 +129,19 @@ def w8a8_matmul(
 
     keep = None
     idx = None
+    if protect_idx is None and protect_k > 0 and _fused_front_end_ok(x2, protect_k, inn):
+        # column maxima, then selection + quantization + side operands in one launch
+        k = min(int(protect_k), inn)
+        colws = torch.empty(((T + 1023) // 1024) * inn, dtype=torch.float32, device=device)
+        q_x = torch.empty((T, inn), dtype=torch.int8, device=device)
+        act_scale = torch.empty(T, dtype=torch.float32, device=device)
+        xp = torch.empty((T, k), dtype=torch.float32, device=device)
+        wp = torch.empty((out, k), dtype=torch.float32, device=device)
+        nat.call("qs_w8a8_protect_quant", nat.ptr(x2), xdt, inn, T, inn, k, nat.ptr(q_w), nat.ptr(sc_w), out,
+                 nat.ptr(colws), nat.ptr(q_x), nat.ptr(act_scale), nat.ptr(xp), nat.ptr(wp), None, None, stream)
+        nat.call("qs_w8a8_gemm", nat.ptr(q_x), nat.ptr(act_scale), nat.ptr(q_w), nat.ptr(sc_w), nat.ptr(xp),
+                 nat.ptr(wp), k, nat.ptr(y), nat.dtype_code(out_dtype), T, out, inn, stream)
+        return y.reshape(*x.shape[:-1], out)
     if protect_idx is None and protect_k > 0:
         k = min(int(protect_k), inn)
         colmax = torch.empty(inn, dtype=torch.float32, device=device)

@@ -192,6 +192,60 @@ def test_gemm_dma_epilogue_operands_match_staged(dev, t, n, p, ydt):
     assert torch.allclose(outs[0][rows].float(), ref.to(dt).float(), rtol=1e-2 if ydt == "bf16" else 1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("t,k,kk,ties", [(1, 512, 1, False), (37, 4096, 8, False), (512, 4096, 8, False),
+                                         (1500, 2048, 16, False), (64, 1024, 4, False), (9, 4096, 8, True),
+                                         (3, 768, 16, True)])
+def test_protect_quant_equals_separate_kernels(dev, dtype, t, k, kk, ties):
+    """qs_w8a8_protect_quant (column maxima, then selection + quantization + side operands in
+    one launch) equals qs_outlier_topk + qs_act_quant_i8 + qs_w8a8_side_gather bit for bit,
+    with an exact tie between two outlier columns, more than 1024 rows, and columns that all
+    tie (the selection's many-candidates path)."""
+    from mrun_pub_amd import _native as nat
+
+    n = 300
+    g = torch.Generator(device=dev)
+    g.manual_seed(t + k + kk)
+    x = torch.randn(t, k, device=dev, generator=g)
+    x[:, torch.randint(0, k, (3,), generator=g, device=dev)] *= 20.0
+    x[:, 7] = 50.0
+    x[:, 9] = 50.0
+    if ties:
+        x = torch.where(torch.arange(t, device=dev)[:, None] % 2 == 0, 1.0, -0.5).expand(t, k).clone()
+    x = x.to(dtype).contiguous()
+    qw = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=g)
+    sw = (torch.rand(n, device=dev, generator=g) + 0.5) / 127
+    code, st = nat.dtype_code(dtype), nat.stream_of(dev)
+    colmax = torch.empty(k, device=dev)
+    idx = torch.empty(kk, dtype=torch.int64, device=dev)
+    keep = torch.empty(k, device=dev)
+    nat.call("qs_outlier_topk", nat.ptr(x), code, k, t, k, kk, nat.ptr(colmax), nat.ptr(idx), nat.ptr(keep), st)
+    q1, s1 = _w().quantize_activation(x, keep)
+    xp1 = torch.empty((t, kk), device=dev)
+    wp1 = torch.empty((n, kk), device=dev)
+    nat.call("qs_w8a8_side_gather", nat.ptr(x), code, k, nat.ptr(qw), nat.ptr(sw), nat.ptr(idx), kk, t, n, k,
+             nat.ptr(xp1), nat.ptr(wp1), st)
+    colws = torch.empty(((t + 1023) // 1024) * k, device=dev)
+    q2 = torch.empty((t, k), dtype=torch.int8, device=dev)
+    s2 = torch.empty(t, device=dev)
+    xp2 = torch.empty((t, kk), device=dev)
+    wp2 = torch.empty((n, kk), device=dev)
+    idx2 = torch.empty(kk, dtype=torch.int64, device=dev)
+    keep2 = torch.empty(k, device=dev)
+    nat.call("qs_w8a8_protect_quant", nat.ptr(x), code, k, t, k, kk, nat.ptr(qw), nat.ptr(sw), n, nat.ptr(colws),
+             nat.ptr(q2), nat.ptr(s2), nat.ptr(xp2), nat.ptr(wp2), nat.ptr(idx2), nat.ptr(keep2), st)
+    torch.cuda.synchronize()
+    assert torch.equal(idx2, idx) and torch.equal(keep2, keep)
+    assert torch.equal(q2, q1) and torch.equal(s2.view(torch.int32), s1.view(torch.int32))
+    assert torch.equal(xp2.view(torch.int32), xp1.view(torch.int32))
+    assert torch.equal(wp2.view(torch.int32), wp1.view(torch.int32))
+    # the product entry point on the fused front end equals the path with the same columns given
+    if dtype != torch.float16:
+        y1 = _w().w8a8_matmul(qw, sw, x, protect_k=kk)
+        y2 = _w().w8a8_matmul(qw, sw, x, protect_idx=idx)
+        assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+
+
 @pytest.mark.parametrize("protect_k", [4, 8, 16, 24])
 def test_w8a8_outlier_protection(dev, protect_k):
     rng, q_w, sc_w = _weights(640, 4096, protect_k)
