@@ -377,7 +377,20 @@ def profile_mfma_kernels(torch, dev, which: str, calls: int) -> dict:
     gen = torch.Generator(device=dev)
     gen.manual_seed(3)
     out: dict = {"profile": which, "calls": calls}
-    if which == "w8a8":
+    if which == "w8a8p":
+        # the whole protect_k=8 call: column maxima, selection + quantization + side operands,
+        # GEMM with the side path (0.1% outlier channels x20, as config 3)
+        N, K = 14336, 4096
+        qw = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen)
+        sw = (torch.rand(N, device=dev, generator=gen) + 0.5) / 127
+        for M in (512, 2048):
+            x = torch.randn(M, K, device=dev, generator=gen)
+            x[:, torch.randint(0, K, (4,), device=dev, generator=gen)] *= 20.0
+            xb = x.to(torch.bfloat16)
+            for _ in range(calls):
+                w8a8.w8a8_matmul(qw, sw, xb, protect_k=8, out_dtype=torch.bfloat16)
+            out[f"m{M}_ops_per_call"] = 2 * M * N * K
+    elif which == "w8a8":
         N, K = 14336, 4096
         qw = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen)
         sw = (torch.rand(N, device=dev, generator=gen) + 0.5) / 127
@@ -561,11 +574,12 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-secondary", action="store_true", help="skip configs 1/3/4/5")
-    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "moe"),
+    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "w8a8p", "moe"),
                     help="for rocprofv3 runs: replay exactly the timed graph of the roofline kernel (28 "
                     "paired gate/up+SwiGLU launches) or of the headline pass, --steps times after "
                     "--warmup replays; a plain 256 MiB device copy x5 (counter calibration); or config 3's "
-                    "fused W8A8 GEMM (M=512 and 2048) / config 4's MoE layer (T=64 and 512), --steps calls each")
+                    "fused W8A8 GEMM (M=512 and 2048), config 3's whole w8a8_matmul with protect_k=8 (w8a8p) / "
+                    "config 4's MoE layer (T=64 and 512), --steps calls each")
     ap.add_argument("--eager", action="store_true",
                     help="with --profile swiglu/stack: launch the same sequence eagerly instead of replaying "
                     "the graph (counter collection needs eager dispatches)")
@@ -597,7 +611,7 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"profile": "copy", "launches": 5, "read_bytes": n, "write_bytes": n}), flush=True)
         return 0
-    if args.profile in ("w8a8", "moe"):
+    if args.profile in ("w8a8", "w8a8p", "moe"):
         print(json.dumps(profile_mfma_kernels(torch, dev, args.profile, args.steps)), flush=True)
         return 0
     arena, pages = build_stack(torch, dev)
