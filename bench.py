@@ -207,9 +207,10 @@ def cpu_baselines_per_config(seconds: float = 2.0) -> dict:
     return out
 
 
-def _graph_time(torch, stream, fn, calls: int, reps: int = 20) -> float:
+def _graph_time(torch, stream, fn, calls: int, reps: int = 50, warmup: int = 10) -> float:
     """Median seconds per call of ``fn`` (one launch sequence), captured ``calls`` times in
-    a graph; each replay is timed with its own pair of HIP events on ``stream``."""
+    a graph; each of ``reps`` replays after ``warmup`` untimed ones is timed with its own
+    pair of HIP events on ``stream`` (the median of >= 50 runs after 10 warm-ups)."""
     with torch.cuda.stream(stream):
         fn(0)
         torch.cuda.synchronize()
@@ -217,7 +218,7 @@ def _graph_time(torch, stream, fn, calls: int, reps: int = 20) -> float:
         with torch.cuda.graph(g, stream=stream):
             for i in range(calls):
                 fn(i)
-        per = _replay_times(torch, stream, g, reps, warmup=2)
+        per = _replay_times(torch, stream, g, reps, warmup=warmup)
     return _median(per) / calls
 
 
@@ -731,7 +732,7 @@ def main() -> int:
             if mm == m:
                 continue
             cm = DecodeChain(torch, dev, pages, mm, gen)
-            tp = _graph_time(torch, stream, lambda _i, c=cm: c.per_linear(), 1, reps=20)
+            tp = _graph_time(torch, stream, lambda _i, c=cm: c.per_linear(), 1)
             batches[f"config2_stack_m{mm}"] = {
                 "ms_per_pass": round(tp * 1e3, 4),
                 "GB/s": round(algorithmic_bytes_per_pass(mm) / tp / 1e9, 1),

@@ -397,12 +397,23 @@ __global__ __launch_bounds__(256) void k_lowbit_slot(LowbitParams p, int gps, fl
 //  * Per group and row tile, lane l takes quarter q = l >> 4 (G/4 codes) of weight row
 //    n = l & 15 and the same k range of activation row m = l & 15:
 //    v_mfma_f32_16x16x32_bf16 with A = x and B = (OFF + code) pairs, G/32 MFMAs from zero,
-//    so D[m][n] = R = sum_k x (OFF + c), and
+//    so D[m][n] = R = sum_k x (OFF + c), and (int2: OFF = 0, the pairs from FP4
+//    conversions of the code bytes and the activations in the matching order)
 //      y[m][n] += scale * (R - (OFF + zero) * S0[m, g]),
 //    S0 the group's activation sum: a second MFMA of the same A with an all-ones B, which
 //    lands in the D layout (m = 4 (l >> 4) + r) and serves every row tile.
 // Rows m >= M read as 0 and issue no activation loads.
 // ----------------------------------------------------------------------------------
+// int2 B operands come from FP4 conversions (as in k_lowbit_valu): a code byte gives the
+// bf16 pairs (c0, c2) and (c1, c3).  An MFMA takes two bytes' pairs as
+// (c0, c2, c1, c3, c4, c6, c5, c7), so the activations of those 8 k are arranged the same
+// way: (x0,x1),(x2,x3),(x4,x5),(x6,x7) -> (x0,x2),(x1,x3),(x4,x6),(x5,x7).
+__device__ __forceinline__ i32x4 fp4_pair_order(i32x4 v) {
+  const uint32_t a = (uint32_t)v[0], b = (uint32_t)v[1], c = (uint32_t)v[2], d = (uint32_t)v[3];
+  return i32x4{(int)__builtin_amdgcn_perm(b, a, 0x05040100u), (int)__builtin_amdgcn_perm(b, a, 0x07060302u),
+               (int)__builtin_amdgcn_perm(d, c, 0x05040100u), (int)__builtin_amdgcn_perm(d, c, 0x07060302u)};
+}
+
 constexpr int kGkMaxWaves = 16;
 template <int G>
 constexpr int kGkGroupsShort = G == 64 ? 8 : 4;  // two row tiles, every activation in VGPRs
@@ -429,7 +440,7 @@ struct GkLds {
 template <int BITS, int G, int SM, int ZM, int NGR, int RT>
 __global__ __launch_bounds__(kGkMaxWaves * 64) void k_lowbit_gk(LowbitParams p) {
   using L = GkLds<BITS, G, SM, ZM, NGR, RT>;
-  constexpr float OFF = BITS == 3 ? 8.f : 4.f;
+  constexpr float OFF = BITS == 3 ? 8.f : 0.f;
   constexpr int CB = L::CB;
   constexpr int QB = CB / 4;        // code bytes of a lane quarter
   constexpr int QC = G / 4;         // codes of a lane quarter
@@ -489,7 +500,7 @@ __global__ __launch_bounds__(kGkMaxWaves * 64) void k_lowbit_gk(LowbitParams p) 
     for (int j = 0; j < NJ; ++j) {
       i32x4 v = {0, 0, 0, 0};
       if (mval) v = *reinterpret_cast<const i32x4*>(xr + (int64_t)g * G + 8 * j);
-      xv[b][j] = v;
+      xv[b][j] = BITS == 2 ? fp4_pair_order(v) : v;
     }
   };
 #pragma unroll
@@ -551,13 +562,36 @@ __global__ __launch_bounds__(kGkMaxWaves * 64) void k_lowbit_gk(LowbitParams p) 
       uint32_t cf[3];
       field(rt, i, cf);
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (BITS == 2) {
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        u32x4 bw;
+        for (int wd = 0; wd < NJ / 2; ++wd) {  // one code word = 16 codes = two MFMAs
+          const uint32_t lo = cf[wd] & 0x33333333u, hi = (cf[wd] >> 2) & 0x33333333u;
+          const bf16x2 pl[4] = {__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(lo, 2.f, 0),
+                                __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(lo, 2.f, 1),
+                                __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(lo, 2.f, 2),
+                                __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(lo, 2.f, 3)};
+          const bf16x2 ph[4] = {__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(hi, 2.f, 0),
+                                __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(hi, 2.f, 1),
+                                __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(hi, 2.f, 2),
+                                __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(hi, 2.f, 3)};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bw[e] = code_pair<BITS>(cf, BITS * (8 * j + 2 * e), p.pair_mask, p.pair_base);
-        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[b][j]),
-                                                    __builtin_bit_cast(bf16x8, bw), d, 0, 0, 0);
+          for (int h = 0; h < 2; ++h) {
+            const u32x4 bw = {__builtin_bit_cast(uint32_t, pl[2 * h]), __builtin_bit_cast(uint32_t, ph[2 * h]),
+                              __builtin_bit_cast(uint32_t, pl[2 * h + 1]), __builtin_bit_cast(uint32_t, ph[2 * h + 1])};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[b][2 * wd + h]),
+                                                        __builtin_bit_cast(bf16x8, bw), d, 0, 0, 0);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          u32x4 bw;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bw[e] = code_pair<BITS>(cf, BITS * (8 * j + 2 * e), p.pair_mask, p.pair_base);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[b][j]),
+                                                      __builtin_bit_cast(bf16x8, bw), d, 0, 0, 0);
+        }
       }
       float sc, cz;
       scale_zero(rt, i, sc, cz);
