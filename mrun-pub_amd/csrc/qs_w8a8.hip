@@ -1456,10 +1456,17 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
   // keeps its partial LDS waits.
   if constexpr (PRE) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt unconstrained
   frag(fa, 0, 0);
-  auto step = [&](int kt, bool chk) {
+  // last: kt may be the final step (no next tile).  The main loop's steps never are, so
+  // their body has no branch: the compiler cannot see the LDS wait inside the barrier
+  // asm, and at a join with a path that skips it, it would wait for the next tile's
+  // fragment reads before the MFMAs of slice 1 instead of letting them overlap.
+  // sched_barrier keeps the phases in this order (reads ahead of the MFMAs that hide them)
+  auto step = [&](int kt, bool chk, bool last) {
     frag(fb, kt, 1);
+    __builtin_amdgcn_sched_barrier(0);
     mma(fa);
-    if (kt + 1 < KT) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (!last || kt + 1 < KT) {
       if constexpr (NEWER == 8)
         asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       else if constexpr (NEWER == 6)
@@ -1469,13 +1476,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
       dma(kt + 4, chk);
       frag(fa, kt + 1, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
     mma(fb);
+    __builtin_amdgcn_sched_barrier(0);
   };
-  // PRE: the last four steps, whose copies may be step KT's, run in a loop of their own
-  const int kmain = !PRE ? KT : (KT > 4 ? KT - 4 : 0);
+  // PRE: the last four steps, whose copies may be step KT's, run in a loop of their own;
+  // otherwise the last step alone
+  const int kmain = !PRE ? KT - 1 : (KT > 4 ? KT - 4 : 0);
   int kt = 0;
-  for (; kt < kmain; ++kt) step(kt, false);
-  for (; kt < KT; ++kt) step(kt, true);
+  for (; kt < kmain; ++kt) step(kt, false, false);
+  for (; kt < KT; ++kt) step(kt, true, true);
   // every copy (including the ones past K) has landed before the epilogue reuses LDS
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   gemm_epilogue_t<BM, BN, WM, WN, EPI, NT, PRE>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn, tid, lane,
