@@ -364,15 +364,16 @@ struct Bd2Shape {
 // same-box timings of the config-2 shapes at M = 16 / 32:
 //  * rows up to 2048 k: one slice, 16-row workgroups of 8 waves along K (q/k/v 4.9 / 6.0 us,
 //    o 4.8 / 6.0 us; a K split with its reduce launch costs 2-3 us more);
-//  * the paired SwiGLU (1536 k): one slice, 4 waves along K; 16-row workgroups at M <= 16,
-//    64-row ones above (their 96 KiB activation slice allows one workgroup per CU, and 140
-//    of them still fit one round): 10.8 / 14.3 us;
+//  * the paired SwiGLU (1536 k): one slice, 4 waves along K, 48-row workgroups: 187 of
+//    them for 8960 rows, one round on 256 CUs even when the 96 KiB activation slice of M = 32
+//    allows one workgroup per CU (10.4 / 11.9 us; 16-row workgroups 10.7 / 23.0, 64-row
+//    ones 140 workgroups, 11.8 / 14.3);
 //  * longer rows: 64-row workgroups, slices of at most kBd2MaxCS chunks to about 256
 //    workgroups, 2 or 4 waves along K (1536 x 8960: 10 slices, 9.1 / 11.5 us).
 Bd2Shape bd2_shape(const int64_t* N, int n_lin, int P, int64_t K, int64_t M) {
   const int C = (int)(K / 64);
   if (C <= 32) {
-    if (P == 2) return Bd2Shape{M <= 16 ? 1 : 4, 4, 1, C};
+    if (P == 2) return Bd2Shape{3, 4, 1, C};
     return Bd2Shape{1, 8, 1, C};
   }
   Bd2Shape sh{4, 1, 1, C};
@@ -403,7 +404,7 @@ void bd2_launch_mt(const Bd2Params& p, const Bd2Shape& sh, int64_t tiles, hipStr
     hipLaunchKernelGGL((k_bd2<P, MT, WR_, WK_, F16>), grid, dim3(WR_ * WK_ * 64), lds, s, p);         \
     return;                                                                                           \
   }
-  QS_BD2(4, 1) QS_BD2(4, 2) QS_BD2(4, 4) QS_BD2(1, 4) QS_BD2(1, 8)
+  QS_BD2(4, 1) QS_BD2(4, 2) QS_BD2(4, 4) QS_BD2(3, 4) QS_BD2(1, 8)
 #undef QS_BD2
 }
 
