@@ -94,8 +94,8 @@ int bdec_prepare(BdecParams& p, const void* x, int x_dtype, int64_t ldx, int64_t
 }
 
 // ---------------------------------------------------------------------------------
-// k_bd2: one workgroup = (16 * WR weight rows, K slice); its WR * WK waves own 16 rows x
-// a contiguous part of the slice each.  The slice's activations [M, slice] reach LDS by
+// k_bd2: one workgroup = (RS <= 16 * WR weight rows, K slice); its WR * WK waves own 16 rows
+// (masked past the workgroup's RS) x a contiguous part of the slice each.  The slice's activations [M, slice] reach LDS by
 // DMA (buffer_load ... lds, 1 KiB per wave instruction, 16-byte chunk j of row m at slot
 // j ^ (m & 15), so the 16 rows of a fragment read fall in distinct banks); the wave's
 // weight chunks (64 k of 16 rows, 16 bytes per lane) are all requested right behind the
@@ -104,7 +104,7 @@ int bdec_prepare(BdecParams& p, const void* x, int x_dtype, int64_t ldx, int64_t
 // of one activation row.  The WK parts are summed in fixed order through LDS; with S > 1
 // slices the fp32 partial sums go to the workspace and k_bd2_reduce sums them in slice
 // order and stores the epilogue.  WK, S and the slice length -- the K order of every sum --
-// depend on (N, K) only (WR, the rows per workgroup, may follow M: it changes no sum), and
+// depend on (N, K) only (WR and RS, the rows per workgroup, may follow M: they change no sum), and
 // an MFMA sums each output over its k in a fixed order whatever the other rows hold, so a
 // row's result does not depend on the rest of the batch.
 // ---------------------------------------------------------------------------------
@@ -118,6 +118,7 @@ struct Bd2Params {
   int64_t ldx;
   int M, K, C;   // C = K / 64
   int S, CS;     // slices and 64-k chunks per slice (even: 16-chunk LDS row groups)
+  int RS;        // weight rows per workgroup (a multiple of 4, at most 16 * WR)
   int n_lin, n_total;
   int vec;       // outputs and partial rows allow 4-wide stores
   BdecLin lin[4];
@@ -131,114 +132,17 @@ __device__ __forceinline__ void bd2_copy16(__amdgpu_buffer_rsrc_t r, uint8_t* ds
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
 }
 
+// Sections 6-7 of k_bd2: the WK parts of the wave's 16 rows summed in order through
+// LDS (bsm, WK * WR * P * MT * 64 f32x4), then the epilogue (S == 1) or the slice's partial
+// sums (S > 1).  n0: the wave's first row; N: the row bound (the workgroup's share).
 template <int P, int MT, int WR, int WK, bool F16>
-__global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
-  typedef Half<F16> H;
-  typedef typename H::vec hvec;
-  constexpr int NW = WR * WK;
-  constexpr int R = 16 * WR;
-  extern __shared__ __attribute__((aligned(1024))) uint8_t bsm[];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = wave % WR, wk = wave / WR;
-  const int col = lane & 15, grp = lane >> 4;
-  const int tile = (int)blockIdx.x / p.S;
-  const int s = (int)blockIdx.x - tile * p.S;
-  int li = 0;
-  if (P == 1) {
-#pragma unroll
-    for (int j = 1; j < 4; ++j)
-      if (j < p.n_lin && tile >= p.lin[j].tile_begin) li = j;
-  }
-  const BdecLin& L0 = p.lin[li];
-  const int N = L0.N;
-  const int n0 = (tile - L0.tile_begin) * R + 16 * wr;  // this wave's 16 rows
-  const int c0 = s * p.CS;
-  const int cs = min(p.CS, p.C - c0);  // chunks of this slice, >= 1
-  const int kbeg = c0 * 64;
-  const int NCH = p.CS * 8;  // 16-byte chunks per staged activation row
-
-  // 1. row scales: the oldest requests, so the wait below covers them
-  const int nr = n0 + col;
-  float sc[P];
-#pragma unroll
-  for (int pl = 0; pl < P; ++pl) sc[pl] = p.lin[P == 2 ? pl : li].scales[nr < N ? nr : N - 1];
-
-  // 2. the activation slice [16 MT rows][NCH chunks] -> LDS; rows >= M and chunks past the
-  //    slice read out of the buffer's range (zero, no memory access)
-  const int xlim = p.M * (int)p.ldx * 2;
-  const __amdgpu_buffer_rsrc_t xr =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x), (short)0, xlim, 0x00020000);
-  const int total = 16 * MT * NCH;
-  for (int u0 = wave * 64; u0 < total; u0 += NW * 64) {
-    const int u = u0 + lane;
-    const int m = u / NCH, jj = u - m * NCH, j = jj ^ (m & 15);
-    const bool ok = m < p.M && j < 8 * cs;
-    bd2_copy16(xr, bsm + 16 * u0, ok ? (m * (int)p.ldx + kbeg + 8 * j) * 2 : xlim);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 3. this wave's part of the slice: every chunk requested at once (zero past the part
-  //    and for rows >= N, whose lane offsets lie past the buffer)
-  const int PS = (cs + WK - 1) / WK;
-  const int cb = wk * PS;
-  const int ce = min(cs, cb + PS);
-  const int wlim = N * p.K;
-  const int wlane = nr * p.K + kbeg + 16 * grp;
-  i32x4 wv[kBd2MaxPS][P];
-#pragma unroll
-  for (int pl = 0; pl < P; ++pl) {
-    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t*>(p.lin[P == 2 ? pl : li].codes), (short)0, wlim, 0x00020000);
-#pragma unroll
-    for (int c = 0; c < kBd2MaxPS; ++c)
-      wv[c][pl] = __builtin_bit_cast(
-          i32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, cb + c < ce ? wlane + 64 * (cb + c) : wlim, 0, 0));
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  // 4. this wave's copies have landed once at most its kBd2MaxPS * P weight loads are
-  //    outstanding; the barrier then makes every wave's copies visible
-  static_assert(kBd2MaxPS * P == 8 || kBd2MaxPS * P == 16, "wait counts below");
-  if constexpr (kBd2MaxPS * P == 16)
-    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-
-  // 5. MFMA over the part
-  f32x4 acc[P][MT];
-#pragma unroll
-  for (int pl = 0; pl < P; ++pl)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[pl][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int c = 0; c < kBd2MaxPS; ++c) {
-    if (cb + c < ce) {
-      const int j = 8 * (cb + c) + 2 * grp;  // chunk of k = 64 (cb + c) + 16 grp in the slice
-      hvec xa[MT][2];
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const int m = 16 * t + col;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          xa[t][h] = *reinterpret_cast<const hvec*>(bsm + 16 * (m * NCH + ((j + h) ^ (m & 15))));
-      }
-#pragma unroll
-      for (int pl = 0; pl < P; ++pl) {
-        hvec b0, b1;
-        H::deq(wv[c][pl], sc[pl], b0, b1);
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          acc[pl][t] = H::mma(b0, xa[t][0], acc[pl][t]);
-          acc[pl][t] = H::mma(b1, xa[t][1], acc[pl][t]);
-        }
-      }
-    }
-  }
-
+__device__ __forceinline__ void bd2_finish(const Bd2Params& p, const BdecLin& L0, const f32x4 (&acc)[P][MT],
+                                           uint8_t* bsm, int wr, int wk, int lane, int col, int grp, int n0,
+                                           int N, int s, bool sync_first) {
   // 6. the WK parts summed in order wk = 0, 1, ... through LDS
   f32x4 out[P][MT];
   if constexpr (WK > 1) {
-    __syncthreads();  // every wave is done with the activation slice
+    if (sync_first) __syncthreads();  // every wave is done with the LDS activation slice
     f32x4* red = reinterpret_cast<f32x4*>(bsm);  // [WK][WR][P][MT][64]
 #pragma unroll
     for (int pl = 0; pl < P; ++pl)
@@ -308,6 +212,113 @@ __global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
     }
 }
 
+template <int P, int MT, int WR, int WK, bool F16>
+__global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
+  typedef Half<F16> H;
+  typedef typename H::vec hvec;
+  constexpr int NW = WR * WK;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t bsm[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave % WR, wk = wave / WR;
+  const int col = lane & 15, grp = lane >> 4;
+  const int tile = (int)blockIdx.x / p.S;
+  const int s = (int)blockIdx.x - tile * p.S;
+  int li = 0;
+  if (P == 1) {
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      if (j < p.n_lin && tile >= p.lin[j].tile_begin) li = j;
+  }
+  const BdecLin& L0 = p.lin[li];
+  const int tb = (tile - L0.tile_begin) * p.RS;  // the workgroup's first row
+  const int N = min(L0.N, tb + p.RS);             // rows past this bound are another workgroup's
+  const int n0 = tb + 16 * wr;                    // this wave's 16 rows (masked at N)
+  const int c0 = s * p.CS;
+  const int cs = min(p.CS, p.C - c0);  // chunks of this slice, >= 1
+  const int kbeg = c0 * 64;
+  const int NCH = p.CS * 8;  // 16-byte chunks per staged activation row
+
+  // 1. row scales: the oldest requests, so the wait below covers them
+  const int nr = n0 + col;
+  float sc[P];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) sc[pl] = p.lin[P == 2 ? pl : li].scales[nr < N ? nr : tb];
+
+  // 2. the activation slice [16 MT rows][NCH chunks] -> LDS; rows >= M and chunks past the
+  //    slice read out of the buffer's range (zero, no memory access)
+  const int xlim = p.M * (int)p.ldx * 2;
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x), (short)0, xlim, 0x00020000);
+  const int total = 16 * MT * NCH;
+  for (int u0 = wave * 64; u0 < total; u0 += NW * 64) {
+    const int u = u0 + lane;
+    const int m = u / NCH, jj = u - m * NCH, j = jj ^ (m & 15);
+    const bool ok = m < p.M && j < 8 * cs;
+    bd2_copy16(xr, bsm + 16 * u0, ok ? (m * (int)p.ldx + kbeg + 8 * j) * 2 : xlim);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. this wave's part of the slice: every chunk requested at once (zero past the part
+  //    and for rows >= N, whose lane offsets lie past the buffer)
+  const int PS = (cs + WK - 1) / WK;
+  const int cb = wk * PS;
+  const int ce = min(cs, cb + PS);
+  const int wlim = L0.N * p.K;
+  const int wlane = nr < N ? nr * p.K + kbeg + 16 * grp : wlim;  // rows past N: no access
+  i32x4 wv[kBd2MaxPS][P];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl) {
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(p.lin[P == 2 ? pl : li].codes), (short)0, wlim, 0x00020000);
+#pragma unroll
+    for (int c = 0; c < kBd2MaxPS; ++c)
+      wv[c][pl] = __builtin_bit_cast(
+          i32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, cb + c < ce && nr < N ? wlane + 64 * (cb + c) : wlim, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 4. this wave's copies have landed once at most its kBd2MaxPS * P weight loads are
+  //    outstanding; the barrier then makes every wave's copies visible
+  static_assert(kBd2MaxPS * P == 8 || kBd2MaxPS * P == 16, "wait counts below");
+  if constexpr (kBd2MaxPS * P == 16)
+    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+
+  // 5. MFMA over the part
+  f32x4 acc[P][MT];
+#pragma unroll
+  for (int pl = 0; pl < P; ++pl)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[pl][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < kBd2MaxPS; ++c) {
+    if (cb + c < ce) {
+      const int j = 8 * (cb + c) + 2 * grp;  // chunk of k = 64 (cb + c) + 16 grp in the slice
+      hvec xa[MT][2];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int m = 16 * t + col;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          xa[t][h] = *reinterpret_cast<const hvec*>(bsm + 16 * (m * NCH + ((j + h) ^ (m & 15))));
+      }
+#pragma unroll
+      for (int pl = 0; pl < P; ++pl) {
+        hvec b0, b1;
+        H::deq(wv[c][pl], sc[pl], b0, b1);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acc[pl][t] = H::mma(b0, xa[t][0], acc[pl][t]);
+          acc[pl][t] = H::mma(b1, xa[t][1], acc[pl][t]);
+        }
+      }
+    }
+  }
+
+  bd2_finish<P, MT, WR, WK, F16>(p, L0, acc, bsm, wr, wk, lane, col, grp, n0, N, s, true);
+}
+
 // Slice sums of k_bd2 in slice order and the epilogue: one thread per (row m, 4 columns
 // of the partial row); every linear's N is a multiple of 4 (the host checks).
 template <int P, bool F16>
@@ -357,6 +368,7 @@ __global__ __launch_bounds__(128) void k_bd2_reduce(Bd2Params p) {
 
 struct Bd2Shape {
   int WR, WK, S, CS;
+  int RS;  // rows per workgroup: a multiple of 4, at most 16 * WR
 };
 
 // Split.  The K order of every sum -- WK waves per slice and S slices -- depends on (N, K)
@@ -364,19 +376,25 @@ struct Bd2Shape {
 // same-box timings of the config-2 shapes at M = 16 / 32:
 //  * rows up to 2048 k: one slice, 16-row workgroups of 8 waves along K (q/k/v 4.9 / 6.0 us,
 //    o 4.8 / 6.0 us; a K split with its reduce launch costs 2-3 us more);
-//  * the paired SwiGLU (1536 k): one slice, 4 waves along K, 48-row workgroups: 187 of
-//    them for 8960 rows, one round on 256 CUs even when the 96 KiB activation slice of M = 32
-//    allows one workgroup per CU (10.4 / 11.9 us; 16-row workgroups 10.7 / 23.0, 64-row
-//    ones 140 workgroups, 11.8 / 14.3);
+//  * the paired SwiGLU (1536 k): one slice, 4 waves along K, about one workgroup per CU
+//    (a CU streams its weights at a limited rate, so the CU with the most rows sets the
+//    time): rows per workgroup ceil(N / 256) rounded up to 4, as 16-row MFMA tiles with
+//    the rows past the workgroup's share masked (no loads, no stores).  8960 rows: 249
+//    workgroups of 36 rows (48-row ones: 10.4 / 11.9 us; 16-row ones 10.7 / 23.0; 64-row
+//    ones 11.8 / 14.3; the 96 KiB activation slice of M = 32 allows one workgroup per CU);
 //  * longer rows: 64-row workgroups, slices of at most kBd2MaxCS chunks to about 256
 //    workgroups, 2 or 4 waves along K (1536 x 8960: 10 slices, 9.1 / 11.5 us).
 Bd2Shape bd2_shape(const int64_t* N, int n_lin, int P, int64_t K, int64_t M) {
   const int C = (int)(K / 64);
   if (C <= 32) {
-    if (P == 2) return Bd2Shape{3, 4, 1, C};
-    return Bd2Shape{1, 8, 1, C};
+    if (P == 2) {
+      // about one workgroup per CU: rows per workgroup a multiple of 4 in [16, 48]
+      const int rs = (int)std::min<int64_t>(48, std::max<int64_t>(16, (cdiv(N[0], 256) + 3) / 4 * 4));
+      return Bd2Shape{(rs + 15) / 16, 4, 1, C, rs};
+    }
+    return Bd2Shape{1, 8, 1, C, 16};
   }
-  Bd2Shape sh{4, 1, 1, C};
+  Bd2Shape sh{4, 1, 1, C, 64};
   int64_t tiles = 0;
   for (int i = 0; i < (P == 2 ? 1 : n_lin); ++i) tiles += cdiv(N[i], 16 * sh.WR);
   // slices: enough for about 256 workgroups and for the LDS cap, at most kBd2MaxS; then
@@ -404,7 +422,7 @@ void bd2_launch_mt(const Bd2Params& p, const Bd2Shape& sh, int64_t tiles, hipStr
     hipLaunchKernelGGL((k_bd2<P, MT, WR_, WK_, F16>), grid, dim3(WR_ * WK_ * 64), lds, s, p);         \
     return;                                                                                           \
   }
-  QS_BD2(4, 1) QS_BD2(4, 2) QS_BD2(4, 4) QS_BD2(3, 4) QS_BD2(1, 8)
+  QS_BD2(4, 1) QS_BD2(4, 2) QS_BD2(4, 4) QS_BD2(3, 4) QS_BD2(2, 4) QS_BD2(1, 4) QS_BD2(1, 8)
 #undef QS_BD2
 }
 
@@ -415,12 +433,13 @@ int bd2_launch(Bd2Params& p, const Bd2Shape& sh, void* workspace, size_t workspa
   for (int i = 0; i < (P == 2 ? 1 : p.n_lin); ++i) {
     p.lin[i].tile_begin = (int)tiles;
     p.lin[i].n_begin = nb;
-    tiles += cdiv(p.lin[i].N, 16 * sh.WR);
+    tiles += cdiv(p.lin[i].N, sh.RS);
     nb += p.lin[i].N;
   }
   p.n_total = nb;
   p.S = sh.S;
   p.CS = sh.CS;
+  p.RS = sh.RS;
   if (p.S > 1) {
     const size_t need = (size_t)p.S * P * p.M * p.n_total * sizeof(float);
     if (!workspace || workspace_bytes < need)
