@@ -797,25 +797,41 @@ __global__ __launch_bounds__(256) void k_protect_quant(ProtectParams p) {
     }
   }
   // 2. the 16 maxima of 16-lane groups are 16 distinct keys (or 0 where a group holds no
-  //    column), so each of the kk <= 16 largest keys is >= the smallest of them, T.  The
-  //    keys >= T (a few dozen for ordinary data) go to LDS, and each candidate's rank (the
-  //    candidates above it) places it: rank < kk is selected, at position rank.
+  //    column).  T, the smallest of those with fewer than kk larger ones, is the kk-th
+  //    largest group maximum (0 when fewer than kk groups hold a column): at least kk keys
+  //    are >= T, so each of the kk <= 16 largest keys is >= T.  The keys >= T (about kk
+  //    to 2 kk for ordinary data) go to LDS, and each candidate's rank (the candidates
+  //    above it) places it: rank < kk is selected, at position rank.
+  //    The barriers of the selection wait for LDS only (s_waitcnt lgkmcnt(0) + s_barrier):
+  //    the activation rows requested above stay in flight through it.
   unsigned long long g = dpp_max_u64<0x111, 0xf>(mine);
   g = dpp_max_u64<0x112, 0xf>(g);
   g = dpp_max_u64<0x114, 0xf>(g);
   g = dpp_max_u64<0x118, 0xf>(g);
   if ((lane & 15) == 15) gmax[wave * 4 + (lane >> 4)] = g;
-  __syncthreads();
-  unsigned long long T = gmax[0];
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  unsigned long long T;
+  {
+    const unsigned long long v = gmax[lane & 15];
+    int larger = 0;
 #pragma unroll
-  for (int w = 1; w < 16; ++w) T = gmax[w] < T ? gmax[w] : T;
+    for (int w = 0; w < 16; ++w) larger += gmax[w] > v ? 1 : 0;
+    unsigned long long t = larger < p.kk ? ~v : 0ull;  // the row maximum of ~v is ~(min v)
+    t = dpp_max_u64<0x111, 0xf>(t);
+    t = dpp_max_u64<0x112, 0xf>(t);
+    t = dpp_max_u64<0x114, 0xf>(t);
+    t = dpp_max_u64<0x118, 0xf>(t);
+    const unsigned tlo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)t, 15);
+    const unsigned thi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(t >> 32), 15);
+    T = ~(((unsigned long long)thi << 32) | tlo);
+  }
 #pragma unroll
   for (int j = 0; j < VM; ++j)
     if (key[j] != 0ull && key[j] >= T) {  // rare: one LDS atomic per candidate
       const int pos = atomicAdd(&ncand, 1);
       if (pos < 256) cand[pos] = key[j];
     }
-  __syncthreads();
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   const int n = ncand;  // uniform
   if (n <= 256) {
     if (tid < n) {  // each candidate's rank counts the larger ones
@@ -851,8 +867,32 @@ __global__ __launch_bounds__(256) void k_protect_quant(ProtectParams p) {
       }
     }
   }
-  __syncthreads();
-  // 3. the workgroup's rows, quantized with keep factor 0 at the selected columns
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // 3. side operands requested now, stored after the quantization (their gathers land
+  //    while it runs): the side activations of the workgroup's rows and a slice of the
+  //    side weights (kWpPrefetch per thread; a remainder, if any, afterwards)
+  const bool xside = tid < (4 / WPR) * p.kk;
+  const int xrow = row0 + tid / p.kk, xpp = tid % p.kk;
+  float xv = 0.f;
+  if (xside && xrow < p.M) xv = load_x<XT>(p.x, (int64_t)xrow * p.ldx + sel[xpp]);
+  const int nper = (p.N + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int nb = (int)blockIdx.x * nper;
+  const int wtot = nper * p.kk;
+  constexpr int kWpPrefetch = 4;
+  int wqv[kWpPrefetch];
+  float wsv[kWpPrefetch];
+#pragma unroll
+  for (int u = 0; u < kWpPrefetch; ++u) {
+    const int i = tid + 256 * u;
+    const int n = nb + i / p.kk, pp = i % p.kk;
+    wqv[u] = 0;
+    wsv[u] = 0.f;
+    if (i < wtot && n < p.N) {
+      wqv[u] = p.qw[(int64_t)n * K + sel[pp]];
+      wsv[u] = p.sw[n];
+    }
+  }
+  // 4. the workgroup's rows, quantized with keep factor 0 at the selected columns
   constexpr int E = XT == QS_F32 ? 4 : 8;
   auto keep4 = [&](int ch, int h) -> f32x4 {
     const int c0 = ch * E + 4 * h;  // a multiple of 4: the 4 bits share a word
@@ -860,15 +900,15 @@ __global__ __launch_bounds__(256) void k_protect_quant(ProtectParams p) {
     return f32x4{(w & 1u) ? 0.f : 1.f, (w & 2u) ? 0.f : 1.f, (w & 4u) ? 0.f : 1.f, (w & 8u) ? 0.f : 1.f};
   };
   act_quant_compute<XT, CPL, WPR>(qrow, true, keep4, p.q, K, p.scale, row, p.M, K);
-  // 4. side activations of the workgroup's rows
-  if (tid < (4 / WPR) * p.kk) {
-    const int row = row0 + tid / p.kk, pp = tid % p.kk;
-    if (row < p.M) p.xp[(int64_t)row * p.kk + pp] = load_x<XT>(p.x, (int64_t)row * p.ldx + sel[pp]);
+  // 5. the side operands
+  if (xside && xrow < p.M) p.xp[(int64_t)xrow * p.kk + xpp] = xv;
+#pragma unroll
+  for (int u = 0; u < kWpPrefetch; ++u) {
+    const int i = tid + 256 * u;
+    const int n = nb + i / p.kk, pp = i % p.kk;
+    if (i < wtot && n < p.N) p.wp[(int64_t)n * p.kk + pp] = static_cast<float>(wqv[u]) * wsv[u];
   }
-  // 5. a slice of the side weights
-  const int nper = (p.N + (int)gridDim.x - 1) / (int)gridDim.x;
-  const int nb = (int)blockIdx.x * nper;
-  for (int i = tid; i < nper * p.kk; i += 256) {
+  for (int i = tid + 256 * kWpPrefetch; i < wtot; i += 256) {
     const int n = nb + i / p.kk, pp = i % p.kk;
     if (n < p.N) p.wp[(int64_t)n * p.kk + pp] = static_cast<float>(p.qw[(int64_t)n * K + sel[pp]]) * p.sw[n];
   }
