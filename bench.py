@@ -410,7 +410,7 @@ def profile_mfma_kernels(torch, dev, which: str, calls: int) -> dict:
             (torch.rand(E, 2 * I, device=dev, generator=gen) + 0.5) / 127,
             torch.randint(-127, 128, (E, H, I), dtype=torch.int8, device=dev, generator=gen),
             (torch.rand(E, H, device=dev, generator=gen) + 0.5) / 127, dev)
-        backend = moe.Int8ExpertBackend([layer])
+        backend = moe.Int8ExpertBackend([layer], w8a16=which == "moe16")
         for T in (64, 512):
             tw, ti = moe.route_topk(torch.randn(T, E, device=dev, generator=gen), topk)
             xs = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16)
@@ -495,6 +495,7 @@ def secondary_measurements(torch, dev, stream) -> dict:
         torch.randint(-127, 128, (E, H, I), dtype=torch.int8, device=dev, generator=gen),
         (torch.rand(E, H, device=dev, generator=gen) + 0.5) / 127, dev)
     backend = moe.Int8ExpertBackend([layer])
+    backend16 = moe.Int8ExpertBackend([layer], w8a16=True)
     page_bytes = layer.layout.gate_up_codes_bytes + layer.layout.gate_up_scales_bytes + \
         layer.layout.down_codes_bytes + layer.layout.down_scales_bytes
     for T in (64, 512):
@@ -502,13 +503,15 @@ def secondary_measurements(torch, dev, stream) -> dict:
         xs = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16)
         tw, ti = moe.route_topk(logits, topk)
         active = int(torch.unique(ti).numel())
-        tt = _graph_time(torch, stream, lambda i: backend.moe(0, xs, ti, tw), 10)
         byts = active * page_bytes + T * H * 2 * 2
         ops = 2 * T * topk * (2 * I * H + H * I)
-        res[f"config4_moe_t{T}"] = {"us": round(tt * 1e6, 2), "GB/s": round(byts / tt / 1e9, 1),
-                                    "hbm_frac": round(byts / tt / 1e9 / HBM_PEAK_GBS, 4),
-                                    "TOPS": round(ops / tt / 1e12, 2), "active_experts": active}
-    del layer, backend
+        # W8A8 flow, then the weight-only (W8A16) flow over the same pages and routes
+        for key, bk in ((f"config4_moe_t{T}", backend), (f"config4_moe_w8a16_t{T}", backend16)):
+            tt = _graph_time(torch, stream, lambda i: bk.moe(0, xs, ti, tw), 10)
+            res[key] = {"us": round(tt * 1e6, 2), "GB/s": round(byts / tt / 1e9, 1),
+                        "hbm_frac": round(byts / tt / 1e9 / HBM_PEAK_GBS, 4),
+                        "TOPS": round(ops / tt / 1e12, 2), "active_experts": active}
+    del layer, backend, backend16
     res.update(paged_moe_measurement(torch, dev, E, topk, H, I))
 
     # config 5: packed int3/int2 GEMV, G=64 fp16 scale+zero, [11008,4096] and [4096,11008]
@@ -575,12 +578,12 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-secondary", action="store_true", help="skip configs 1/3/4/5")
-    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "w8a8p", "moe"),
+    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "w8a8p", "moe", "moe16"),
                     help="for rocprofv3 runs: replay exactly the timed graph of the roofline kernel (28 "
                     "paired gate/up+SwiGLU launches) or of the headline pass, --steps times after "
                     "--warmup replays; a plain 256 MiB device copy x5 (counter calibration); or config 3's "
                     "fused W8A8 GEMM (M=512 and 2048), config 3's whole w8a8_matmul with protect_k=8 (w8a8p) / "
-                    "config 4's MoE layer (T=64 and 512), --steps calls each")
+                    "config 4's MoE layer (T=64 and 512; moe16: the weight-only flow), --steps calls each")
     ap.add_argument("--eager", action="store_true",
                     help="with --profile swiglu/stack: launch the same sequence eagerly instead of replaying "
                     "the graph (counter collection needs eager dispatches)")
@@ -612,7 +615,7 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"profile": "copy", "launches": 5, "read_bytes": n, "write_bytes": n}), flush=True)
         return 0
-    if args.profile in ("w8a8", "w8a8p", "moe"):
+    if args.profile in ("w8a8", "w8a8p", "moe", "moe16"):
         print(json.dumps(profile_mfma_kernels(torch, dev, args.profile, args.steps)), flush=True)
         return 0
     arena, pages = build_stack(torch, dev)

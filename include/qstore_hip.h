@@ -279,6 +279,22 @@ int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* 
                            int G, int64_t N, int64_t K, int64_t max_rows, int swiglu, void* out,
                            int out_dtype, void* stream);
 
+/* Replaces grouped_bf16_mm / _grouped_bf16_kernel (qwen3_moe_cuda.py:2473-2510, 2117-2157)
+ * as used by PackedBF16ExpertBackend.moe (:2978-3046), over int8 expert pages (the weight-
+ * only W8A16 grouped variant): for every group g with rows [starts[g], starts[g]+counts[g])
+ * and weights w + slot(g)*w_stride ([N_w, K] int8 rows, scales w_scale + slot(g)*ws_stride):
+ *   out[row, n] = sum_k float(x[row, k]) * float(bf16(float(code[n, k]) * w_scale[n]))
+ * (fp32 accumulate, F32 or BF16 out), x bf16.  row_ids nullable: x[row] is source row
+ * row_ids[row] of a (the reference's source.index_select(0, token_ids)); ids outside
+ * [0, src_rows) read zeros.  swiglu != 0: N_w = 2N, out = bf16(bf16(silu(bf16(gate))) *
+ * bf16(up)) with gate from weight row n and up from row n + N (the reference's
+ * F.silu(gate) * up on bf16 halves).  K % 64 == 0; max_rows as qs_moe_grouped_gemm_i8. */
+int qs_moe_grouped_gemm_w8a16(const void* a, const int64_t* row_ids, int64_t src_rows,
+                              const int8_t* w, int64_t w_stride, const float* w_scale,
+                              int64_t ws_stride, const int32_t* starts, const int32_t* counts,
+                              const int32_t* slots, int G, int64_t N, int64_t K, int64_t max_rows,
+                              int swiglu, void* out, int out_dtype, void* stream);
+
 /* Replaces stable_route_reduce / _stable_route_reduce_kernel (qwen3_moe_cuda.py:2561-2664,
  * 2160-2182): out[t, h] = sum over rank r = 0..k-1 (in order) of
  * float(y[inverse[t*k+r], h]) * coef[inverse[t*k+r]], each product rounded to fp32.  A

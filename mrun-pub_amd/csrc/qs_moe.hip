@@ -768,6 +768,199 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream(MoeGemmParams p) {
   }
 }
 
+// W8A16 streaming grouped GEMM: k_moe_stream's walk (XCD-grouped row blocks, each wave
+// streaming its weight rows over the full K through a window of W chunks in registers)
+// with bf16 routed rows and no activation quantization.  Each weight piece is dequantized
+// in registers to bf16(float(code) * w_scale[n]) (the W8A16 weight contract of the qrow
+// path) and multiplied by v_mfma_f32_16x16x32_bf16 with fp32 accumulation: lane l's 16
+// codes at k offset o of its weight row (l & 15) are the B operands of two MFMAs (codes
+// o .. o + 7 and o + 8 .. o + 15), whose A operands are the same k elements of staged row
+// (l & 15) of a 16-row tile.  The rows are staged in K phases of KPH elements (MC rows of
+// KPH bf16 plus 16 bytes of pad in LDS), so every K fits: a phase boundary is a workgroup
+// barrier and a restage while the weight window stays in flight.  KPH is a multiple of
+// W chunks, so the window's register slot of chunk c stays c % W.  With row_ids, staged
+// row r of the group is source row row_ids[start + r] (the reference's
+// source.index_select(token_ids) folded into the staging); an id outside [0, src_rows)
+// stages zeros.
+struct MoeW16Params {
+  const uint16_t* a;      // bf16 [src_rows or A, K]
+  const int64_t* row_ids; // nullable gather of the routed rows
+  int64_t src_rows;
+  const int8_t* w;
+  int64_t w_stride;       // bytes
+  const float* ws;
+  int64_t ws_stride;      // floats
+  const int32_t* starts;
+  const int32_t* counts;
+  const int32_t* slots;   // nullable
+  int N, K, KPH;
+  void* out;
+  int out_dtype;
+};
+
+template <int P, int NB, int MT, int W, int WAVES, int PAIR>
+__global__ __launch_bounds__(WAVES * 64) void k_moe_stream_w16(MoeW16Params p) {
+  static_assert(P == 1 || NB == 2, "SwiGLU streams the gate and up tiles of one row block");
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int MC = 16 * MT;
+  constexpr int NT = WAVES * 64;
+  constexpr int RW = MoeStreamCfg<P, NB>::RW;
+  constexpr int CB = PAIR ? 128 : 64;  // codes of a weight row per chunk
+  constexpr int PL = PAIR ? 2 : 1;     // 16-code pieces per lane per chunk
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, q = lane >> 4;
+  const int total = gridDim.x * gridDim.y, lin = blockIdx.y * gridDim.x + blockIdx.x;
+  const int per_xcd = total / 8;
+  const int logical = lin < 8 * per_xcd ? (lin % 8) * per_xcd + lin / 8 : lin;
+  const int g = logical / gridDim.x, bx = logical - g * gridDim.x;
+  const int count = p.counts[g];
+  if (count == 0) return;
+  const int start = p.starts[g];
+  const int slot = p.slots ? p.slots[g] : g;
+  const int K = p.K, C = K / CB, KPH = p.KPH, CPH = KPH / CB;
+  const int xstride = 2 * KPH + 16;  // bytes per staged row
+  const int n0 = (bx * WAVES + wave) * RW;
+  const bool live = n0 < p.N;
+  const int lo = PAIR ? 32 * q : 16 * q;  // the lane's code offset within a chunk
+  const int8_t* wexp = p.w + (int64_t)slot * p.w_stride;
+  const int8_t* wr[NB];
+  float wsc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int nb = P == 2 ? min(n0 + col, p.N - 1) + b * p.N : min(n0 + 16 * b + col, p.N - 1);
+    wr[b] = wexp + (int64_t)nb * K + lo;
+    wsc[b] = p.ws[(int64_t)slot * p.ws_stride + nb];
+  }
+
+  // rows m0 .. m0 + mc of the group, elements k0 .. k0 + KPH (or K), 8 loads in flight
+  auto stage = [&](int m0, int mc, int k0) {
+    const int ppr = min(KPH, K - k0) >> 3;  // 16-byte pieces per staged row
+    const int tot = mc * ppr;
+    for (int i0 = 0; i0 < tot; i0 += 8 * NT) {
+      i32x4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        int i = i0 + j * NT + tid;
+        i = i < tot ? i : 0;
+        const int t = i / ppr, pc = i - t * ppr;
+        int64_t r = start + m0 + t;
+        bool ok = true;
+        if (p.row_ids) {
+          r = p.row_ids[r];
+          ok = r >= 0 && r < p.src_rows;
+        }
+        v[j] = ok ? *reinterpret_cast<const i32x4*>(p.a + r * K + k0 + pc * 8) : i32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + j * NT + tid;
+        if (i < tot) {
+          const int t = i / ppr, pc = i - t * ppr;
+          *reinterpret_cast<i32x4*>(lds + t * xstride + pc * 16) = v[j];
+        }
+      }
+    }
+  };
+
+  for (int m0 = 0; m0 < count; m0 += MC) {
+    const int mc = min(MC, count - m0);
+    i32x4 wv[W][NB][PL];
+#pragma unroll
+    for (int u = 0; u < W; ++u) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int j = 0; j < PL; ++j)
+          wv[u][b][j] = *reinterpret_cast<const i32x4*>(wr[b] + (int64_t)min(u, C - 1) * CB + 16 * j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    stage(m0, mc, 0);
+    __syncthreads();
+
+    f32x4 acc[MT][NB];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[mt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int cb = 0;  // first chunk of the staged phase
+    for (int c0 = 0; c0 < C; c0 += W) {
+      if (c0 - cb == CPH) {
+        cb = c0;
+        __syncthreads();  // every wave is done with the previous phase
+        stage(m0, mc, cb * CB);
+        __syncthreads();
+      }
+#pragma unroll
+      for (int u = 0; u < W; ++u) {
+        const int c = c0 + u;
+        if (c < C) {
+          const uint8_t* xa = lds + col * xstride + 2 * ((c - cb) * CB + lo);
+#pragma unroll
+          for (int j = 0; j < PL; ++j) {
+            bf16x8 wb[NB][2];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) deq16_bf16(wv[u][b][j], wsc[b], wb[b][0], wb[b][1]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              if (mt * 16 < mc) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                  const bf16x8 av = *reinterpret_cast<const bf16x8*>(xa + mt * 16 * xstride + 32 * j + 16 * h);
+#pragma unroll
+                  for (int b = 0; b < NB; ++b)
+                    acc[mt][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, wb[b][h], acc[mt][b], 0, 0, 0);
+                }
+              }
+            }
+          }
+        }
+        const int cn = min(c + W, C - 1);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+#pragma unroll
+          for (int j = 0; j < PL; ++j) wv[u][b][j] = *reinterpret_cast<const i32x4*>(wr[b] + (int64_t)cn * CB + 16 * j);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    // lane l holds D[row 4(l >> 4) + r of the tile][column l & 15]
+    if (live) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int ml = mt * 16 + 4 * q + r;
+          if (ml >= mc) continue;
+          const int64_t row = start + m0 + ml;
+          if constexpr (P == 2) {
+            const int no = n0 + col;
+            if (no < p.N) {
+              const float gt = bf16_bits_to_f32(f32_to_bf16_bits(acc[mt][0][r]));
+              const float ut = bf16_bits_to_f32(f32_to_bf16_bits(acc[mt][1][r]));
+              const float sl = bf16_bits_to_f32(f32_to_bf16_bits(silu_f(gt)));
+              static_cast<uint16_t*>(p.out)[row * p.N + no] = f32_to_bf16_bits(mul_rn(sl, ut));
+            }
+          } else {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+              const int no = n0 + 16 * b + col;
+              if (no < p.N) {
+                if (p.out_dtype == QS_F32)
+                  static_cast<float*>(p.out)[row * p.N + no] = acc[mt][b][r];
+                else
+                  static_cast<uint16_t*>(p.out)[row * p.N + no] = f32_to_bf16_bits(acc[mt][b][r]);
+              }
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();  // the next pass overwrites the staged rows
+  }
+}
+
 // ----------------------------------------------------------------------------------
 // stable rank-order reduce
 // ----------------------------------------------------------------------------------
@@ -981,7 +1174,74 @@ void launch_moe_stream(const MoeGemmParams& p, int G, int MT, hipStream_t s) {
     else launch_moe_stream_mt<P, NB, 1, 0>(p, G, s);
   }
 }
+// K phase of k_moe_stream_w16: the whole K when MC staged rows fit kMoeStreamLds, else
+// the fewest phases of a multiple of W chunks each that fit.
+int moe_w16_phase(int MT, int64_t K, int CB, int W) {
+  const int64_t C = K / CB;
+  for (int64_t kp = 1; kp <= C; ++kp) {
+    const int64_t cph = kp == 1 ? C : cdiv(cdiv(C, kp), W) * W;
+    if ((size_t)16 * MT * (size_t)(2 * cph * CB + 16) <= kMoeStreamLds) return (int)(cph * CB);
+  }
+  return 0;
+}
+
+template <int P, int NB, int MT, int PAIR>
+void launch_moe_w16_mt(MoeW16Params p, int G, hipStream_t s) {
+  constexpr int WAVES = P == 2 ? (MT == 1 ? 4 : 8) : 4;
+  constexpr int WP = P == 2 ? 2 : (NB >= 2 ? 1 : 2);  // 128-byte chunks in flight
+  constexpr int W = PAIR ? WP : 2 * WP;
+  constexpr int RW = MoeStreamCfg<P, NB>::RW;
+  p.KPH = moe_w16_phase(MT, p.K, PAIR ? 128 : 64, W);
+  const size_t lds = (size_t)16 * MT * (size_t)(2 * p.KPH + 16);
+  const dim3 grid((unsigned)cdiv(p.N, RW * WAVES), (unsigned)G), block(WAVES * 64);
+  hipLaunchKernelGGL((k_moe_stream_w16<P, NB, MT, W, WAVES, PAIR>), grid, block, lds, s, p);
+}
+
+template <int P, int NB>
+void launch_moe_w16(const MoeW16Params& p, int G, int MT, hipStream_t s) {
+  if (p.K % 128 == 0) {
+    if (MT == 4) launch_moe_w16_mt<P, NB, 4, 1>(p, G, s);
+    else if (MT == 2) launch_moe_w16_mt<P, NB, 2, 1>(p, G, s);
+    else launch_moe_w16_mt<P, NB, 1, 1>(p, G, s);
+  } else {
+    if (MT == 4) launch_moe_w16_mt<P, NB, 4, 0>(p, G, s);
+    else if (MT == 2) launch_moe_w16_mt<P, NB, 2, 0>(p, G, s);
+    else launch_moe_w16_mt<P, NB, 1, 0>(p, G, s);
+  }
+}
 }  // namespace
+
+extern "C" int qs_moe_grouped_gemm_w8a16(const void* a, const int64_t* row_ids, int64_t src_rows,
+                                         const int8_t* w, int64_t w_stride, const float* w_scale,
+                                         int64_t ws_stride, const int32_t* starts, const int32_t* counts,
+                                         const int32_t* slots, int G, int64_t N, int64_t K,
+                                         int64_t max_rows, int swiglu, void* out, int out_dtype,
+                                         void* stream) {
+  if (!a || !w || !w_scale || !starts || !counts || !out)
+    return fail(QS_ERR_INVALID, "moe_grouped_gemm_w8a16: null pointer");
+  if (G < 1 || G > 65535 || N <= 0 || K <= 0 || src_rows < 0)
+    return fail(QS_ERR_INVALID, "moe_grouped_gemm_w8a16: bad shape");
+  if (N > (1 << 30) || K > (1 << 20)) return fail(QS_ERR_LIMIT, "moe_grouped_gemm_w8a16: N or K too large");
+  if (K % 64 != 0) return fail(QS_ERR_UNSUPPORTED, "moe_grouped_gemm_w8a16: K must be a multiple of 64");
+  if (!aligned(a, 16) || !aligned(w, 16) || w_stride % 16 != 0)
+    return fail(QS_ERR_UNSUPPORTED, "moe_grouped_gemm_w8a16: operands must be 16-byte aligned");
+  if (swiglu && out_dtype != QS_BF16) return fail(QS_ERR_INVALID, "moe_grouped_gemm_w8a16: SwiGLU output is BF16");
+  if (out_dtype != QS_BF16 && out_dtype != QS_F32)
+    return fail(QS_ERR_INVALID, "moe_grouped_gemm_w8a16: out F32 or BF16");
+  if (max_rows < 0) return fail(QS_ERR_INVALID, "moe_grouped_gemm_w8a16: max_rows must be >= 0");
+  if (src_rows > (int64_t)1 << 40) return fail(QS_ERR_LIMIT, "moe_grouped_gemm_w8a16: src_rows too large");
+  MoeW16Params p{static_cast<const uint16_t*>(a), row_ids, src_rows, w, w_stride, w_scale, ws_stride,
+                 starts, counts, slots, (int)N, (int)K, 0, out, out_dtype};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // row tiles sized for twice the mean rows per group, as the int8 stream
+  const int64_t mean = max_rows > 0 ? cdiv(max_rows, G) : 16;
+  const int MT = 2 * mean <= 16 ? 1 : (2 * mean <= 32 ? 2 : 4);
+  if (swiglu) launch_moe_w16<2, 2>(p, G, MT, s);
+  else if (K <= 1024) launch_moe_w16<1, 4>(p, G, MT, s);
+  else if (K <= 2048) launch_moe_w16<1, 2>(p, G, MT, s);
+  else launch_moe_w16<1, 1>(p, G, MT, s);
+  return hip_check(hipGetLastError(), "k_moe_stream_w16 launch");
+}
 
 extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* w,
                                       int64_t w_stride, const float* w_scale, int64_t ws_stride,

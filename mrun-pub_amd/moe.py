@@ -29,6 +29,7 @@ from . import _native as nat
 
 IMPL_ROUTE = "hip-gfx950-stable-route-v1"
 IMPL_GROUPED = "hip-gfx950-grouped-w8a8-mfma-i8-v1"
+IMPL_GROUPED_W8A16 = "hip-gfx950-grouped-w8a16-mfma-bf16-v1"
 
 
 def _align(n: int, a: int = 4096) -> int:
@@ -278,6 +279,64 @@ def grouped_int8_mm(
     return out, IMPL_GROUPED
 
 
+@torch.inference_mode()
+def grouped_w8a16_mm(
+    rows: torch.Tensor,
+    weights: torch.Tensor,
+    weight_scales: torch.Tensor,
+    starts: torch.Tensor,
+    counts: torch.Tensor,
+    *,
+    row_ids: torch.Tensor | None = None,
+    group_slots: torch.Tensor | None = None,
+    max_rows: int | None = None,
+    swiglu: bool = False,
+    out_dtype: torch.dtype = torch.bfloat16,
+) -> tuple[torch.Tensor, str]:
+    """Weight-only ragged grouped GEMM over int8 expert pages:
+    ``out[start_g + m] = rows[start_g + m] @ bf16(weights[slot(g)] * scales)^T``.
+
+    The counterpart of the reference's ``grouped_bf16_mm`` (qwen3_moe_cuda.py:2473-2510)
+    with the experts' bf16 weights given as int8 codes and per-row scales, dequantized in
+    registers to ``bf16(float(code) * scale)`` (the W8A16 weight contract); ``rows`` stay
+    bf16, so no activation is quantized.  ``row_ids`` folds the gather
+    ``source.index_select(0, token_ids)`` (qwen3_moe_cuda.py:3020) into the kernel:
+    ``rows`` is then the unpermuted source and queue row ``r`` reads ``rows[row_ids[r]]``.
+    ``swiglu=True`` returns ``bf16(silu(gate) * up)`` of width ``N/2`` as
+    ``grouped_int8_mm`` does.
+    """
+    if rows.dtype != torch.bfloat16:
+        raise ValueError("grouped W8A16 rows must be bfloat16")
+    G, n_w, K = _grouped_contract(rows, weights, weight_scales, starts, counts, group_slots)
+    device = nat.require_device(rows, weights, weight_scales, starts, counts, group_slots, row_ids)
+    n_out = n_w // 2 if swiglu else n_w
+    if swiglu and n_w % 2:
+        raise ValueError("SwiGLU weights need an even number of rows")
+    src = rows.contiguous()
+    if row_ids is not None:
+        if row_ids.ndim != 1:
+            raise ValueError("row_ids must be a vector")
+        ids = row_ids.to(torch.int64).contiguous()
+        A = int(ids.numel())
+    else:
+        ids = None
+        A = int(src.shape[0])
+    out = torch.empty((A, n_out), dtype=out_dtype, device=device)
+    st = starts.to(torch.int32).contiguous()
+    ct = counts.to(torch.int32).contiguous()
+    sl = None if group_slots is None else group_slots.to(torch.int32).contiguous()
+    rows_bound = A if max_rows is None else int(max_rows)
+    if rows_bound < 0:
+        raise ValueError("max_rows must be non-negative")
+    nat.call(
+        "qs_moe_grouped_gemm_w8a16", nat.ptr(src), nat.ptr(ids), int(src.shape[0]), nat.ptr(weights),
+        int(weights.stride(0)), nat.ptr(weight_scales), int(weight_scales.stride(0)), nat.ptr(st), nat.ptr(ct),
+        nat.ptr(sl), G, n_out, K, rows_bound, int(bool(swiglu)), nat.ptr(out), nat.dtype_code(out_dtype),
+        nat.stream_of(device),
+    )
+    return out, IMPL_GROUPED_W8A16
+
+
 # ---- expert pages and backend ------------------------------------------------------------------
 
 
@@ -353,22 +412,29 @@ class Int8ExpertLayer:
 
 
 class Int8ExpertBackend:
-    """``backend.moe(layer, source, top_indices, top_weights)`` with int8 experts (W8A8).
+    """``backend.moe(layer, source, top_indices, top_weights)`` with int8 experts.
 
-    Flow per layer: stable route compile -> gather + per-row int8 quantization ->
-    grouped gate_up GEMM with the fused BF16 SwiGLU epilogue -> per-row requantization ->
-    grouped down GEMM -> fixed rank-order reduce -> model dtype.
+    Flow per layer (W8A8, the default): stable route compile -> gather + per-row int8
+    quantization -> grouped gate_up GEMM with the fused BF16 SwiGLU epilogue -> per-row
+    requantization -> grouped down GEMM -> fixed rank-order reduce -> model dtype.
+
+    ``w8a16=True`` is the weight-only flow of the reference's PackedBF16ExpertBackend.moe
+    (qwen3_moe_cuda.py:2978-3046) over the same int8 pages: the routed bf16 rows are
+    gathered inside the gate_up kernel, both grouped GEMMs multiply bf16 activations by
+    weights dequantized to ``bf16(code * scale)``, and nothing is quantized per token.
     """
 
     def __init__(self, layers: list[Int8ExpertLayer] | None = None, *, dtype: torch.dtype = torch.bfloat16,
-                 page_cache=None):
+                 page_cache=None, w8a16: bool = False):
         """``layers``: resident expert layers; ``page_cache``: an ``expert_cache.ExpertPageCache``
-        serving the layers' pages from host memory instead (slot-indirect binding)."""
+        serving the layers' pages from host memory instead (slot-indirect binding);
+        ``w8a16``: weight-only expert math (bf16 activations)."""
         if not layers and page_cache is None:
             raise ValueError("Int8ExpertBackend needs resident layers or a page cache")
         self.layers = layers or []
         self.page_cache = page_cache
         self.dtype = dtype
+        self.w8a16 = bool(w8a16)
         self.stats = {"grouped_kernel_calls": 0, "route_compiler_calls": 0, "expert_assignments": 0}
         self._experts: dict[tuple[torch.device, int], torch.Tensor] = {}
 
@@ -401,14 +467,7 @@ class Int8ExpertBackend:
         E = page.num_experts
         # fp32 coefficients: the reduce widens them to fp32 anyway
         token_ids, coef, starts, counts, inverse, _ = _route_impl(top_indices, top_weights, E, True, coef_f32=True)
-        rows_q, rows_s = quantize_rows(source, token_ids)
-        activated, _ = grouped_int8_mm(
-            rows_q, rows_s, page.gate_up, page.gate_up_scales, starts, counts, swiglu=True
-        )
-        act_q, act_s = quantize_rows(activated)
-        expert_output, _ = grouped_int8_mm(
-            act_q, act_s, page.down, page.down_scales, starts, counts, out_dtype=self.dtype
-        )
+        expert_output = self._experts_math(page, source, token_ids, starts, counts, None)
         out = stable_route_reduce(
             expert_output, coef, token_ids, counts, top_indices,
             self._expert_ids(source.device, E), inverse_assignments=inverse, out_dtype=self._reduce_dtype(),
@@ -417,6 +476,28 @@ class Int8ExpertBackend:
         self.stats["route_compiler_calls"] += 1
         self.stats["expert_assignments"] += int(top_indices.numel())
         return out.to(self.dtype)
+
+    def _experts_math(self, page, source, token_ids, starts, counts, slots) -> torch.Tensor:
+        """gate_up + SwiGLU and down over the routed queue; [A, H] in the model dtype."""
+        if self.w8a16:
+            src = source if source.dtype == torch.bfloat16 else source.to(torch.bfloat16)
+            activated, _ = grouped_w8a16_mm(
+                src, page.gate_up, page.gate_up_scales, starts, counts, row_ids=token_ids, group_slots=slots,
+                swiglu=True,
+            )
+            expert_output, _ = grouped_w8a16_mm(
+                activated, page.down, page.down_scales, starts, counts, group_slots=slots, out_dtype=self.dtype
+            )
+            return expert_output
+        rows_q, rows_s = quantize_rows(source, token_ids)
+        activated, _ = grouped_int8_mm(
+            rows_q, rows_s, page.gate_up, page.gate_up_scales, starts, counts, group_slots=slots, swiglu=True
+        )
+        act_q, act_s = quantize_rows(activated)
+        expert_output, _ = grouped_int8_mm(
+            act_q, act_s, page.down, page.down_scales, starts, counts, group_slots=slots, out_dtype=self.dtype
+        )
+        return expert_output
 
     def _moe_paged(self, layer, source, top_indices, top_weights, *, prefill: bool) -> torch.Tensor:
         """Same flow over the experts of this step only: the page cache binds each routed
@@ -437,14 +518,7 @@ class Int8ExpertBackend:
             token_ids, coef, starts, counts, inverse, _ = _route_impl(
                 compact, top_weights, int(selected.numel()), True, coef_f32=True
             )
-        rows_q, rows_s = quantize_rows(source, token_ids)
-        activated, _ = grouped_int8_mm(
-            rows_q, rows_s, page.gate_up, page.gate_up_scales, starts, counts, group_slots=slots, swiglu=True
-        )
-        act_q, act_s = quantize_rows(activated)
-        expert_output, _ = grouped_int8_mm(
-            act_q, act_s, page.down, page.down_scales, starts, counts, group_slots=slots, out_dtype=self.dtype
-        )
+        expert_output = self._experts_math(page, source, token_ids, starts, counts, slots)
         out = stable_route_reduce(
             expert_output, coef, token_ids, counts, top_indices, selected, inverse_assignments=inverse,
             out_dtype=self._reduce_dtype(),

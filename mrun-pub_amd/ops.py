@@ -19,6 +19,7 @@ torch's current stream, and allocates its outputs fresh; no operator mutates an 
 | ``moe_router(logits, top_k, norm_topk, out_dtype)`` | router qwen3_moe_cuda.py:3702-3707 |
 | ``moe_route(top_indices, top_weights, num_experts)`` | ``grouped_route_tensors_with_inverse`` olmoe_cuda.py:1108-1135 |
 | ``grouped_int8_mm(rows_q, row_scales, weights, weight_scales, starts, counts, group_slots, max_rows, swiglu, out_dtype)`` | ``grouped_fp8_mm(_strided)`` olmoe_cuda.py:1197-1252, qwen3_moe_cuda.py:2257-2310 |
+| ``grouped_w8a16_mm(rows, weights, weight_scales, starts, counts, row_ids, group_slots, max_rows, swiglu, out_dtype)`` | ``grouped_bf16_mm`` qwen3_moe_cuda.py:2473-2510 (weight-only, int8 pages) |
 | ``route_reduce(expert_output, coefficients, inverse, rows, top_k)`` | ``stable_route_reduce`` qwen3_moe_cuda.py:2561-2664 |
 | ``lowbit_matmul(packed, scales, zeros, x, bits, group_size, in_features)`` | ``QStoreInt3/Int2.matmul`` qstore.py:1318-1341, 1451-1474 |
 """
@@ -179,6 +180,25 @@ def _(rows_q, row_scales, weights, weight_scales, starts, counts, group_slots=No
     return rows_q.new_empty((rows_q.shape[0], n), dtype=out_dtype)
 
 
+@_op("grouped_w8a16_mm")
+def grouped_w8a16_mm(rows: torch.Tensor, weights: torch.Tensor, weight_scales: torch.Tensor, starts: torch.Tensor,
+                     counts: torch.Tensor, row_ids: Optional[torch.Tensor] = None,
+                     group_slots: Optional[torch.Tensor] = None, max_rows: int = 0, swiglu: bool = False,
+                     out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    y, _tag = _moe.grouped_w8a16_mm(rows, weights, weight_scales, starts, counts, row_ids=row_ids,
+                                    group_slots=group_slots, max_rows=max_rows or None, swiglu=swiglu,
+                                    out_dtype=out_dtype)
+    return y
+
+
+@grouped_w8a16_mm.register_fake
+def _(rows, weights, weight_scales, starts, counts, row_ids=None, group_slots=None, max_rows=0, swiglu=False,
+      out_dtype=torch.bfloat16):
+    n = weights.shape[1] // 2 if swiglu else weights.shape[1]
+    A = rows.shape[0] if row_ids is None else row_ids.shape[0]
+    return rows.new_empty((A, n), dtype=out_dtype)
+
+
 @_op("route_reduce")
 def route_reduce(expert_output: torch.Tensor, coefficients: torch.Tensor, inverse: torch.Tensor, rows: int,
                  top_k: int) -> torch.Tensor:
@@ -221,4 +241,4 @@ def _(packed, scales, zeros, x, bits, group_size, in_features):
 
 
 OPS = ("qrow_dequant", "qrow_matmul", "qrow_swiglu", "qrow_top2", "act_quant", "int8_gemm", "w8a8_matmul",
-       "moe_router", "moe_route", "grouped_int8_mm", "route_reduce", "lowbit_matmul")
+       "moe_router", "moe_route", "grouped_int8_mm", "grouped_w8a16_mm", "route_reduce", "lowbit_matmul")

@@ -9,10 +9,16 @@ Restates (reference paths relative to /root/reference):
                            analogue of ``quantize_fp8_activation`` olmoe_cuda.py:1173-1176)
 * ``grouped_int8_mm``   -- per-group exact int GEMM with the epilogue
                            ``(acc * a_scale[m]) * w_scale[n]`` (olmoe_cuda.py:185-238)
+* ``grouped_w8a16_mm``  -- ``_grouped_bf16_kernel`` (qwen3_moe_cuda.py:2117-2157) over
+                           weights ``bf16(float(code) * scale)``: fp32 result of the bf16
+                           GEMM, bf16 SwiGLU halves as PackedBF16ExpertBackend.moe
+                           (:3020-3033)
 * ``stable_route_reduce`` -- CPU branch qwen3_moe_cuda.py:2655-2664
 * ``moe_forward``       -- the W8A8-shaped expert flow of FP8ExpertBackend.moe
                            (olmoe_cuda.py:1308-1420) with the stable reducer
                            (qwen3_moe_cuda.py:2911-2920) and bf16 boundaries
+* ``moe_forward_w8a16`` -- the weight-only flow of PackedBF16ExpertBackend.moe
+                           (qwen3_moe_cuda.py:2978-3046) on int8 pages, stable reducer
 * ``moe_dense_reference`` -- per-expert float math of streamed_moe_forward
                            (moe_safetensors.py:603-627), weights dequantized to fp32, in float64
 * ``moe_streamed_reference`` -- the same in the model dtype (bf16 / fp32 roundings)
@@ -24,7 +30,9 @@ routines for the router; exact integer brute force for the grouped GEMM; the den
 per-expert formulation for the whole layer (tolerance).  ``moe_dense_reference`` and
 ``moe_streamed_reference`` are pinned by tests/golden/moe_forward.npz, written by the
 reference's own streamed_moe_forward on a tiny Qwen3-MoE layer: fp32 within 1e-6, and the
-bf16 restatement reproduces the reference's residual bit for bit.
+bf16 restatement reproduces the reference's residual bit for bit.  ``grouped_w8a16_mm``
+is pinned by the same golden: its per-expert outputs, accumulated in the reference's
+expert order, give the reference's bf16 residual bit for bit.
 """
 
 from __future__ import annotations
@@ -93,6 +101,32 @@ def grouped_int8_mm(rows_q, row_scales, weights, weight_scales, starts, counts, 
     return out
 
 
+def grouped_w8a16_mm(rows, weights, weight_scales, starts, counts, *, slots=None, swiglu: bool = False,
+                     out_bf16: bool = True):
+    """Per group: ``rows @ bf16(code * scale)^T``, summed in float64 and rounded once to
+    fp32 (the kernel's fp32 accumulation order is not fixed); SwiGLU takes gate rows
+    ``[0, N)`` and up rows ``[N, 2N)`` with the bf16 roundings of the reference's eager
+    ``F.silu(gate) * up`` on bf16 halves."""
+    rows = np.asarray(rows, dtype=np.float32)
+    n_w = weights.shape[1]
+    n_out = n_w // 2 if swiglu else n_w
+    out = np.zeros((rows.shape[0], n_out), dtype=np.float32)
+    for g in range(len(starts)):
+        s0, c = int(starts[g]), int(counts[g])
+        if c == 0:
+            continue
+        slot = g if slots is None else int(slots[g])
+        w = round_bf16(weights[slot].astype(np.float32) * weight_scales[slot][:, None]).astype(np.float64)
+        v = (rows[s0 : s0 + c].astype(np.float64) @ w.T).astype(np.float32)
+        if swiglu:
+            gt = round_bf16(v[:, :n_out])
+            ut = round_bf16(v[:, n_out:])
+            out[s0 : s0 + c] = round_bf16(round_bf16(silu_f32(gt)) * ut)
+        else:
+            out[s0 : s0 + c] = round_bf16(v) if out_bf16 else v
+    return out
+
+
 def stable_route_reduce(expert_output, coefficients, inverse, rows: int, k: int):
     eo = np.asarray(expert_output, dtype=np.float32)
     cf = np.asarray(coefficients, dtype=np.float32)
@@ -113,6 +147,17 @@ def moe_forward(source, top_indices, top_weights, gate_up, gate_up_scales, down,
     act = grouped_int8_mm(q, s, gate_up, gate_up_scales, starts, counts, swiglu=True)
     q2, s2 = quantize_rows(act)
     y = grouped_int8_mm(q2, s2, down, down_scales, starts, counts)
+    return round_bf16(stable_route_reduce(y, coef, inverse, rows, k))
+
+
+def moe_forward_w8a16(source, top_indices, top_weights, gate_up, gate_up_scales, down, down_scales):
+    """Weight-only int8 expert layer (bf16 activations), returns bf16-rounded fp32 [T, H]."""
+    E = gate_up.shape[0]
+    rows, k = top_indices.shape
+    token_ids, coef, starts, counts, inverse = route_stable(top_indices, top_weights, E)
+    x = round_bf16(np.asarray(source, dtype=np.float32))[token_ids]
+    act = grouped_w8a16_mm(x, gate_up, gate_up_scales, starts, counts, swiglu=True)
+    y = grouped_w8a16_mm(act, down, down_scales, starts, counts)
     return round_bf16(stable_route_reduce(y, coef, inverse, rows, k))
 
 

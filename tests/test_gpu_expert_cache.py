@@ -84,6 +84,20 @@ def test_route_prefetch_stages_evicted_next_layer_pages(dev, tmp_path):
     cache.close()
 
 
+def test_paged_w8a16_backend_equals_resident(dev, tmp_path):
+    """The weight-only flow over paged experts (slot-indirect binding, evictions) gives the
+    resident weight-only flow's results bit for bit."""
+    ec, moe = _mods()
+    store, resident = _setup(tmp_path, dev)
+    resident = moe.Int8ExpertBackend(resident.layers, w8a16=True)
+    cache = ec.ExpertPageCache(store, device=dev, cache_mb=40 * store.layout.page_stride / 1e6, max_active_pages=16)
+    paged = moe.Int8ExpertBackend(page_cache=cache, w8a16=True)
+    for layer, x, idx, w in _steps(dev, 3, 16):
+        assert torch.equal(paged.moe(layer, x, idx, w), resident.moe(layer, x, idx, w)), layer
+    assert cache.stats.evictions > 0
+    cache.close()
+
+
 def test_cache_holds_everything_after_one_pass(dev, tmp_path):
     ec, moe = _mods()
     store, resident = _setup(tmp_path, dev, L=2, E=8)

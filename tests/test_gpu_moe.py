@@ -296,3 +296,96 @@ def test_moe_layer_config4(dev, T):
     assert y.dtype == torch.bfloat16 and y.shape == (T, H)
     ref = om.moe_forward(x, ti.cpu().numpy(), tw.float().cpu().numpy(), gu, gus, dn, dns)
     assert oq.rel_l2(y.float().cpu().numpy(), ref) <= 1e-3
+
+
+# ---- weight-only (W8A16) grouped GEMM over the same int8 pages --------------------------
+
+
+def _w16_rows(rng, n, H):
+    return oq.round_bf16(rng.standard_normal((n, H)).astype(np.float32))
+
+
+@pytest.mark.parametrize("swiglu", [False, True])
+# K = H: one staged phase (256, 2048), 64-code chunks (320), several K phases (4096 at
+# 64 rows, 12288)
+@pytest.mark.parametrize("H,max_rows", [(256, None), (320, None), (2048, None), (4096, 4000), (12288, None)])
+def test_grouped_w8a16_matches_oracle(dev, swiglu, H, max_rows):
+    rng = np.random.default_rng(17)
+    E, I, T, k = 16, 128, 40, 4
+    gu, gus, dn, dns = _layer(rng, E, H, I)
+    top = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
+    tok, coef, starts, counts, inv = om.route_stable(top, np.ones((T, k), np.float32), E)
+    rows = _w16_rows(rng, T * k, H)
+    layer = _moe().Int8ExpertLayer.from_arrays(*(torch.from_numpy(v) for v in (gu, gus, dn, dns)), dev)
+    args = (_t(rows, dev, torch.bfloat16), layer.gate_up, layer.gate_up_scales, _t(starts, dev), _t(counts, dev))
+    if swiglu:
+        out, tag = _moe().grouped_w8a16_mm(*args, swiglu=True, max_rows=max_rows)
+        assert tag.startswith("hip-gfx950-")
+        ref = om.grouped_w8a16_mm(rows, gu, gus, starts, counts, swiglu=True)
+        assert oq.rel_l2(out.float().cpu().numpy(), ref) <= 1e-3
+    else:
+        out, _ = _moe().grouped_w8a16_mm(*args, out_dtype=torch.float32, max_rows=max_rows)
+        ref = om.grouped_w8a16_mm(rows, gu, gus, starts, counts, out_bf16=False)
+        # exact bf16 products, fp32 sums in another order than the oracle's float64 sum
+        assert oq.rel_l2(out.cpu().numpy(), ref) <= 1e-5
+        o16, _ = _moe().grouped_w8a16_mm(*args, max_rows=max_rows)
+        assert torch.equal(o16, out.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("max_rows", [0, 16, 400, 4000])  # row tiles of 32, 16, 64, 64 rows
+def test_grouped_w8a16_row_tiles_gather_and_slots(dev, max_rows):
+    """Skewed routing (expert 0 takes every token) over several row passes; the in-kernel
+    gather (row_ids) equals gathering first; slot indirection equals compact weights; an
+    id outside the source reads zeros."""
+    rng = np.random.default_rng(19)
+    E, H, I, T, k = 8, 2048, 128, 200, 2
+    gu, gus, dn, dns = _layer(rng, E, H, I)
+    top = np.stack([np.concatenate([[0], 1 + rng.permutation(E - 1)[: k - 1]]) for _ in range(T)]).astype(np.int64)
+    tok, coef, starts, counts, inv = om.route_stable(top, np.ones((T, k), np.float32), E)
+    assert counts.max() == T
+    src = _w16_rows(rng, T, H)
+    layer = _moe().Int8ExpertLayer.from_arrays(*(torch.from_numpy(v) for v in (gu, gus, dn, dns)), dev)
+    st, ct = _t(starts, dev), _t(counts, dev)
+    got, _ = _moe().grouped_w8a16_mm(_t(src, dev, torch.bfloat16), layer.gate_up, layer.gate_up_scales, st, ct,
+                                     row_ids=_t(tok, dev), max_rows=max_rows, swiglu=True)
+    ref = om.grouped_w8a16_mm(src[tok], gu, gus, starts, counts, swiglu=True)
+    assert oq.rel_l2(got.float().cpu().numpy(), ref) <= 1e-3
+    pre, _ = _moe().grouped_w8a16_mm(_t(src[tok], dev, torch.bfloat16), layer.gate_up, layer.gate_up_scales, st, ct,
+                                     max_rows=max_rows, swiglu=True)
+    assert torch.equal(got, pre)
+    perm = rng.permutation(E)
+    slots = np.argsort(perm).astype(np.int32)
+    phys = _moe().Int8ExpertLayer.from_arrays(*(torch.from_numpy(v[perm]) for v in (gu, gus, dn, dns)), dev)
+    act = _t(_w16_rows(rng, T * k, I), dev, torch.bfloat16)
+    o1, _ = _moe().grouped_w8a16_mm(act, phys.down, phys.down_scales, st, ct, group_slots=_t(slots, dev),
+                                    max_rows=max_rows)
+    o2, _ = _moe().grouped_w8a16_mm(act, layer.down, layer.down_scales, st, ct, max_rows=max_rows)
+    assert torch.equal(o1, o2)
+    bad = tok.copy()
+    bad[3] = T  # outside the source
+    ob, _ = _moe().grouped_w8a16_mm(_t(src, dev, torch.bfloat16), layer.gate_up, layer.gate_up_scales, st, ct,
+                                    row_ids=_t(bad, dev), max_rows=max_rows, swiglu=True)
+    assert torch.all(ob[3] == 0) and torch.equal(ob[:3], got[:3]) and torch.equal(ob[4:], got[4:])
+
+
+@pytest.mark.parametrize("T", [64, 512])
+def test_moe_layer_config4_w8a16(dev, T):
+    """BASELINE config 4 through the weight-only flow: bf16 activations, no per-token
+    quantization; closer to the float formulation than the W8A8 flow."""
+    rng = np.random.default_rng(T + 1)
+    E, k, H, I = 128, 8, 2048, 768
+    gu, gus, dn, dns = _layer(rng, E, H, I)
+    gus /= np.sqrt(H)
+    dns /= np.sqrt(I)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    x = oq.round_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    layer = _moe().Int8ExpertLayer.from_arrays(*(torch.from_numpy(v) for v in (gu, gus, dn, dns)), dev)
+    tw, ti = _moe().route_topk(_t(logits, dev), k)
+    y = _moe().Int8ExpertBackend([layer], w8a16=True).moe(0, _t(x, dev, torch.bfloat16), ti, tw)
+    assert y.dtype == torch.bfloat16 and y.shape == (T, H)
+    idx, w = ti.cpu().numpy(), tw.float().cpu().numpy()
+    ref = om.moe_forward_w8a16(x, idx, w, gu, gus, dn, dns)
+    assert oq.rel_l2(y.float().cpu().numpy(), ref) <= 1e-3
+    y8 = _moe().Int8ExpertBackend([layer]).moe(0, _t(x, dev, torch.bfloat16), ti, tw)
+    dense = om.moe_dense_reference(x, idx, w, gu, gus, dn, dns)
+    assert oq.rel_l2(y.float().cpu().numpy(), dense) < oq.rel_l2(y8.float().cpu().numpy(), dense)

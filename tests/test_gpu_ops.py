@@ -71,13 +71,14 @@ def _step(Q, o):
     act = Q.grouped_int8_mm(qx, sx, o["gu"], o["gus"], starts, counts, None, 0, True, torch.bfloat16)
     red = Q.route_reduce(act.float(), coef.float(), inv, o["np"]["T"], o["np"]["k"])
     lb = Q.lowbit_matmul(o["packed"], o["lsc"], None, y32, 3, 128, 256)
-    return h, y, y32, top_i, top_v, w, idx, tok, act, red, lb
+    act16 = Q.grouped_w8a16_mm(o["src"], o["gu"], o["gus"], starts, counts, tok, None, 0, True, torch.bfloat16)
+    return h, y, y32, top_i, top_v, w, idx, tok, act, red, lb, act16
 
 
 def test_ops_against_oracle(dev, Q):
     o = _operands(dev)
     n = o["np"]
-    h, y, y32, top_i, top_v, w, idx, tok, act, red, lb = _step(Q, o)
+    h, y, y32, top_i, top_v, w, idx, tok, act, red, lb, act16 = _step(Q, o)
     h_ref = oq.qrow_swiglu(n["gc"], n["gs"], n["uc"], n["us"], n["x"])
     assert oq.rel_l2(h.float().cpu().numpy(), h_ref) <= BF16_TOL
     hb = h.float().cpu().numpy()
@@ -97,6 +98,8 @@ def test_ops_against_oracle(dev, Q):
     tk, cf, st, cn, iv = om.route_stable(ridx, rw, n["E"])
     act_ref = om.grouped_int8_mm(q_r, s_r, n["gu"], n["gus"], st, cn, swiglu=True)
     assert np.array_equal(act.float().cpu().numpy(), act_ref)
+    act16_ref = om.grouped_w8a16_mm(n["src"][r_tok], n["gu"], n["gus"], st, cn, swiglu=True)
+    assert oq.rel_l2(act16.float().cpu().numpy(), act16_ref) <= BF16_TOL
     red_ref = om.stable_route_reduce(act_ref, cf, iv, n["T"], n["k"])
     assert np.array_equal(red.cpu().numpy(), red_ref)
     lb_ref = ol.lowbit_matmul(n["packed"], n["lsc"], y32.cpu().numpy(), 256, 3, 128)

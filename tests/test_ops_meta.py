@@ -48,5 +48,9 @@ def test_fake_shapes(ops):
     g = q.grouped_int8_mm(_e(40, 64, dtype=torch.int8), _e(40), _e(32, 96, 64, dtype=torch.int8), _e(32, 96),
                           _e(32, dtype=torch.int32), _e(32, dtype=torch.int32), None, 0, True, torch.bfloat16)
     assert g.shape == (40, 48)
+    g16 = q.grouped_w8a16_mm(_e(10, 64, dtype=torch.bfloat16), _e(32, 96, 64, dtype=torch.int8), _e(32, 96),
+                             _e(32, dtype=torch.int32), _e(32, dtype=torch.int32), _e(40, dtype=torch.int64), None,
+                             0, True, torch.bfloat16)
+    assert g16.shape == (40, 48) and g16.dtype == torch.bfloat16
     assert q.route_reduce(_e(40, 16), _e(40), _e(40, dtype=torch.int64), 10, 4).shape == (10, 16)
     assert q.lowbit_matmul(_e(96, 24, dtype=torch.uint8), _e(96, 1), None, _e(2, 64), 3, 64, 64).shape == (2, 96)
