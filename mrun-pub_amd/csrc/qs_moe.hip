@@ -781,7 +781,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream(MoeGemmParams p) {
 // W chunks, so the window's register slot of chunk c stays c % W.  With row_ids, staged
 // row r of the group is source row row_ids[start + r] (the reference's
 // source.index_select(token_ids) folded into the staging); an id outside [0, src_rows)
-// stages zeros.
+// stages zeros.  A pass's ids are requested before its weight window and kept in LDS
+// (after the staged rows), so no staging load waits on an id load.
 struct MoeW16Params {
   const uint16_t* a;      // bf16 [src_rows or A, K]
   const int64_t* row_ids; // nullable gather of the routed rows
@@ -833,6 +834,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream_w16(MoeW16Params p) {
     wsc[b] = p.ws[(int64_t)slot * p.ws_stride + nb];
   }
 
+  int64_t* rid = reinterpret_cast<int64_t*>(lds + MC * xstride);  // [MC] source rows, -1 = zeros
   // rows m0 .. m0 + mc of the group, elements k0 .. k0 + KPH (or K), 8 loads in flight
   auto stage = [&](int m0, int mc, int k0) {
     const int ppr = min(KPH, K - k0) >> 3;  // 16-byte pieces per staged row
@@ -844,13 +846,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream_w16(MoeW16Params p) {
         int i = i0 + j * NT + tid;
         i = i < tot ? i : 0;
         const int t = i / ppr, pc = i - t * ppr;
-        int64_t r = start + m0 + t;
-        bool ok = true;
-        if (p.row_ids) {
-          r = p.row_ids[r];
-          ok = r >= 0 && r < p.src_rows;
-        }
-        v[j] = ok ? *reinterpret_cast<const i32x4*>(p.a + r * K + k0 + pc * 8) : i32x4{0, 0, 0, 0};
+        const int64_t r = p.row_ids ? rid[t] : start + m0 + t;
+        v[j] = r >= 0 ? *reinterpret_cast<const i32x4*>(p.a + r * K + k0 + pc * 8) : i32x4{0, 0, 0, 0};
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -865,6 +862,9 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream_w16(MoeW16Params p) {
 
   for (int m0 = 0; m0 < count; m0 += MC) {
     const int mc = min(MC, count - m0);
+    int64_t id = -1;
+    if (p.row_ids && tid < mc) id = p.row_ids[start + m0 + tid];
+    __builtin_amdgcn_sched_barrier(0);
     i32x4 wv[W][NB][PL];
 #pragma unroll
     for (int u = 0; u < W; ++u) {
@@ -875,6 +875,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream_w16(MoeW16Params p) {
           wv[u][b][j] = *reinterpret_cast<const i32x4*>(wr[b] + (int64_t)min(u, C - 1) * CB + 16 * j);
         __builtin_amdgcn_sched_barrier(0);
       }
+    }
+    if (p.row_ids) {
+      if (tid < mc) rid[tid] = id >= 0 && id < p.src_rows ? id : -1;
+      __syncthreads();
     }
     stage(m0, mc, 0);
     __syncthreads();
@@ -1176,37 +1180,56 @@ void launch_moe_stream(const MoeGemmParams& p, int G, int MT, hipStream_t s) {
 }
 // K phase of k_moe_stream_w16: the whole K when MC staged rows fit kMoeStreamLds, else
 // the fewest phases of a multiple of W chunks each that fit.
-int moe_w16_phase(int MT, int64_t K, int CB, int W) {
+int moe_w16_phase(int MT, int64_t K, int CB, int W, size_t cap) {
   const int64_t C = K / CB;
   for (int64_t kp = 1; kp <= C; ++kp) {
     const int64_t cph = kp == 1 ? C : cdiv(cdiv(C, kp), W) * W;
-    if ((size_t)16 * MT * (size_t)(2 * cph * CB + 16) <= kMoeStreamLds) return (int)(cph * CB);
+    if ((size_t)16 * MT * (size_t)(2 * cph * CB + 16 + 8) <= cap) return (int)(cph * CB);
   }
   return 0;
 }
 
-template <int P, int NB, int MT, int PAIR>
-void launch_moe_w16_mt(MoeW16Params p, int G, hipStream_t s) {
-  constexpr int WAVES = P == 2 ? (MT == 1 ? 4 : 8) : 4;
-  constexpr int WP = P == 2 ? 2 : (NB >= 2 ? 1 : 2);  // 128-byte chunks in flight
+// Launch shapes of k_moe_stream_w16, measured on config-4 shapes (E 128, H 2048, I 768):
+// SwiGLU as the int8 stream (4 waves for one row tile, else 8; two 128-byte chunks in
+// flight).  Plain products with 64-row passes (MT = 4) use 4 waves of NB tiles and cap the
+// staged slice at 72 KB so that two or three workgroups share a CU (T = 512 down
+// 74 -> 51 us); shorter passes use 8 waves of at most 2 tiles (T = 64 down 41 -> 36 us).
+// The dequantization costs 2.5 VALU operations per code, so the stream needs more waves
+// per SIMD than the int8 one to keep its loads in flight.
+template <int P, int NB, int MT, int PAIR, int WAVES>
+void launch_moe_w16_mt(MoeW16Params p, int G, size_t cap, hipStream_t s) {
+  constexpr int WP = P == 2 ? 2 : (NB >= 2 ? 1 : 2);  // w16 chunks in flight
   constexpr int W = PAIR ? WP : 2 * WP;
   constexpr int RW = MoeStreamCfg<P, NB>::RW;
-  p.KPH = moe_w16_phase(MT, p.K, PAIR ? 128 : 64, W);
-  const size_t lds = (size_t)16 * MT * (size_t)(2 * p.KPH + 16);
+  p.KPH = moe_w16_phase(MT, p.K, PAIR ? 128 : 64, W, cap);
+  const size_t lds = (size_t)16 * MT * (size_t)(2 * p.KPH + 16 + 8);  // staged rows + their ids
   const dim3 grid((unsigned)cdiv(p.N, RW * WAVES), (unsigned)G), block(WAVES * 64);
   hipLaunchKernelGGL((k_moe_stream_w16<P, NB, MT, W, WAVES, PAIR>), grid, block, lds, s, p);
 }
 
-template <int P, int NB>
-void launch_moe_w16(const MoeW16Params& p, int G, int MT, hipStream_t s) {
-  if (p.K % 128 == 0) {
-    if (MT == 4) launch_moe_w16_mt<P, NB, 4, 1>(p, G, s);
-    else if (MT == 2) launch_moe_w16_mt<P, NB, 2, 1>(p, G, s);
-    else launch_moe_w16_mt<P, NB, 1, 1>(p, G, s);
+template <int P, int NB, int MT, int WAVES>
+void launch_moe_w16_pair(const MoeW16Params& p, int G, size_t cap, hipStream_t s) {
+  if (p.K % 128 == 0) launch_moe_w16_mt<P, NB, MT, 1, WAVES>(p, G, cap, s);
+  else launch_moe_w16_mt<P, NB, MT, 0, WAVES>(p, G, cap, s);
+}
+
+void launch_moe_w16(const MoeW16Params& p, int G, int MT, bool swiglu, hipStream_t s) {
+  const int64_t K = p.K;
+  if (swiglu) {
+    if (MT == 4) launch_moe_w16_pair<2, 2, 4, 8>(p, G, kMoeStreamLds, s);
+    else if (MT == 2) launch_moe_w16_pair<2, 2, 2, 8>(p, G, kMoeStreamLds, s);
+    else launch_moe_w16_pair<2, 2, 1, 4>(p, G, kMoeStreamLds, s);
+  } else if (MT == 4) {
+    constexpr size_t cap = 72 * 1024;
+    if (K <= 1024) launch_moe_w16_pair<1, 4, 4, 4>(p, G, cap, s);
+    else if (K <= 2048) launch_moe_w16_pair<1, 2, 4, 4>(p, G, cap, s);
+    else launch_moe_w16_pair<1, 1, 4, 4>(p, G, cap, s);
+  } else if (MT == 2) {
+    if (K <= 2048) launch_moe_w16_pair<1, 2, 2, 8>(p, G, kMoeStreamLds, s);
+    else launch_moe_w16_pair<1, 1, 2, 8>(p, G, kMoeStreamLds, s);
   } else {
-    if (MT == 4) launch_moe_w16_mt<P, NB, 4, 0>(p, G, s);
-    else if (MT == 2) launch_moe_w16_mt<P, NB, 2, 0>(p, G, s);
-    else launch_moe_w16_mt<P, NB, 1, 0>(p, G, s);
+    if (K <= 2048) launch_moe_w16_pair<1, 2, 1, 8>(p, G, kMoeStreamLds, s);
+    else launch_moe_w16_pair<1, 1, 1, 8>(p, G, kMoeStreamLds, s);
   }
 }
 }  // namespace
@@ -1236,10 +1259,7 @@ extern "C" int qs_moe_grouped_gemm_w8a16(const void* a, const int64_t* row_ids, 
   // row tiles sized for twice the mean rows per group, as the int8 stream
   const int64_t mean = max_rows > 0 ? cdiv(max_rows, G) : 16;
   const int MT = 2 * mean <= 16 ? 1 : (2 * mean <= 32 ? 2 : 4);
-  if (swiglu) launch_moe_w16<2, 2>(p, G, MT, s);
-  else if (K <= 1024) launch_moe_w16<1, 4>(p, G, MT, s);
-  else if (K <= 2048) launch_moe_w16<1, 2>(p, G, MT, s);
-  else launch_moe_w16<1, 1>(p, G, MT, s);
+  launch_moe_w16(p, G, MT, swiglu != 0, s);
   return hip_check(hipGetLastError(), "k_moe_stream_w16 launch");
 }
 
