@@ -515,7 +515,10 @@ __global__ __launch_bounds__(kGkMaxWaves * 64) void k_lowbit_gk(LowbitParams p) 
     const int t = lane + 64 * u;
     if (t < TWT) lw[t] = sw[u];
   }
-  __syncthreads();
+  // the staging area is the wave's own: its LDS writes complete in order before its reads,
+  // so no workgroup barrier (each wave starts as soon as its own codes have landed)
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
   // the lane's quarter field of group i in row tile rt: QB bytes at i * CB + q * QB of its
   // row (2- or 4-byte aligned), as a little-endian bit field
