@@ -416,7 +416,7 @@ __device__ __forceinline__ i32x4 fp4_pair_order(i32x4 v) {
 
 constexpr int kGkMaxWaves = 16;
 template <int G>
-constexpr int kGkGroupsShort = G == 64 ? 8 : 4;  // two row tiles, every activation in VGPRs
+constexpr int kGkGroupsShort = G == 64 ? 8 : 4;  // 2-3 row tiles, every activation in VGPRs
 template <int G>
 constexpr int kGkGroupsLong = G == 64 ? 12 : 6;  // one row tile, activations streamed
 template <int G, int NGR>
@@ -637,10 +637,12 @@ void launch_gk_n(const LowbitParams& p, hipStream_t s) {
   }
 }
 
-// the short form (two row tiles) while its waves fit a workgroup
+// the short form (two or three row tiles) while its waves fit a workgroup
 template <int BITS, int G>
 void launch_gk(const LowbitParams& p, hipStream_t s) {
-  if (p.ng <= kGkMaxWaves * kGkGroupsShort<G>) launch_gk_n<BITS, G, kGkGroupsShort<G>, 2>(p, s);
+  // int2 takes three row tiles per workgroup: 11008 rows make 230 workgroups, at most one
+  // per CU (9.8 us against 10.9 us with two tiles at M=8); int3 keeps two (12.9 against 13.3)
+  if (p.ng <= kGkMaxWaves * kGkGroupsShort<G>) launch_gk_n<BITS, G, kGkGroupsShort<G>, BITS == 2 ? 3 : 2>(p, s);
   else launch_gk_n<BITS, G, kGkGroupsLong<G>, 1>(p, s);
 }
 
