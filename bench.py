@@ -369,6 +369,34 @@ def paged_moe_measurement(torch, dev, E: int, topk: int, H: int, I: int, layers:
     return res
 
 
+def profile_lowbit(torch, dev, calls: int) -> dict:
+    """Eager launches of config 5 (int3 / int2 G64, fp16 scale + zero, both shapes, M = 1
+    and 8), ``calls`` per case on weight copies that rotate past the Infinity Cache, for
+    kernel traces and counter runs; prints each case's algorithmic bytes."""
+    from mrun_pub_amd import lowbit
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    out: dict = {"profile": "lowbit", "calls": calls}
+    for bits in (3, 2):
+        for (N5, K5) in ((11008, 4096), (4096, 11008)):
+            rb = K5 * bits // 8
+            ng = K5 // 64
+            copies = max(2, (512 << 20) // (N5 * rb) + 1)
+            packed = torch.randint(0, 256, (copies, N5, rb), dtype=torch.uint8, device=dev, generator=gen)
+            sc = ((torch.rand(copies, N5, ng, device=dev, generator=gen) + 0.5) / 7).to(torch.float16)
+            zp = (torch.rand(copies, N5, ng, device=dev, generator=gen) * 7).to(torch.float16)
+            pages = [lowbit.LowbitPage("w", bits, 64, K5, packed[c], sc[c], zp[c]) for c in range(copies)]
+            for M5 in (1, 8):
+                x5 = torch.randn(M5, K5, device=dev, generator=gen).to(torch.bfloat16)
+                for i in range(calls):
+                    lowbit.lowbit_matmul(pages[i % copies], x5)
+                out[f"int{bits}_{N5}x{K5}_m{M5}_bytes"] = N5 * rb + 2 * 2 * N5 * ng + 2 * M5 * K5 + 4 * M5 * N5
+            del packed, sc, zp, pages
+    torch.cuda.synchronize()
+    return out
+
+
 def profile_mfma_kernels(torch, dev, which: str, calls: int) -> dict:
     """Eager launches of config 3's fused W8A8 GEMM or config 4's MoE layer, for counter runs
     (MFMA utilisation, HBM bytes); prints the algorithmic figures to compare against."""
@@ -578,12 +606,13 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-secondary", action="store_true", help="skip configs 1/3/4/5")
-    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "w8a8p", "moe", "moe16"),
+    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "w8a8p", "moe", "moe16", "lowbit"),
                     help="for rocprofv3 runs: replay exactly the timed graph of the roofline kernel (28 "
                     "paired gate/up+SwiGLU launches) or of the headline pass, --steps times after "
                     "--warmup replays; a plain 256 MiB device copy x5 (counter calibration); or config 3's "
                     "fused W8A8 GEMM (M=512 and 2048), config 3's whole w8a8_matmul with protect_k=8 (w8a8p) / "
-                    "config 4's MoE layer (T=64 and 512; moe16: the weight-only flow), --steps calls each")
+                    "config 4's MoE layer (T=64 and 512; moe16: the weight-only flow), or config 5's low-bit "
+                    "GEMV/GEMM (both shapes, int3/int2, M=1 and 8), --steps calls each")
     ap.add_argument("--eager", action="store_true",
                     help="with --profile swiglu/stack: launch the same sequence eagerly instead of replaying "
                     "the graph (counter collection needs eager dispatches)")
@@ -617,6 +646,9 @@ def main() -> int:
         return 0
     if args.profile in ("w8a8", "w8a8p", "moe", "moe16"):
         print(json.dumps(profile_mfma_kernels(torch, dev, args.profile, args.steps)), flush=True)
+        return 0
+    if args.profile == "lowbit":
+        print(json.dumps(profile_lowbit(torch, dev, args.steps)), flush=True)
         return 0
     arena, pages = build_stack(torch, dev)
     gen = torch.Generator(device=dev)
