@@ -223,6 +223,19 @@ int qs_moe_route(const void* top_idx, int idx_dtype, const void* top_w, int w_dt
                  int k, int E, int64_t* token_ids, float* coef, int32_t* starts, int32_t* counts,
                  int64_t* inverse, void* stream);
 
+/* qs_moe_route plus the W8A8 per-token quantization of the T source rows
+ * (quantize_fp8_activation olmoe_cuda.py:1173-1176 with the int8 recipe of
+ * w8a8.py:118-121, applied before the gather of FP8ExpertBackend.moe :1340-1345):
+ * q[t] / scale[t] = the codes and scale of source row t, unpermuted, in the same launch as
+ * the route when E * T * k <= 2^22 and the rows are 16-byte aligned with H % 8 == 0
+ * (otherwise two launches).  A row's codes do not depend on its expert, so
+ * qs_moe_grouped_gemm_i8_rows(q, scale, token_ids, ...) multiplies exactly the rows
+ * qs_moe_gather_quant(source, token_ids) would produce. */
+int qs_moe_route_quant(const void* top_idx, int idx_dtype, const void* top_w, int w_dtype, int64_t T,
+                       int k, int E, int64_t* token_ids, float* coef, int32_t* starts, int32_t* counts,
+                       int64_t* inverse, const void* source, int src_dtype, int64_t ld_src, int64_t H,
+                       int8_t* q, float* scale, void* stream);
+
 /* Replaces build_expert_queue / build_expert_queue_flat / build_expert_queue_device
  * (src/mrun/engine/kernels/expert_queue.py:242-470): compiles A router packets into
  * expert-major ranges in STABLE order (equal to the reference's CPU argsort(stable=True)).
@@ -278,6 +291,16 @@ int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* 
                            const int32_t* starts, const int32_t* counts, const int32_t* slots,
                            int G, int64_t N, int64_t K, int64_t max_rows, int swiglu, void* out,
                            int out_dtype, void* stream);
+
+/* qs_moe_grouped_gemm_i8 whose queue row r reads a[row_ids[r]] and a_scale[row_ids[r]]
+ * (the gather source.index_select(0, token_ids) of FP8ExpertBackend.moe, olmoe_cuda.py:
+ * 1340-1345, folded into the kernel's staging; ids outside [0, src_rows) read zero rows).
+ * Needs the streaming kernel: 16 staged rows of K + 28 bytes must fit 144 KiB of LDS. */
+int qs_moe_grouped_gemm_i8_rows(const int8_t* a, const float* a_scale, const int64_t* row_ids,
+                                int64_t src_rows, const int8_t* w, int64_t w_stride, const float* w_scale,
+                                int64_t ws_stride, const int32_t* starts, const int32_t* counts,
+                                const int32_t* slots, int G, int64_t N, int64_t K, int64_t max_rows,
+                                int swiglu, void* out, int out_dtype, void* stream);
 
 /* Replaces grouped_bf16_mm / _grouped_bf16_kernel (qwen3_moe_cuda.py:2473-2510, 2117-2157)
  * as used by PackedBF16ExpertBackend.moe (:2978-3046), over int8 expert pages (the weight-

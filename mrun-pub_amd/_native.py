@@ -68,11 +68,13 @@ SIGNATURES: dict[str, tuple] = {
     "qs_w8a8_gemm": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _I, _L, _L, _L, _P]),
     "qs_moe_router": (_I, [_P, _I, _L, _I, _I, _I, _P, _P, _I, _P]),
     "qs_moe_route": (_I, [_P, _I, _P, _I, _L, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "qs_moe_route_quant": (_I, [_P, _I, _P, _I, _L, _I, _I, _P, _P, _P, _P, _P, _P, _I, _L, _L, _P, _P, _P]),
     "qs_expert_queue_build": (_I, [_P, _I, _P, _P, _P, _I, _P, _P, _L, _I, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
     "qs_expert_queue_scatter_workspace_bytes": (ctypes.c_size_t, [_L, _I]),
     "qs_expert_queue_scatter": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _L, _P, ctypes.c_size_t, _P, _P, _P]),
     "qs_moe_gather_quant": (_I, [_P, _I, _L, _P, _L, _L, _P, _P, _P]),
     "qs_moe_grouped_gemm_i8": (_I, [_P, _P, _P, _L, _P, _L, _P, _P, _P, _I, _L, _L, _L, _I, _P, _I, _P]),
+    "qs_moe_grouped_gemm_i8_rows": (_I, [_P, _P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _I, _L, _L, _L, _I, _P, _I, _P]),
     "qs_moe_grouped_gemm_w8a16": (_I, [_P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _I, _L, _L, _L, _I, _P, _I, _P]),
     "qs_moe_route_reduce": (_I, [_P, _I, _P, _P, _L, _I, _L, _P, _P]),
     "qs_moe_route_reduce_to": (_I, [_P, _I, _P, _P, _L, _I, _L, _P, _I, _P]),

@@ -278,11 +278,11 @@ constexpr int kParWaves = 8;
 constexpr int kParSegs = 8;
 
 template <int IT, int WT>
-__global__ __launch_bounds__(kParWaves * 64) void k_moe_route_par(
-    const void* __restrict__ top_idx, const void* __restrict__ top_w, int A, int k, int E,
-    int64_t* __restrict__ token_ids, float* __restrict__ coef, int32_t* __restrict__ starts,
-    int32_t* __restrict__ counts, int64_t* __restrict__ inverse) {
-  const int e = blockIdx.x;
+__device__ __forceinline__ void route_par_body(int e, const void* __restrict__ top_idx,
+                                               const void* __restrict__ top_w, int A, int k, int E,
+                                               int64_t* __restrict__ token_ids, float* __restrict__ coef,
+                                               int32_t* __restrict__ starts, int32_t* __restrict__ counts,
+                                               int64_t* __restrict__ inverse) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   auto expert_of = [&](int i) -> int {
     if constexpr (IT == QS_I64) return (int)static_cast<const int64_t*>(top_idx)[i];
@@ -357,6 +357,14 @@ __global__ __launch_bounds__(kParWaves * 64) void k_moe_route_par(
     }
 }
 
+template <int IT, int WT>
+__global__ __launch_bounds__(kParWaves * 64) void k_moe_route_par(
+    const void* __restrict__ top_idx, const void* __restrict__ top_w, int A, int k, int E,
+    int64_t* __restrict__ token_ids, float* __restrict__ coef, int32_t* __restrict__ starts,
+    int32_t* __restrict__ counts, int64_t* __restrict__ inverse) {
+  route_par_body<IT, WT>((int)blockIdx.x, top_idx, top_w, A, k, E, token_ids, coef, starts, counts, inverse);
+}
+
 // ----------------------------------------------------------------------------------
 // routed-row quantization
 // ----------------------------------------------------------------------------------
@@ -405,13 +413,12 @@ struct Piece8 {
 
 constexpr int kQuantPieces = 8;  // pieces per lane kept in registers
 
+// one wave quantizes row a (source row rows[a], or a)
 template <int XT>
-__global__ __launch_bounds__(256) void k_moe_gather_quant8(const void* __restrict__ src, int64_t ld_src,
-                                                           const int64_t* __restrict__ rows, int64_t A,
-                                                           int H, int8_t* __restrict__ q,
-                                                           float* __restrict__ scale) {
+__device__ __forceinline__ void gather_quant8_row(int64_t a, const void* __restrict__ src, int64_t ld_src,
+                                                  const int64_t* __restrict__ rows, int64_t A, int H,
+                                                  int8_t* __restrict__ q, float* __restrict__ scale) {
   const int lane = threadIdx.x & 63;
-  const int64_t a = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (a >= A) return;
   const int64_t r = rows ? rows[a] : a;
   const char* xr = static_cast<const char*>(src) + r * ld_src * (XT == QS_F32 ? 4 : 2);
@@ -462,6 +469,30 @@ __global__ __launch_bounds__(256) void k_moe_gather_quant8(const void* __restric
   else quantize(std::false_type{});
 }
 
+template <int XT>
+__global__ __launch_bounds__(256) void k_moe_gather_quant8(const void* __restrict__ src, int64_t ld_src,
+                                                           const int64_t* __restrict__ rows, int64_t A,
+                                                           int H, int8_t* __restrict__ q,
+                                                           float* __restrict__ scale) {
+  gather_quant8_row<XT>((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), src, ld_src, rows, A, H, q, scale);
+}
+
+// The route compiler (k_moe_route_par) and the per-token quantization of the T source
+// rows in one launch: workgroups 0 .. E - 1 compile the route, the rest quantize 8 source
+// rows each (a wave per row).  The two parts are independent; the grouped GEMM then reads
+// the quantized rows through token_ids (a row's codes and scale do not depend on which
+// expert it is routed to, so they equal the quantization of the gathered rows).
+template <int IT, int WT, int XT>
+__global__ __launch_bounds__(kParWaves * 64) void k_moe_route_quant(
+    const void* __restrict__ top_idx, const void* __restrict__ top_w, int A, int k, int E,
+    int64_t* __restrict__ token_ids, float* __restrict__ coef, int32_t* __restrict__ starts,
+    int32_t* __restrict__ counts, int64_t* __restrict__ inverse, const void* __restrict__ src,
+    int64_t ld_src, int64_t T, int H, int8_t* __restrict__ q, float* __restrict__ scale) {
+  const int b = (int)blockIdx.x;
+  if (b < E) route_par_body<IT, WT>(b, top_idx, top_w, A, k, E, token_ids, coef, starts, counts, inverse);
+  else gather_quant8_row<XT>((int64_t)(b - E) * kParWaves + (threadIdx.x >> 6), src, ld_src, nullptr, T, H, q, scale);
+}
+
 // ----------------------------------------------------------------------------------
 // ragged grouped int8 GEMM
 // ----------------------------------------------------------------------------------
@@ -479,6 +510,8 @@ struct MoeGemmParams {
   int K;
   void* out;             // [A, N]
   int out_dtype;
+  const int64_t* row_ids;  // k_moe_stream, nullable: queue row r reads a / as at row_ids[r]
+  int64_t src_rows;        // rows of a and as when row_ids is given
 };
 
 __device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + expf(-g))); }
@@ -644,6 +677,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream(MoeGemmParams p) {
   const int xstride = K + 16;
   int8_t* xs = reinterpret_cast<int8_t*>(lds);                 // [MC][K + 16]
   float* asl = reinterpret_cast<float*>(lds + MC * xstride);   // [MC]
+  int64_t* rid = reinterpret_cast<int64_t*>(asl + MC);          // [MC] with row_ids: source rows, -1 = zeros
   const int n0 = (bx * WAVES + wave) * RW;
   const bool live = n0 < p.N;
   const int lo = PAIR ? 32 * q : 16 * q;  // the lane's byte offset within a chunk
@@ -661,6 +695,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream(MoeGemmParams p) {
 
   for (int m0 = 0; m0 < count; m0 += MC) {
     const int mc = min(MC, count - m0);
+    // the pass's source row ids, requested before the weight window
+    int64_t id = -1;
+    if (p.row_ids && tid < mc) id = p.row_ids[start + m0 + tid];
+    __builtin_amdgcn_sched_barrier(0);
     i32x4 wv[W][NB][PL];
 #pragma unroll
     for (int u = 0; u < W; ++u) {
@@ -672,6 +710,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream(MoeGemmParams p) {
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    if (p.row_ids) {
+      if (tid < mc) rid[tid] = id >= 0 && id < p.src_rows ? id : -1;
+      __syncthreads();
+    }
     // routed rows m0 .. m0 + mc of the group and their scales -> LDS, 8 loads in flight
     const int tot = mc * ppr;
     const int8_t* arows = p.a + (int64_t)(start + m0) * K;
@@ -682,7 +724,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream(MoeGemmParams p) {
         int i = i0 + j * NT + tid;
         i = i < tot ? i : 0;
         const int t = i / ppr, pc = i - t * ppr;
-        v[j] = *reinterpret_cast<const i32x4*>(arows + (int64_t)t * K + pc * 16);
+        if (p.row_ids) {
+          const int64_t r = rid[t];
+          v[j] = r >= 0 ? *reinterpret_cast<const i32x4*>(p.a + r * K + pc * 16) : i32x4{0, 0, 0, 0};
+        } else {
+          v[j] = *reinterpret_cast<const i32x4*>(arows + (int64_t)t * K + pc * 16);
+        }
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -693,7 +740,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream(MoeGemmParams p) {
         }
       }
     }
-    if (tid < mc) asl[tid] = p.as[start + m0 + tid];
+    if (tid < mc) asl[tid] = p.row_ids ? (rid[tid] >= 0 ? p.as[rid[tid]] : 0.f) : p.as[start + m0 + tid];
     __syncthreads();
 
     i32x4 acc[MT][NB];
@@ -1104,6 +1151,48 @@ extern "C" int qs_moe_route(const void* top_idx, int idx_dtype, const void* top_
   return hip_check(hipGetLastError(), "k_moe_route launch");
 }
 
+extern "C" int qs_moe_route_quant(const void* top_idx, int idx_dtype, const void* top_w, int w_dtype,
+                                  int64_t T, int k, int E, int64_t* token_ids, float* coef, int32_t* starts,
+                                  int32_t* counts, int64_t* inverse, const void* source, int src_dtype,
+                                  int64_t ld_src, int64_t H, int8_t* q, float* scale, void* stream) {
+  if (!top_idx || !top_w || !token_ids || !coef || !starts || !counts || !source || !q || !scale)
+    return fail(QS_ERR_INVALID, "moe_route_quant: null pointer");
+  if (T < 0 || k < 1 || E < 1 || H <= 0 || ld_src < H) return fail(QS_ERR_INVALID, "moe_route_quant: bad shape");
+  if (E > kRouteMaxE) return fail(QS_ERR_LIMIT, "moe_route_quant: at most %d experts", kRouteMaxE);
+  if (T * k > (int64_t)1 << 28 || H > INT32_MAX) return fail(QS_ERR_LIMIT, "moe_route_quant: too many assignments");
+  if (src_dtype != QS_BF16 && src_dtype != QS_F32) return fail(QS_ERR_INVALID, "moe_route_quant: source F32 or BF16");
+  const int A = (int)(T * k);
+  const int64_t esize = src_dtype == QS_F32 ? 4 : 2;
+  const bool fused = (int64_t)A * E <= ((int64_t)1 << 22) && H % 8 == 0 && aligned(source, 16) &&
+                     (ld_src * esize) % 16 == 0 && aligned(q, 8) && T > 0;
+  if (!fused) {
+    const int st = qs_moe_route(top_idx, idx_dtype, top_w, w_dtype, T, k, E, token_ids, coef, starts, counts,
+                                inverse, stream);
+    if (st) return st;
+    return qs_moe_gather_quant(source, src_dtype, ld_src, nullptr, T, H, q, scale, stream);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(E + cdiv(T, kParWaves)));
+#define QS_RQ(IT, WT)                                                                                    \
+  do {                                                                                                   \
+    if (src_dtype == QS_BF16)                                                                            \
+      hipLaunchKernelGGL((k_moe_route_quant<IT, WT, QS_BF16>), grid, dim3(kParWaves * 64), 0, s, top_idx,  \
+                         top_w, A, k, E, token_ids, coef, starts, counts, inverse, source, ld_src, T,      \
+                         (int)H, q, scale);                                                              \
+    else                                                                                                 \
+      hipLaunchKernelGGL((k_moe_route_quant<IT, WT, QS_F32>), grid, dim3(kParWaves * 64), 0, s, top_idx,   \
+                         top_w, A, k, E, token_ids, coef, starts, counts, inverse, source, ld_src, T,      \
+                         (int)H, q, scale);                                                              \
+  } while (0)
+  if (idx_dtype == QS_I64 && w_dtype == QS_F32) QS_RQ(QS_I64, QS_F32);
+  else if (idx_dtype == QS_I64 && w_dtype == QS_BF16) QS_RQ(QS_I64, QS_BF16);
+  else if (idx_dtype == QS_I32 && w_dtype == QS_F32) QS_RQ(QS_I32, QS_F32);
+  else if (idx_dtype == QS_I32 && w_dtype == QS_BF16) QS_RQ(QS_I32, QS_BF16);
+  else return fail(QS_ERR_INVALID, "moe_route_quant: indices I32/I64, weights F32/BF16");
+#undef QS_RQ
+  return hip_check(hipGetLastError(), "k_moe_route_quant launch");
+}
+
 extern "C" int qs_moe_gather_quant(const void* source, int src_dtype, int64_t ld_src,
                                    const int64_t* rows, int64_t A, int64_t H, int8_t* q,
                                    float* scale, void* stream) {
@@ -1148,7 +1237,7 @@ void launch_moe_gemm(const MoeGemmParams& p, int G, hipStream_t s) {
 
 // LDS bytes of k_moe_stream for MT row tiles; 0 when it does not fit.
 size_t moe_stream_lds(int MT, int64_t K) {
-  const size_t b = (size_t)16 * MT * (size_t)(K + 16) + (size_t)16 * MT * 4;
+  const size_t b = (size_t)16 * MT * (size_t)(K + 16) + (size_t)16 * MT * (4 + 8);
   return b <= kMoeStreamLds ? b : 0;
 }
 
@@ -1263,12 +1352,11 @@ extern "C" int qs_moe_grouped_gemm_w8a16(const void* a, const int64_t* row_ids, 
   return hip_check(hipGetLastError(), "k_moe_stream_w16 launch");
 }
 
-extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* w,
-                                      int64_t w_stride, const float* w_scale, int64_t ws_stride,
-                                      const int32_t* starts, const int32_t* counts,
-                                      const int32_t* slots, int G, int64_t N, int64_t K,
-                                      int64_t max_rows, int swiglu, void* out, int out_dtype,
-                                      void* stream) {
+namespace {
+int grouped_gemm_i8(const int8_t* a, const float* a_scale, const int64_t* row_ids, int64_t src_rows,
+                    const int8_t* w, int64_t w_stride, const float* w_scale, int64_t ws_stride,
+                    const int32_t* starts, const int32_t* counts, const int32_t* slots, int G, int64_t N,
+                    int64_t K, int64_t max_rows, int swiglu, void* out, int out_dtype, void* stream) {
   if (!a || !a_scale || !w || !w_scale || !starts || !counts || !out)
     return fail(QS_ERR_INVALID, "moe_grouped_gemm: null pointer");
   if (G < 1 || G > 65535 || N <= 0 || K <= 0) return fail(QS_ERR_INVALID, "moe_grouped_gemm: bad shape");
@@ -1279,7 +1367,9 @@ extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, con
   if (swiglu && out_dtype != QS_BF16) return fail(QS_ERR_INVALID, "moe_grouped_gemm: SwiGLU output is BF16");
   if (out_dtype != QS_BF16 && out_dtype != QS_F32) return fail(QS_ERR_INVALID, "moe_grouped_gemm: out F32 or BF16");
   if (max_rows < 0) return fail(QS_ERR_INVALID, "moe_grouped_gemm: max_rows must be >= 0");
-  MoeGemmParams p{a, a_scale, w, w_stride, w_scale, ws_stride, starts, counts, slots, (int)N, (int)K, out, out_dtype};
+  if (src_rows < 0) return fail(QS_ERR_INVALID, "moe_grouped_gemm: src_rows must be >= 0");
+  MoeGemmParams p{a, a_scale, w, w_stride, w_scale, ws_stride, starts, counts, slots, (int)N, (int)K, out, out_dtype,
+                  row_ids, src_rows};
   hipStream_t s = static_cast<hipStream_t>(stream);
   // Streaming kernel: row tiles sized for twice the mean rows per group (max_rows / G),
   // so that most groups take one pass over their weights; 0 = unknown -> 2 tiles.
@@ -1296,6 +1386,9 @@ extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, con
     else launch_moe_stream<1, 1>(p, G, MT, s);
     return hip_check(hipGetLastError(), "k_moe_stream launch");
   }
+  if (row_ids)
+    return fail(QS_ERR_UNSUPPORTED, "moe_grouped_gemm: row_ids need the streaming kernel (16 staged rows of K + 28 "
+                "bytes within %d bytes of LDS)", (int)kMoeStreamLds);
   const int C = (int)(K / 64);
   // K split so that each wave holds at most 16 chunks of 64 k of its tile (<= 1024 threads)
   if (swiglu) {
@@ -1307,6 +1400,28 @@ extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, con
     else launch_moe_gemm<1, 16>(p, G, s);
   }
   return hip_check(hipGetLastError(), "k_moe_gemm launch");
+}
+}  // namespace
+
+extern "C" int qs_moe_grouped_gemm_i8(const int8_t* a, const float* a_scale, const int8_t* w,
+                                      int64_t w_stride, const float* w_scale, int64_t ws_stride,
+                                      const int32_t* starts, const int32_t* counts,
+                                      const int32_t* slots, int G, int64_t N, int64_t K,
+                                      int64_t max_rows, int swiglu, void* out, int out_dtype,
+                                      void* stream) {
+  return grouped_gemm_i8(a, a_scale, nullptr, 0, w, w_stride, w_scale, ws_stride, starts, counts, slots, G, N, K,
+                         max_rows, swiglu, out, out_dtype, stream);
+}
+
+extern "C" int qs_moe_grouped_gemm_i8_rows(const int8_t* a, const float* a_scale, const int64_t* row_ids,
+                                           int64_t src_rows, const int8_t* w, int64_t w_stride,
+                                           const float* w_scale, int64_t ws_stride, const int32_t* starts,
+                                           const int32_t* counts, const int32_t* slots, int G, int64_t N,
+                                           int64_t K, int64_t max_rows, int swiglu, void* out, int out_dtype,
+                                           void* stream) {
+  if (!row_ids) return fail(QS_ERR_INVALID, "moe_grouped_gemm_rows: null row_ids");
+  return grouped_gemm_i8(a, a_scale, row_ids, src_rows, w, w_stride, w_scale, ws_stride, starts, counts, slots, G,
+                         N, K, max_rows, swiglu, out, out_dtype, stream);
 }
 
 extern "C" int qs_moe_route_reduce_to(const void* expert_out, int y_dtype, const float* coef,

@@ -65,7 +65,11 @@ def route_topk(
 # ---- route compiler ----------------------------------------------------------------------
 
 
-def _route_impl(top_indices, top_weights, num_experts: int, include_inverse: bool, coef_f32: bool = False):
+def _route_impl(top_indices, top_weights, num_experts: int, include_inverse: bool, coef_f32: bool = False,
+                quant_source: torch.Tensor | None = None):
+    """The route plan; with ``quant_source`` ([T, H] bf16/fp32) also the per-token int8
+    codes and scales of its T rows (unpermuted), in the same launch where possible
+    (qs_moe_route_quant) -- appended to the returned tuple as ``(q, scale)``."""
     started = time.perf_counter()
     if top_indices.ndim != 2 or top_weights.shape != top_indices.shape:
         raise ValueError("route tensors must both have shape [rows, top_k]")
@@ -89,15 +93,32 @@ def _route_impl(top_indices, top_weights, num_experts: int, include_inverse: boo
     starts = torch.empty(num_experts, dtype=torch.int32, device=device)
     counts = torch.empty(num_experts, dtype=torch.int32, device=device)
     inverse = torch.empty(A, dtype=torch.long, device=device) if include_inverse else None
-    nat.call(
-        "qs_moe_route", nat.ptr(ti), nat.dtype_code(ti.dtype), nat.ptr(tw), nat.dtype_code(tw.dtype),
-        rows, top_k, int(num_experts), nat.ptr(token_ids), nat.ptr(coef), nat.ptr(starts),
-        nat.ptr(counts), nat.ptr(inverse), nat.stream_of(device),
-    )
+    if quant_source is None:
+        nat.call(
+            "qs_moe_route", nat.ptr(ti), nat.dtype_code(ti.dtype), nat.ptr(tw), nat.dtype_code(tw.dtype),
+            rows, top_k, int(num_experts), nat.ptr(token_ids), nat.ptr(coef), nat.ptr(starts),
+            nat.ptr(counts), nat.ptr(inverse), nat.stream_of(device),
+        )
+        quant = ()
+    else:
+        src = quant_source.contiguous()
+        if src.ndim != 2 or int(src.shape[0]) != rows:
+            raise ValueError("quant_source must have one row per routed token")
+        nat.require_device(src)
+        H = int(src.shape[1])
+        q = torch.empty((rows, H), dtype=torch.int8, device=device)
+        sc = torch.empty(rows, dtype=torch.float32, device=device)
+        nat.call(
+            "qs_moe_route_quant", nat.ptr(ti), nat.dtype_code(ti.dtype), nat.ptr(tw), nat.dtype_code(tw.dtype),
+            rows, top_k, int(num_experts), nat.ptr(token_ids), nat.ptr(coef), nat.ptr(starts),
+            nat.ptr(counts), nat.ptr(inverse), nat.ptr(src), nat.dtype_code(src.dtype), H, H, nat.ptr(q),
+            nat.ptr(sc), nat.stream_of(device),
+        )
+        quant = (q, sc)
     # coefficients keep the routing-weight dtype, as the reference's index_select does
     # (the kernel's fp32 copy of a bf16 weight is exact, so coef_f32 loses nothing)
     coef = coef if (tw.dtype == torch.float32 or coef_f32) else coef.to(tw.dtype)
-    return token_ids, coef, starts, counts, inverse, time.perf_counter() - started
+    return (token_ids, coef, starts, counts, inverse, time.perf_counter() - started) + quant
 
 
 def grouped_route_tensors(top_indices, top_weights, *, num_experts: int):
@@ -249,8 +270,13 @@ def grouped_int8_mm(
     max_rows: int | None = None,
     swiglu: bool = False,
     out_dtype: torch.dtype = torch.bfloat16,
+    row_ids: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, str]:
     """Ragged grouped ``out[start_g + m] = (acc * a_scale) * w_scale`` for each group g.
+
+    With ``row_ids``, queue row ``r`` reads ``rows_q[row_ids[r]]`` and its scale (the
+    gather ``index_select(0, token_ids)`` folded into the kernel; ``rows_q`` are then the
+    T quantized source rows).
 
     ``weights[slot(g)]`` is ``[N, K]`` int8 (``weights`` may be a strided view into an
     expert-page arena); ``swiglu=True`` treats rows ``[0, N/2)`` as gate and ``[N/2, N)``
@@ -260,22 +286,29 @@ def grouped_int8_mm(
     pass (:2747), and only sizes the kernel's row tile.
     """
     G, n_w, K = _grouped_contract(rows_q, weights, weight_scales, starts, counts, group_slots)
-    device = nat.require_device(rows_q, row_scales, weights, weight_scales, starts, counts, group_slots)
+    device = nat.require_device(rows_q, row_scales, weights, weight_scales, starts, counts, group_slots, row_ids)
     n_out = n_w // 2 if swiglu else n_w
     if swiglu and n_w % 2:
         raise ValueError("SwiGLU weights need an even number of rows")
-    out = torch.empty((int(rows_q.shape[0]), n_out), dtype=out_dtype, device=device)
+    if row_ids is not None and row_ids.ndim != 1:
+        raise ValueError("row_ids must be a vector")
+    A = int(rows_q.shape[0]) if row_ids is None else int(row_ids.numel())
+    out = torch.empty((A, n_out), dtype=out_dtype, device=device)
     st = starts.to(torch.int32).contiguous()
     ct = counts.to(torch.int32).contiguous()
     sl = None if group_slots is None else group_slots.to(torch.int32).contiguous()
-    rows_bound = int(rows_q.shape[0]) if max_rows is None else int(max_rows)
+    rows_bound = A if max_rows is None else int(max_rows)
     if rows_bound < 0:
         raise ValueError("max_rows must be non-negative")
-    nat.call(
-        "qs_moe_grouped_gemm_i8", nat.ptr(rows_q), nat.ptr(row_scales), nat.ptr(weights), int(weights.stride(0)),
-        nat.ptr(weight_scales), int(weight_scales.stride(0)), nat.ptr(st), nat.ptr(ct), nat.ptr(sl), G, n_out, K,
-        rows_bound, int(bool(swiglu)), nat.ptr(out), nat.dtype_code(out_dtype), nat.stream_of(device),
-    )
+    tail = (nat.ptr(weights), int(weights.stride(0)), nat.ptr(weight_scales), int(weight_scales.stride(0)), nat.ptr(st),
+            nat.ptr(ct), nat.ptr(sl), G, n_out, K, rows_bound, int(bool(swiglu)), nat.ptr(out),
+            nat.dtype_code(out_dtype), nat.stream_of(device))
+    if row_ids is None:
+        nat.call("qs_moe_grouped_gemm_i8", nat.ptr(rows_q), nat.ptr(row_scales), *tail)
+    else:
+        ids = row_ids.to(torch.int64).contiguous()
+        nat.call("qs_moe_grouped_gemm_i8_rows", nat.ptr(rows_q), nat.ptr(row_scales), nat.ptr(ids),
+                 int(rows_q.shape[0]), *tail)
     return out, IMPL_GROUPED
 
 
@@ -466,8 +499,15 @@ class Int8ExpertBackend:
         page = self.layers[layer]
         E = page.num_experts
         # fp32 coefficients: the reduce widens them to fp32 anyway
-        token_ids, coef, starts, counts, inverse, _ = _route_impl(top_indices, top_weights, E, True, coef_f32=True)
-        expert_output = self._experts_math(page, source, token_ids, starts, counts, None)
+        src_q = None
+        if self.w8a8_fused_route(source):
+            token_ids, coef, starts, counts, inverse, _, q, s = _route_impl(
+                top_indices, top_weights, E, True, coef_f32=True, quant_source=source
+            )
+            src_q = (q, s)
+        else:
+            token_ids, coef, starts, counts, inverse, _ = _route_impl(top_indices, top_weights, E, True, coef_f32=True)
+        expert_output = self._experts_math(page, source, token_ids, starts, counts, None, src_q)
         out = stable_route_reduce(
             expert_output, coef, token_ids, counts, top_indices,
             self._expert_ids(source.device, E), inverse_assignments=inverse, out_dtype=self._reduce_dtype(),
@@ -477,8 +517,17 @@ class Int8ExpertBackend:
         self.stats["expert_assignments"] += int(top_indices.numel())
         return out.to(self.dtype)
 
-    def _experts_math(self, page, source, token_ids, starts, counts, slots) -> torch.Tensor:
-        """gate_up + SwiGLU and down over the routed queue; [A, H] in the model dtype."""
+    def w8a8_fused_route(self, source) -> bool:
+        """The W8A8 flow quantizes the T source rows in the route's launch and gathers them
+        in the gate/up kernel when the rows are 16-byte aligned with H % 8 == 0."""
+        H = int(source.shape[-1])
+        return (not self.w8a16 and source.dtype in (torch.bfloat16, torch.float32) and H % 8 == 0 and H <= 8192
+                and source.is_contiguous() and source.data_ptr() % 16 == 0)
+
+    def _experts_math(self, page, source, token_ids, starts, counts, slots, src_q=None) -> torch.Tensor:
+        """gate_up + SwiGLU and down over the routed queue; [A, H] in the model dtype.
+        ``src_q``: the per-token codes and scales of the T source rows (route_quant), read
+        through ``token_ids`` by the gate/up kernel."""
         if self.w8a16:
             src = source if source.dtype == torch.bfloat16 else source.to(torch.bfloat16)
             activated, _ = grouped_w8a16_mm(
@@ -489,10 +538,16 @@ class Int8ExpertBackend:
                 activated, page.down, page.down_scales, starts, counts, group_slots=slots, out_dtype=self.dtype
             )
             return expert_output
-        rows_q, rows_s = quantize_rows(source, token_ids)
-        activated, _ = grouped_int8_mm(
-            rows_q, rows_s, page.gate_up, page.gate_up_scales, starts, counts, group_slots=slots, swiglu=True
-        )
+        if src_q is not None:
+            activated, _ = grouped_int8_mm(
+                src_q[0], src_q[1], page.gate_up, page.gate_up_scales, starts, counts, group_slots=slots,
+                swiglu=True, row_ids=token_ids,
+            )
+        else:
+            rows_q, rows_s = quantize_rows(source, token_ids)
+            activated, _ = grouped_int8_mm(
+                rows_q, rows_s, page.gate_up, page.gate_up_scales, starts, counts, group_slots=slots, swiglu=True
+            )
         act_q, act_s = quantize_rows(activated)
         expert_output, _ = grouped_int8_mm(
             act_q, act_s, page.down, page.down_scales, starts, counts, group_slots=slots, out_dtype=self.dtype

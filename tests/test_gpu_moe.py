@@ -389,3 +389,54 @@ def test_moe_layer_config4_w8a16(dev, T):
     y8 = _moe().Int8ExpertBackend([layer]).moe(0, _t(x, dev, torch.bfloat16), ti, tw)
     dense = om.moe_dense_reference(x, idx, w, gu, gus, dn, dns)
     assert oq.rel_l2(y.float().cpu().numpy(), dense) < oq.rel_l2(y8.float().cpu().numpy(), dense)
+
+
+# ---- route + source quantization in one launch, gathered in the gate/up kernel ---------
+
+
+@pytest.mark.parametrize("T,E,k,H,dtype", [(64, 128, 8, 2048, torch.bfloat16), (512, 128, 8, 2048, torch.bfloat16),
+                                           (7, 5, 3, 256, torch.float32), (33, 16, 4, 200, torch.bfloat16),
+                                           (16385, 64, 4, 64, torch.bfloat16)])
+def test_route_quant_equals_route_then_quantize(dev, T, E, k, H, dtype):
+    """qs_moe_route_quant (one launch; the last two cases take its two-launch fallback:
+    H % 8 != 0, and A * E > 2^22) gives qs_moe_route's plan and quantize_rows' codes and
+    scales of the unpermuted source rows, bit for bit."""
+    rng = np.random.default_rng(T + E + H)
+    top = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
+    w = _t(rng.random((T, k)).astype(np.float32), dev)
+    src = _t(rng.standard_normal((T, H)).astype(np.float32) * 3, dev, dtype)
+    src[min(3, T - 1)] = 0  # a zero row: scale 1
+    ti = _t(top, dev)
+    got = _moe()._route_impl(ti, w, E, True, coef_f32=True, quant_source=src)
+    want = _moe()._route_impl(ti, w, E, True, coef_f32=True)
+    for a, b in zip(got[:5], want[:5]):
+        assert torch.equal(a, b)
+    q, s = _moe().quantize_rows(src)
+    assert torch.equal(got[6], q) and torch.equal(got[7], s)
+
+
+@pytest.mark.parametrize("swiglu", [False, True])
+@pytest.mark.parametrize("max_rows", [0, 16, 4000])
+def test_grouped_int8_rows_equals_gathered(dev, swiglu, max_rows):
+    """grouped_int8_mm over the T quantized source rows through row_ids equals it over the
+    gathered rows, bit for bit (skewed groups take several passes); an id outside the
+    source reads a zero row."""
+    rng = np.random.default_rng(23)
+    E, H, I, T, k = 8, 2048, 128, 200, 2
+    gu, gus, dn, dns = _layer(rng, E, H, I)
+    top = np.stack([np.concatenate([[0], 1 + rng.permutation(E - 1)[: k - 1]]) for _ in range(T)]).astype(np.int64)
+    tok, coef, starts, counts, inv = om.route_stable(top, np.ones((T, k), np.float32), E)
+    layer = _moe().Int8ExpertLayer.from_arrays(*(torch.from_numpy(v) for v in (gu, gus, dn, dns)), dev)
+    q = _t(rng.integers(-127, 128, size=(T, H), dtype=np.int8), dev)
+    s = _t(rng.uniform(0.01, 0.1, size=T).astype(np.float32), dev)
+    st, ct, td = _t(starts, dev), _t(counts, dev), _t(tok, dev)
+    got, _ = _moe().grouped_int8_mm(q, s, layer.gate_up, layer.gate_up_scales, st, ct, swiglu=swiglu,
+                                    max_rows=max_rows, row_ids=td)
+    want, _ = _moe().grouped_int8_mm(q[td], s[td], layer.gate_up, layer.gate_up_scales, st, ct, swiglu=swiglu,
+                                     max_rows=max_rows)
+    assert torch.equal(got, want)
+    bad = tok.copy()
+    bad[5] = T
+    ob, _ = _moe().grouped_int8_mm(q, s, layer.gate_up, layer.gate_up_scales, st, ct, swiglu=swiglu,
+                                   max_rows=max_rows, row_ids=_t(bad, dev))
+    assert torch.all(ob[5] == 0) and torch.equal(ob[:5], got[:5]) and torch.equal(ob[6:], got[6:])
