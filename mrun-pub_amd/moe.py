@@ -447,9 +447,12 @@ class Int8ExpertLayer:
 class Int8ExpertBackend:
     """``backend.moe(layer, source, top_indices, top_weights)`` with int8 experts.
 
-    Flow per layer (W8A8, the default): stable route compile -> gather + per-row int8
-    quantization -> grouped gate_up GEMM with the fused BF16 SwiGLU epilogue -> per-row
-    requantization -> grouped down GEMM -> fixed rank-order reduce -> model dtype.
+    Flow per layer (W8A8, the default): stable route compile and per-row int8
+    quantization of the T source rows (one launch) -> grouped gate_up GEMM gathering the
+    routed rows' codes, with the fused BF16 SwiGLU epilogue -> per-row requantization ->
+    grouped down GEMM -> fixed rank-order reduce -> model dtype.  (Unaligned sources, or H
+    not a multiple of 8 or above 8192, gather and quantize the A routed rows instead: the
+    same codes.)
 
     ``w8a16=True`` is the weight-only flow of the reference's PackedBF16ExpertBackend.moe
     (qwen3_moe_cuda.py:2978-3046) over the same int8 pages: the routed bf16 rows are
@@ -566,14 +569,20 @@ class Int8ExpertBackend:
             page, slots = table
             E = int(slots.numel())
             selected = self._expert_ids(source.device, E)
-            token_ids, coef, starts, counts, inverse, _ = _route_impl(top_indices, top_weights, E, True, coef_f32=True)
+            route_idx = top_indices
         else:
             selected, page, slots = cache.acquire_slot_binding(layer, top_indices, protect=not prefill)
-            compact = torch.searchsorted(selected, top_indices)
-            token_ids, coef, starts, counts, inverse, _ = _route_impl(
-                compact, top_weights, int(selected.numel()), True, coef_f32=True
+            route_idx = torch.searchsorted(selected, top_indices)
+            E = int(selected.numel())
+        src_q = None
+        if self.w8a8_fused_route(source):
+            token_ids, coef, starts, counts, inverse, _, q, s = _route_impl(
+                route_idx, top_weights, E, True, coef_f32=True, quant_source=source
             )
-        expert_output = self._experts_math(page, source, token_ids, starts, counts, slots)
+            src_q = (q, s)
+        else:
+            token_ids, coef, starts, counts, inverse, _ = _route_impl(route_idx, top_weights, E, True, coef_f32=True)
+        expert_output = self._experts_math(page, source, token_ids, starts, counts, slots, src_q)
         out = stable_route_reduce(
             expert_output, coef, token_ids, counts, top_indices, selected, inverse_assignments=inverse,
             out_dtype=self._reduce_dtype(),
