@@ -503,7 +503,7 @@ class Int8ExpertBackend:
         E = page.num_experts
         # fp32 coefficients: the reduce widens them to fp32 anyway
         src_q = None
-        if self.w8a8_fused_route(source):
+        if self._fused_route_ok(source):
             token_ids, coef, starts, counts, inverse, _, q, s = _route_impl(
                 top_indices, top_weights, E, True, coef_f32=True, quant_source=source
             )
@@ -520,7 +520,7 @@ class Int8ExpertBackend:
         self.stats["expert_assignments"] += int(top_indices.numel())
         return out.to(self.dtype)
 
-    def w8a8_fused_route(self, source) -> bool:
+    def _fused_route_ok(self, source) -> bool:
         """The W8A8 flow quantizes the T source rows in the route's launch and gathers them
         in the gate/up kernel when the rows are 16-byte aligned with H % 8 == 0."""
         H = int(source.shape[-1])
@@ -575,7 +575,7 @@ class Int8ExpertBackend:
             route_idx = torch.searchsorted(selected, top_indices)
             E = int(selected.numel())
         src_q = None
-        if self.w8a8_fused_route(source):
+        if self._fused_route_ok(source):
             token_ids, coef, starts, counts, inverse, _, q, s = _route_impl(
                 route_idx, top_weights, E, True, coef_f32=True, quant_source=source
             )
