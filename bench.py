@@ -620,7 +620,7 @@ def main() -> int:
     if args.gpus != 1:
         print(
             f"bench.py: this build measures one MI355X only (--gpus {args.gpus} requested); "
-            "the QStore path is single-GPU here, multi-GPU sharding is described in DESIGN.md",
+            "the QStore path is single-GPU here (sharding by output rows / experts is design only)",
             file=sys.stderr,
         )
         return 2
