@@ -440,3 +440,34 @@ def test_grouped_int8_rows_equals_gathered(dev, swiglu, max_rows):
     ob, _ = _moe().grouped_int8_mm(q, s, layer.gate_up, layer.gate_up_scales, st, ct, swiglu=swiglu,
                                    max_rows=max_rows, row_ids=_t(bad, dev))
     assert torch.all(ob[5] == 0) and torch.equal(ob[:5], got[:5]) and torch.equal(ob[6:], got[6:])
+
+
+@pytest.mark.parametrize("w8a16", [False, True])
+def test_moe_layer_graph_replays_equal_eager(dev, w8a16):
+    """The whole layer (route + quantization launch, gathered gate/up, requantization,
+    down, reduce; or the weight-only flow) captured in a HIP graph: three replays with
+    eager work and synchronizations between them each equal the eager result bit for bit."""
+    rng = np.random.default_rng(29)
+    E, k, H, I, T = 32, 4, 512, 256, 48
+    gu, gus, dn, dns = _layer(rng, E, H, I)
+    layer = _moe().Int8ExpertLayer.from_arrays(*(torch.from_numpy(v) for v in (gu, gus, dn, dns)), dev)
+    backend = _moe().Int8ExpertBackend([layer], w8a16=w8a16)
+    x = _t(rng.standard_normal((T, H)).astype(np.float32), dev, torch.bfloat16)
+    tw, ti = _moe().route_topk(_t(rng.standard_normal((T, E)).astype(np.float32), dev), k)
+    eager = backend.moe(0, x, ti, tw)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        backend.moe(0, x, ti, tw)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = backend.moe(0, x, ti, tw)
+    for rep in range(3):
+        backend.moe(0, x, ti, tw)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
