@@ -279,15 +279,19 @@ def test_w8a8_prefill_config3_bf16(dev, m):
     xb = oq.round_bf16(x)
     dq, ds = torch.from_numpy(q_w).to(dev), torch.from_numpy(sc_w).to(dev)
     dx = torch.from_numpy(xb).to(dev).to(torch.bfloat16)
-    # int32 accumulators bit-exact against the oracle on a row sample
     q, s = _w().quantize_activation(dx)
     qr, sr = ow.act_quant(xb)
     assert np.array_equal(q.cpu().numpy(), qr) and np.array_equal(s.cpu().numpy(), sr)
-    acc = _w()._int8_gemm(q, dq).cpu().numpy()
+    # the oracle's int32 accumulators for every row: int8 products summed in float64 are
+    # exact (|acc| <= 127 * 127 * 4096 < 2^53), checked against the integer GEMM on a sample
+    acc_ref = np.rint(qr.astype(np.float64) @ q_w.astype(np.float64).T).astype(np.int64)
     rows = np.arange(0, m, 97)
-    assert np.array_equal(acc[rows], ow.int8_gemm(qr[rows], q_w))
+    assert np.array_equal(acc_ref[rows], ow.int8_gemm(qr[rows], q_w))
+    acc = _w()._int8_gemm(q, dq).cpu().numpy()
+    assert np.array_equal(acc, acc_ref)
+    # the fused GEMM + epilogue against the epilogue applied to the oracle's accumulators
     y = _w().w8a8_matmul(dq, ds, dx, out_dtype=torch.bfloat16)
-    ref = oq.round_bf16((acc.astype(np.float32) * sr[:, None]).astype(np.float32) * sc_w[None, :])
+    ref = oq.round_bf16((acc_ref.astype(np.float32) * sr[:, None]).astype(np.float32) * sc_w[None, :])
     assert np.array_equal(y.float().cpu().numpy().view(np.uint32), ref.view(np.uint32))
 
 
