@@ -143,15 +143,24 @@ def _out_buffer(out: torch.Tensor | None, m: int, n: int, dtype: torch.dtype, de
 # bf16/f16 call with at least 16 activation rows: in same-box A/B timings of the config-2
 # shapes they match or beat the 16-row-tile kernels at M = 16 and beat them at M = 32
 # (1536 x 8960: 25.4 -> 11.5 us, paired SwiGLU 8960 x 1536: 18.5 -> 14.3 us).
+# Fewer rows take them where they measured faster than the 16-row-tile kernels that serve
+# M 5..15 (same box, config-2 shapes): the paired SwiGLU from 5 rows (11.7 -> 10.7 us at
+# M = 8, 13.4 -> 10.8 at M = 12), rows longer than 2048 from 8 (1536 x 8960: 10.6 ->
+# 9.9 us at M = 8, 15.2 -> 10.1 at M = 12); short rows keep the tiles below 16 (1536 x 1536
+# at M = 12: 4.89 against 5.03 us).  M <= 4 stays on the register-activation GEMV, whose
+# rows equal single-row results bit for bit (and whose chained M = 4 pass is faster).
 BATCHED_MIN_M = 16
+BATCHED_MIN_M_SWIGLU = 5
+BATCHED_MIN_M_LONG = 8
 BATCHED_MAX_K = 16384
 
 
 def _batched_eligible(x2: torch.Tensor, codes: list[torch.Tensor], swiglu: bool = False) -> bool:
     m, k = int(x2.shape[0]), int(x2.shape[1])
     ns = [int(c.shape[0]) for c in codes]
+    min_m = BATCHED_MIN_M_SWIGLU if swiglu else (BATCHED_MIN_M_LONG if k > 2048 else BATCHED_MIN_M)
     return (x2.dtype in (torch.bfloat16, torch.float16) and (not swiglu or x2.dtype == torch.bfloat16)
-            and m >= BATCHED_MIN_M and k % 128 == 0 and k <= BATCHED_MAX_K
+            and m >= min_m and k % 128 == 0 and k <= BATCHED_MAX_K
             and (k <= 2048 or all(n % 4 == 0 for n in ns))
             and x2.stride(0) == k and x2.data_ptr() % 16 == 0 and all(c.data_ptr() % 16 == 0 for c in codes))
 
