@@ -55,3 +55,32 @@ def test_version_and_error_string_without_gpu():
     assert b"null" in lib.qs_last_error()
     with pytest.raises(ValueError):
         nat.check(st, "qs_qrow_matmul")
+
+
+def test_moe_entry_point_validation_without_gpu():
+    """The MoE entry points added for the weight-only flow and the fused route reject bad
+    arguments before any device work (status codes as documented in the header)."""
+    import mrun_pub_amd._native as nat
+
+    if not nat.LIB_PATH.exists():
+        pytest.skip("library not built")
+    lib = nat.load()
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    # weight-only grouped GEMM: null pointers, K not a multiple of 64, SwiGLU output dtype
+    st = lib.qs_moe_grouped_gemm_w8a16(None, None, 0, fake, 0, fake, 0, fake, fake, None, 1, 64, 128, 0, 0, fake,
+                                       nat.QS_BF16, None)
+    assert st == nat.QS_ERR_INVALID and b"null" in lib.qs_last_error()
+    st = lib.qs_moe_grouped_gemm_w8a16(fake, None, 0, fake, 0, fake, 0, fake, fake, None, 1, 64, 100, 0, 0, fake,
+                                       nat.QS_BF16, None)
+    assert st == nat.QS_ERR_UNSUPPORTED and b"multiple of 64" in lib.qs_last_error()
+    st = lib.qs_moe_grouped_gemm_w8a16(fake, None, 0, fake, 0, fake, 0, fake, fake, None, 1, 64, 128, 0, 1, fake,
+                                       nat.QS_F32, None)
+    assert st == nat.QS_ERR_INVALID and b"SwiGLU" in lib.qs_last_error()
+    # gathered int8 grouped GEMM: row_ids required
+    st = lib.qs_moe_grouped_gemm_i8_rows(fake, fake, None, 4, fake, 0, fake, 0, fake, fake, None, 1, 64, 128, 0, 0,
+                                         fake, nat.QS_BF16, None)
+    assert st == nat.QS_ERR_INVALID and b"row_ids" in lib.qs_last_error()
+    # fused route + quantization: dtype checks
+    st = lib.qs_moe_route_quant(fake, nat.QS_I64, fake, nat.QS_F32, 4, 2, 8, fake, fake, fake, fake, None, fake,
+                                nat.QS_F16, 64, 64, fake, fake, None)
+    assert st == nat.QS_ERR_INVALID and b"F32 or BF16" in lib.qs_last_error()
