@@ -501,8 +501,8 @@ class Int8ExpertBackend:
         del prefill
         page = self.layers[layer]
         E = page.num_experts
-        # fp32 coefficients: the reduce widens them to fp32 anyway
         src_q = None
+        # fp32 coefficients: the reduce widens them to fp32 anyway
         if self._fused_route_ok(source):
             token_ids, coef, starts, counts, inverse, _, q, s = _route_impl(
                 top_indices, top_weights, E, True, coef_f32=True, quant_source=source
