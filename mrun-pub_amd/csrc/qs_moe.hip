@@ -1242,12 +1242,14 @@ size_t moe_stream_lds(int MT, int64_t K) {
 }
 
 // Launch shapes measured on config-4 shapes (E 128, H 2048, I 768, T 64 / 512):
-// SwiGLU streams with 4 waves when one row tile is staged (T = 64: 70 us vs 76 us with 8)
-// and 8 waves for more; two 128-byte chunks in flight.  Plain products keep 128 bytes
+// SwiGLU streams with 4 waves when one row tile is staged (T = 64: 70 us vs 76 us with 8),
+// 8 waves for two and 12 for four; two 128-byte chunks in flight.  Plain products keep 128 bytes
 // of each weight row in flight for NB >= 2 tiles per wave, 256 for one.
 template <int P, int NB, int MT, int PAIR, int WAVES_SET = 0>
 void launch_moe_stream_mt(const MoeGemmParams& p, int G, hipStream_t s) {
-  constexpr int WAVES = WAVES_SET ? WAVES_SET : (P == 2 ? (MT == 1 ? 4 : 8) : 4);
+  // SwiGLU with 64-row passes: 12 waves (N = 768: four workgroups per expert, two full
+  // rounds of the CUs at 128 experts; T = 512 gate/up 85.3 -> 82.6 us against 8 waves)
+  constexpr int WAVES = WAVES_SET ? WAVES_SET : (P == 2 ? (MT == 1 ? 4 : (MT == 4 ? 12 : 8)) : 4);
   constexpr int WP = P == 2 ? 2 : (NB >= 2 ? 1 : 2);  // 128-byte chunks in flight
   constexpr int W = PAIR ? WP : 2 * WP;
   constexpr int RW = MoeStreamCfg<P, NB>::RW;
@@ -1279,7 +1281,7 @@ int moe_w16_phase(int MT, int64_t K, int CB, int W, size_t cap) {
 }
 
 // Launch shapes of k_moe_stream_w16, measured on config-4 shapes (E 128, H 2048, I 768):
-// SwiGLU as the int8 stream (4 waves for one row tile, else 8; two 128-byte chunks in
+// SwiGLU with 8 waves for one or two row tiles and 12 for four (two 128-byte chunks in
 // flight).  Plain products with 64-row passes (MT = 4) use 4 waves of NB tiles and cap the
 // staged slice at 72 KB so that two or three workgroups share a CU (T = 512 down
 // 74 -> 51 us); shorter passes use 8 waves of at most 2 tiles (T = 64 down 41 -> 36 us).
@@ -1305,9 +1307,9 @@ void launch_moe_w16_pair(const MoeW16Params& p, int G, size_t cap, hipStream_t s
 void launch_moe_w16(const MoeW16Params& p, int G, int MT, bool swiglu, hipStream_t s) {
   const int64_t K = p.K;
   if (swiglu) {
-    if (MT == 4) launch_moe_w16_pair<2, 2, 4, 8>(p, G, kMoeStreamLds, s);
+    if (MT == 4) launch_moe_w16_pair<2, 2, 4, 12>(p, G, kMoeStreamLds, s);  // 102.1 -> 91.2 us at T = 512 (8 waves)
     else if (MT == 2) launch_moe_w16_pair<2, 2, 2, 8>(p, G, kMoeStreamLds, s);
-    else launch_moe_w16_pair<2, 2, 1, 4>(p, G, kMoeStreamLds, s);
+    else launch_moe_w16_pair<2, 2, 1, 8>(p, G, kMoeStreamLds, s);  // T = 64 layer 128.8 -> 125.3 us (4 waves)
   } else if (MT == 4) {
     constexpr size_t cap = 72 * 1024;
     if (K <= 1024) launch_moe_w16_pair<1, 4, 4, 4>(p, G, cap, s);
