@@ -25,8 +25,17 @@ import numpy as np
 
 
 def int8_gemm(qx: np.ndarray, qw: np.ndarray) -> np.ndarray:
-    """``[T,K] int8 @ [N,K] int8^T -> [T,N] int32`` (exact; int64 then narrowed)."""
-    acc = np.asarray(qx, dtype=np.int64) @ np.asarray(qw, dtype=np.int64).T
+    """``[T,K] int8 @ [N,K] int8^T -> [T,N] int32`` (exact).
+
+    Evaluated as a float64 GEMM: every product is at most 128*128 = 2^14 in magnitude and
+    every partial sum of K terms at most K * 2^14, so for K <= 2^38 each partial sum is an
+    integer below 2^53 and the float64 evaluation is exact in any summation order (this
+    lets the config-3 sizes run through BLAS in seconds; numpy's int64 matmul has no BLAS).
+    """
+    qx = np.asarray(qx, dtype=np.int8)
+    qw = np.asarray(qw, dtype=np.int8)
+    assert qx.shape[-1] <= 2**38
+    acc = qx.astype(np.float64) @ qw.astype(np.float64).T
     assert np.abs(acc).max(initial=0) < 2**31
     return acc.astype(np.int32)
 

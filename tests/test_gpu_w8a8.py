@@ -334,3 +334,28 @@ def test_enable_w8a8_twice_then_disable(dev, tmp_path):
     assert "matmul" not in vars(store)
     assert torch.equal(store.matmul("L0.q", x), base)
     disable_w8a8(store)  # no-op
+
+
+@pytest.mark.parametrize("m", [512, 2048])
+def test_w8a8_protect8_config3(dev, m):
+    """The bench's ``w8a8_matmul_protect8`` call at config-3 size: bf16 x [M,4096] with 0.1%
+    outlier channels x20, W [14336,4096], protect_k=8 (the reference's default for
+    ``enable_w8a8``, w8a8.py:130-160).  fp32 output within 1e-5 of the oracle; the bf16
+    output is that value rounded once (1e-3)."""
+    rng, q_w, sc_w = _weights(14336, 4096, 300 + m)
+    x = rng.standard_normal((m, 4096)).astype(np.float32)
+    x[:, rng.permutation(4096)[:4]] *= 20.0
+    xb = oq.round_bf16(x)
+    dq, ds = torch.from_numpy(q_w).to(dev), torch.from_numpy(sc_w).to(dev)
+    dx = torch.from_numpy(xb).to(dev).to(torch.bfloat16)
+    ref = ow.w8a8_matmul(q_w, sc_w, xb, protect_k=8)
+    y = _w().w8a8_matmul(dq, ds, dx, protect_k=8)
+    assert y.dtype == torch.float32 and y.shape == (m, 14336)
+    err = oq.rel_l2(y.cpu().numpy(), ref)
+    assert err <= F32_TOL, err
+    yb = _w().w8a8_matmul(dq, ds, dx, protect_k=8, out_dtype=torch.bfloat16)
+    err = oq.rel_l2(yb.float().cpu().numpy(), oq.round_bf16(ref))
+    assert err <= 1e-3, err
+    # protection matters at this size: without it the error is far larger
+    y0 = _w().w8a8_matmul(dq, ds, dx)
+    assert oq.rel_l2(y0.cpu().numpy(), ref) > 10 * F32_TOL

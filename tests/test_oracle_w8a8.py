@@ -32,6 +32,18 @@ def test_int8_gemm_brute_force():
     # extreme magnitudes: K * 127^2 stays within int32 for K = 4096
     big = np.full((1, 4096), 127, np.int8)
     assert ow.int8_gemm(big, -big)[0, 0] == -4096 * 127 * 127
+    # the float64 evaluation equals numpy's integer matmul on full-width random operands,
+    # -128 included (a lossy float32 evaluation would fail here)
+    qx = rng.integers(-128, 128, size=(33, 14336), dtype=np.int8)
+    qw = rng.integers(-128, 128, size=(50, 14336), dtype=np.int8)
+    qx[0] = -128
+    qw[0] = -128
+    qx[1] = 127
+    qw[1] = 127
+    qw[1, 0] = 126  # an odd sum above 2^24: not representable in float32
+    exact = qx.astype(np.int64) @ qw.astype(np.int64).T
+    assert np.array_equal(ow.int8_gemm(qx, qw), exact)
+    assert not np.array_equal((qx.astype(np.float32) @ qw.astype(np.float32).T).astype(np.int64), exact)
 
 
 def test_act_quant_matches_reference_torch_composition():
