@@ -93,21 +93,17 @@ int qs_qrow_matmul_multi(const void* x, int x_dtype, int64_t ldx, int n_linear,
  * for bit.
  *   workspace: qs_qrow_batched_workspace_bytes(M, n_linear, N, K, swiglu) bytes, 16-byte
  *              aligned (0 when K is not split), contents clobbered; calls that run
- *              concurrently (other streams) need their own;
- *   counters:  unused (qs_qrow_batched_counters returns 0); may be null. */
+ *              concurrently (other streams) need their own. */
 size_t qs_qrow_batched_workspace_bytes(int64_t M, int n_linear, const int64_t* N, int64_t K,
                                        int swiglu);
-int64_t qs_qrow_batched_counters(int n_linear, const int64_t* N, int swiglu);
 int qs_qrow_matmul_batched(const void* x, int x_dtype, int64_t ldx, int n_linear,
                            const int8_t* const* codes, const float* const* scales,
                            void* const* y, const int64_t* ldy, const int64_t* N, int64_t M,
-                           int64_t K, void* workspace, size_t workspace_bytes, int32_t* counters,
-                           int64_t n_counters, void* stream);
+                           int64_t K, void* workspace, size_t workspace_bytes, void* stream);
 int qs_qrow_swiglu_batched(const void* x, int64_t ldx, const int8_t* gate_codes,
                            const float* gate_scales, const int8_t* up_codes,
                            const float* up_scales, void* y, int64_t ldy, int64_t M, int64_t N,
-                           int64_t K, void* workspace, size_t workspace_bytes, int32_t* counters,
-                           int64_t n_counters, void* stream);
+                           int64_t K, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Replaces fused_qrow_swiglu + _qrow_w8a16_paired_swiglu_kernel
  * (dense_qstore_cuda.py:1053-1102, 515-575); reference contract
@@ -256,19 +252,18 @@ int qs_expert_queue_build(const void* experts, int expert_dtype, const int64_t* 
                           void* stream);
 
 /* Replaces scatter_committed / scatter_committed_device (expert_queue.py:487-560):
- * valid[q] = (epochs[q] == active_epochs[token_ids[q]]) (uint8), and for every row t
- * reduced[t, h] = sum over its valid packets q in ascending queue order of
- * fp32(float(expert_out[q, h]) * coefficients[q]), accumulated from 0 in that order (the
- * roundings of the reference's index_add_; no atomics, same bits on every call).  Packets
- * are identified per row by their route slot (< top_k <= 64).  workspace:
- * qs_expert_queue_scatter_workspace_bytes(rows, top_k) bytes.  rows <= 65535. */
-size_t qs_expert_queue_scatter_workspace_bytes(int64_t rows, int top_k);
-int qs_expert_queue_scatter(const int64_t* token_ids, const int64_t* route_slots,
-                            const float* coefficients, const int64_t* epochs,
+ * valid[q] = (token_ids[q] in [0, rows) and epochs[q] == active_epochs[token_ids[q]])
+ * (uint8), and for every row t reduced[t, h] = sum over the valid packets of token t, in
+ * ascending queue order, of fp32(float(expert_out[q, h]) * coefficients[q]), accumulated
+ * from 0 in that order (the order and roundings of the reference's index_add_; packets are
+ * matched to rows by token alone, as there; no atomics in the sum, same bits on every
+ * call).  workspace: qs_expert_queue_scatter_workspace_bytes(rows, A) bytes.  A, rows and
+ * H below 2^31. */
+size_t qs_expert_queue_scatter_workspace_bytes(int64_t rows, int64_t A);
+int qs_expert_queue_scatter(const int64_t* token_ids, const float* coefficients, const int64_t* epochs,
                             const int64_t* active_epochs, const void* expert_out, int out_dtype,
-                            int64_t ld_out, int64_t A, int64_t rows, int top_k, int64_t H,
-                            void* workspace, size_t workspace_bytes, float* reduced,
-                            uint8_t* valid, void* stream);
+                            int64_t ld_out, int64_t A, int64_t rows, int64_t H, void* workspace,
+                            size_t workspace_bytes, float* reduced, uint8_t* valid, void* stream);
 
 /* Routed-row quantization (int8 analogue of quantize_fp8_activation,
  * olmoe_cuda.py:1173-1176, with the W8A8 recipe of w8a8.py:118-121):
@@ -405,6 +400,7 @@ int qs_pager_release(qs_pager* pager, int slot, void* compute_stream);
  * Replace the per-page event ordering of the MoE page cache,
  * src/mrun/engine/qwen3_moe_cuda.py:1490-1614 (_acquire_resident, acquire_slot_binding). */
 int qs_pager_acquire_many(qs_pager* pager, const int* slots, int n, void* compute_stream);
+/* release_many refuses (QS_ERR_INVALID, nothing changed) a batch that lists a slot twice. */
 int qs_pager_release_many(qs_pager* pager, const int* slots, int n, void* compute_stream);
 /* Block the host until every queued copy has landed. */
 int qs_pager_sync(qs_pager* pager);

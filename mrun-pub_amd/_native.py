@@ -50,9 +50,8 @@ SIGNATURES: dict[str, tuple] = {
     "qs_qrow_matmul_row_stable": (_I, [_P, _I, _L, _P, _P, _P, _L, _L, _L, _L, _P]),
     "qs_qrow_matmul_multi": (_I, [_P, _I, _L, _I, _P, _P, _P, _P, _P, _L, _L, _P]),
     "qs_qrow_batched_workspace_bytes": (ctypes.c_size_t, [_L, _I, _P, _L, _I]),
-    "qs_qrow_batched_counters": (_L, [_I, _P, _I]),
-    "qs_qrow_matmul_batched": (_I, [_P, _I, _L, _I, _P, _P, _P, _P, _P, _L, _L, _P, ctypes.c_size_t, _P, _L, _P]),
-    "qs_qrow_swiglu_batched": (_I, [_P, _L, _P, _P, _P, _P, _P, _L, _L, _L, _L, _P, ctypes.c_size_t, _P, _L, _P]),
+    "qs_qrow_matmul_batched": (_I, [_P, _I, _L, _I, _P, _P, _P, _P, _P, _L, _L, _P, ctypes.c_size_t, _P]),
+    "qs_qrow_swiglu_batched": (_I, [_P, _L, _P, _P, _P, _P, _P, _L, _L, _L, _L, _P, ctypes.c_size_t, _P]),
     "qs_qrow_swiglu": (_I, [_P, _L, _P, _P, _P, _P, _P, _L, _L, _L, _L, _P]),
     "qs_qrow_top2_workspace_bytes": (ctypes.c_size_t, [_L, _L]),
     "qs_qrow_top2": (_I, [_P, _I, _L, _P, _P, _L, _L, _L, _L, _P, ctypes.c_size_t, _P, _P, _P]),
@@ -70,8 +69,8 @@ SIGNATURES: dict[str, tuple] = {
     "qs_moe_route": (_I, [_P, _I, _P, _I, _L, _I, _I, _P, _P, _P, _P, _P, _P]),
     "qs_moe_route_quant": (_I, [_P, _I, _P, _I, _L, _I, _I, _P, _P, _P, _P, _P, _P, _I, _L, _L, _P, _P, _P]),
     "qs_expert_queue_build": (_I, [_P, _I, _P, _P, _P, _I, _P, _P, _L, _I, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
-    "qs_expert_queue_scatter_workspace_bytes": (ctypes.c_size_t, [_L, _I]),
-    "qs_expert_queue_scatter": (_I, [_P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _I, _L, _P, ctypes.c_size_t, _P, _P, _P]),
+    "qs_expert_queue_scatter_workspace_bytes": (ctypes.c_size_t, [_L, _L]),
+    "qs_expert_queue_scatter": (_I, [_P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _P, ctypes.c_size_t, _P, _P, _P]),
     "qs_moe_gather_quant": (_I, [_P, _I, _L, _P, _L, _L, _P, _P, _P]),
     "qs_moe_grouped_gemm_i8": (_I, [_P, _P, _P, _L, _P, _L, _P, _P, _P, _I, _L, _L, _L, _I, _P, _I, _P]),
     "qs_moe_grouped_gemm_i8_rows": (_I, [_P, _P, _P, _L, _P, _L, _P, _L, _P, _P, _P, _I, _L, _L, _L, _I, _P, _I, _P]),

@@ -508,18 +508,10 @@ extern "C" size_t qs_qrow_batched_workspace_bytes(int64_t M, int n_linear, const
   return sh.S > 1 ? (size_t)sh.S * P * std::min<int64_t>(M, 32) * cols * sizeof(float) : 0;
 }
 
-extern "C" int64_t qs_qrow_batched_counters(int n_linear, const int64_t* N, int swiglu) {
-  (void)n_linear;
-  (void)N;
-  (void)swiglu;
-  return 0;  // the kernels need no counters (the argument stays for ABI stability)
-}
-
 extern "C" int qs_qrow_matmul_batched(const void* x, int x_dtype, int64_t ldx, int n_linear,
                                       const int8_t* const* codes, const float* const* scales, void* const* y,
                                       const int64_t* ldy, const int64_t* N, int64_t M, int64_t K,
-                                      void* workspace, size_t workspace_bytes, int32_t* counters,
-                                      int64_t n_counters, void* stream) {
+                                      void* workspace, size_t workspace_bytes, void* stream) {
   if (n_linear < 1 || n_linear > 4) return fail(QS_ERR_LIMIT, "qrow batched: 1..4 linears");
   if (!codes || !scales || !y || !ldy || !N) return fail(QS_ERR_INVALID, "qrow batched: null array");
   BdecParams p;
@@ -533,15 +525,13 @@ extern "C" int qs_qrow_matmul_batched(const void* x, int x_dtype, int64_t ldx, i
     if (!aligned(codes[i], 16)) return fail(QS_ERR_UNSUPPORTED, "qrow batched: weight rows must be 16-byte aligned");
     p.lin[i] = BdecLin{codes[i], scales[i], y[i], ldy[i], (int)N[i], 0, 0};
   }
-  (void)counters;
-  (void)n_counters;
   return bd2_run<1>(p, N, n_linear, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int qs_qrow_swiglu_batched(const void* x, int64_t ldx, const int8_t* gate_codes,
                                       const float* gate_scales, const int8_t* up_codes, const float* up_scales,
                                       void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
-                                      size_t workspace_bytes, int32_t* counters, int64_t n_counters, void* stream) {
+                                      size_t workspace_bytes, void* stream) {
   if (!gate_codes || !gate_scales || !up_codes || !up_scales || !y)
     return fail(QS_ERR_INVALID, "swiglu batched: null pointer");
   if (N <= 0 || N > ((int64_t)1 << 30) || ldy < N) return fail(QS_ERR_INVALID, "swiglu batched: bad N/ldy");
@@ -553,8 +543,6 @@ extern "C" int qs_qrow_swiglu_batched(const void* x, int64_t ldx, const int8_t* 
   p.n_lin = 2;
   p.lin[0] = BdecLin{gate_codes, gate_scales, y, ldy, (int)N, 0, 0};
   p.lin[1] = BdecLin{up_codes, up_scales, nullptr, 0, (int)N, 0, 0};
-  (void)counters;
-  (void)n_counters;
   const int64_t Ns[1] = {N};
   return bd2_run<2>(p, Ns, 1, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

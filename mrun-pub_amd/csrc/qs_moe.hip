@@ -122,7 +122,6 @@ __global__ __launch_bounds__(256) void k_moe_router(const void* __restrict__ log
 constexpr int kRouteWaves = 16;
 constexpr int kRouteMaxE = 512;
 constexpr int kRouteBatch = 8;  // 64-assignment segments a wave loads before using them
-constexpr int kRouteStage = 8192;  // assignments staged in LDS (64 KB)
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 
@@ -138,17 +137,17 @@ __global__ __launch_bounds__(1024) void k_moe_route(const void* __restrict__ top
   __shared__ int base[kRouteMaxE];
   __shared__ int wave_tot[kRouteMaxE / 64];
   __shared__ int total;
-  // queues of up to kRouteStage assignments are built in LDS and written out coalesced
-  // (one workgroup's scattered 64-lane stores are what limits this kernel otherwise)
-  __shared__ int st_tok[kRouteStage];
-  __shared__ float st_coef[kRouteStage];
-  const bool staged = A <= kRouteStage;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   auto expert_of = [&](int i) -> int {
-    if constexpr (IT == QS_I64) return (int)static_cast<const int64_t*>(top_idx)[i];
-    else return static_cast<const int32_t*>(top_idx)[i];
+    // int64 ids are range-checked before narrowing (2^32 + 3 is not expert 3)
+    if constexpr (IT == QS_I64) {
+      const int64_t x = static_cast<const int64_t*>(top_idx)[i];
+      return x >= 0 && x < E ? (int)x : -1;
+    } else {
+      return static_cast<const int32_t*>(top_idx)[i];
+    }
   };
   for (int i = tid; i < kRouteWaves * kRouteMaxE; i += 1024) (&cnt[0][0])[i] = 0;
   __syncthreads();
@@ -238,13 +237,8 @@ __global__ __launch_bounds__(1024) void k_moe_route(const void* __restrict__ top
       if (ok && rank == n_same - 1) cnt[wave][e] += n_same;
       __builtin_amdgcn_wave_barrier();
       if (ok) {
-        if (staged) {
-          st_tok[dest] = i / k;
-          st_coef[dest] = wb[j];
-        } else {
-          token_ids[dest] = i / k;
-          coef[dest] = wb[j];
-        }
+        token_ids[dest] = i / k;
+        coef[dest] = wb[j];
         if (inverse) inverse[i] = dest;
       } else if (valid && inverse) {
         inverse[i] = -1;  // expert outside [0, E): no queue row
@@ -254,17 +248,9 @@ __global__ __launch_bounds__(1024) void k_moe_route(const void* __restrict__ top
   // Assignments with an expert outside [0, E) are left out of the queue.  The rows they
   // leave free at its end get token 0 and coefficient 0, so a consumer that walks all A
   // rows never reads an unwritten index.
-  if (staged) {
-    __syncthreads();
-    for (int q = tid; q < A; q += 1024) {
-      token_ids[q] = q < total ? st_tok[q] : 0;
-      coef[q] = q < total ? st_coef[q] : 0.f;
-    }
-  } else {
-    for (int q = total + tid; q < A; q += 1024) {
-      token_ids[q] = 0;
-      coef[q] = 0.f;
-    }
+  for (int q = total + tid; q < A; q += 1024) {
+    token_ids[q] = 0;
+    coef[q] = 0.f;
   }
 }
 
@@ -285,8 +271,13 @@ __device__ __forceinline__ void route_par_body(int e, const void* __restrict__ t
                                                int64_t* __restrict__ inverse) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   auto expert_of = [&](int i) -> int {
-    if constexpr (IT == QS_I64) return (int)static_cast<const int64_t*>(top_idx)[i];
-    else return static_cast<const int32_t*>(top_idx)[i];
+    // int64 ids are range-checked before narrowing (2^32 + 3 is not expert 3)
+    if constexpr (IT == QS_I64) {
+      const int64_t x = static_cast<const int64_t*>(top_idx)[i];
+      return x >= 0 && x < E ? (int)x : -1;
+    } else {
+      return static_cast<const int32_t*>(top_idx)[i];
+    }
   };
   const int nseg = (A + 63) / 64;
   const int per = (nseg + kParWaves - 1) / kParWaves;

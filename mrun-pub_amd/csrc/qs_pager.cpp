@@ -13,6 +13,7 @@
 // copy has landed.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <new>
 #include <vector>
 
@@ -41,6 +42,9 @@ struct qs_pager {
   std::vector<hipEvent_t> events;
   std::vector<int> refs;
   std::vector<int> pool;
+  // release_many's duplicate check: seen[slot] == stamp marks a slot of the current batch
+  std::vector<unsigned> seen;
+  unsigned stamp = 0;
 };
 
 namespace {
@@ -82,6 +86,7 @@ extern "C" int qs_pager_create(void* device_arena, size_t slot_bytes, int slots,
   p->ready.assign(slots, nullptr);
   p->ready_done.assign(slots, 1);  // never sealed: nothing to wait for
   p->freed.assign(slots, -1);
+  p->seen.assign(slots, 0);
   for (int i = 0; !st && i < slots; ++i)
     st = hip_check(hipEventCreateWithFlags(&p->ready[i], hipEventDisableTiming), "hipEventCreate");
   if (st) {
@@ -168,12 +173,23 @@ extern "C" int qs_pager_acquire_many(qs_pager* p, const int* slots, int n, void*
   return QS_OK;
 }
 
-// One "free" event recorded for the whole batch; each slot drops its previous event.
+// One "free" event recorded for the whole batch; each slot drops its previous event.  A
+// slot listed twice is refused before anything changes: its second reference would drop
+// the batch's own event to zero refs and return it to the pool while the slot still
+// points at it.
 extern "C" int qs_pager_release_many(qs_pager* p, const int* slots, int n, void* compute_stream) {
   if (!p || n < 0 || (n > 0 && !slots)) return fail(QS_ERR_INVALID, "pager_release_many: bad arguments");
   for (int i = 0; i < n; ++i)
     if (slots[i] < 0 || slots[i] >= p->slots) return fail(QS_ERR_INVALID, "pager_release_many: slot out of range");
   if (n == 0) return QS_OK;
+  if (++p->stamp == 0) {  // the stamp wrapped: clear the marks once
+    std::fill(p->seen.begin(), p->seen.end(), 0u);
+    p->stamp = 1;
+  }
+  for (int i = 0; i < n; ++i) {
+    if (p->seen[slots[i]] == p->stamp) return fail(QS_ERR_INVALID, "pager_release_many: slot %d listed twice", slots[i]);
+    p->seen[slots[i]] = p->stamp;
+  }
   int e = -1;
   int st = take_event(p, &e);
   if (st) return st;

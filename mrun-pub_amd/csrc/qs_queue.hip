@@ -9,15 +9,19 @@
 //                     deadline.  A packet whose expert lies outside [0, E) is left out; the
 //                     queue rows it frees at the end get token 0, expert -1, slot -1 and epoch
 //                     INT64_MIN.
-//   k_fill_i64      : fills an int64 array (in place of a memset, so that graph capture
+//   k_fill_i32      : fills an int32 array (in place of a memset, so that graph capture
 //                     records a kernel node).
-//   k_queue_inverse : per packet q: valid[q] = (epoch[q] == active[token[q]]) and
-//                     inverse[token[q] * top_k + slot[q]] = q (the packet that carries route
-//                     slot `slot` of that row).
-//   k_queue_reduce  : per row t and 256 hidden columns: the row's valid packets, taken in
-//                     ascending queue order, summed as acc = acc + fp32(float(y[q]) * coef[q])
-//                     from acc = 0 -- the order and roundings of an index_add_ over the valid
-//                     packets -- with no atomics, so the result is the same on every call.
+//   scatter         : a stable counting sort of the valid packets by token, then a reduce.
+//                     valid[q] = (token in [0, rows) and epoch[q] == active[token[q]]), as the
+//                     reference's index_add_ counts them (by token alone, whatever the route
+//                     slot); k_scatter_count counts each row's valid packets,
+//                     k_scan_exclusive turns the counts into row ranges, k_scatter_place drops
+//                     each packet into its row's range, k_scatter_rank re-orders every range
+//                     by ascending queue index (a packet's rank = the number of smaller indices
+//                     in its range), and k_scatter_reduce sums each row's range in that order
+//                     as acc = acc + fp32(float(y[q]) * coef[q]) from acc = 0 -- the order and
+//                     roundings of the reference's index_add_ -- with no atomics in the sum,
+//                     so the result is the same on every call.  Rows are a grid-stride loop.
 #include "qs_common.h"
 
 #include <limits.h>
@@ -27,7 +31,6 @@ namespace {
 
 constexpr int kQueueWaves = 16;
 constexpr int kQueueMaxE = 512;
-constexpr int kQueueMaxTopK = 64;
 
 template <int IT>
 __device__ __forceinline__ int64_t ld_index(const void* p, int64_t i) {
@@ -158,62 +161,102 @@ __global__ __launch_bounds__(1024) void k_queue_build(QueueBuildArgs p) {
   }
 }
 
-__global__ __launch_bounds__(256) void k_fill_i64(int64_t* __restrict__ dst, int64_t n, int64_t value) {
+__global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ dst, int64_t n, int32_t value) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) dst[i] = value;
 }
 
-__global__ __launch_bounds__(256) void k_queue_inverse(const int64_t* __restrict__ token_ids,
-                                                       const int64_t* __restrict__ route_slots,
+// valid[q] and the number of valid packets per row
+__global__ __launch_bounds__(256) void k_scatter_count(const int64_t* __restrict__ token_ids,
                                                        const int64_t* __restrict__ epochs,
-                                                       const int64_t* __restrict__ active, int64_t A,
-                                                       int64_t rows, int top_k, int64_t* __restrict__ inverse,
-                                                       uint8_t* __restrict__ valid) {
+                                                       const int64_t* __restrict__ active, int64_t A, int64_t rows,
+                                                       uint8_t* __restrict__ valid, int32_t* __restrict__ counts) {
   for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < A; q += (int64_t)gridDim.x * 256) {
     const int64_t t = token_ids[q];
-    const int64_t s = route_slots[q];
-    const bool in = t >= 0 && t < rows && s >= 0 && s < top_k;
-    const bool ok = in && epochs[q] == active[t];
+    const bool ok = t >= 0 && t < rows && epochs[q] == active[t];
     valid[q] = ok ? 1 : 0;
-    if (ok) inverse[t * top_k + s] = q;
+    if (ok) atomicAdd(&counts[t], 1);
   }
 }
 
-template <int YT>
-__global__ __launch_bounds__(256) void k_queue_reduce(const void* __restrict__ y, int64_t ldy,
-                                                      const float* __restrict__ coef,
-                                                      const int64_t* __restrict__ inverse, int top_k,
-                                                      int H, float* __restrict__ out) {
-  __shared__ int64_t order[kQueueMaxTopK];
-  __shared__ int n_valid;
-  const int64_t t = blockIdx.y;
-  if (threadIdx.x == 0) {
-    // the row's packets in ascending queue order (insertion sort of at most top_k entries)
-    int n = 0;
-    for (int s = 0; s < top_k; ++s) {
-      const int64_t q = inverse[t * top_k + s];
-      if (q < 0) continue;
-      int j = n++;
-      while (j > 0 && order[j - 1] > q) {
-        order[j] = order[j - 1];
-        --j;
-      }
-      order[j] = q;
-    }
-    n_valid = n;
-  }
+// In-place exclusive prefix sum of n int32 values, one workgroup: each thread sums a
+// contiguous chunk, the chunk sums are scanned in LDS (Hillis-Steele), then each thread
+// writes its chunk's prefixes.
+__global__ __launch_bounds__(1024) void k_scan_exclusive(int32_t* __restrict__ v, int64_t n) {
+  __shared__ int32_t buf[2][1024];
+  const int tid = threadIdx.x;
+  const int64_t chunk = (n + 1023) / 1024;
+  const int64_t b = tid * chunk;
+  const int64_t e = b + chunk < n ? b + chunk : n;
+  int32_t sum = 0;
+  for (int64_t i = b; i < e; ++i) sum += v[i];
+  buf[0][tid] = sum;
   __syncthreads();
+  int cur = 0;
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int32_t add = tid >= off ? buf[cur][tid - off] : 0;
+    buf[cur ^ 1][tid] = buf[cur][tid] + add;
+    cur ^= 1;
+    __syncthreads();
+  }
+  int32_t run = buf[cur][tid] - sum;  // exclusive prefix of this chunk
+  for (int64_t i = b; i < e; ++i) {
+    const int32_t c = v[i];
+    v[i] = run;
+    run += c;
+  }
+}
+
+// each valid packet into its row's range (arrival order within the range)
+__global__ __launch_bounds__(256) void k_scatter_place(const int64_t* __restrict__ token_ids,
+                                                       const uint8_t* __restrict__ valid, int64_t A,
+                                                       const int32_t* __restrict__ starts,
+                                                       int32_t* __restrict__ cursor, int32_t* __restrict__ tmp) {
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < A; q += (int64_t)gridDim.x * 256) {
+    if (!valid[q]) continue;
+    const int64_t t = token_ids[q];
+    tmp[starts[t] + atomicAdd(&cursor[t], 1)] = (int32_t)q;
+  }
+}
+
+// each valid packet's rank among its row's packets (ascending queue index): the row's
+// range in ascending queue order, whatever order the placement left
+__global__ __launch_bounds__(256) void k_scatter_rank(const int64_t* __restrict__ token_ids,
+                                                      const uint8_t* __restrict__ valid, int64_t A,
+                                                      const int32_t* __restrict__ starts,
+                                                      const int32_t* __restrict__ tmp, int32_t* __restrict__ order) {
+  for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < A; q += (int64_t)gridDim.x * 256) {
+    if (!valid[q]) continue;
+    const int64_t t = token_ids[q];
+    const int32_t b = starts[t], e = starts[t + 1];
+    int32_t r = 0;
+    for (int32_t j = b; j < e; ++j) r += tmp[j] < (int32_t)q ? 1 : 0;
+    order[b + r] = (int32_t)q;
+  }
+}
+
+// per row t (grid-stride over rows) and 256 hidden columns: the row's packets in
+// ascending queue order, acc = acc + fp32(float(y[q]) * coef[q]) from 0
+template <int YT>
+__global__ __launch_bounds__(256) void k_scatter_reduce(const void* __restrict__ y, int64_t ldy,
+                                                        const float* __restrict__ coef,
+                                                        const int32_t* __restrict__ starts,
+                                                        const int32_t* __restrict__ order, int64_t rows, int H,
+                                                        float* __restrict__ out) {
   const int h = blockIdx.x * 256 + threadIdx.x;
   if (h >= H) return;
-  float acc = 0.f;
-  for (int j = 0; j < n_valid; ++j) {
-    const int64_t q = order[j];
-    float v;
-    if constexpr (YT == QS_F32) v = static_cast<const float*>(y)[q * ldy + h];
-    else if constexpr (YT == QS_BF16) v = bf16_bits_to_f32(static_cast<const uint16_t*>(y)[q * ldy + h]);
-    else v = f16_bits_to_f32(static_cast<const uint16_t*>(y)[q * ldy + h]);
-    acc = add_rn(acc, mul_rn(v, coef[q]));
+  for (int64_t t = blockIdx.y; t < rows; t += gridDim.y) {
+    float acc = 0.f;
+    const int32_t b = starts[t], e = starts[t + 1];
+    for (int32_t j = b; j < e; ++j) {
+      const int64_t q = order[j];
+      float v;
+      if constexpr (YT == QS_F32) v = static_cast<const float*>(y)[q * ldy + h];
+      else if constexpr (YT == QS_BF16) v = bf16_bits_to_f32(static_cast<const uint16_t*>(y)[q * ldy + h]);
+      else v = f16_bits_to_f32(static_cast<const uint16_t*>(y)[q * ldy + h]);
+      acc = add_rn(acc, mul_rn(v, coef[q]));
+    }
+    out[t * H + h] = acc;
   }
-  out[t * H + h] = acc;
 }
 
 unsigned grid_for(int64_t n) {
@@ -268,41 +311,46 @@ extern "C" int qs_expert_queue_build(const void* experts, int expert_dtype, cons
   return hip_check(hipGetLastError(), "k_queue_build launch");
 }
 
-extern "C" size_t qs_expert_queue_scatter_workspace_bytes(int64_t rows, int top_k) {
-  if (rows <= 0 || top_k <= 0) return 0;
-  return (size_t)(rows * top_k) * sizeof(int64_t);
+// workspace (int32): starts[rows + 1] | cursor[rows] | tmp[A] | order[A]
+extern "C" size_t qs_expert_queue_scatter_workspace_bytes(int64_t rows, int64_t A) {
+  if (rows <= 0 || A < 0) return 0;
+  return (size_t)(2 * rows + 1 + 2 * A) * sizeof(int32_t);
 }
 
-extern "C" int qs_expert_queue_scatter(const int64_t* token_ids, const int64_t* route_slots,
-                                       const float* coefficients, const int64_t* epochs,
+extern "C" int qs_expert_queue_scatter(const int64_t* token_ids, const float* coefficients, const int64_t* epochs,
                                        const int64_t* active_epochs, const void* expert_out, int out_dtype,
-                                       int64_t ld_out, int64_t A, int64_t rows, int top_k, int64_t H,
-                                       void* workspace, size_t workspace_bytes, float* reduced,
-                                       uint8_t* valid, void* stream) {
-  if (!active_epochs || !reduced || !workspace || (A > 0 && (!token_ids || !route_slots || !coefficients ||
-                                                             !epochs || !expert_out || !valid)))
+                                       int64_t ld_out, int64_t A, int64_t rows, int64_t H, void* workspace,
+                                       size_t workspace_bytes, float* reduced, uint8_t* valid, void* stream) {
+  if (!active_epochs || !reduced || !workspace ||
+      (A > 0 && (!token_ids || !coefficients || !epochs || !expert_out || !valid)))
     return fail(QS_ERR_INVALID, "expert_queue_scatter: null pointer");
-  if (A < 0 || rows < 1 || top_k < 1 || H < 1 || ld_out < H)
-    return fail(QS_ERR_INVALID, "expert_queue_scatter: bad shape");
-  if (top_k > kQueueMaxTopK) return fail(QS_ERR_LIMIT, "expert_queue_scatter: top_k at most %d", kQueueMaxTopK);
-  if (H > INT_MAX || rows > 65535) return fail(QS_ERR_LIMIT, "expert_queue_scatter: at most 65535 rows");
-  if (workspace_bytes < qs_expert_queue_scatter_workspace_bytes(rows, top_k))
+  if (A < 0 || rows < 1 || H < 1 || ld_out < H) return fail(QS_ERR_INVALID, "expert_queue_scatter: bad shape");
+  if (H > INT_MAX || A >= INT_MAX || rows >= INT_MAX)
+    return fail(QS_ERR_LIMIT, "expert_queue_scatter: packets, rows and hidden size below 2^31");
+  if (workspace_bytes < qs_expert_queue_scatter_workspace_bytes(rows, A))
     return fail(QS_ERR_INVALID, "expert_queue_scatter: workspace smaller than qs_expert_queue_scatter_workspace_bytes()");
   if (out_dtype != QS_F32 && out_dtype != QS_BF16 && out_dtype != QS_F16)
     return fail(QS_ERR_INVALID, "expert_queue_scatter: expert outputs F32, BF16 or F16");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int64_t* inverse = static_cast<int64_t*>(workspace);
-  const int64_t slots_total = rows * top_k;
-  hipLaunchKernelGGL(k_fill_i64, dim3(grid_for(slots_total)), dim3(256), 0, s, inverse, slots_total, (int64_t)-1);
-  if (A > 0)
-    hipLaunchKernelGGL(k_queue_inverse, dim3(grid_for(A)), dim3(256), 0, s, token_ids, route_slots, epochs,
-                       active_epochs, A, rows, top_k, inverse, valid);
-  const dim3 grid((unsigned)cdiv(H, 256), (unsigned)rows);
+  int32_t* starts = static_cast<int32_t*>(workspace);
+  int32_t* cursor = starts + rows + 1;
+  int32_t* tmp = cursor + rows;
+  int32_t* order = tmp + A;
+  // counts (then starts, in place) and cursors start at zero: one fill kernel over both
+  hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(2 * rows + 1)), dim3(256), 0, s, starts, 2 * rows + 1, 0);
+  if (A > 0) {
+    hipLaunchKernelGGL(k_scatter_count, dim3(grid_for(A)), dim3(256), 0, s, token_ids, epochs, active_epochs, A,
+                       rows, valid, starts);
+    hipLaunchKernelGGL(k_scan_exclusive, dim3(1), dim3(1024), 0, s, starts, rows + 1);
+    hipLaunchKernelGGL(k_scatter_place, dim3(grid_for(A)), dim3(256), 0, s, token_ids, valid, A, starts, cursor, tmp);
+    hipLaunchKernelGGL(k_scatter_rank, dim3(grid_for(A)), dim3(256), 0, s, token_ids, valid, A, starts, tmp, order);
+  }
+  const dim3 grid((unsigned)cdiv(H, 256), (unsigned)(rows < 65535 ? rows : 65535));
   if (out_dtype == QS_F32)
-    hipLaunchKernelGGL(k_queue_reduce<QS_F32>, grid, dim3(256), 0, s, expert_out, ld_out, coefficients, inverse, top_k, (int)H, reduced);
+    hipLaunchKernelGGL(k_scatter_reduce<QS_F32>, grid, dim3(256), 0, s, expert_out, ld_out, coefficients, starts, order, rows, (int)H, reduced);
   else if (out_dtype == QS_BF16)
-    hipLaunchKernelGGL(k_queue_reduce<QS_BF16>, grid, dim3(256), 0, s, expert_out, ld_out, coefficients, inverse, top_k, (int)H, reduced);
+    hipLaunchKernelGGL(k_scatter_reduce<QS_BF16>, grid, dim3(256), 0, s, expert_out, ld_out, coefficients, starts, order, rows, (int)H, reduced);
   else
-    hipLaunchKernelGGL(k_queue_reduce<QS_F16>, grid, dim3(256), 0, s, expert_out, ld_out, coefficients, inverse, top_k, (int)H, reduced);
+    hipLaunchKernelGGL(k_scatter_reduce<QS_F16>, grid, dim3(256), 0, s, expert_out, ld_out, coefficients, starts, order, rows, (int)H, reduced);
   return hip_check(hipGetLastError(), "expert queue scatter launch");
 }

@@ -264,15 +264,14 @@ def _scatter(plan: ExpertQueuePlan, expert_outputs: torch.Tensor, active_epochs:
     A = plan.assignments
     reduced = torch.empty((plan.num_rows, H), dtype=torch.float32, device=device)
     valid = torch.empty(A, dtype=torch.uint8, device=device)
-    ws_bytes = int(nat.load().qs_expert_queue_scatter_workspace_bytes(plan.num_rows, plan.top_k))
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    ws_bytes = int(nat.load().qs_expert_queue_scatter_workspace_bytes(plan.num_rows, A))
+    ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=device)
     active = active_epochs.to(torch.int64).contiguous()
     coef = plan.coefficients.to(torch.float32).contiguous()
     nat.call(
-        "qs_expert_queue_scatter", nat.ptr(plan.token_ids.to(torch.int64).contiguous()),
-        nat.ptr(plan.route_slots.to(torch.int64).contiguous()), nat.ptr(coef),
+        "qs_expert_queue_scatter", nat.ptr(plan.token_ids.to(torch.int64).contiguous()), nat.ptr(coef),
         nat.ptr(plan.epochs.to(torch.int64).contiguous()), nat.ptr(active), nat.ptr(y), nat.dtype_code(y.dtype),
-        int(y.stride(0)) if A else H, A, plan.num_rows, plan.top_k, H, nat.ptr(ws), ws_bytes, nat.ptr(reduced),
+        int(y.stride(0)) if A else H, A, plan.num_rows, H, nat.ptr(ws), ws_bytes, nat.ptr(reduced),
         nat.ptr(valid), nat.stream_of(device),
     )
     return reduced, valid.view(torch.bool)

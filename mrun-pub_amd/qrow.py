@@ -183,12 +183,12 @@ def _run_batched(x2: torch.Tensor, pages: list[tuple[torch.Tensor, torch.Tensor]
         if swiglu:
             (gc, gs), (uc, us) = pages
             nat.call("qs_qrow_swiglu_batched", nat.ptr(xb), k, nat.ptr(gc), nat.ptr(gs), nat.ptr(uc), nat.ptr(us),
-                     nat.ptr(outs[0][m0:]), ns[0], mm, ns[0], k, nat.ptr(ws), ws_bytes, None, 0, stream)
+                     nat.ptr(outs[0][m0:]), ns[0], mm, ns[0], k, nat.ptr(ws), ws_bytes, stream)
         else:
             nat.call("qs_qrow_matmul_batched", nat.ptr(xb), nat.dtype_code(x2.dtype), k, len(pages),
                      nat.pointer_array([nat.ptr(c) for c, _ in pages]), nat.pointer_array([nat.ptr(sc) for _, sc in pages]),
                      nat.pointer_array([nat.ptr(o[m0:]) for o in outs]), n_arr, n_arr, mm, k, nat.ptr(ws), ws_bytes,
-                     None, 0, stream)
+                     stream)
 
 
 @torch.inference_mode()

@@ -94,7 +94,8 @@ def test_route_drops_out_of_range_both_kernels(dev, T, E, k):
     rng = np.random.default_rng(T)
     top = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
     bad = rng.random((T, k)) < 0.01
-    top[bad] = rng.choice([-3, -1, E, E + 7], size=int(bad.sum()))
+    # int64 ids are range-checked before any narrowing: 2**32 + 3 is not expert 3
+    top[bad] = rng.choice([-3, -1, E, E + 7, 2**32 + 3, -(2**32) + 1], size=int(bad.sum()))
     w = rng.random((T, k)).astype(np.float32)
     tok, coef, starts, counts, inv, _ = _moe().grouped_route_tensors_with_inverse(_t(top, dev), _t(w, dev), num_experts=E)
     keep = ~bad

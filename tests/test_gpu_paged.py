@@ -145,3 +145,32 @@ def test_paged_errors(dev, store_dir):
         st.matmul("l0.q", torch.zeros(1, 255, dtype=torch.bfloat16, device=dev))
     assert all(h == 0 for h in st.ring.held), "a failed call must release its slot"
     st.close()
+
+
+def test_pager_release_many_refuses_a_slot_listed_twice(dev):
+    """A release batch that names one slot twice is refused with nothing changed (its second
+    reference would hand the batch's event back to the pool while the slot still waits on
+    it); distinct batches keep working, and a refill of a released slot lands whole."""
+    import ctypes
+
+    from mrun_pub_amd import _native as nat
+
+    arena = torch.zeros(4 * 4096, dtype=torch.uint8, device=dev)
+    handle = ctypes.c_void_p()
+    nat.call("qs_pager_create", nat.ptr(arena), 4096, 4, 4096, ctypes.byref(handle))
+    try:
+        stream = nat.stream_of(dev)
+        with pytest.raises(ValueError, match="listed twice"):
+            nat.call("qs_pager_release_many", handle, (ctypes.c_int * 3)(1, 2, 1), 3, stream)
+        nat.call("qs_pager_release_many", handle, (ctypes.c_int * 2)(1, 2), 2, stream)
+        nat.call("qs_pager_release_many", handle, (ctypes.c_int * 1)(1), 1, stream)
+        host = torch.arange(4096, dtype=torch.int32).to(torch.uint8).pin_memory()
+        for slot in (1, 2):
+            nat.call("qs_pager_submit", handle, slot, host.data_ptr(), 4096, 0)
+            nat.call("qs_pager_seal", handle, slot)
+        nat.call("qs_pager_acquire_many", handle, (ctypes.c_int * 2)(1, 2), 2, stream)
+        torch.cuda.synchronize()
+        assert torch.equal(arena[4096:8192].cpu(), host) and torch.equal(arena[8192:12288].cpu(), host)
+        assert not arena[:4096].any() and not arena[12288:].any()
+    finally:
+        nat.call("qs_pager_destroy", handle)

@@ -140,3 +140,52 @@ def test_device_builder_drops_out_of_range_experts(dev):
     assert plan.token_ids.tolist()[:3] == [0, 1, 0] and plan.expert_ids.tolist()[3] == -1
     with pytest.raises(AssertionError):
         plan.assert_valid()
+
+
+def test_scatter_matches_rows_by_token_alone(dev):
+    """An unvalidated flat plan may carry two packets with the same (token, route slot) or a
+    slot outside [0, top_k): the reference's index_add_ counts every packet whose epoch
+    matches, by token alone (expert_queue.py:487-514), and so does the device scatter,
+    with the same bits on every call."""
+    q = _q()
+    tok = np.array([0, 1, 0, 2, 0, 1], np.int64)
+    exp = np.array([3, 1, 2, 0, 1, 2], np.int64)
+    slot = np.array([1, 0, 1, 9, 0, -4], np.int64)  # (0, 1) twice; slots 9 and -4 out of range
+    cf = np.array([0.5, 0.25, 0.75, 1.5, 2.0, 3.0], np.float32)
+    ep = np.array([4, 5, 6], np.int64)
+    plan = q.build_expert_queue_flat(_t(tok, dev), _t(exp, dev), _t(slot, dev), _t(cf, dev), num_rows=3,
+                                     num_experts=4, top_k=2, epochs=_t(ep, dev), deadlines=_t(ep, dev),
+                                     validate=False)
+    rng = np.random.default_rng(8)
+    out = rng.standard_normal((6, 33)).astype(np.float32)
+    act = np.array([4, 5, 6], np.int64)
+    ref = {f: getattr(plan, f).cpu().numpy() for f in FIELDS}
+    r_red, r_valid = oe.scatter(ref, out, act, 3)
+    assert r_valid.all()
+    first = None
+    for _ in range(3):
+        red, valid = q.scatter_committed(plan, _t(out, dev), active_epochs=_t(act, dev))
+        assert np.array_equal(valid.cpu().numpy(), r_valid)
+        assert np.array_equal(red.cpu().numpy().view(np.uint32), r_red.view(np.uint32))
+        first = red if first is None else first
+        assert torch.equal(red, first)
+
+
+def test_scatter_more_rows_than_one_grid_dimension(dev):
+    """A prefill queue of 70,000 token rows (more than 65,535, the limit of one grid
+    dimension): every row reduced, against the oracle."""
+    q = _q()
+    rows, E, k, H = 70000, 16, 2, 8
+    rng = np.random.default_rng(70)
+    top = np.stack([rng.permutation(E)[:k] for _ in range(rows)]).astype(np.int64)
+    w = rng.random((rows, k)).astype(np.float32)
+    ep = rng.integers(0, 3, size=rows)
+    plan = q.build_expert_queue_device(_t(top, dev), _t(w, dev), num_experts=E, epochs=_t(ep, dev),
+                                       deadlines=_t(ep, dev))
+    out = rng.standard_normal((rows * k, H)).astype(np.float32)
+    act = np.where(rng.random(rows) < 0.9, ep, ep + 1)
+    red, valid = q.scatter_committed_device(plan, _t(out, dev), active_epochs=_t(act, dev))
+    ref = {f: getattr(plan, f).cpu().numpy() for f in FIELDS}
+    r_red, r_valid = oe.scatter(ref, out, act, rows)
+    assert np.array_equal(valid.cpu().numpy(), r_valid)
+    assert np.array_equal(red.cpu().numpy().view(np.uint32), r_red.view(np.uint32))
