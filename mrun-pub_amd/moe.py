@@ -423,12 +423,16 @@ class Int8ExpertLayer:
         H, I = L.hidden_size, L.intermediate_size
         ps = L.page_stride
         base = arena.view(torch.int8)
-        # strided [E, N, K] views into the pages (no copies)
-        self.gate_up = base.as_strided((E, 2 * I, H), (ps, H, 1), L.gate_up_codes_offset)
-        self.down = base.as_strided((E, H, I), (ps, I, 1), L.down_codes_offset)
+        # strided [E, N, K] views into the pages (no copies); as_strided offsets count from
+        # the start of the storage, so the arena's own offset (a slab inside a larger
+        # allocation) is added
+        o8 = base.storage_offset()
+        self.gate_up = base.as_strided((E, 2 * I, H), (ps, H, 1), o8 + L.gate_up_codes_offset)
+        self.down = base.as_strided((E, H, I), (ps, I, 1), o8 + L.down_codes_offset)
         fl = arena.view(torch.float32)
-        self.gate_up_scales = fl.as_strided((E, 2 * I), (ps // 4, 1), L.gate_up_scales_offset // 4)
-        self.down_scales = fl.as_strided((E, H), (ps // 4, 1), L.down_scales_offset // 4)
+        o32 = fl.storage_offset()
+        self.gate_up_scales = fl.as_strided((E, 2 * I), (ps // 4, 1), o32 + L.gate_up_scales_offset // 4)
+        self.down_scales = fl.as_strided((E, H), (ps // 4, 1), o32 + L.down_scales_offset // 4)
 
     @classmethod
     def from_arrays(cls, gate_up, gate_up_scales, down, down_scales, device) -> "Int8ExpertLayer":
@@ -562,8 +566,14 @@ class Int8ExpertBackend:
         expert (a compact group id) to its cache slot, and the grouped GEMMs read the pages
         in place through ``group_slots``."""
         cache = self.page_cache
-        table = cache.acquire_layer_table(layer, top_indices, protect=not prefill)
-        if table is not None:
+        transient = prefill and getattr(cache, "prefill_page_policy", None) == "transient-frequency-v1"
+        table = None if transient else cache.acquire_layer_table(layer, top_indices, protect=not prefill)
+        if transient:
+            # the layer runs from the cache's transient slab (qwen3_moe_cuda.py:2850-2854)
+            selected, page, slots = cache.acquire_transient_prefill(layer, top_indices)
+            route_idx = torch.searchsorted(selected, top_indices)
+            E = int(selected.numel())
+        elif table is not None:
             # every page of the layer is resident: groups are the expert ids themselves and
             # the device slot table binds them, with no host synchronisation
             page, slots = table

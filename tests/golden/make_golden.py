@@ -12,6 +12,10 @@ Sections (pass their names after the reference root to write only those; default
 * ``core``     -- w8a8.npz, codecs.npz, moe.npz
 * ``moe_forward`` -- moe_forward.npz: streamed_moe_forward's expert math on a tiny layer
 * ``queue``    -- queue.npz: build_expert_queue / build_expert_queue_flat / scatter_committed
+* ``page_cache`` -- page_cache.json: the reference's ExpertPageCache (device "cpu") driven
+  through seeded random sequences of decode / prefill slot-binding acquires, transient
+  prefills and resets, with its whole host state recorded after every call, plus its page
+  trace manifest
 * ``refstore`` -- refstore/legacy (a store in the reference's own test layout,
   tests/test_qstore_cache.py:19-46) and refstore/v3 (a v3 store sealed by the reference's
   provenance functions), with refstore.npz / refstore.json holding what the reference's
@@ -29,6 +33,9 @@ Functions covered (reference file:line):
 * streamed_moe_forward (per-expert math) src/mrun/engine/moe_safetensors.py:404, 585-627
 * QStore.weight / embed_rows / matmul, _load_qstore_manifest
                                        src/mrun/engine/kernels/qstore.py:326-373, 1026-1128
+* ExpertPageCache (slot policy, decode protection, transient-frequency-v1 prefill, the
+  mrun-qwen3-moe-page-trace-v1 trace)
+                                       src/mrun/engine/qwen3_moe_cuda.py:983-1777
 * build_source/builder/derived_provenance
                                        src/mrun/store_provenance.py:86-275, 390-412
 """
@@ -163,12 +170,95 @@ def main(ref_root: str, sections: list[str]) -> None:
         moe_forward_section(files)
     manifest_path = HERE / "golden_manifest.json"
     manifest = json.loads(manifest_path.read_text()) if manifest_path.exists() else {}
+    if "page_cache" in sections:
+        path = page_cache_section()
+        manifest[path.name] = hashlib.sha256(path.read_bytes()).hexdigest()
     for name, arrs in files.items():
         path = HERE / name
         np.savez(path, **arrs)
         manifest[name] = hashlib.sha256(path.read_bytes()).hexdigest()
     manifest_path.write_text(json.dumps(manifest, indent=1, sort_keys=True) + "\n")
     print(json.dumps(manifest, indent=1))
+
+
+def _tiny_fp8_store(root: Path, layers: int, experts: int) -> Path:
+    """A packed expert store in the reference's FP8 file format (manifest fields of
+    qwen3_moe_cuda.py:780-795), pages filled with a byte pattern, written by this script."""
+    from mrun.engine.qwen3_moe_cuda import ExpertPageLayout
+
+    layout = ExpertPageLayout.create(hidden_size=4, intermediate_size=2)
+    pages = (np.arange(layout.page_stride, dtype=np.int64)[None, :] + 17 * np.arange(layers * experts)[:, None])
+    root.mkdir(parents=True, exist_ok=True)
+    (root / "experts.fp8").write_bytes((pages % 256).astype(np.uint8).tobytes())
+    (root / "manifest.json").write_text(json.dumps({
+        "schema_version": "qwen3-moe-packed-expert-store-v1", "codec": "rowwise-e4m3fn-paged-v1",
+        "data_file": "experts.fp8", "layers": layers, "num_experts": experts, "layout": layout.as_dict()}))
+    return root
+
+
+def page_cache_section() -> Path:
+    import tempfile
+
+    import torch
+
+    from mrun.engine.qwen3_moe_cuda import ExpertPageCache, PackedFP8ExpertStore
+
+    configs = [
+        dict(name="lfu_transient", layers=3, experts=6, max_active=4, capacity=4,
+             cache_policy="layer-frequency-lru-v1", prefill="transient-frequency-v1", steps=40, seed=1),
+        dict(name="lfu_transient_wide", layers=2, experts=8, max_active=6, capacity=9,
+             cache_policy="layer-frequency-lru-v1", prefill="transient-frequency-v1", steps=40, seed=2),
+        dict(name="global", layers=3, experts=5, max_active=3, capacity=5,
+             cache_policy="global-lru-v1", prefill="cache-fill-v1", steps=30, seed=3),
+        dict(name="lfu", layers=4, experts=5, max_active=4, capacity=7,
+             cache_policy="layer-frequency-lru-v1", prefill="cache-fill-v1", steps=30, seed=4),
+    ]
+    out = {"configs": []}
+    with tempfile.TemporaryDirectory() as tmp:
+        for cfg in configs:
+            rng = np.random.default_rng(cfg["seed"])
+            store = PackedFP8ExpertStore(_tiny_fp8_store(Path(tmp) / cfg["name"], cfg["layers"], cfg["experts"]))
+            stride = store.layout.page_stride
+            cache = ExpertPageCache(store, device="cpu", cache_mb=cfg["capacity"] * stride / 1e6,
+                                    max_active_pages=cfg["max_active"], cache_policy=cfg["cache_policy"],
+                                    page_binding_policy="slot-indirect-v1", prefill_page_policy=cfg["prefill"],
+                                    route_prefetch=False, page_trace=True)
+            assert cache.capacity == cfg["capacity"]
+            ops = []
+            for _ in range(cfg["steps"]):
+                r = rng.random()
+                layer = int(rng.integers(0, cfg["layers"]))
+                n_exp = int(rng.integers(1, cfg["max_active"] + 1))
+                experts = rng.choice(cfg["experts"], size=n_exp, replace=False)
+                routed = [int(e) for e in rng.choice(experts, size=int(rng.integers(n_exp, 3 * n_exp + 1)))]
+                routed += [int(e) for e in experts]  # every chosen expert is routed at least once
+                rng.shuffle(routed)
+                idx = torch.tensor([routed])
+                if r < 0.05:
+                    clear = bool(rng.random() < 0.5)
+                    cache.reset(clear_pages=clear)
+                    op = {"op": "reset", "clear_pages": clear}
+                elif r < 0.40 and cfg["prefill"] == "transient-frequency-v1":
+                    sel, _, gs = cache.acquire_transient_prefill(layer, idx)
+                    op = {"op": "transient", "layer": layer, "routed": routed, "selected": sel.tolist(),
+                          "group_slots": gs.tolist()}
+                else:
+                    protect = bool(rng.random() < 0.6)
+                    sel, _, slots = cache.acquire_slot_binding(layer, idx, protect=protect)
+                    op = {"op": "acquire", "layer": layer, "routed": routed, "protect": protect,
+                          "selected": sel.tolist(), "slots": slots.tolist()}
+                op["entries"] = [[k[0], k[1], int(v)] for k, v in cache.entries.items()]
+                op["decode_protected"] = sorted([list(k) for k in cache.decode_protected])
+                op["layer_entry_counts"] = list(cache.layer_entry_counts)
+                op["free_slots"] = list(cache.free_slots)
+                stats = cache.stats.as_dict()
+                op["stats"] = [stats[k] for k in sorted(stats)]
+                ops.append(op)
+            out["configs"].append({**cfg, "page_stride": stride, "ops": ops, "stats_keys": sorted(stats),
+                                   "trace": cache.export_page_trace(), "trace_status": cache.page_trace_status()})
+    path = HERE / "page_cache.json"
+    path.write_text(json.dumps(out, sort_keys=True) + "\n")
+    return path
 
 
 def core_section(files: dict) -> None:
@@ -342,7 +432,7 @@ def moe_forward_section(files: dict) -> None:
     files["moe_forward.npz"] = arrays
 
 
-SECTIONS = ("core", "refstore", "queue", "moe_forward")
+SECTIONS = ("core", "refstore", "queue", "moe_forward", "page_cache")
 
 if __name__ == "__main__":
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"

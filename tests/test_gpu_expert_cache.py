@@ -168,3 +168,142 @@ def test_preload_makes_layers_use_the_device_table(dev, tmp_path):
     for layer, x, idx, w in steps:
         assert torch.equal(paged.moe(layer, x, idx, w), resident.moe(layer, x, idx, w))
     small.close()
+
+
+# ---- transient-frequency-v1 prefill and the page trace on the device --------------------------
+
+
+def _gold_cache_store(tmp_path, cfg):
+    """An int8 expert store with the golden run's geometry (H 4, I 2: one 4096-byte page)."""
+    ec, _ = _mods()
+    rng = np.random.default_rng(cfg["seed"])
+    L, E = cfg["layers"], cfg["experts"]
+    arrays = (rng.integers(-127, 128, size=(L, E, 4, 4), dtype=np.int8), rng.random((L, E, 4), dtype=np.float32),
+              rng.integers(-127, 128, size=(L, E, 4, 2), dtype=np.int8), rng.random((L, E, 4), dtype=np.float32))
+    return ec.PackedInt8ExpertStore(ec.write_int8_expert_store(tmp_path / cfg["name"], *arrays))
+
+
+@pytest.mark.parametrize("which", [0, 1, 2, 3])
+def test_cache_replays_the_reference_cache_and_moves_the_right_bytes(dev, tmp_path, which):
+    """The reference cache's recorded sequences (tests/golden/page_cache.json) through the
+    HIP-backed cache: the same decisions, statistics and trace, and after every call every
+    cache slot holds its page's bytes and every slab position the routed page's bytes."""
+    import json
+    from pathlib import Path
+
+    ec, _ = _mods()
+    cfg = json.loads((Path(__file__).resolve().parent / "golden" / "page_cache.json").read_text())["configs"][which]
+    store = _gold_cache_store(tmp_path, cfg)
+    stride = store.layout.page_stride
+    assert stride == cfg["page_stride"]
+    pages = torch.from_numpy(np.array(store._pages()))  # noqa: SLF001 - the expected bytes
+    cache = ec.ExpertPageCache(store, device=dev, cache_mb=cfg["capacity"] * stride / 1e6,
+                               max_active_pages=cfg["max_active"], cache_policy=cfg["cache_policy"],
+                               prefill_page_policy=cfg["prefill"], page_trace=True, route_prefetch=False)
+    assert cache.capacity == cfg["capacity"]
+    for i, op in enumerate(cfg["ops"]):
+        where = (cfg["name"], i, op["op"])
+        idx = torch.tensor([op.get("routed", [0])], device=dev)
+        if op["op"] == "reset":
+            cache.reset(clear_pages=op["clear_pages"])
+        elif op["op"] == "acquire":
+            sel, _, slots = cache.acquire_slot_binding(op["layer"], idx, protect=op["protect"])
+            assert (sel.tolist(), slots.tolist()) == (op["selected"], op["slots"]), where
+        else:
+            sel, views, gs = cache.acquire_transient_prefill(op["layer"], idx)
+            assert (sel.tolist(), gs.tolist()) == (op["selected"], op["group_slots"]), where
+            torch.cuda.synchronize()
+            slab = cache.slab.cpu()
+            for g, e in enumerate(op["selected"]):
+                assert torch.equal(slab[gs[g].item()], pages[store.global_page(op["layer"], e)]), where
+        cache.release()
+        torch.cuda.synchronize()
+        assert [[k[0], k[1], v] for k, v in cache.entries.items()] == op["entries"], where
+        assert sorted(list(k) for k in cache.decode_protected) == op["decode_protected"], where
+        assert cache.layer_entry_counts == op["layer_entry_counts"], where
+        stats = cache.stats.as_dict()
+        assert [stats[k] for k in cfg["stats_keys"]] == op["stats"], where
+        held = cache.cache.cpu()
+        for (layer, expert, slot) in op["entries"]:
+            assert torch.equal(held[slot], pages[store.global_page(layer, expert)]), (where, layer, expert)
+    assert cache.export_page_trace() == cfg["trace"]
+    cache.close()
+
+
+def test_transient_prefill_equals_resident_and_keeps_the_decode_set(dev, tmp_path):
+    """Under transient-frequency-v1 a prefill layer runs from the slab: its output equals the
+    resident backend's bit for bit, the pages another request's decode steps protect stay
+    in their slots, and only the hottest pages of the prompt are admitted (within the
+    layer quota)."""
+    ec, moe = _mods()
+    store, resident = _setup(tmp_path, dev, L=2, E=16)
+    # 16 cache slots (the active-set bound), quotas of 8 per layer, and a 16-page slab
+    cache = ec.ExpertPageCache(store, device=dev, cache_mb=0, max_active_pages=16,
+                               cache_policy="layer-frequency-lru-v1", prefill_page_policy="transient-frequency-v1")
+    assert cache.capacity == 16 and cache.policy.layer_quotas == (8, 8)
+    assert cache.slab is not None and cache.device_bytes == (16 + 16) * store.layout.page_stride
+    paged = moe.Int8ExpertBackend(page_cache=cache)
+    g = torch.Generator(device="cpu").manual_seed(7)
+
+    def routes(T, k, experts):
+        logits = torch.full((T, 16), -30.0)
+        logits[:, experts] = torch.randn(T, len(experts), generator=g)
+        w, idx = torch.softmax(logits, -1).topk(k, -1)
+        x = torch.randn(T, 256, generator=g).to(torch.bfloat16)
+        return x.to(dev), idx.to(dev), (w / w.sum(-1, keepdim=True)).to(torch.bfloat16).to(dev)
+
+    # a decode request settles on four experts of each layer
+    for layer in (0, 1):
+        x, idx, w = routes(2, 4, [1, 3, 5, 7])
+        assert torch.equal(paged.moe(layer, x, idx, w), resident.moe(layer, x, idx, w))
+    decode_set = set(cache.decode_protected)
+    slots_before = {k: cache.entries[k] for k in decode_set}
+    assert len(decode_set) == 8
+    # a long prompt scans every expert of both layers
+    for layer in (0, 1):
+        x, idx, w = routes(64, 8, list(range(16)))
+        out = paged.moe(layer, x, idx, w, prefill=True)
+        assert torch.equal(out, resident.moe(layer, x, idx, w))
+    torch.cuda.synchronize()
+    assert set(cache.decode_protected) == decode_set
+    assert {k: cache.entries[k] for k in decode_set} == slots_before
+    st = cache.stats
+    assert st.transient_prefill_acquires == 2 and st.transient_prefill_pages == 32
+    assert st.transient_prefill_resident_materialization_d2d_bytes == 8 * store.layout.page_stride
+    # quota 8 per layer, 4 held by decode pages: four seats each for the prompt's hottest pages
+    assert st.transient_prefill_admitted_pages == 8
+    assert cache.layer_entry_counts == [8, 8]
+    # the decode request goes on with its pages still resident (hits only)
+    hits = st.page_hits
+    for layer in (0, 1):
+        x, idx, w = routes(2, 4, [1, 3, 5, 7])
+        assert torch.equal(paged.moe(layer, x, idx, w), resident.moe(layer, x, idx, w))
+    assert cache.stats.page_hits == hits + 8 and cache.stats.page_misses == st.page_misses
+    # the same prompt again: pages admitted by the first prefill now come from the cache
+    for layer in (0, 1):
+        x, idx, w = routes(64, 8, list(range(16)))
+        assert torch.equal(paged.moe(layer, x, idx, w, prefill=True), resident.moe(layer, x, idx, w))
+    cache.close()
+
+
+def test_page_trace_on_the_device_cache(dev, tmp_path):
+    """Decode and prefill acquires are traced; tracing turns the device slot-table binding
+    off (it reads routes on the host) and leaves results unchanged."""
+    ec, moe = _mods()
+    store, resident = _setup(tmp_path, dev, L=2, E=16)
+    cache = ec.ExpertPageCache(store, device=dev, cache_mb=40 * store.layout.page_stride / 1e6, max_active_pages=16,
+                               page_trace=True)
+    cache.preload()
+    paged = moe.Int8ExpertBackend(page_cache=cache)
+    steps = _steps(dev, 2, 16, steps=2)
+    for i, (layer, x, idx, w) in enumerate(steps):
+        assert torch.equal(paged.moe(layer, x, idx, w, prefill=i < 2), resident.moe(layer, x, idx, w))
+    assert cache.device_table_stats["device_table_layers"] == 0
+    m = cache.export_page_trace()
+    assert [(e["phase"], e["step"], e["layer"]) for e in m["events"]] == [
+        ("prefill", 0, 0), ("prefill", 0, 1), ("decode", 0, 0), ("decode", 0, 1)]
+    for e, (layer, _, idx, _) in zip(m["events"], steps):
+        vals, counts = torch.unique(idx.cpu(), return_counts=True)
+        assert e["pages"] == [[int(v), int(c)] for v, c in zip(vals, counts)]
+    assert cache.page_trace_status()["events"] == 4 and cache.drain_page_trace() == m
+    cache.close()
