@@ -113,8 +113,7 @@ def cpu_baseline(seconds: float = 6.0, m: int = 1, threads: int | None = None) -
     from oracle import cpu_path
 
     prev = torch.get_num_threads()
-    if threads:
-        torch.set_num_threads(threads)
+    torch.set_num_threads(threads or os.cpu_count() or prev)
     try:
         rng = np.random.default_rng(0)
         layer = [
@@ -150,7 +149,7 @@ def cpu_baselines_per_config(seconds: float = 2.0) -> dict:
     from oracle import cpu_path
 
     rng = np.random.default_rng(7)
-    all_threads = torch.get_num_threads()
+    all_threads = os.cpu_count() or torch.get_num_threads()
     out: dict = {"cpu_model": _cpu_model(), "threads_all": all_threads}
 
     def both(name, fn, unit_per_call, unit, sample):
@@ -246,7 +245,9 @@ def _replay_times(torch, stream, graph, reps: int, warmup: int) -> list[float]:
 
 def paged_measurement(torch, dev, pages, x_h, x_i, passes: int = 6) -> dict:
     """Config 2 as BASELINE words it: the same stack streamed from pinned host memory in
-    2 MiB pages through the HBM slot ring (PCIe-inclusive; never the headline value)."""
+    2 MiB pages through the HBM slot ring (PCIe-inclusive; never the headline value), from
+    a pinned tier holding the whole stack and, in bounded mode, through three pinned
+    staging buffers refilled from a store file's mapping."""
     from mrun_pub_amd.paged import PAGE_BYTES, TRANSFER_BYTES, PagedQStore, PinnedHostTier
 
     tier = PinnedHostTier.from_pages({p.name: p for L in pages for p in L.values()})
@@ -262,39 +263,54 @@ def paged_measurement(torch, dev, pages, x_h, x_i, passes: int = 6) -> dict:
     del dst
     store = PagedQStore(tier, device=dev, compute_dtype="bf16", slots=4, depth=3)
 
-    def one_pass():
-        for L in range(LAYERS):
-            for n in ("q", "k", "v"):
-                store.matmul(f"L{L}.{n}", x_h)
-            store.matmul(f"L{L}.o", x_h)
-            store.fused_swiglu(f"L{L}.gate", f"L{L}.up", x_h)
-            store.matmul(f"L{L}.down", x_i)
+    def timed(store, store_passes):
+        def one_pass():
+            for L in range(LAYERS):
+                for n in ("q", "k", "v"):
+                    store.matmul(f"L{L}.{n}", x_h)
+                store.matmul(f"L{L}.o", x_h)
+                store.fused_swiglu(f"L{L}.gate", f"L{L}.up", x_h)
+                store.matmul(f"L{L}.down", x_i)
 
-    one_pass()  # the successor oracle learns the order
-    torch.cuda.synchronize()
-    h0 = dict(store.ring.stats)
-    t0 = time.perf_counter()
-    for _ in range(passes):
-        one_pass()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / passes
-    st = store.ring.stats
-    moved = (st["h2d_bytes"] - h0["h2d_bytes"]) / passes
+        one_pass()  # the successor oracle learns the order
+        torch.cuda.synchronize()
+        h0 = dict(store.ring.stats)
+        t0 = time.perf_counter()
+        for _ in range(store_passes):
+            one_pass()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / store_passes
+        st = store.ring.stats
+        moved = (st["h2d_bytes"] - h0["h2d_bytes"]) / store_passes
+        return {
+            "ms_per_pass": round(dt * 1e3, 3),
+            "tokens_per_s": round(x_h.shape[0] / dt, 2),
+            "h2d_GB/s": round(moved / dt / 1e9, 2),
+            "pages_per_pass": (st["h2d_pages"] - h0["h2d_pages"]) // store_passes,
+            "hits": st["hits"] - h0["hits"],
+            "misses": st["misses"] - h0["misses"],
+            "bytes_per_pass": int(moved),
+        }
+
+    res = {"raw_pinned_h2d_GB/s": round(raw_gbs, 2), "page_bytes": PAGE_BYTES, "max_transfer_bytes": TRANSFER_BYTES,
+           "slots": 4, "depth": 3}
+    res.update(timed(store, passes))
+    res["pinned_bytes"] = tier.nbytes
     store.close()
-    return {
-        "ms_per_pass": round(dt * 1e3, 3),
-        "tokens_per_s": round(x_h.shape[0] / dt, 2),
-        "h2d_GB/s": round(moved / dt / 1e9, 2),
-        "raw_pinned_h2d_GB/s": round(raw_gbs, 2),
-        "page_bytes": PAGE_BYTES,
-        "pages_per_pass": (st["h2d_pages"] - h0["h2d_pages"]) // passes,
-        "max_transfer_bytes": TRANSFER_BYTES,
-        "slots": 4,
-        "depth": 3,
-        "hits": st["hits"] - h0["hits"],
-        "misses": st["misses"] - h0["misses"],
-        "bytes_per_pass": int(moved),
-    }
+    del store, tier
+    # bounded mode: three pinned staging buffers refilled from the store file's mapping
+    # (the file written here sits in the page cache, as a store read once does)
+    import tempfile
+
+    from mrun_pub_amd.store import write_qstore
+
+    with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
+        write_qstore(tmp, {p.name: (p.codes.cpu().numpy(), p.scales.cpu().numpy()) for L in pages for p in L.values()},
+                     legacy=True)
+        staged = PagedQStore(tmp, device=dev, compute_dtype="bf16", slots=4, depth=3, staging_buffers=3)
+        res["bounded_staging"] = {**timed(staged, passes), "staging_buffers": 3, "pinned_bytes": staged.tier.nbytes}
+        staged.close()
+    return res
 
 
 def paged_moe_measurement(torch, dev, E: int, topk: int, H: int, I: int, layers: int = 2,

@@ -404,6 +404,13 @@ int qs_pager_acquire_many(qs_pager* pager, const int* slots, int n, void* comput
 int qs_pager_release_many(qs_pager* pager, const int* slots, int n, void* compute_stream);
 /* Block the host until every queued copy has landed. */
 int qs_pager_sync(qs_pager* pager);
+/* Host-side view of one slot's last sealed copies, for a caller that reuses the host
+ * buffer a copy read from (the bounded pinned staging of _RingPrefetch._stage,
+ * qstore.py:622-659, waits on its slot event for the same reason): slot_landed returns 1
+ * when they have landed, 0 when not yet (negative on error); wait_landed blocks until
+ * they have. */
+int qs_pager_slot_landed(qs_pager* pager, int slot);
+int qs_pager_wait_landed(qs_pager* pager, int slot);
 
 #ifdef __cplusplus
 }

@@ -90,6 +90,8 @@ SIGNATURES: dict[str, tuple] = {
     "qs_pager_acquire_many": (_I, [_P, _P, _I, _P]),
     "qs_pager_release_many": (_I, [_P, _P, _I, _P]),
     "qs_pager_sync": (_I, [_P]),
+    "qs_pager_slot_landed": (_I, [_P, _I]),
+    "qs_pager_wait_landed": (_I, [_P, _I]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -206,6 +206,28 @@ extern "C" int qs_pager_release_many(qs_pager* p, const int* slots, int n, void*
   return QS_OK;
 }
 
+// Whether the copies last sealed into `slot` have landed (1) or not (0): a host-side
+// query of the slot's ready event, for callers that reuse the host source of a copy.
+extern "C" int qs_pager_slot_landed(qs_pager* p, int slot) {
+  if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_slot_landed: bad arguments");
+  if (p->ready_done[slot]) return 1;
+  hipError_t q = hipEventQuery(p->ready[slot]);
+  if (q == hipSuccess) {
+    p->ready_done[slot] = 1;
+    return 1;
+  }
+  return q == hipErrorNotReady ? 0 : hip_check(q, "hipEventQuery(ready)");
+}
+
+// Block the host until the copies last sealed into `slot` have landed.
+extern "C" int qs_pager_wait_landed(qs_pager* p, int slot) {
+  if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_wait_landed: bad arguments");
+  if (p->ready_done[slot]) return QS_OK;
+  int st = hip_check(hipEventSynchronize(p->ready[slot]), "hipEventSynchronize(ready)");
+  if (!st) p->ready_done[slot] = 1;
+  return st;
+}
+
 extern "C" int qs_pager_acquire(qs_pager* p, int slot, void* compute_stream) {
   if (!p || slot < 0 || slot >= p->slots) return fail(QS_ERR_INVALID, "pager_acquire: bad arguments");
   return qs_pager_acquire_many(p, &slot, 1, compute_stream);

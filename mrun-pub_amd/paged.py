@@ -7,11 +7,12 @@ Mirrors the CUDA paged path of ``QStore`` with its successor-oracle prefetch rin
 
 Differences of design, same observable contract:
 
-* The host tier is ONE pinned allocation holding every qrow block as ``[codes][pad]
-  [scales]`` (each block 4096-aligned), filled once from the memory-mapped store.  The
-  reference re-stages every block from the mmap into reusable pinned buffers on worker
-  threads; here the pageable->pinned copy is paid once, so the steady state is bounded by
-  the PCIe link alone.
+* Two host sides.  By default the host tier is ONE pinned allocation holding every qrow
+  block as ``[codes][pad][scales]`` (each block 4096-aligned), filled once from the
+  memory-mapped store: the pageable->pinned copy is paid once, so the steady state is
+  bounded by the PCIe link alone.  For a store larger than pinned memory,
+  ``staging_buffers=K`` keeps K pinned buffers only and re-stages every transfer from the
+  mapping on worker threads, as the reference does (``MappedStagingTier``).
 * The HBM side is a fixed ring of ``slots`` equal slots in one device allocation.  A
   block is a run of contiguous ``page_bytes`` (2 MiB) pages of the tier and travels as
   transfers of up to ``transfer_bytes`` (64 MiB, so one transfer per block) on the
@@ -136,8 +137,86 @@ class PinnedHostTier:
         return max((_align(b.span, 256) for b in self.blocks.values()), default=256)
 
 
+class MappedStagingTier:
+    """Bounded pinned staging between a memory-mapped store and the HBM ring.
+
+    The bounded mode of the paged path, for stores that do not fit in pinned memory (the
+    reference's ring stages every block this way, qstore.py:613-659): ``buffers`` pinned
+    buffers of the largest block's slot span, allocated once on the calling thread.
+    ``fill(j, name)`` copies one block's codes and scales from the store's mapping into
+    buffer ``j`` in the slot layout ``[codes][pad to 256][scales]`` on a worker thread,
+    the codes in ``chunk_bytes`` pieces over ``copy_threads`` threads (the copies release
+    the interpreter lock, so the pieces run in parallel); the ring then issues the H2D
+    from that buffer.  Only the caller's thread talks to the pager.
+    """
+
+    def __init__(self, reader: QStoreReader, *, buffers: int = 3, copy_threads: int = 3,
+                 chunk_bytes: int = 8 << 20):
+        from concurrent.futures import ThreadPoolExecutor
+
+        if buffers < 1 or copy_threads < 1 or chunk_bytes < 1:
+            raise ValueError("staging needs at least one buffer, one copy thread and a positive chunk")
+        self.reader = reader
+        self.blocks: dict[str, HostBlock] = {}
+        for name in reader.qrow_names():
+            out, inn = (int(v) for v in reader.blocks[name]["shape"])
+            self.blocks[name] = HostBlock(name, out, inn, 0, _slot_layout(out, inn))
+        self.buffer_bytes = _align(max((b.span for b in self.blocks.values()), default=256), 4096)
+        self.buffers = [torch.empty(self.buffer_bytes, dtype=torch.uint8, pin_memory=True) for _ in range(buffers)]
+        self.nbytes = self.buffer_bytes * len(self.buffers)
+        self.chunk_bytes = int(chunk_bytes)
+        self._worker = ThreadPoolExecutor(max_workers=1, thread_name_prefix="qstore-stage")
+        self._copiers = ThreadPoolExecutor(max_workers=int(copy_threads), thread_name_prefix="qstore-stage-cp")
+        self.stats = {"staged_blocks": 0, "staged_bytes": 0}
+
+    @property
+    def max_slot_bytes(self) -> int:
+        return max((_align(b.span, 256) for b in self.blocks.values()), default=256)
+
+    def codes(self, name: str) -> np.ndarray:
+        return self.reader.qrow(name)[0]
+
+    def scales(self, name: str) -> np.ndarray:
+        return self.reader.qrow(name)[1]
+
+    def buffer_ptr(self, j: int) -> int:
+        return self.buffers[j].data_ptr()
+
+    def _copy(self, j: int, name: str) -> None:
+        b = self.blocks[name]
+        codes, scales = self.reader.qrow(name)
+        dst = self.buffers[j].numpy()
+        n = b.out_features * b.in_features
+        src = np.asarray(codes).reshape(-1).view(np.uint8)
+        pieces = [(a, min(n, a + self.chunk_bytes)) for a in range(0, n, self.chunk_bytes)]
+        if len(pieces) > 2:
+            for f in [self._copiers.submit(np.copyto, dst[a:e], src[a:e]) for a, e in pieces]:
+                f.result()
+        else:
+            np.copyto(dst[:n], src)
+        sc = np.asarray(scales, dtype=np.float32).reshape(-1).view(np.uint8)
+        np.copyto(dst[b.scale_offset:b.scale_offset + sc.size], sc)
+        self.stats["staged_blocks"] += 1
+        self.stats["staged_bytes"] += b.span
+
+    def fill(self, j: int, name: str):
+        """Start copying block ``name`` into buffer ``j``; returns its future."""
+        return self._worker.submit(self._copy, j, name)
+
+    def close(self) -> None:
+        self._worker.shutdown(wait=True)
+        self._copiers.shutdown(wait=True)
+
+
 class RingPrefetch:
-    """Successor-oracle prefetch ring over HBM slots (qstore.py:486-660 ``_RingPrefetch``)."""
+    """Successor-oracle prefetch ring over HBM slots (qstore.py:486-660 ``_RingPrefetch``).
+
+    With a ``PinnedHostTier`` every transfer reads the tier in place.  With a
+    ``MappedStagingTier`` a block first goes through one of its pinned buffers: a prefetch
+    starts the buffer fill on the staging worker and its H2D is issued by the first ring
+    call after the fill has finished (or by ``take`` of that block, which waits for it);
+    a buffer is refilled only after the H2D that read it has landed.
+    """
 
     def __init__(self, tier: PinnedHostTier, device: torch.device, *, slots: int = 3, depth: int = 2,
                  page_bytes: int = PAGE_BYTES, transfer_bytes: int = TRANSFER_BYTES):
@@ -159,6 +238,12 @@ class RingPrefetch:
                      ctypes.byref(handle))
         self._pager = handle
         self.held = [0] * self.n_slots
+        self.staging = tier if isinstance(tier, MappedStagingTier) else None
+        n_buf = len(self.staging.buffers) if self.staging is not None else 0
+        # staging buffer j: None (free), ("fill", name) while its copy runs, or ("h2d", slot)
+        # until the transfer that reads it has landed
+        self._buf_state: list = [None] * n_buf
+        self._pending: OrderedDict[str, tuple[int, object, int]] = OrderedDict()  # name -> (buffer, fill, slot)
         self.inflight: OrderedDict[str, int] = OrderedDict()
         self.successor: dict[str, str] = {}
         self.last_access: str | None = None
@@ -171,10 +256,14 @@ class RingPrefetch:
             "successor_entries": 0,
             "h2d_bytes": 0,
             "h2d_pages": 0,
+            "staging_waits": 0,
         }
 
     # -- lifecycle -----------------------------------------------------------------
     def close(self) -> None:
+        for _, fill, _ in self._pending.values():
+            fill.result()
+        self._pending.clear()
         if self._pager is not None:
             torch.cuda.current_stream(self.device).synchronize()
             nat.call("qs_pager_destroy", self._pager)
@@ -197,17 +286,26 @@ class RingPrefetch:
 
     def take(self, name: str) -> CompactQRowPage | None:
         """Prefetched page for ``name`` (ordered after its copy on the current stream) or None."""
+        self._pump()
         slot = self.inflight.pop(name, None)
         if slot is None:
             self.stats["misses"] += 1
             return None
         self.stats["hits"] += 1
+        if name in self._pending:  # its fill is still running: wait for it, then copy
+            j, fill, _ = self._pending.pop(name)
+            fill.result()
+            self._send_staged(j, slot, name)
         return self._hold(slot, name)
 
     def load(self, name: str) -> CompactQRowPage:
         """Miss path: copy ``name`` into a slot now and hand it out."""
         slot = self._issue(name)
         self.inflight.pop(name, None)
+        if name in self._pending:
+            j, fill, _ = self._pending.pop(name)
+            fill.result()
+            self._send_staged(j, slot, name)
         return self._hold(slot, name)
 
     def _hold(self, slot: int, name: str) -> CompactQRowPage:
@@ -227,6 +325,7 @@ class RingPrefetch:
 
     def observe(self, name: str) -> None:
         """Record access order and prefetch the predicted successors (qstore.py:561-573)."""
+        self._pump()
         if self.last_access is not None and self.last_access != name:
             self.successor[self.last_access] = name
             self.stats["successor_entries"] = len(self.successor)
@@ -244,7 +343,13 @@ class RingPrefetch:
             slot = self._free_slot(protect=wanted)
             if slot is None:
                 return
-            self._submit(slot, nxt)
+            if self.staging is not None:
+                j = self._free_buffer(block=False)
+                if j is None:  # every buffer is being filled: no prefetch this time
+                    return
+                self._start_fill(j, slot, nxt)
+            else:
+                self._submit(slot, nxt)
             self.stats["prefetches"] += 1
             self.stats["prefetch_bytes"] += self.tier.blocks[nxt].compact_bytes
 
@@ -258,9 +363,64 @@ class RingPrefetch:
         for key, s in list(self.inflight.items()):
             if not self.held[s] and key not in protect:
                 self.inflight.pop(key)
+                if key in self._pending:  # its fill may still be running: let it end, unsent
+                    j, fill, _ = self._pending.pop(key)
+                    fill.result()
+                    self._buf_state[j] = None
                 self.stats["evicted_unused"] += 1
                 return s
         return None
+
+    # -- bounded staging (MappedStagingTier) -----------------------------------------------
+    def _start_fill(self, j: int, slot: int, name: str) -> None:
+        self._buf_state[j] = ("fill", name)
+        self._pending[name] = (j, self.staging.fill(j, name), slot)
+        self.inflight[name] = slot
+
+    def _send_staged(self, j: int, slot: int, name: str) -> None:
+        """H2D of a filled staging buffer into its slot; the buffer stays busy until it lands."""
+        b = self.tier.blocks[name]
+        nat.call("qs_pager_submit", self._pager, slot, self.staging.buffer_ptr(j), b.span, 0)
+        nat.call("qs_pager_seal", self._pager, slot)
+        self._buf_state[j] = ("h2d", slot)
+        self.stats["h2d_bytes"] += b.span
+        self.stats["h2d_pages"] += -(-b.span // self.page_bytes)
+
+    def _pump(self) -> None:
+        """Issue the H2D of every prefetch whose buffer fill has finished (in order)."""
+        for name, (j, fill, slot) in list(self._pending.items()):
+            if not fill.done():
+                break
+            fill.result()
+            del self._pending[name]
+            self._send_staged(j, slot, name)
+
+    def _free_buffer(self, *, block: bool) -> int | None:
+        """A staging buffer that may be refilled: a free one, else one whose transfer has
+        landed; with ``block``, wait for the oldest transfer (or fill) to end."""
+        for j, st in enumerate(self._buf_state):
+            if st is None:
+                return j
+        for j, st in enumerate(self._buf_state):
+            if st[0] == "h2d" and nat.load().qs_pager_slot_landed(self._pager, st[1]) == 1:
+                self._buf_state[j] = None
+                return j
+        if not block:
+            return None
+        self.stats["staging_waits"] += 1
+        for j, st in enumerate(self._buf_state):
+            if st[0] == "h2d":
+                nat.call("qs_pager_wait_landed", self._pager, st[1])
+                self._buf_state[j] = None
+                return j
+        # every buffer is filling for a prefetch: send the oldest, then wait for it to land
+        name, (j, fill, slot) = next(iter(self._pending.items()))
+        fill.result()
+        del self._pending[name]
+        self._send_staged(j, slot, name)
+        nat.call("qs_pager_wait_landed", self._pager, slot)
+        self._buf_state[j] = None
+        return j
 
     def _issue(self, name: str) -> int:
         slot = self.inflight.get(name)
@@ -273,6 +433,13 @@ class RingPrefetch:
         return slot
 
     def _submit(self, slot: int, name: str) -> None:
+        if self.staging is not None:  # a miss: stage it now and send it
+            j = self._free_buffer(block=True)
+            self._buf_state[j] = ("fill", name)
+            self.staging.fill(j, name).result()
+            self.inflight[name] = slot
+            self._send_staged(j, slot, name)
+            return
         b = self.tier.blocks[name]
         src = self.tier.host.data_ptr() + b.host_offset
         nat.call("qs_pager_submit", self._pager, slot, src, b.span, 0)
@@ -303,7 +470,12 @@ class PagedQStore:
         page_bytes: int = PAGE_BYTES,
         transfer_bytes: int = TRANSFER_BYTES,
         enable_prefetch_ring: bool = True,
+        staging_buffers: int | None = None,
     ) -> None:
+        """``staging_buffers=None``: every qrow block is copied once into one pinned host tier
+        (the store must fit in pinned memory).  ``staging_buffers=K``: bounded mode -- only K
+        pinned buffers of the largest block, refilled from the store's mapping for every
+        transfer (a store of any size)."""
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError("PagedQStore requires a HIP (cuda) device")
@@ -311,11 +483,17 @@ class PagedQStore:
             raise ValueError("compute_dtype must be fp32, bf16 or fp16")
         self.compute_dtype = _DTYPES[compute_dtype]
         self.reader: QStoreReader | None = None
-        if isinstance(store, PinnedHostTier):
+        if isinstance(store, (PinnedHostTier, MappedStagingTier)):
+            if staging_buffers is not None:
+                raise ValueError("staging_buffers applies to a store directory or reader, not a host tier")
             self.tier = store
+            self.reader = store.reader if isinstance(store, MappedStagingTier) else None
         else:
             self.reader = store if isinstance(store, QStoreReader) else QStoreReader(store)
-            self.tier = PinnedHostTier.from_reader(self.reader)
+            if staging_buffers is None:
+                self.tier = PinnedHostTier.from_reader(self.reader)
+            else:
+                self.tier = MappedStagingTier(self.reader, buffers=int(staging_buffers))
         self.ring = RingPrefetch(self.tier, self.device, slots=slots, depth=depth, page_bytes=page_bytes,
                                  transfer_bytes=transfer_bytes)
         self.prefetch = bool(enable_prefetch_ring)
@@ -466,3 +644,5 @@ class PagedQStore:
         if self.ring is not None:
             self.ring.close()
         self.ring = None
+        if isinstance(self.tier, MappedStagingTier):
+            self.tier.close()

@@ -174,3 +174,54 @@ def test_pager_release_many_refuses_a_slot_listed_twice(dev):
         assert not arena[:4096].any() and not arena[12288:].any()
     finally:
         nat.call("qs_pager_destroy", handle)
+
+
+@pytest.mark.parametrize("buffers,slots,depth", [(3, 3, 2), (2, 2, 1), (1, 4, 3), (4, 5, 3)])
+@pytest.mark.parametrize("m", [1, 4])
+def test_bounded_staging_pages_a_store_larger_than_its_pinned_budget(dev, store_dir, buffers, slots, depth, m):
+    """Bounded mode (``staging_buffers``): pinned memory holds ``buffers`` blocks of the
+    largest size only (a fraction of the store), every transfer is re-staged from the
+    store's mapping, and the results equal the resident store bit for bit -- with the ring
+    hitting, after mispredicts, and with the ring off (every block a miss)."""
+    from mrun_pub_amd.dense_store import DenseQStore
+    from mrun_pub_amd.paged import MappedStagingTier, PagedQStore
+
+    d, _ = store_dir
+    xs = _inputs(dev, m)
+    resident = DenseQStore(d, device=dev, compute_dtype="bf16")
+    store_bytes = resident.prepare_fully_resident()
+    plain = _pass(resident, xs)
+    # small chunks so the parallel piece copy runs on these blocks too
+    paged = PagedQStore(d, device=dev, compute_dtype="bf16", slots=slots, depth=depth, staging_buffers=buffers)
+    assert isinstance(paged.tier, MappedStagingTier) and len(paged.tier.buffers) == buffers
+    paged.tier.chunk_bytes = 16 << 10
+    assert paged.tier.nbytes < store_bytes  # the store does not fit in the pinned budget
+    runs = [_pass(paged, xs) for _ in range(3)]
+    # a mispredicted order (reversed pass), then the learned order again
+    runs.append(list(reversed(_pass_reversed(paged, xs))))
+    runs.append(_pass(paged, xs))
+    stats = paged.ring_stats()
+    paged.synchronize()
+    for run in runs:
+        for got, want in zip(run, plain):
+            assert torch.equal(got, want), "bounded staging must equal the resident path bit for bit"
+    assert stats["hits"] > 0 and paged.tier.stats["staged_blocks"] >= stats["hits"] + stats["misses"] - 2
+    paged.disable_ring()
+    for got, want in zip(_pass(paged, xs), plain):
+        assert torch.equal(got, want)
+    paged.close()
+    resident.close()
+
+
+def _pass_reversed(store, xs):
+    """The calls of ``_pass`` in reverse order (outputs listed in reverse)."""
+    out = [store.weight("lm_head"), store.matmul("odd", xs[80])]
+    for layer in ("l1", "l0"):
+        out.append(store.matmul(f"{layer}.down", xs[384]))
+        out.append(store.fused_swiglu(f"{layer}.gate", f"{layer}.up", xs[256])[0])
+        if layer == "l0":
+            out.append(store.matmul("l0.o", xs[192]))
+            out.append(store.matmul_row_stable("l0.v", xs[256]))
+            out.append(store.matmul("l0.k", xs[256]))
+        out.append(store.matmul(f"{layer}.q", xs[256]))
+    return out
