@@ -330,8 +330,9 @@ int qs_moe_route_reduce_to(const void* expert_out, int y_dtype, const float* coe
 
 /* ---- packed int3 / int2 ("qrow3" / "qrow2") --------------------------------------------
  * packed: uint8 [N, row_bytes], each row an LSB-first bitstream of K codes of `bits` bits
- * (code k at bits [bits*k, bits*k + bits)); scales [N, K/G] (F32 or F16); zeros [N, K/G]
- * (F16/F32) or nullptr with a fixed `offset`:  w[n,k] = (float(code) - zero) * scale.
+ * (code k at bits [bits*k, bits*k + bits)); scales [N, ceil(K/G)] (F32 or F16); zeros
+ * likewise (F16/F32) or nullptr with a fixed `offset`:  w[n,k] = (float(code) - zero) *
+ * scale[n, k/G].
  * The reference layout is zeros = nullptr, offset 4 (int3) / 1 (int2), F32 scales, G = 128
  * (src/mrun/engine/kernels/qstore_int3.py:30-56, qstore_int2.py:24-63); the asymmetric
  * G = 64 variant passes F16 scales and F16 zero points. */
@@ -346,9 +347,10 @@ int qs_lowbit_dequant(const uint8_t* packed, int64_t row_bytes, const void* scal
 size_t qs_lowbit_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int group_size);
 
 /* Replaces QStoreInt3.matmul / QStoreInt2.matmul (qstore.py:1318-1341, 1451-1474):
- * y[m,n] = sum_k x[m,k] * w[n,k] in fp32, y F32 [M, N].  x BF16 or F32; bits 2 or 3;
- * group_size 64 or 128; K % group_size == 0; rows 4-byte aligned.  workspace: device
- * memory of at least qs_lowbit_workspace_bytes(...) bytes, contents clobbered. */
+ * y[m,n] = sum_k x[m,k] * w[n,k] in fp32, y F32 [M, N].  x BF16 or F32; bits 2 or 3; any
+ * group size and K (the tiled kernels take G 64 / 128 with whole groups and 4-byte aligned
+ * rows, every other layout a scalar-decode kernel).  workspace: device memory of at least
+ * qs_lowbit_workspace_bytes(...) bytes, contents clobbered. */
 int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uint8_t* packed,
                    int64_t row_bytes, const void* scales, int scale_dtype, const void* zeros,
                    int zero_dtype, float offset, int bits, int group_size, float* y, int64_t ldy,

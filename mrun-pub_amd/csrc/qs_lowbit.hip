@@ -20,7 +20,11 @@
 //                  quarter group per lane, K split over the waves of a workgroup
 //   k_lowbit_slot  M <= 16 fp32 rows (split into bf16 terms): one whole group per lane
 //   k_lowbit_mfma  any aligned-to-4 layout (fallback), four lanes per group
+//   k_lowbit_any   every other layout (any group size, a short last group, unaligned
+//                  rows): one wave per weight row, scalar decode
 #include "qs_common.h"
+
+#include <limits.h>
 
 namespace qs {
 
@@ -990,6 +994,55 @@ __global__ __launch_bounds__(256) void k_lowbit_dequant(LowbitParams p, int bits
   out[i] = mul_rn(static_cast<float>(code) - z, sc);
 }
 
+// Any layout the tiled kernels refuse (a group size other than 64 / 128, K not a multiple
+// of the group size -- a short last group --, rows not 4-byte aligned): one wave per weight
+// row, at most kAnyRows activation rows per launch.  Each lane decodes its codes like
+// k_lowbit_dequant, multiplies them into its fp32 partial sums in k order, and a wave sum
+// finishes each row.  A correctness path: the reference runs these stores on the CPU.
+constexpr int kAnyRows = 8;
+
+template <int XT>
+__global__ __launch_bounds__(256) void k_lowbit_any(LowbitParams p, int bits, int G, const void* __restrict__ x,
+                                                    int64_t ldx) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= p.N) return;
+  float acc[kAnyRows];
+#pragma unroll
+  for (int m = 0; m < kAnyRows; ++m) acc[m] = 0.f;
+  const uint8_t* row = p.packed + n * p.row_bytes;
+  for (int64_t k = lane; k < p.K; k += 64) {
+    const int64_t bit = k * bits;
+    uint32_t v = row[bit >> 3] >> (bit & 7);
+    if ((bit & 7) + bits > 8) v |= (uint32_t)row[(bit >> 3) + 1] << (8 - (bit & 7));
+    const uint32_t code = v & ((1u << bits) - 1);
+    const int64_t si = n * p.ng + k / G;
+    const float sc = p.scale_f16 ? f16_bits_to_f32(static_cast<const uint16_t*>(p.scales)[si])
+                                 : static_cast<const float*>(p.scales)[si];
+    float z = p.offset;
+    if (p.zeros)
+      z = p.zero_f16 ? f16_bits_to_f32(static_cast<const uint16_t*>(p.zeros)[si])
+                     : static_cast<const float*>(p.zeros)[si];
+    const float w = mul_rn(static_cast<float>(code) - z, sc);
+#pragma unroll
+    for (int m = 0; m < kAnyRows; ++m) {
+      if (m < p.M) {
+        float xv;
+        if constexpr (XT == QS_F32) xv = static_cast<const float*>(x)[m * ldx + k];
+        else xv = bf16_bits_to_f32(static_cast<const uint16_t*>(x)[m * ldx + k]);
+        acc[m] = fmaf(xv, w, acc[m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kAnyRows; ++m) {
+    if (m < p.M) {
+      const float t = wave_sum(acc[m]);
+      if (lane == 0) p.y[m * p.ldy + n] = t;
+    }
+  }
+}
+
 namespace {
 constexpr size_t kSlotLds = 64 * 1024;  // activations + group sums of one workgroup's K range
 
@@ -1049,11 +1102,14 @@ int check_lowbit(const void* packed, int64_t row_bytes, const void* scales, int 
                  int64_t N, int64_t K) {
   if (!packed || !scales) return fail(QS_ERR_INVALID, "lowbit: null pointer");
   if (bits != 2 && bits != 3) return fail(QS_ERR_UNSUPPORTED, "lowbit: bits must be 2 or 3");
-  if (G != 64 && G != 128) return fail(QS_ERR_UNSUPPORTED, "lowbit: group size must be 64 or 128");
-  if (N <= 0 || K <= 0 || K % G != 0) return fail(QS_ERR_UNSUPPORTED, "lowbit: K must be a positive multiple of the group size");
+  if (G <= 0 || N <= 0 || K <= 0 || N > INT_MAX || K > INT_MAX) return fail(QS_ERR_INVALID, "lowbit: bad shape");
   if (row_bytes < (K * bits + 7) / 8) return fail(QS_ERR_INVALID, "lowbit: row_bytes too small");
-  if (row_bytes % 4 != 0 || !aligned(packed, 4)) return fail(QS_ERR_UNSUPPORTED, "lowbit: rows must be 4-byte aligned");
   return QS_OK;
+}
+
+// the tiled kernels' layout: G 64 or 128, whole groups, 4-byte aligned rows
+bool tiled_layout(const void* packed, int64_t row_bytes, int G, int64_t K) {
+  return (G == 64 || G == 128) && K % G == 0 && row_bytes % 4 == 0 && aligned(packed, 4);
 }
 }  // namespace
 }  // namespace qs
@@ -1075,6 +1131,32 @@ extern "C" int qs_lowbit_gemv(const void* x, int x_dtype, int64_t ldx, const uin
   if (zeros && zero_dtype != QS_F32 && zero_dtype != QS_F16) return fail(QS_ERR_INVALID, "lowbit_gemv: zeros F32 or F16");
   if (M < 0 || ldx < K || ldy < N) return fail(QS_ERR_INVALID, "lowbit_gemv: bad leading dimension");
   if (M == 0) return QS_OK;
+  if (!tiled_layout(packed, row_bytes, group_size, K)) {
+    LowbitParams p{};
+    p.packed = packed;
+    p.row_bytes = row_bytes;
+    p.scales = scales;
+    p.zeros = zeros;
+    p.scale_f16 = scale_dtype == QS_F16;
+    p.zero_f16 = zero_dtype == QS_F16;
+    p.offset = offset;
+    p.ldy = ldy;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.ng = (int)cdiv(K, group_size);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t xe = x_dtype == QS_F32 ? 4 : 2;
+    for (int64_t m0 = 0; m0 < M; m0 += kAnyRows) {
+      p.M = (int)(M - m0 < kAnyRows ? M - m0 : kAnyRows);
+      p.y = y + m0 * ldy;
+      const void* xm = static_cast<const char*>(x) + m0 * ldx * xe;
+      if (x_dtype == QS_F32)
+        hipLaunchKernelGGL(k_lowbit_any<QS_F32>, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, s, p, bits, group_size, xm, ldx);
+      else
+        hipLaunchKernelGGL(k_lowbit_any<QS_BF16>, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, s, p, bits, group_size, xm, ldx);
+    }
+    return hip_check(hipGetLastError(), "k_lowbit_any launch");
+  }
   const int rows_per_x = x_dtype == QS_F32 ? 3 : 1;
   const int mb = x_dtype == QS_F32 ? 5 : 16;  // activation rows per MFMA tile
   const int ng = (int)(K / group_size);

@@ -16,6 +16,10 @@ Sections (pass their names after the reference root to write only those; default
   through seeded random sequences of decode / prefill slot-binding acquires, transient
   prefills and resets, with its whole host state recorded after every call, plus its page
   trace manifest
+* ``lowbit_store`` -- lowbit_store/ (an int3 and an int2 store in the reference's layout,
+  tests/test_qstore_int3.py:24-56, with an fp32 extras block, an alias and 24-row matmul
+  chunks) and lowbit_store.npz: what the reference's QStoreInt3 / QStoreInt2 return for
+  them (matmul, matmul_row_stable, embed_rows, fp32)
 * ``refstore`` -- refstore/legacy (a store in the reference's own test layout,
   tests/test_qstore_cache.py:19-46) and refstore/v3 (a v3 store sealed by the reference's
   provenance functions), with refstore.npz / refstore.json holding what the reference's
@@ -170,6 +174,8 @@ def main(ref_root: str, sections: list[str]) -> None:
         moe_forward_section(files)
     manifest_path = HERE / "golden_manifest.json"
     manifest = json.loads(manifest_path.read_text()) if manifest_path.exists() else {}
+    if "lowbit_store" in sections:
+        lowbit_store_section(files)
     if "page_cache" in sections:
         path = page_cache_section()
         manifest[path.name] = hashlib.sha256(path.read_bytes()).hexdigest()
@@ -179,6 +185,50 @@ def main(ref_root: str, sections: list[str]) -> None:
         manifest[name] = hashlib.sha256(path.read_bytes()).hexdigest()
     manifest_path.write_text(json.dumps(manifest, indent=1, sort_keys=True) + "\n")
     print(json.dumps(manifest, indent=1))
+
+
+def lowbit_store_section(files: dict) -> None:
+    import torch
+
+    from mrun.engine.kernels.qstore import QStoreInt2, QStoreInt3
+    from mrun.engine.kernels.qstore_int2 import _quant_row_int2
+    from mrun.engine.kernels.qstore_int3 import _quant_row_int3
+
+    rng = np.random.default_rng(41)
+    root = HERE / "lowbit_store"
+    arrays: dict = {}
+    x = rng.standard_normal((3, 320)).astype(np.float32)
+    ids = np.array([[0, 69, 5], [33, 33, 1]], dtype=np.int64)
+    arrays.update(x=x, ids=ids)
+    for bits, quant, cls in ((3, _quant_row_int3, QStoreInt3), (2, _quant_row_int2, QStoreInt2)):
+        W = rng.standard_normal((70, 320)).astype(np.float32)
+        W2 = rng.standard_normal((50, 320)).astype(np.float32)
+        p1, s1 = quant(W)
+        p2, s2 = quant(W2)
+        norm = rng.standard_normal(320).astype(np.float32)
+        d = root / f"toy-int{bits}"
+        d.mkdir(parents=True, exist_ok=True)
+        (d / f"weights.i{bits}").write_bytes(p1.tobytes() + p2.tobytes())
+        (d / "scales.f32").write_bytes(s1.tobytes() + s2.tobytes())
+        (d / "extras.f32").write_bytes(norm.tobytes())
+        blk = lambda p, sc, w_off, s_off, n: {"kind": f"qrow{bits}", "shape": [n, 320], "w_off": w_off,  # noqa: E731
+                                             "row_bytes": p.shape[1], "s_off": s_off, "n_groups": sc.shape[1],
+                                             "group_size": 128}
+        (d / "manifest.json").write_text(json.dumps({
+            "model_name": "toy", "arch": "qwen2", "dtype": f"int{bits}", "group_size": 128, "config": {},
+            "matmul_chunk_rows": 24,
+            "blocks": {"A": blk(p1, s1, 0, 0, 70), "B": blk(p2, s2, p1.nbytes, s1.nbytes, 50),
+                       "norm": {"kind": "fp32", "shape": [320], "e_off": 0}, "A2": {"alias": "A"}}}))
+        store = cls("toy", root=root)
+        t = f"i{bits}"
+        xt = torch.from_numpy(x)
+        for name in ("A", "B"):
+            arrays[f"{t}_{name}_matmul"] = store.matmul(name, xt).numpy()
+            arrays[f"{t}_{name}_row_stable"] = store.matmul_row_stable(name, xt).numpy()
+        arrays[f"{t}_A2_embed"] = store.embed_rows("A2", ids).numpy()
+        arrays[f"{t}_norm"] = store.fp32("norm").numpy()
+        store.close()
+    files["lowbit_store.npz"] = arrays
 
 
 def _tiny_fp8_store(root: Path, layers: int, experts: int) -> Path:
@@ -432,7 +482,7 @@ def moe_forward_section(files: dict) -> None:
     files["moe_forward.npz"] = arrays
 
 
-SECTIONS = ("core", "refstore", "queue", "moe_forward", "page_cache")
+SECTIONS = ("core", "refstore", "queue", "moe_forward", "page_cache", "lowbit_store")
 
 if __name__ == "__main__":
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"

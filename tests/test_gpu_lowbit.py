@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import json
+
 import numpy as np
 import pytest
 import torch
@@ -173,3 +175,74 @@ def test_gemv_multirow_reference_layout_g128(dev, bits, m):
         y = _lb().lowbit_matmul(_page(dev, packed, scales, K, bits, 128), torch.from_numpy(x).to(dev).to(torch.bfloat16))
         ref = ol.lowbit_matmul(packed, scales, x, K, bits, 128)
         assert oq.rel_l2(y.cpu().numpy(), ref) <= F32_TOL
+
+
+@pytest.mark.parametrize("bits", [3, 2])
+@pytest.mark.parametrize("cache_mb", [None, 0.0, 0.01])
+def test_reference_store_matches_the_reference_reader(dev, bits, cache_mb):
+    """The reference's own QStoreInt3 / QStoreInt2 on a reference-layout store
+    (tests/golden/lowbit_store.npz, 24-row matmul chunks, an fp32 extras block, an alias)
+    against the device reader with every block resident (``cache_mb=None``), every block
+    streamed in 24-row chunks (0), and the first block resident and the second streamed
+    (0.01 MB holds A only).  Products within 1e-5, rows, fp32 blocks and the dequantized
+    weight bit for bit; a streamed block equals the resident one within the same bound."""
+    from pathlib import Path
+
+    gold = Path(__file__).resolve().parent / "golden"
+    g = np.load(gold / "lowbit_store.npz", allow_pickle=False)
+    d = gold / "lowbit_store" / f"toy-int{bits}"
+    store = _lb().DeviceLowbitQStore(d, device=dev, cache_mb=cache_mb)
+    resident = _lb().DeviceLowbitQStore(d, device=dev)
+    t = f"i{bits}"
+    x = torch.from_numpy(g["x"]).to(dev)
+    for name in ("A", "B"):
+        y = store.matmul(name, x)
+        assert oq.rel_l2(y.cpu().numpy(), g[f"{t}_{name}_matmul"]) <= F32_TOL
+        yr = store.matmul_row_stable(name, x)
+        assert oq.rel_l2(yr.cpu().numpy(), g[f"{t}_{name}_row_stable"]) <= F32_TOL
+        for r in range(3):  # row-stable rows equal single-row products
+            assert torch.equal(yr[r], store.matmul_row_stable(name, x[r:r + 1])[0])
+        assert oq.rel_l2(y.cpu().numpy(), resident.matmul(name, x).cpu().numpy()) <= F32_TOL
+        man = json.loads((d / "manifest.json").read_text())["blocks"][name]
+        packed = np.fromfile(d / f"weights.i{bits}", dtype=np.uint8)[man["w_off"]:]
+        out = man["shape"][0]
+        packed = packed[: out * man["row_bytes"]].reshape(out, man["row_bytes"])
+        sc = np.fromfile(d / "scales.f32", dtype=np.float32)[man["s_off"] // 4:][: out * man["n_groups"]]
+        full = ol.dequant(packed, sc.reshape(out, man["n_groups"]), 320, bits, 128)
+        assert np.array_equal(store.weight(name).cpu().numpy(), full)
+        blocks = list(store.row_blocks(name, bs=16))
+        assert [(a, b) for a, b, _ in blocks] == [(a, min(a + 16, out)) for a in range(0, out, 16)]
+        assert np.array_equal(torch.cat([w for _, _, w in blocks]).cpu().numpy(), full)
+    e = store.embed_rows("A2", g["ids"])
+    assert np.array_equal(e.cpu().numpy(), g[f"{t}_A2_embed"])
+    assert np.array_equal(store.fp32("norm").cpu().numpy(), g[f"{t}_norm"])
+    streamed = {None: 0, 0.0: 2, 0.01: 1}[cache_mb]
+    assert store.stats["resident_blocks"] == 2 - streamed
+    if streamed:
+        assert store.stats["streamed_chunks"] > store.stats["streamed_calls"] > 0
+    store.close()
+    resident.close()
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("K,G", [(17, 4), (320, 128), (100, 32), (200, 64), (1000, 128), (77, 77)])
+@pytest.mark.parametrize("m", [1, 3, 11])
+def test_gemv_any_layout(dev, bits, K, G, m):
+    """Layouts the tiled kernels refuse -- group sizes other than 64 / 128, a short last
+    group (scales [N, ceil(K/G)]), rows that are not 4-byte multiples -- in the reference's
+    symmetric layout (fixed offset, fp32 scales) and the asymmetric one (fp16 scale + zero),
+    more than eight activation rows included, against the oracle."""
+    rng = np.random.default_rng(bits * 1000 + K + G + m)
+    N, ng = 45, -(-K // G)
+    codes = rng.integers(0, 1 << bits, size=(N, K), dtype=np.uint8)
+    packed = ol.pack_codes(codes, bits)
+    scales = rng.uniform(0.001, 0.02, size=(N, ng)).astype(np.float32)
+    s16 = (rng.uniform(0.5, 1.5, size=(N, ng)) / 7).astype(np.float16)
+    z16 = rng.uniform(0, (1 << bits) - 1, size=(N, ng)).astype(np.float16)
+    x = oq.round_bf16(rng.standard_normal((m, K)).astype(np.float32))
+    for xdt in (torch.bfloat16, torch.float32):
+        xd = torch.from_numpy(x).to(dev).to(xdt)
+        y = _lb().lowbit_matmul(_page(dev, packed, scales, K, bits, G), xd)
+        assert oq.rel_l2(y.cpu().numpy(), ol.lowbit_matmul(packed, scales, x, K, bits, G)) <= F32_TOL
+        y = _lb().lowbit_matmul(_page(dev, packed, s16, K, bits, G, z16), xd)
+        assert oq.rel_l2(y.cpu().numpy(), ol.lowbit_matmul(packed, s16, x, K, bits, G, zeros=z16)) <= F32_TOL
