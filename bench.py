@@ -728,10 +728,25 @@ def main() -> int:
 
     value = algorithmic_bytes_per_pass(m) / per_pass / 1e9
     sw_gbs = swiglu_launch_bytes(m) / sw_s / 1e9
-    traffic = None
+    traffic = trace = None
     traffic_file = ROOT / "profiles" / "traffic.json"
     if traffic_file.exists():
-        traffic = json.loads(traffic_file.read_text()).get(f"qrow_swiglu_m{m}")
+        committed = json.loads(traffic_file.read_text())
+        traffic = committed.get(f"qrow_swiglu_m{m}")
+        tr = committed.get(f"qrow_swiglu_m{m}_trace")
+        if tr:
+            # the committed kernel trace of this same graph: its per-launch median and what
+            # HIP events read inside the traced process, beside this run's event figure
+            t_gbs = swiglu_launch_bytes(m) / (tr["median_us"] * 1e-6) / 1e9
+            trace = {
+                "median_us": tr["median_us"],
+                "achieved": round(t_gbs, 1),
+                "frac": round(t_gbs / HBM_PEAK_GBS, 4),
+                "rel_diff_vs_event_frac": round(abs(t_gbs - sw_gbs) / sw_gbs, 4),
+                "event_us_under_tracer": tr["event_us_under_tracer"],
+                "tracer_share_us": round(tr["event_us_under_tracer"] - tr["event_us_plain"], 3),
+                "source": "profiles/decode_gemv_m1.md (rocprofv3 --kernel-trace of bench.py --profile swiglu)",
+            }
     out = {
         "metric": "HBM GB/s (% peak) int8 QStore decode GEMV; TOPS (% MFMA peak) W8A8/MoE",
         "value": round(value, 1),
@@ -774,6 +789,7 @@ def main() -> int:
             "launch_us": round(sw_s * 1e6, 3),
             "bytes_per_launch": swiglu_launch_bytes(m),
             "timing": f"median of {len(sw_times)} replays of a graph of the 28 launches, / 28",
+            "trace": trace,
         },
     }
     if not args.no_secondary:
