@@ -1,7 +1,8 @@
 // Batched-decode W8A16 qrow linears on gfx950 (1 <= M <= 32 bf16/f16 activation rows).
 //
 // Kernels
-//   k_bd2<P, MT, WR, WK, F16> : one workgroup = (16 * WR weight rows of P planes, K slice);
+//   k_bd2<P, MT, WR, WK, F16, MS2> : one workgroup = (16 * WR weight rows of P planes, K slice;
+//                               MS2: one 16-row half of 17..32 activation rows);
 //                               P = 2 pairs the gate and up rows of a SwiGLU tile.  The
 //                               slice's activations reach LDS by DMA and serve all of the
 //                               workgroup's rows; the weights stream from HBM into VGPRs,
@@ -104,7 +105,8 @@ int bdec_prepare(BdecParams& p, const void* x, int x_dtype, int64_t ldx, int64_t
 // of one activation row.  The WK parts are summed in fixed order through LDS; with S > 1
 // slices the fp32 partial sums go to the workspace and k_bd2_reduce sums them in slice
 // order and stores the epilogue.  WK, S and the slice length -- the K order of every sum --
-// depend on (N, K) only (WR and RS, the rows per workgroup, may follow M: they change no sum), and
+// depend on (N, K) only (WR and RS, the rows per workgroup, and the activation-row split
+// may follow M: they change no sum), and
 // an MFMA sums each output over its k in a fixed order whatever the other rows hold, so a
 // row's result does not depend on the rest of the batch.
 // ---------------------------------------------------------------------------------
@@ -138,7 +140,7 @@ __device__ __forceinline__ void bd2_copy16(__amdgpu_buffer_rsrc_t r, uint8_t* ds
 template <int P, int MT, int WR, int WK, bool F16>
 __device__ __forceinline__ void bd2_finish(const Bd2Params& p, const BdecLin& L0, const f32x4 (&acc)[P][MT],
                                            uint8_t* bsm, int wr, int wk, int lane, int col, int grp, int n0,
-                                           int N, int s, bool sync_first) {
+                                           int N, int s, int m0, bool sync_first) {
   // 6. the WK parts summed in order wk = 0, 1, ... through LDS
   f32x4 out[P][MT];
   if constexpr (WK > 1) {
@@ -166,7 +168,7 @@ __device__ __forceinline__ void bd2_finish(const Bd2Params& p, const BdecLin& L0
       for (int t = 0; t < MT; ++t) out[pl][t] = acc[pl][t];
   }
 
-  // 7. lane holds D[n = nb + q][m = 16 t + col]
+  // 7. lane holds D[n = nb + q][m = m0 + 16 t + col]
   const int nb = n0 + 4 * grp;
   if (nb >= N) return;
   const bool full = p.vec && nb + 3 < N;
@@ -174,7 +176,7 @@ __device__ __forceinline__ void bd2_finish(const Bd2Params& p, const BdecLin& L0
     uint16_t* y = static_cast<uint16_t*>(L0.y);
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      const int m = 16 * t + col;
+      const int m = m0 + 16 * t + col;
       if (m >= p.M) continue;
       uint16_t o[4];
 #pragma unroll
@@ -199,7 +201,7 @@ __device__ __forceinline__ void bd2_finish(const Bd2Params& p, const BdecLin& L0
   for (int pl = 0; pl < P; ++pl)
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      const int m = 16 * t + col;
+      const int m = m0 + 16 * t + col;
       if (m >= p.M) continue;
       float* pr = p.part + (((int64_t)s * P + pl) * p.M + m) * p.n_total + L0.n_begin + nb;
       if (full) {
@@ -212,7 +214,7 @@ __device__ __forceinline__ void bd2_finish(const Bd2Params& p, const BdecLin& L0
     }
 }
 
-template <int P, int MT, int WR, int WK, bool F16>
+template <int P, int MT, int WR, int WK, bool F16, bool MS2>
 __global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
   typedef Half<F16> H;
   typedef typename H::vec hvec;
@@ -222,8 +224,17 @@ __global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave % WR, wk = wave / WR;
   const int col = lane & 15, grp = lane >> 4;
-  const int tile = (int)blockIdx.x / p.S;
-  const int s = (int)blockIdx.x - tile * p.S;
+  // unit u = (row tile, slice).  MS2: activation rows 0-15 and 16-31 of a unit in two
+  // workgroups, blocks 16q + j and 16q + 8 + j (j < 8; the host launches MS2 only when the
+  // unit count is a multiple of 8), so both halves run on one XCD (blocks are dealt to the
+  // 8 XCDs round robin) and the second reads the unit's weights from that XCD's L2
+  int u = (int)blockIdx.x, m0 = 0;
+  if constexpr (MS2) {
+    u = (((int)blockIdx.x >> 4) << 3) + ((int)blockIdx.x & 7);
+    m0 = ((int)blockIdx.x & 8) << 1;
+  }
+  const int tile = u / p.S;
+  const int s = u - tile * p.S;
   int li = 0;
   if (P == 1) {
 #pragma unroll
@@ -252,10 +263,10 @@ __global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x), (short)0, xlim, 0x00020000);
   const int total = 16 * MT * NCH;
   for (int u0 = wave * 64; u0 < total; u0 += NW * 64) {
-    const int u = u0 + lane;
-    const int m = u / NCH, jj = u - m * NCH, j = jj ^ (m & 15);
-    const bool ok = m < p.M && j < 8 * cs;
-    bd2_copy16(xr, bsm + 16 * u0, ok ? (m * (int)p.ldx + kbeg + 8 * j) * 2 : xlim);
+    const int e = u0 + lane;
+    const int m = e / NCH, jj = e - m * NCH, j = jj ^ (m & 15);
+    const bool ok = m0 + m < p.M && j < 8 * cs;
+    bd2_copy16(xr, bsm + 16 * u0, ok ? ((m0 + m) * (int)p.ldx + kbeg + 8 * j) * 2 : xlim);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -316,7 +327,7 @@ __global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
     }
   }
 
-  bd2_finish<P, MT, WR, WK, F16>(p, L0, acc, bsm, wr, wk, lane, col, grp, n0, N, s, true);
+  bd2_finish<P, MT, WR, WK, F16>(p, L0, acc, bsm, wr, wk, lane, col, grp, n0, N, s, m0, true);
 }
 
 // Slice sums of k_bd2 in slice order and the epilogue: one thread per (row m, 4 columns
@@ -368,14 +379,19 @@ __global__ __launch_bounds__(128) void k_bd2_reduce(Bd2Params p) {
 
 struct Bd2Shape {
   int WR, WK, S, CS;
-  int RS;  // rows per workgroup: a multiple of 4, at most 16 * WR
+  int RS;      // rows per workgroup: a multiple of 4, at most 16 * WR
+  int MS = 1;  // activation-row splits (2: one 16-row half of M = 17..32 per workgroup)
 };
 
 // Split.  The K order of every sum -- WK waves per slice and S slices -- depends on (N, K)
 // only; WR (rows per workgroup, which does not change any sum) may follow M.  From
 // same-box timings of the config-2 shapes at M = 16 / 32:
 //  * rows up to 2048 k: one slice, 16-row workgroups of 8 waves along K (q/k/v 4.9 / 6.0 us,
-//    o 4.8 / 6.0 us; a K split with its reduce launch costs 2-3 us more);
+//    o 4.8 / 6.0 us; a K split with its reduce launch costs 2-3 us more).  For M > 16 the
+//    activation rows split in two (MS = 2): two workgroups per 16-row unit, 16 activation
+//    rows each, so q/k/v takes 256 workgroups with half the staged slice each; the chained
+//    M = 32 pass went 1.022 -> 0.980 ms (the same split for the SwiGLU and the long rows
+//    made it slower: their dequant is repeated per half);
 //  * the paired SwiGLU (1536 k): one slice, 4 waves along K, about one workgroup per CU
 //    (a CU streams its weights at a limited rate, so the CU with the most rows sets the
 //    time): rows per workgroup ceil(N / 256) rounded up to 4, as 16-row MFMA tiles with
@@ -392,7 +408,7 @@ Bd2Shape bd2_shape(const int64_t* N, int n_lin, int P, int64_t K, int64_t M) {
       const int rs = (int)std::min<int64_t>(48, std::max<int64_t>(16, (cdiv(N[0], 256) + 3) / 4 * 4));
       return Bd2Shape{(rs + 15) / 16, 4, 1, C, rs};
     }
-    return Bd2Shape{1, 8, 1, C, 16};
+    return Bd2Shape{1, 8, 1, C, 16, 2};
   }
   Bd2Shape sh{4, 1, 1, C, 64};
   int64_t tiles = 0;
@@ -419,7 +435,7 @@ void bd2_launch_mt(const Bd2Params& p, const Bd2Shape& sh, int64_t tiles, hipStr
   const size_t lds = std::max(xbytes, rbytes);
 #define QS_BD2(WR_, WK_)                                                                              \
   if (sh.WR == WR_ && sh.WK == WK_) {                                                                 \
-    hipLaunchKernelGGL((k_bd2<P, MT, WR_, WK_, F16>), grid, dim3(WR_ * WK_ * 64), lds, s, p);         \
+    hipLaunchKernelGGL((k_bd2<P, MT, WR_, WK_, F16, false>), grid, dim3(WR_ * WK_ * 64), lds, s, p);  \
     return;                                                                                           \
   }
   QS_BD2(4, 1) QS_BD2(4, 2) QS_BD2(4, 4) QS_BD2(3, 4) QS_BD2(2, 4) QS_BD2(1, 4) QS_BD2(1, 8)
@@ -447,7 +463,18 @@ int bd2_launch(Bd2Params& p, const Bd2Shape& sh, void* workspace, size_t workspa
     if (!aligned(workspace, 16)) return fail(QS_ERR_INVALID, "qrow batched: workspace must be 16-byte aligned");
   }
   p.part = static_cast<float*>(workspace);
-  if (p.M > 16) {
+  bool split = false;
+  if constexpr (P == 1) {
+    split = p.M > 16 && sh.MS == 2 && (tiles * sh.S) % 8 == 0 && sh.WR == 1 && sh.WK == 8;
+    if (split) {  // one 16-row half of the activations per workgroup, two workgroups per unit
+      const dim3 grid((unsigned)(2 * tiles * sh.S));
+      const size_t lds = std::max((size_t)16 * sh.CS * 8 * 16, (size_t)8 * 64 * 16);
+      if (f16) hipLaunchKernelGGL((k_bd2<1, 1, 1, 8, true, true>), grid, dim3(512), lds, s, p);
+      else hipLaunchKernelGGL((k_bd2<1, 1, 1, 8, false, true>), grid, dim3(512), lds, s, p);
+    }
+  }
+  if (split) {
+  } else if (p.M > 16) {
     if (f16) bd2_launch_mt<P, 2, true>(p, sh, tiles, s);
     else bd2_launch_mt<P, 2, false>(p, sh, tiles, s);
   } else {
