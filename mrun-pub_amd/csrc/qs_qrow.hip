@@ -793,6 +793,18 @@ __device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, floa
   constexpr int P = SWI ? 2 : 1;
   constexpr int W = U < kGemvXgWindow ? U : kGemvXgWindow;  // chunks in flight
   const int lane = threadIdx.x & 63;
+  // Every argument the loads below need, requested in one batch: left to itself the
+  // compiler asks for them in three dependent rounds (the row bound, the activation row,
+  // then past the issue-order barriers the weight rows), one scalar-cache miss each,
+  // before the first weight byte is requested.
+  if constexpr (SWI) {
+    asm volatile("" ::"s"(p.x), "s"(p.ldx), "s"(p.M), "s"(p.K), "s"(rows), "s"(p.lin[0].codes),
+                 "s"(p.lin[0].scales), "s"(p.lin[1].codes), "s"(p.lin[1].scales), "s"(p.lin[0].tile_begin));
+  } else {
+    asm volatile("" ::"s"(p.x), "s"(p.ldx), "s"(p.M), "s"(p.K), "s"(rows), "s"(p.n_lin), "s"(p.lin[0].codes),
+                 "s"(p.lin[0].scales), "s"(p.lin[0].tile_begin), "s"(p.lin[1].tile_begin),
+                 "s"(p.lin[2].tile_begin), "s"(p.lin[3].tile_begin));
+  }
   const int K = p.K;
   const int F = K >> 10;
   const int r0 = (int)blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
