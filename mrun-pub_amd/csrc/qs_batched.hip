@@ -233,6 +233,16 @@ __global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
     u = (((int)blockIdx.x >> 4) << 3) + ((int)blockIdx.x & 7);
     m0 = ((int)blockIdx.x & 8) << 1;
   }
+  // One argument from each 64-byte argument line the prologue reads, requested in one
+  // batch at entry.  Left to itself the compiler asks for the arguments in dependent
+  // rounds (the slice count, then the linears' first tiles, then the selected linear's
+  // fields at a computed offset), a scalar-cache miss each, before the first row scale is
+  // requested; with every line fetched at entry the later rounds hit the scalar cache.
+  static_assert(offsetof(Bd2Params, lin) + 3 * sizeof(BdecLin) < 256, "argument lines");
+  if constexpr (P == 1)
+    asm volatile("" ::"s"(p.S), "s"(p.lin[0].N), "s"(p.lin[1].tile_begin), "s"(p.lin[3].tile_begin));
+  else
+    asm volatile("" ::"s"(p.S), "s"(p.lin[0].N));
   const int tile = u / p.S;
   const int s = u - tile * p.S;
   int li = 0;
