@@ -455,6 +455,9 @@ __global__ __launch_bounds__(kGkMaxWaves * 64) void k_lowbit_gk(LowbitParams p) 
   static_assert(RT == 1 || PF == NGR, "row tiles share the wave's activations");
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  // one argument of each 64-byte argument line, requested together at entry (the compiler
+  // otherwise waits for the first line before asking for the second)
+  asm volatile("" ::"s"(p.x), "s"(p.M));
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int W = blockDim.x >> 6;

@@ -487,6 +487,21 @@ __global__ __launch_bounds__(kParWaves * 64) void k_moe_route_quant(
 // ----------------------------------------------------------------------------------
 // ragged grouped int8 GEMM
 // ----------------------------------------------------------------------------------
+// A group's routed-row count, first queue row and weight slot, requested together: without
+// a slot table the slot word is read from the starts array (a valid address either way) and
+// a select drops it, so no load waits behind the null test or the empty-group exit (the
+// three dependent global loads had delayed every workgroup's first weight request).
+struct GroupMeta {
+  int count, start, slot;
+};
+__device__ __forceinline__ GroupMeta group_meta(const int32_t* counts, const int32_t* starts, const int32_t* slots,
+                                                int g) {
+  const int32_t* sp = slots ? slots : starts;
+  const int c = counts[g], st = starts[g], sv = sp[g];
+  asm volatile("" ::"s"(c), "s"(st), "s"(sv));
+  return GroupMeta{c, st, slots ? sv : g};
+}
+
 struct MoeGemmParams {
   const int8_t* a;       // [A, K] routed rows, expert-major
   const float* as;       // [A]
@@ -517,10 +532,11 @@ __global__ __launch_bounds__(P * KW * 64) void k_moe_gemm(MoeGemmParams p) {
   const int ks = wave / P;
   const int col = lane & 15, grp = lane >> 4;
   const int g = blockIdx.y;
-  const int count = p.counts[g];
+  const GroupMeta gm = group_meta(p.counts, p.starts, p.slots, g);
+  const int count = gm.count;
   if (count == 0) return;
-  const int start = p.starts[g];
-  const int slot = p.slots ? p.slots[g] : g;
+  const int start = gm.start;
+  const int slot = gm.slot;
   const int C = p.K / 64;
   const int ntiles = (p.N + 15) / 16;
   const int tile0 = blockIdx.x * NT;
@@ -660,10 +676,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream(MoeGemmParams p) {
   const int per_xcd = total / 8;
   const int logical = lin < 8 * per_xcd ? (lin % 8) * per_xcd + lin / 8 : lin;
   const int g = logical / gridDim.x, bx = logical - g * gridDim.x;
-  const int count = p.counts[g];
+  const GroupMeta gm = group_meta(p.counts, p.starts, p.slots, g);
+  const int count = gm.count;
   if (count == 0) return;
-  const int start = p.starts[g];
-  const int slot = p.slots ? p.slots[g] : g;
+  const int start = gm.start;
+  const int slot = gm.slot;
   const int K = p.K, C = K / CB;
   const int xstride = K + 16;
   int8_t* xs = reinterpret_cast<int8_t*>(lds);                 // [MC][K + 16]
@@ -853,10 +870,11 @@ __global__ __launch_bounds__(WAVES * 64) void k_moe_stream_w16(MoeW16Params p) {
   const int per_xcd = total / 8;
   const int logical = lin < 8 * per_xcd ? (lin % 8) * per_xcd + lin / 8 : lin;
   const int g = logical / gridDim.x, bx = logical - g * gridDim.x;
-  const int count = p.counts[g];
+  const GroupMeta gm = group_meta(p.counts, p.starts, p.slots, g);
+  const int count = gm.count;
   if (count == 0) return;
-  const int start = p.starts[g];
-  const int slot = p.slots ? p.slots[g] : g;
+  const int start = gm.start;
+  const int slot = gm.slot;
   const int K = p.K, C = K / CB, KPH = p.KPH, CPH = KPH / CB;
   const int xstride = 2 * KPH + 16;  // bytes per staged row
   const int n0 = (bx * WAVES + wave) * RW;
