@@ -423,10 +423,15 @@ template <int G>
 constexpr int kGkGroupsShort = G == 64 ? 8 : 4;  // 2-3 row tiles, every activation in VGPRs
 template <int G>
 constexpr int kGkGroupsLong = G == 64 ? 12 : 6;  // one row tile, activations streamed
-template <int G, int NGR>
-// the long form keeps two groups of activations in flight: 4096 x 11008 at M=8, int2
-// 12.4 -> 11.6 us and int3 13.7 -> 13.4 us against eight (twelve: 14.8 / 16.4 us)
-constexpr int kGkPrefetch = NGR == kGkGroupsShort<G> ? NGR : 2;
+// int2 with G = 64 and at most 64 groups takes 4 groups per wave (16 waves): 11008 x 4096
+// at M=8 9.58 -> 9.17 us; int3 keeps 8 (4: 12.9 -> 15.8 us)
+template <int BITS, int G>
+constexpr int kGkGroupsShortFine = BITS == 2 && G == 64 ? 4 : kGkGroupsShort<G>;
+template <int G, int NGR, int RT>
+// the short form (RT > 1) holds every activation of the wave in VGPRs; the long form keeps
+// two groups of activations in flight: 4096 x 11008 at M=8, int2 12.4 -> 11.6 us and int3
+// 13.7 -> 13.4 us against eight (twelve: 14.8 / 16.4 us)
+constexpr int kGkPrefetch = RT > 1 ? NGR : 2;
 
 template <int BITS, int G, int SM, int ZM, int NGR, int RT>
 struct GkLds {
@@ -451,7 +456,7 @@ __global__ __launch_bounds__(kGkMaxWaves * 64) void k_lowbit_gk(LowbitParams p) 
   constexpr int QB = CB / 4;        // code bytes of a lane quarter
   constexpr int QC = G / 4;         // codes of a lane quarter
   constexpr int NJ = G / 32;        // MFMAs per group
-  constexpr int PF = kGkPrefetch<G, NGR>;
+  constexpr int PF = kGkPrefetch<G, NGR, RT>;
   static_assert(RT == 1 || PF == NGR, "row tiles share the wave's activations");
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -651,7 +656,10 @@ template <int BITS, int G>
 void launch_gk(const LowbitParams& p, hipStream_t s) {
   // int2 takes three row tiles per workgroup: 11008 rows make 230 workgroups, at most one
   // per CU (9.8 us against 10.9 us with two tiles at M=8); int3 keeps two (12.9 against 13.3)
-  if (p.ng <= kGkMaxWaves * kGkGroupsShort<G>) launch_gk_n<BITS, G, kGkGroupsShort<G>, BITS == 2 ? 3 : 2>(p, s);
+  constexpr int RT = BITS == 2 ? 3 : 2;
+  constexpr int FINE = kGkGroupsShortFine<BITS, G>;
+  if (FINE != kGkGroupsShort<G> && p.ng <= kGkMaxWaves * FINE) launch_gk_n<BITS, G, FINE, RT>(p, s);
+  else if (p.ng <= kGkMaxWaves * kGkGroupsShort<G>) launch_gk_n<BITS, G, kGkGroupsShort<G>, RT>(p, s);
   else launch_gk_n<BITS, G, kGkGroupsLong<G>, 1>(p, s);
 }
 

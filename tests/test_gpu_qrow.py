@@ -79,9 +79,11 @@ def test_matmul_bf16_w8a16(dev, m, n, k):
     assert err <= BF16_TOL, err
 
 
-@pytest.mark.parametrize("m", [1, 16])
-def test_matmul_fp16(dev, m):
-    rng, codes, scales = _case(512, 1024, seed=m)
+@pytest.mark.parametrize("m,n", [(1, 512), (16, 512), (23, 512), (32, 512), (32, 200)])
+def test_matmul_fp16(dev, m, n):
+    """f16 rows; at M > 16 the 512-row case takes the activation-row split (32 units of 16
+    rows), the 200-row case (13 units) the unsplit launch."""
+    rng, codes, scales = _case(n, 1024, seed=m)
     x = oq.round_f16(rng.standard_normal((m, 1024)).astype(np.float32))
     y = _qrow().qrow_matmul(_dev(codes, dev), _dev(scales, dev), _dev(x, dev, torch.float16))
     assert y.dtype == torch.float16
