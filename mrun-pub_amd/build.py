@@ -8,6 +8,7 @@ with the source tree.  Always recompiles every source (the build check must comp
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -37,6 +38,10 @@ COMMON_FLAGS = [
     # products and sums round separately unless a kernel asks for fmaf explicitly (the
     # reference's epilogues and reducers are unfused fp32 operations)
     "-ffp-contract=off",
+    # kernels with scalar arguments get their first 16 argument dwords preloaded into SGPRs
+    # by the hardware (gfx950), so their first loads do not wait for an argument fetch
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
     "-Wno-unused-command-line-argument",
     f"-I{PKG_DIR.parent / 'include'}",
 ]
@@ -46,14 +51,34 @@ def _sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
+def _scratch_kernels(remarks: str) -> list[str]:
+    """Kernels whose resource-usage remarks report scratch memory (stack or spills)."""
+    bad, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and name and int(m.group(1)) > 0:
+            bad.append(f"{name} ({m.group(1)} bytes/lane)")
+    return bad
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.name + ".o")
     cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
     if src.suffix == ".hip":
-        cmd.insert(1, "-xhip")
+        # every kernel must run without scratch memory: a run-time index into a local array
+        # or a spill puts values in scratch, whose accesses share the vector-memory wait
+        # counter with the weight stream (a 1.6x slower decode pass when it happened)
+        cmd[1:1] = ["-xhip", "-Rpass-analysis=kernel-resource-usage"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
+    bad = _scratch_kernels(proc.stderr)
+    if bad:
+        raise RuntimeError(f"{src.name}: kernels use scratch memory: " + "; ".join(bad))
     return obj
 
 

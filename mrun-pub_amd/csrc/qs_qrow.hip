@@ -26,6 +26,10 @@
 //                                 its own weight bytes into registers; otherwise the
 //                                 activations are staged in LDS.  Also the row-stable
 //                                 (batch invariant) lane.
+//   k_gemv_xg / k_gemv_xg_swi : k_gemv_valu's register-activation path (up to 4 bf16/f16
+//                                 rows) with scalar kernel arguments, the ones its first
+//                                 loads need leading, so the hardware preloads them into
+//                                 SGPRs before the wave starts (no argument load round).
 //   k_gemv_top2_xg / k_gemv_top2: the same row work with a running top-2 per wave
 //                                 instead of stores (fused head + top-2), persistent.
 //   k_generic                   : any shape / alignment, one wave per output row.
@@ -937,8 +941,61 @@ __device__ __forceinline__ bool gemv_wave_xg(const QrowParams& p, int rows, floa
 
 
 template <int XT, int MB, int U, int TB, bool SWI>
+__device__ __forceinline__ void gemv_valu_body(const QrowParams& p, int rows, uint8_t* xs);
+
+template <int XT, int MB, int U, int TB, bool SWI>
 __global__ __launch_bounds__((kGemvWaves<XT, MB, U, SWI> * 64)) void k_gemv_valu(QrowParams p, int rows) {
   extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+  gemv_valu_body<XT, MB, U, TB, SWI>(p, rows, xs);
+}
+
+// The register path with scalar arguments.  The hardware preloads the first 14 argument
+// dwords into SGPRs (16 user SGPRs, 2 of them the argument segment address; the build
+// asks for them with -amdgpu-kernarg-preload-count=16), so the arguments the first loads
+// need come first, 8-byte ones on even dwords: activations, K, the row count, the first
+// linear's rows (SwiGLU: both linears), the linears' first rows.  Same-box graph timing
+// of the paired SwiGLU launch at M = 1: 6.556 us with the parameter block, 6.530 with
+// scalar arguments, 6.470 preloaded.
+template <int XT, int MB, int U, int TB>
+__global__ __launch_bounds__((kGemvWaves<XT, MB, U, true> * 64)) void k_gemv_xg_swi(
+    const void* x, int64_t ldx, int K, int rows, const int8_t* gc, const float* gs, const int8_t* uc,
+    const float* us, int M, void* y, int64_t ldy) {
+  QrowParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.M = MB == 1 ? 1 : M;
+  p.K = K;
+  p.n_lin = 2;
+  p.lin[0] = QrowLin{gc, gs, y, ldy, rows, 0};
+  p.lin[1] = QrowLin{uc, us, nullptr, 0, rows, 0};
+  gemv_valu_body<XT, MB, U, TB, true>(p, rows, nullptr);
+}
+
+template <int XT, int MB, int U, int TB>
+__global__ __launch_bounds__((kGemvWaves<XT, MB, U, false> * 64)) void k_gemv_xg(
+    const void* x, int64_t ldx, int K, int rows, int n_lin, int t1, const int8_t* c0, const float* s0, int t2,
+    int t3, int M, const int8_t* c1, const float* s1, const int8_t* c2, const float* s2, const int8_t* c3,
+    const float* s3, void* y0, int64_t ldy0, void* y1, int64_t ldy1, void* y2, int64_t ldy2, void* y3,
+    int64_t ldy3, int n0, int n1, int n2, int n3) {
+  // the wave's linear picked here with scalar selects: the body then sees one linear and
+  // indexes nothing at run time (a run-time index into the local block puts it in scratch)
+  constexpr int WPB = kGemvWaves<XT, MB, U, false>;
+  const int r0 = (int)blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool l1 = n_lin > 1 && r0 >= t1, l2 = n_lin > 2 && r0 >= t2, l3 = n_lin > 3 && r0 >= t3;
+  QrowParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.M = MB == 1 ? 1 : M;
+  p.K = K;
+  p.n_lin = 1;
+  p.lin[0] = QrowLin{l3 ? c3 : l2 ? c2 : l1 ? c1 : c0, l3 ? s3 : l2 ? s2 : l1 ? s1 : s0,
+                     l3 ? y3 : l2 ? y2 : l1 ? y1 : y0,   l3 ? ldy3 : l2 ? ldy2 : l1 ? ldy1 : ldy0,
+                     l3 ? n3 : l2 ? n2 : l1 ? n1 : n0,   l3 ? t3 : l2 ? t2 : l1 ? t1 : 0};
+  gemv_valu_body<XT, MB, U, TB, false>(p, rows, nullptr);
+}
+
+template <int XT, int MB, int U, int TB, bool SWI>
+__device__ __forceinline__ void gemv_valu_body(const QrowParams& p, int rows, uint8_t* xs) {
   const int lane = threadIdx.x & 63;
   const int M = p.M;
   float acc[SWI ? 2 : 1][MB];
@@ -1533,8 +1590,19 @@ template <int XT, int MB, int U, int TB, bool SWI>
 void launch_valu_u(const QrowParams& q, int rows, size_t lds, hipStream_t s) {
   constexpr int WPB = kGemvWaves<XT, MB, U, SWI>;
   const dim3 grid((unsigned)cdiv(rows, WPB)), block(WPB * 64);
-  const size_t l = kGemvXg<XT, MB, U> ? 0 : lds;  // no LDS activations on the register path
-  hipLaunchKernelGGL((k_gemv_valu<XT, MB, U, TB, SWI>), grid, block, l, s, q, rows);
+  if constexpr (kGemvXg<XT, MB, U>) {  // no LDS activations on the register path
+    const QrowLin* L = q.lin;
+    if constexpr (SWI)
+      hipLaunchKernelGGL((k_gemv_xg_swi<XT, MB, U, TB>), grid, block, 0, s, q.x, q.ldx, q.K, rows, L[0].codes,
+                         L[0].scales, L[1].codes, L[1].scales, q.M, L[0].y, L[0].ldy);
+    else
+      hipLaunchKernelGGL((k_gemv_xg<XT, MB, U, TB>), grid, block, 0, s, q.x, q.ldx, q.K, rows, q.n_lin,
+                         L[1].tile_begin, L[0].codes, L[0].scales, L[2].tile_begin, L[3].tile_begin, q.M, L[1].codes,
+                         L[1].scales, L[2].codes, L[2].scales, L[3].codes, L[3].scales, L[0].y, L[0].ldy, L[1].y,
+                         L[1].ldy, L[2].y, L[2].ldy, L[3].y, L[3].ldy, L[0].N, L[1].N, L[2].N, L[3].N);
+  } else {
+    hipLaunchKernelGGL((k_gemv_valu<XT, MB, U, TB, SWI>), grid, block, lds, s, q, rows);
+  }
 }
 
 template <int XT, int MB, int TB, bool SWI>

@@ -84,3 +84,19 @@ def test_moe_entry_point_validation_without_gpu():
     st = lib.qs_moe_route_quant(fake, nat.QS_I64, fake, nat.QS_F32, 4, 2, 8, fake, fake, fake, fake, None, fake,
                                 nat.QS_F16, 64, 64, fake, fake, None)
     assert st == nat.QS_ERR_INVALID and b"F32 or BF16" in lib.qs_last_error()
+
+
+def test_build_rejects_kernels_that_use_scratch():
+    """The build fails on a kernel whose resource remarks report scratch memory."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("qs_build", ROOT / "mrun-pub_amd" / "build.py")
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    remarks = "\n".join([
+        "a.hip:1:1: remark: Function Name: k_fine [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:1:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:9:1: remark: Function Name: k_stack [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:9:1: remark:     ScratchSize [bytes/lane]: 200 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert build._scratch_kernels(remarks) == ["k_stack (200 bytes/lane)"]
