@@ -395,6 +395,13 @@ void* qs_pager_slot_ptr(qs_pager* pager, int slot);
 int qs_pager_submit(qs_pager* pager, int slot, const void* host, size_t bytes, size_t dst_offset);
 /* Mark the end of the slot's submissions (records its ready event). */
 int qs_pager_seal(qs_pager* pager, int slot);
+/* host[0..count * slot_bytes) -> slots [slot, slot + count) (whole slots, contiguous in the
+ * arena) on the copy stream, then each slot sealed: submit + seal for a run of slots with
+ * the copy in max_transfer pieces.  With qs_pager_submit, replaces the miss path of the MoE
+ * page cache (src/mrun/engine/qwen3_moe_cuda.py:1490-1567, _acquire_resident: one H2D of the
+ * staged misses, then index_copy_ into the cache slots): here each run of consecutive pages
+ * moves straight into its consecutive slots. */
+int qs_pager_submit_run(qs_pager* pager, int slot, int count, const void* host);
 int qs_pager_acquire(qs_pager* pager, int slot, void* compute_stream);
 int qs_pager_release(qs_pager* pager, int slot, void* compute_stream);
 /* acquire/release for slots[0..n) in one call (an expert layer's active set).

@@ -85,6 +85,7 @@ SIGNATURES: dict[str, tuple] = {
     "qs_pager_slot_ptr": (_P, [_P, _I]),
     "qs_pager_submit": (_I, [_P, _I, _P, ctypes.c_size_t, ctypes.c_size_t]),
     "qs_pager_seal": (_I, [_P, _I]),
+    "qs_pager_submit_run": (_I, [_P, _I, _I, _P]),
     "qs_pager_acquire": (_I, [_P, _I, _P]),
     "qs_pager_release": (_I, [_P, _I, _P]),
     "qs_pager_acquire_many": (_I, [_P, _P, _I, _P]),

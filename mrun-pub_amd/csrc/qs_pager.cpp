@@ -114,29 +114,59 @@ extern "C" void* qs_pager_slot_ptr(qs_pager* p, int slot) {
   return p->arena + p->slot_bytes * (size_t)slot;
 }
 
+namespace {
+// The slot's last consumer must be done before a copy overwrites it.  The wait is taken on
+// the host (a query, and a block only when the host is a whole ring ahead of the GPU): a
+// copy stream made to wait on a compute-stream event can stall the host inside the
+// following hipMemcpyAsync until that event fires, and the link then idles between blocks.
+int wait_slot_free(qs_pager* p, int slot) {
+  if (p->freed[slot] < 0) return QS_OK;
+  hipEvent_t ev = p->events[p->freed[slot]];
+  hipError_t q = hipEventQuery(ev);
+  if (q == hipErrorNotReady) q = hipEventSynchronize(ev);
+  int st = hip_check(q, "slot free event");
+  if (st) return st;
+  drop_free_ref(p, slot);
+  return QS_OK;
+}
+
+int copy_h2d(qs_pager* p, char* dst, const char* src, size_t bytes) {
+  for (size_t off = 0; off < bytes; off += p->max_transfer) {
+    const size_t n = bytes - off < p->max_transfer ? bytes - off : p->max_transfer;
+    int st = hip_check(hipMemcpyAsync(dst + off, src + off, n, hipMemcpyHostToDevice, p->copy), "hipMemcpyAsync");
+    if (st) return st;
+  }
+  return QS_OK;
+}
+}  // namespace
+
 extern "C" int qs_pager_submit(qs_pager* p, int slot, const void* host, size_t bytes,
                                size_t dst_offset) {
   if (!p || !host || slot < 0 || slot >= p->slots)
     return fail(QS_ERR_INVALID, "pager_submit: bad arguments");
   if (dst_offset + bytes > p->slot_bytes) return fail(QS_ERR_LIMIT, "pager_submit: range exceeds the slot");
-  if (p->freed[slot] >= 0) {
-    // The slot's last consumer must be done before the copy overwrites it.  The wait is
-    // taken on the host (a query, and a block only when the host is a whole ring ahead of
-    // the GPU): a copy stream made to wait on a compute-stream event can stall the host
-    // inside the following hipMemcpyAsync until that event fires, and the link then
-    // idles between blocks.
-    hipEvent_t ev = p->events[p->freed[slot]];
-    hipError_t q = hipEventQuery(ev);
-    if (q == hipErrorNotReady) q = hipEventSynchronize(ev);
-    int st = hip_check(q, "slot free event");
+  int st = wait_slot_free(p, slot);
+  if (st) return st;
+  return copy_h2d(p, p->arena + p->slot_bytes * (size_t)slot + dst_offset, static_cast<const char*>(host), bytes);
+}
+
+// A run of whole slots from one contiguous host range: every slot's previous consumer is
+// waited for, the range moves in max_transfer pieces (not one copy per slot), then every
+// slot is sealed.  A layer change refills ~125 consecutive expert pages into consecutive
+// slots, so its copies become a few large transfers.
+extern "C" int qs_pager_submit_run(qs_pager* p, int slot, int count, const void* host) {
+  if (!p || !host || slot < 0 || count < 1 || count > p->slots - slot)
+    return fail(QS_ERR_INVALID, "pager_submit_run: bad arguments");
+  for (int i = 0; i < count; ++i) {
+    int st = wait_slot_free(p, slot + i);
     if (st) return st;
-    drop_free_ref(p, slot);
   }
-  char* dst = p->arena + p->slot_bytes * (size_t)slot + dst_offset;
-  const char* src = static_cast<const char*>(host);
-  for (size_t off = 0; off < bytes; off += p->max_transfer) {
-    const size_t n = bytes - off < p->max_transfer ? bytes - off : p->max_transfer;
-    int st = hip_check(hipMemcpyAsync(dst + off, src + off, n, hipMemcpyHostToDevice, p->copy), "hipMemcpyAsync");
+  int st = copy_h2d(p, p->arena + p->slot_bytes * (size_t)slot, static_cast<const char*>(host),
+                    p->slot_bytes * (size_t)count);
+  if (st) return st;
+  for (int i = 0; i < count; ++i) {
+    p->ready_done[slot + i] = 0;
+    st = hip_check(hipEventRecord(p->ready[slot + i], p->copy), "hipEventRecord(ready)");
     if (st) return st;
   }
   return QS_OK;

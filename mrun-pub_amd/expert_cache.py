@@ -1034,6 +1034,25 @@ class ExpertPageCache:
         nat.call("qs_pager_submit", self._pager, slot, host_ptr, self.layout.page_stride, 0)
         nat.call("qs_pager_seal", self._pager, slot)
 
+    def _submit_runs(self, pages: list[tuple[int, int]]) -> None:
+        """H2D of ``(slot, host address)`` pages: pages whose slots and host rows both follow
+        each other move as one run (``qs_pager_submit_run``, at most ``TRANSFER_BYTES``
+        each), so a layer change's ~125 consecutive pages are a few large transfers."""
+        stride = self.layout.page_stride
+        cap = max(1, TRANSFER_BYTES // stride)
+        pages = sorted(pages)
+        i = 0
+        while i < len(pages):
+            j = i + 1
+            while (j < len(pages) and j - i < cap and pages[j][0] == pages[j - 1][0] + 1
+                   and pages[j][1] == pages[j - 1][1] + stride):
+                j += 1
+            if j - i == 1:
+                self._submit(*pages[i])
+            else:
+                nat.call("qs_pager_submit_run", self._pager, pages[i][0], j - i, pages[i][1])
+            i = j
+
     def _acquire_slots(self, slots: list[int]) -> None:
         """The compute stream waits for the pending transfers into ``slots``."""
         if slots:
@@ -1045,12 +1064,14 @@ class ExpertPageCache:
         stream: straight from the page's pinned tier row, else through the pinned staging
         buffer (pages only the store holds are read by one gather, in the given order)."""
         staged: list[tuple[int, int, torch.Tensor | None]] = []  # (expert, slot, pageable tier row)
+        direct: list[tuple[int, int]] = []  # (slot, pinned tier row address)
         for expert, slot in misses:
             row = self.host_tier.host_page(layer, expert) if self.host_tier is not None else None
             if row is not None and self.host_tier.pinned:
-                self._submit(slot, row.data_ptr())
+                direct.append((slot, row.data_ptr()))
             else:
                 staged.append((expert, slot, row))
+        self._submit_runs(direct)
         if staged:
             if self._stage_in_flight:  # the previous staging copies must have landed
                 self.synchronize()
@@ -1060,8 +1081,7 @@ class ExpertPageCache:
                 self.store.gather(layer, [expert for expert, _, _ in staged[:n_store]], self.stage)
             for i in range(n_store, len(staged)):
                 self.stage[i].numpy()[:] = staged[i][2].numpy()
-            for i, (_, slot, _) in enumerate(staged):
-                self._submit(slot, self.stage[i].data_ptr())
+            self._submit_runs([(slot, self.stage[i].data_ptr()) for i, (_, slot, _) in enumerate(staged)])
             self._stage_in_flight = True
 
     def acquire_transient_prefill(self, layer: int, top_indices: torch.Tensor):

@@ -225,3 +225,34 @@ def _pass_reversed(store, xs):
             out.append(store.matmul("l0.k", xs[256]))
         out.append(store.matmul(f"{layer}.q", xs[256]))
     return out
+
+
+def test_pager_submit_run_fills_consecutive_slots(dev):
+    """``qs_pager_submit_run`` moves one contiguous host range into consecutive slots in
+    transfer pieces (here 3 slots of 4096 bytes with 5000-byte pieces, so pieces straddle
+    slots), seals every slot, leaves the other slots untouched, waits for a slot's previous
+    consumer, and refuses a run past the last slot."""
+    import ctypes
+
+    from mrun_pub_amd import _native as nat
+
+    arena = torch.zeros(6 * 4096, dtype=torch.uint8, device=dev)
+    handle = ctypes.c_void_p()
+    nat.call("qs_pager_create", nat.ptr(arena), 4096, 6, 5000, ctypes.byref(handle))
+    try:
+        stream = nat.stream_of(dev)
+        host = (torch.arange(3 * 4096, dtype=torch.int32) % 251).to(torch.uint8).pin_memory()
+        nat.call("qs_pager_release_many", handle, (ctypes.c_int * 2)(2, 3), 2, stream)  # a consumer to wait for
+        nat.call("qs_pager_submit_run", handle, 1, 3, host.data_ptr())
+        nat.call("qs_pager_acquire_many", handle, (ctypes.c_int * 3)(1, 2, 3), 3, stream)
+        torch.cuda.synchronize()
+        assert torch.equal(arena[4096:4 * 4096].cpu(), host)
+        assert not arena[:4096].any() and not arena[4 * 4096:].any()
+        for slot in (1, 2, 3):
+            assert nat.load().qs_pager_slot_landed(handle, slot) == 1
+        with pytest.raises(ValueError):
+            nat.call("qs_pager_submit_run", handle, 4, 3, host.data_ptr())
+        with pytest.raises(ValueError):
+            nat.call("qs_pager_submit_run", handle, 0, 0, host.data_ptr())
+    finally:
+        nat.call("qs_pager_destroy", handle)
