@@ -776,7 +776,7 @@ def main() -> int:
             f"{elapsed / args.steps * 1e3:.4f} ms per replay",
         },
         "roofline": {
-            "kernel": "paired gate/up W8A16 + SwiGLU (qs_qrow_swiglu, k_gemv_valu)",
+            "kernel": "paired gate/up W8A16 + SwiGLU (qs_qrow_swiglu, k_gemv_xg_swi)",
             "bound": "hbm",
             "achieved": round(sw_gbs, 1),
             "peak": HBM_PEAK_GBS,
