@@ -266,47 +266,76 @@ __global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
 #pragma unroll
   for (int pl = 0; pl < P; ++pl) sc[pl] = p.lin[P == 2 ? pl : li].scales[nr < N ? nr : tb];
 
-  // 2. the activation slice [16 MT rows][NCH chunks] -> LDS; rows >= M and chunks past the
-  //    slice read out of the buffer's range (zero, no memory access)
-  const int xlim = p.M * (int)p.ldx * 2;
-  const __amdgpu_buffer_rsrc_t xr =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x), (short)0, xlim, 0x00020000);
-  const int total = 16 * MT * NCH;
-  for (int u0 = wave * 64; u0 < total; u0 += NW * 64) {
-    const int e = u0 + lane;
-    const int m = e / NCH, jj = e - m * NCH, j = jj ^ (m & 15);
-    const bool ok = m0 + m < p.M && j < 8 * cs;
-    bd2_copy16(xr, bsm + 16 * u0, ok ? ((m0 + m) * (int)p.ldx + kbeg + 8 * j) * 2 : xlim);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 3. this wave's part of the slice: every chunk requested at once (zero past the part
-  //    and for rows >= N, whose lane offsets lie past the buffer)
+  // Early dequant: the weights are requested first and each chunk is dequantized into bf16
+  // registers as it lands, while the activation copies are still in flight; the MFMAs
+  // follow the barrier.  It holds P * 8 VGPRs per chunk, so the 16-wave paired forms keep
+  // the late order (copies first, dequant after the barrier) to stay out of scratch.
+  constexpr bool EARLY = !(P == 2 && WR * WK > 12);
   const int PS = (cs + WK - 1) / WK;
   const int cb = wk * PS;
   const int ce = min(cs, cb + PS);
   const int wlim = L0.N * p.K;
   const int wlane = nr < N ? nr * p.K + kbeg + 16 * grp : wlim;  // rows past N: no access
   i32x4 wv[kBd2MaxPS][P];
+  // this wave's part of the slice's weights: every chunk requested at once (zero past the
+  // part and for rows >= N, whose lane offsets lie past the buffer)
+  auto load_weights = [&]() {
 #pragma unroll
-  for (int pl = 0; pl < P; ++pl) {
-    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t*>(p.lin[P == 2 ? pl : li].codes), (short)0, wlim, 0x00020000);
+    for (int pl = 0; pl < P; ++pl) {
+      const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<int8_t*>(p.lin[P == 2 ? pl : li].codes), (short)0, wlim, 0x00020000);
+#pragma unroll
+      for (int c = 0; c < kBd2MaxPS; ++c)
+        wv[c][pl] = __builtin_bit_cast(
+            i32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, cb + c < ce && nr < N ? wlane + 64 * (cb + c) : wlim, 0, 0));
+    }
+  };
+  // the activation slice [16 MT rows][NCH chunks] -> LDS; rows >= M and chunks past the
+  // slice read out of the buffer's range (zero, no memory access)
+  const int xlim = p.M * (int)p.ldx * 2;
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x), (short)0, xlim, 0x00020000);
+  auto copy_slice = [&]() {
+    const int total = 16 * MT * NCH;
+    for (int u0 = wave * 64; u0 < total; u0 += NW * 64) {
+      const int e = u0 + lane;
+      const int m = e / NCH, jj = e - m * NCH, j = jj ^ (m & 15);
+      const bool ok = m0 + m < p.M && j < 8 * cs;
+      bd2_copy16(xr, bsm + 16 * u0, ok ? ((m0 + m) * (int)p.ldx + kbeg + 8 * j) * 2 : xlim);
+    }
+  };
+  hvec wb[EARLY ? kBd2MaxPS : 1][P][2];
+  if constexpr (EARLY) {
+    // 2. weights, 3. copies, 4. each weight chunk dequantized as it lands (loads return in
+    //    issue order, so the weights need no copy to land), 5. every copy of this wave has
+    //    landed, and the barrier makes every wave's visible
+    load_weights();
+    __builtin_amdgcn_sched_barrier(0);
+    copy_slice();
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int c = 0; c < kBd2MaxPS; ++c)
-      wv[c][pl] = __builtin_bit_cast(
-          i32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, cb + c < ce && nr < N ? wlane + 64 * (cb + c) : wlim, 0, 0));
+      if (cb + c < ce) {
+#pragma unroll
+        for (int pl = 0; pl < P; ++pl) H::deq(wv[c][pl], sc[pl], wb[c][pl][0], wb[c][pl][1]);
+      }
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  } else {
+    // 2. copies, 3. weights, 4. this wave's copies have landed once at most its
+    //    kBd2MaxPS * P weight loads are outstanding; the barrier then makes every wave's
+    //    copies visible
+    copy_slice();
+    __builtin_amdgcn_sched_barrier(0);
+    load_weights();
+    __builtin_amdgcn_sched_barrier(0);
+    static_assert(kBd2MaxPS * P == 8 || kBd2MaxPS * P == 16, "wait counts below");
+    if constexpr (kBd2MaxPS * P == 16)
+      asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
   }
-  __builtin_amdgcn_sched_barrier(0);
-  // 4. this wave's copies have landed once at most its kBd2MaxPS * P weight loads are
-  //    outstanding; the barrier then makes every wave's copies visible
-  static_assert(kBd2MaxPS * P == 8 || kBd2MaxPS * P == 16, "wait counts below");
-  if constexpr (kBd2MaxPS * P == 16)
-    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
 
-  // 5. MFMA over the part
+  // 6. MFMA over the part
   f32x4 acc[P][MT];
 #pragma unroll
   for (int pl = 0; pl < P; ++pl)
@@ -327,7 +356,12 @@ __global__ __launch_bounds__(WR * WK * 64) void k_bd2(Bd2Params p) {
 #pragma unroll
       for (int pl = 0; pl < P; ++pl) {
         hvec b0, b1;
-        H::deq(wv[c][pl], sc[pl], b0, b1);
+        if constexpr (EARLY) {
+          b0 = wb[c][pl][0];
+          b1 = wb[c][pl][1];
+        } else {
+          H::deq(wv[c][pl], sc[pl], b0, b1);
+        }
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
           acc[pl][t] = H::mma(b0, xa[t][0], acc[pl][t]);
