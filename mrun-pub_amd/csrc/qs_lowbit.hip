@@ -763,10 +763,11 @@ __global__ __launch_bounds__(kValuThreads) void k_lowbit_valu(LowbitParams p) {
   };
   const int nrows = wave_id < p.N ? (p.N - 1 - wave_id) / nwaves + 1 : 0;  // rows of this wave
   const int nbt = (nrows + R - 1) / R;
-  // activations of long rows (J >= 3 pieces per lane): the first kXRegs chunks per thread
-  // are requested before the codes, so the staging below waits for them only, not for the
-  // codes in flight behind them (short rows keep the registers for occupancy instead)
-  constexpr int kXRegs = J >= 3 ? 6 : 0;
+  // the first kXRegs activation chunks per thread are requested before the codes, so the
+  // staging below waits for them only, not for the codes in flight behind them (loads
+  // return in order).  Short rows hold one staging unit: int2 11008 x 4096 went 6.97 ->
+  // 6.58 us at M = 1 and 8.70 -> 8.12 us at M = 2 over staging after the codes.
+  constexpr int kXRegs = J >= 3 ? 6 : 2;
   // staging unit: one 16-byte chunk (int3) or one 16-code word's 32 bytes (int2)
   constexpr int U = BITS == 2 ? 2 : 1;
   constexpr int kXU = kXRegs / U;
