@@ -212,6 +212,34 @@ def test_swiglu(dev, m, n, k):
     assert err <= BF16_TOL, err
 
 
+@pytest.mark.parametrize("n,k", [(8960, 1536), (8193, 512), (12000, 256), (16384, 2048), (16385, 1040),
+                                 (20000, 1536)])
+def test_swiglu_rows_equal_row_blocks(dev, n, k):
+    """At M = 1 a SwiGLU with more rows than one resident round of waves (8192 on 256 CUs)
+    runs its last rows in a later round: every output equals the same row computed in
+    launches of at most 4096 rows bit for bit, whatever the row count and tail kind, and
+    the oracle within the bf16 tolerance."""
+    from mrun_pub_amd.qrow import CompactQRowPage, fused_qrow_swiglu
+
+    rng = np.random.default_rng(n + k)
+    gq = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    uq = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    gs = (rng.uniform(0.5, 1.5, size=n) / 127).astype(np.float32)
+    us = (rng.uniform(0.5, 1.5, size=n) / 127).astype(np.float32)
+    x = oq.round_bf16(rng.standard_normal((1, k)).astype(np.float32))
+    gqd, uqd, gsd, usd = (_dev(a, dev) for a in (gq, uq, gs, us))
+    xd = _dev(x, dev, torch.bfloat16)
+    full = fused_qrow_swiglu(CompactQRowPage("g", 0, n, k, gqd, gsd), CompactQRowPage("u", 0, n, k, uqd, usd), xd)[0]
+    parts = []
+    for a in range(0, n, 4096):
+        e = min(n, a + 4096)
+        parts.append(fused_qrow_swiglu(CompactQRowPage("g", 0, e - a, k, gqd[a:e], gsd[a:e]),
+                                       CompactQRowPage("u", 0, e - a, k, uqd[a:e], usd[a:e]), xd)[0])
+    assert torch.equal(full, torch.cat(parts, dim=1))
+    err = oq.rel_l2(full.float().cpu().numpy(), oq.qrow_swiglu(gq, gs, uq, us, x))
+    assert err <= BF16_TOL, err
+
+
 def test_errors_are_reference_exceptions(dev):
     from mrun_pub_amd.qrow import CompactQRowPage, fused_qrow_matmul, fused_qrow_swiglu
 
