@@ -1532,6 +1532,181 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
                                                 reinterpret_cast<const float*>(tail));
 }
 
+// k_gemm_i8_dma with 128-byte K steps in two LDS stages (k_gemm_i8_p2).  A copy instruction
+// then takes whole 128-byte lines (8 rows x 128 bytes) instead of half lines (16 rows x 64
+// bytes): a probe of this copy ring on 448 workgroups measured 69.8 GB/s of LDS fill per CU
+// with 64 KB in flight, against 42-43 GB/s for the half-line copies with 64 or 96 KB in
+// flight.  Stage p & 1 holds the pair of 64-k steps p; the copies of pair p + 2 go out
+// after the barrier that ends pair p, so one pair is always in flight while the other is
+// multiplied.  One barrier per 128 k.  Rows are 128 bytes; 16-byte chunk c of row r sits
+// at slot c ^ dma_swz8(r), which puts the 16 rows of each ds_read_b128 pass (see
+// dma_swz) in 16 distinct bank groups: a pass reads rows of both parities, and within a
+// parity its 8 rows have distinct (r >> 1) & 7.  Needs K % 128 == 0, 16-byte aligned rows
+// and 256 * ld < 2^31.
+__device__ __forceinline__ int dma_swz8(int r) { return (r >> 1) & 7; }
+
+template <int BM, int BN, int WM, int WN, int EPI, int PRE = 0>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmParams p) {
+  constexpr int BK = 128, S = 2;
+  constexpr int WAVES_M = BM / WM, NW = WAVES_M * (BN / WN), NT = NW * 64;
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int TILE_A = BM * BK, TILE_B = BN * BK;  // bytes per operand per stage
+  constexpr int STAGE = TILE_A + TILE_B;
+  constexpr int JA = BM / 8 / NW, JB = BN / 8 / NW;  // 1 KiB copies per wave per stage
+  static_assert(JA >= 1 && JB >= 1 && JA * 8 * NW == BM && JB * 8 * NW == BN, "whole copies per wave");
+  static_assert(S * STAGE >= (BM + BN) * (kSideLds + 1) * 4, "epilogue staging needs the tile LDS");
+  constexpr int TAIL = PRE ? 4 * tail_floats<BM, BN>() : 0;  // bytes
+  __shared__ __attribute__((aligned(1024))) int8_t lds[S * STAGE + TAIL];
+  int8_t* const tail = lds + S * STAGE;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int tiles_m = (p.M + BM - 1) / BM;
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int G = tiles_m * tiles_n;
+  const int bid = blockIdx.x;
+  int lid = bid;
+  if ((G & 7) == 0) lid = (bid & 7) * (G >> 3) + (bid >> 3);
+  const int tm = lid % tiles_m, tn = lid / tiles_m;
+  const int bm = tm * BM, bn = tn * BN;
+
+  const int64_t arem = (int64_t)(p.M - bm) * p.lda, brem = (int64_t)(p.N - bn) * p.ldb;
+  const int alim = (int)(arem < INT_MAX ? arem : INT_MAX), blim = (int)(brem < INT_MAX ? brem : INT_MAX);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(p.a + (int64_t)bm * p.lda), (short)0, alim, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(p.b + (int64_t)bn * p.ldb), (short)0, blim, 0x00020000);
+  // copy j of this wave covers tile rows 8 * (J * wave + j) + 0..7 of its operand; lane l
+  // lands in row + (l >> 3), slot l & 7, and fetches chunk slot ^ swizzle
+  int aoff[JA], boff[JB];
+#pragma unroll
+  for (int j = 0; j < JA; ++j) {
+    const int r = 8 * (JA * wave + j) + (lane >> 3);
+    aoff[j] = r * (int)p.lda + 16 * ((lane & 7) ^ dma_swz8(r));
+  }
+#pragma unroll
+  for (int j = 0; j < JB; ++j) {
+    const int r = 8 * (JB * wave + j) + (lane >> 3);
+    boff[j] = r * (int)p.ldb + 16 * ((lane & 7) ^ dma_swz8(r));
+  }
+  const int KP = p.K / BK;  // pairs of 64-k steps
+  // PRE: the copy slots of pair KP, which loads nothing otherwise, fetch the epilogue's
+  // operands into the tail (as in k_gemm_i8_dma)
+  auto tail_copies = [&](int8_t* st) {
+    const int tp = p.P > 0 && p.P <= kTailSide ? p.P : 0;
+    const int ncx = (BM * tp + 255) / 256, ncw = (BN * tp + 255) / 256;
+    auto rs = [](const float* base, int64_t n) {  // n floats readable from base
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0,
+                                               (int)(4 * n < INT_MAX ? 4 * n : INT_MAX), 0x00020000);
+    };
+    static_assert(2 + (BM + BN) * kTailSide / 256 <= (JA + JB) * NW, "tail copies fit the pair's slots");
+#pragma unroll
+    for (int j = 0; j < JA + JB; ++j) {
+      const int c = j * NW + wave;  // wave-uniform
+      if (c == 0)
+        lds_copy16(rs(p.as + bm, p.M - bm), tail + 4 * kTailAs, 16 * lane, 0);
+      else if (c == 1)
+        lds_copy16(rs(p.bs + bn, p.N - bn), tail + 4 * kTailBs, 16 * lane, 0);
+      else if (c < 2 + ncx)
+        lds_copy16(rs(p.xp + (int64_t)bm * tp, (int64_t)(p.M - bm) * tp), tail + 4 * kTailXp + 1024 * (c - 2),
+                   16 * lane + 1024 * (c - 2), 0);
+      else if (c < 2 + ncx + ncw)
+        lds_copy16(rs(p.wp + (int64_t)bn * tp, (int64_t)(p.N - bn) * tp),
+                   tail + 4 * (kTailXp + BM * kTailSide) + 1024 * (c - 2 - ncx), 16 * lane + 1024 * (c - 2 - ncx), 0);
+      else
+        lds_copy16(rsa, st + 1024 * c, alim, 0);  // nothing to fetch: out of range, no access
+    }
+  };
+  // pair kp -> stage kp & 1; pairs past K load out of the buffer's range (zero, no memory
+  // access) into a stage that is not read again
+  auto dma = [&](int kp) {
+    const bool live = kp < KP;
+    const int ko = live ? kp * BK : 0;
+    int8_t* st = lds + (kp & (S - 1)) * STAGE;
+    if constexpr (PRE) {
+      if (kp == KP) {
+        tail_copies(st);
+        return;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < JA; ++j) lds_copy16(rsa, st + 1024 * (JA * wave + j), live ? aoff[j] : alim, ko);
+#pragma unroll
+    for (int j = 0; j < JB; ++j) lds_copy16(rsb, st + TILE_A + 1024 * (JB * wave + j), live ? boff[j] : blim, ko);
+  };
+
+  i32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+  const int sl = dma_swz8(lane & 31);  // fragment rows are 32-aligned bases + (lane & 31)
+  const int arow = (wm * WM + (lane & 31)) * BK, brow = TILE_A + (wn * WN + (lane & 31)) * BK;
+  // slice ks (0..3) of pair kp: 32 k; lanes 0-31 take chunk 2 ks, lanes 32-63 chunk 2 ks + 1
+  auto frag = [&](i32x4 (&f)[FM + FN], int kp, int ks) {
+    const int8_t* st = lds + (kp & (S - 1)) * STAGE;
+    const int co = 16 * ((2 * ks + (lane >> 5)) ^ sl);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) f[i] = *reinterpret_cast<const i32x4*>(st + arow + 32 * BK * i + co);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) f[FM + j] = *reinterpret_cast<const i32x4*>(st + brow + 32 * BK * j + co);
+  };
+  auto mma = [&](const i32x4 (&f)[FM + FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[FM + j], f[i], acc[i][j], 0, 0, 0);  // C^T tile
+  };
+  i32x4 fa[FM + FN], fb[FM + FN];
+  dma(0);
+  dma(1);
+  constexpr int NEWER = JA + JB;  // this wave's copies of the newer stage
+  static_assert(NEWER == 8 || NEWER == 6, "wait counts below");
+  if constexpr (NEWER == 8)
+    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+  // a pair-1 copy that took the tail path issued argument loads (lgkmcnt); settle them
+  // here, visibly to the compiler, so that the loop keeps its partial LDS waits
+  if constexpr (PRE) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt unconstrained
+  frag(fa, 0, 0);
+  // Pair kp: slices 0..3, each read one slice ahead of its MFMAs; after the last slice's
+  // reads, this wave's copies of pair kp + 1 have landed (vmcnt(0): they are the only ones
+  // out) and its reads of stage kp & 1 are done (lgkmcnt(0)), so after the barrier the
+  // stage takes the copies of pair kp + 2 while slice 3 is multiplied.
+  auto pair = [&](int kp) {
+    frag(fb, kp, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(fa);
+    __builtin_amdgcn_sched_barrier(0);
+    frag(fa, kp, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(fb);
+    __builtin_amdgcn_sched_barrier(0);
+    frag(fb, kp, 3);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(fa);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kp + 1 < KP) {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (kp + 2 <= KP) dma(kp + 2);
+      frag(fa, kp + 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mma(fb);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int kp = 0; kp < KP; ++kp) pair(kp);
+  // every copy (including the ones past K) has landed before the epilogue reuses LDS
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  gemm_epilogue_t<BM, BN, WM, WN, EPI, NT, PRE>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn, tid, lane,
+                                                reinterpret_cast<const float*>(tail));
+}
+
 // Any shape: one thread per output, exact int32 accumulation.
 __global__ __launch_bounds__(256) void k_gemm_i8_generic(GemmParams p, int epi) {
   const int64_t i = blockIdx.x * 256ll + threadIdx.x;
@@ -1593,14 +1768,27 @@ void launch_gemm(const GemmParams& p, hipStream_t s) {
     const bool pre = EPI != EPI_I32 && p.M % 4 == 0 && p.N % 4 == 0 && aligned(p.as, 16) && aligned(p.bs, 16) &&
                      (!side_tail || (aligned(p.xp, 16) && aligned(p.wp, 16) && ((int64_t)p.M * p.P) % 4 == 0 &&
                                      ((int64_t)p.N * p.P) % 4 == 0));
+    const bool p2 = p.K % 128 == 0;  // whole 128-byte lines per copy (k_gemm_i8_p2)
     if (big) {
       const int G = (int)(cdiv(p.M, 256) * cdiv(p.N, 256));
-      if (pre) hipLaunchKernelGGL((k_gemm_i8_dma<256, 256, 128, 64, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(512), 0, s, p);
-      else hipLaunchKernelGGL((k_gemm_i8_dma<256, 256, 128, 64, EPI>), dim3(G), dim3(512), 0, s, p);
+      if (p2) {
+        if (pre) hipLaunchKernelGGL((k_gemm_i8_p2<256, 256, 128, 64, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((k_gemm_i8_p2<256, 256, 128, 64, EPI>), dim3(G), dim3(512), 0, s, p);
+      } else if (pre) {
+        hipLaunchKernelGGL((k_gemm_i8_dma<256, 256, 128, 64, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(512), 0, s, p);
+      } else {
+        hipLaunchKernelGGL((k_gemm_i8_dma<256, 256, 128, 64, EPI>), dim3(G), dim3(512), 0, s, p);
+      }
     } else {
       const int G = (int)(cdiv(p.M, 256) * cdiv(p.N, 128));
-      if (pre) hipLaunchKernelGGL((k_gemm_i8_dma<256, 128, 64, 64, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(512), 0, s, p);
-      else hipLaunchKernelGGL((k_gemm_i8_dma<256, 128, 64, 64, EPI>), dim3(G), dim3(512), 0, s, p);
+      if (p2) {
+        if (pre) hipLaunchKernelGGL((k_gemm_i8_p2<256, 128, 64, 64, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(512), 0, s, p);
+        else hipLaunchKernelGGL((k_gemm_i8_p2<256, 128, 64, 64, EPI>), dim3(G), dim3(512), 0, s, p);
+      } else if (pre) {
+        hipLaunchKernelGGL((k_gemm_i8_dma<256, 128, 64, 64, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(512), 0, s, p);
+      } else {
+        hipLaunchKernelGGL((k_gemm_i8_dma<256, 128, 64, 64, EPI>), dim3(G), dim3(512), 0, s, p);
+      }
     }
     return;
   }

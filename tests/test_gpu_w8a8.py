@@ -37,10 +37,12 @@ def _weights(out, inn, seed):
         (5, 3, 4),
         (300, 256, 192),
         # DMA-fed kernel edges: one and two 64-byte K steps (the copy ring runs past K),
-        # and the 256 x 256 tiles with ragged M and N
+        # and the 256 x 256 tiles with ragged M and N; K % 128 == 0 takes the 128-byte-step
+        # kernel (one pair at K = 128, two at K = 256)
         (40, 200, 64),
         (260, 130, 128),
         (1030, 8200, 64),
+        (1030, 8200, 256),
     ],
 )
 def test_int8_gemm_int32_bit_exact(dev, t, n, k):
