@@ -1071,12 +1071,24 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, i32x16 (&acc)
 // fp32) or 8-byte (bf16) instruction instead of four scalar ones.  The side path's
 // MFMAs swap their operands the same way and keep their order, so every value equals the
 // one gemm_epilogue computes.  PRE as in gemm_epilogue.
-template <int BM, int BN, int WM, int WN, int EPI, int NT, int PRE>
+//
+// LDSB is the size of the tile LDS at ws0.  When it also holds a 32 x WN block per wave
+// beyond the side-path staging, each wave passes its block of row tile i through that
+// wave-private area (16-byte chunks XOR-swizzled by block row) and stores it with 16
+// bytes per lane, 8 (bf16) or 16 (fp32 / int32) lanes per block row: every store
+// instruction then writes whole 128-byte lines instead of 16- or 32-byte pieces of 32
+// rows.  A wave whose block is ragged or whose rows are not 16-byte aligned stores from
+// registers.
+template <int BM, int BN, int WM, int WN, int EPI, int NT, int PRE, int LDSB = 0>
 __device__ __forceinline__ void gemm_epilogue_t(const GemmParams& p, i32x16 (&acc)[WM / 32][WN / 32], float* ws0,
                                                 int bm, int bn, int wm, int wn, int tid, int lane,
                                                 const float* tail) {
   constexpr int FM = WM / 32, FN = WN / 32;
   static_assert(!PRE || (EPI != EPI_I32 && BM <= 256 && BN <= 256), "tail layout");
+  constexpr int ES = EPI == EPI_BF16 ? 2 : 4;                // output bytes per element
+  constexpr int RB = WN * ES, NCH = RB / 16;                 // block row bytes, 16-byte chunks
+  constexpr int SIDE_B = (BM + BN) * (kSideLds + 1) * 4;     // side-path staging at ws0
+  constexpr bool kRowStore = WN == 64 && LDSB >= SIDE_B + (NT / 64) * 32 * RB;
   const int h = lane >> 5, l32 = lane & 31;
   const bool tside = PRE && p.P > 0 && p.P <= kTailSide;
   const int nsc = (EPI != EPI_I32 && p.P > 0 && !tside) ? (p.P + kSideLds - 1) / kSideLds : 0;
@@ -1103,11 +1115,15 @@ __device__ __forceinline__ void gemm_epilogue_t(const GemmParams& p, i32x16 (&ac
   if ((EPI != EPI_I32 && !PRE) || nsc == 1) __syncthreads();
   // 4-wide stores need 16-byte aligned rows (ldc % 4 == 0, y 16-byte aligned)
   const bool vec = p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
+  const bool rowst = kRowStore && ((int64_t)p.ldc * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0 &&
+                     bn + wn * WN + WN <= p.N;
+  int8_t* const tb = reinterpret_cast<int8_t*>(ws0) + SIDE_B + __builtin_amdgcn_readfirstlane(tid >> 6) * 32 * RB;
   typedef float f32x16 __attribute__((ext_vector_type(16)));
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int lrow = wm * WM + 32 * i + l32;
     const int row = bm + lrow;
+    const bool tr = rowst && bm + wm * WM + 32 * i + 32 <= p.M;  // wave-uniform
     // the side operands of this lane's row (P == 8 tail: two 16-byte LDS reads)
     float xr[kTailSide];
     if (tside) {
@@ -1171,9 +1187,15 @@ __device__ __forceinline__ void gemm_epilogue_t(const GemmParams& p, i32x16 (&ac
         if (row >= p.M || col0 >= p.N) continue;
         const int64_t o = (int64_t)row * p.ldc + col0;
         const bool full = vec && col0 + 3 < p.N;
+        // this lane's four values in the wave's block: row l32, 16-byte chunk q (bf16: its
+        // half h), at the chunk's swizzled place
+        const int q = ES == 2 ? 4 * j + g : 8 * j + 2 * g + h;
+        int8_t* const tw = tb + l32 * RB + 16 * (q ^ (l32 & (NCH - 1))) + (ES == 2 ? 8 * h : 0);
         if constexpr (EPI == EPI_I32) {
           const i32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-          if (full) {
+          if (tr) {
+            *reinterpret_cast<i32x4*>(tw) = v;
+          } else if (full) {
             *reinterpret_cast<i32x4*>(static_cast<int32_t*>(p.c) + o) = v;
           } else {
 #pragma unroll
@@ -1190,7 +1212,9 @@ __device__ __forceinline__ void gemm_epilogue_t(const GemmParams& p, i32x16 (&ac
             if (nsc || tside) v[e] = add_rn(side[4 * g + e], v[e]);
           }
           if constexpr (EPI == EPI_F32) {
-            if (full) {
+            if (tr) {
+              *reinterpret_cast<f32x4*>(tw) = f32x4{v[0], v[1], v[2], v[3]};
+            } else if (full) {
               *reinterpret_cast<f32x4*>(static_cast<float*>(p.c) + o) = f32x4{v[0], v[1], v[2], v[3]};
             } else {
 #pragma unroll
@@ -1201,8 +1225,10 @@ __device__ __forceinline__ void gemm_epilogue_t(const GemmParams& p, i32x16 (&ac
             uint16_t b[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) b[e] = f32_to_bf16_bits(v[e]);
-            if (full) {
-              const uint2 pk = make_uint2(b[0] | (uint32_t)b[1] << 16, b[2] | (uint32_t)b[3] << 16);
+            const uint2 pk = make_uint2(b[0] | (uint32_t)b[1] << 16, b[2] | (uint32_t)b[3] << 16);
+            if (tr) {
+              *reinterpret_cast<uint2*>(tw) = pk;
+            } else if (full) {
               *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.c) + o) = pk;
             } else {
 #pragma unroll
@@ -1211,6 +1237,21 @@ __device__ __forceinline__ void gemm_epilogue_t(const GemmParams& p, i32x16 (&ac
             }
           }
         }
+      }
+    }
+    if (tr) {
+      // the block's rows, 16 bytes per lane: lane l reads chunk l % NCH of block row
+      // RPI s + l / NCH (its swizzled place) and stores it where the row lies in C
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's block writes landed
+      constexpr int RPI = 64 / NCH;
+      const int c = lane & (NCH - 1);
+      char* const cb = static_cast<char*>(p.c) +
+                       ((int64_t)(bm + wm * WM + 32 * i) * p.ldc + bn + wn * WN) * ES + 16 * c;
+#pragma unroll
+      for (int s = 0; s < 32 / RPI; ++s) {
+        const int r = RPI * s + lane / NCH;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(tb + r * RB + 16 * (c ^ (r & (NCH - 1))));
+        *reinterpret_cast<i32x4*>(cb + (int64_t)r * p.ldc * ES) = v;
       }
     }
   }
@@ -1528,8 +1569,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
   for (; kt < KT; ++kt) step(kt, true, true);
   // every copy (including the ones past K) has landed before the epilogue reuses LDS
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  gemm_epilogue_t<BM, BN, WM, WN, EPI, NT, PRE>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn, tid, lane,
-                                                reinterpret_cast<const float*>(tail));
+  gemm_epilogue_t<BM, BN, WM, WN, EPI, NT, PRE, S * STAGE>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn,
+                                                           tid, lane, reinterpret_cast<const float*>(tail));
 }
 
 // k_gemm_i8_dma with 128-byte K steps in two LDS stages (k_gemm_i8_p2).  A copy instruction
@@ -1703,8 +1744,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmP
   for (int kp = 0; kp < KP; ++kp) pair(kp);
   // every copy (including the ones past K) has landed before the epilogue reuses LDS
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  gemm_epilogue_t<BM, BN, WM, WN, EPI, NT, PRE>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn, tid, lane,
-                                                reinterpret_cast<const float*>(tail));
+  gemm_epilogue_t<BM, BN, WM, WN, EPI, NT, PRE, S * STAGE>(p, acc, reinterpret_cast<float*>(lds), bm, bn, wm, wn,
+                                                           tid, lane, reinterpret_cast<const float*>(tail));
 }
 
 // Any shape: one thread per output, exact int32 accumulation.
