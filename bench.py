@@ -208,8 +208,10 @@ def cpu_baselines_per_config(seconds: float = 2.0) -> dict:
 
 def _graph_time(torch, stream, fn, calls: int, reps: int = 50, warmup: int = 10) -> float:
     """Median seconds per call of ``fn`` (one launch sequence), captured ``calls`` times in
-    a graph; each of ``reps`` replays after ``warmup`` untimed ones is timed with its own
-    pair of HIP events on ``stream`` (the median of >= 50 runs after 10 warm-ups)."""
+    a graph; each of ``reps`` replays after untimed ones (``warmup`` at a time, until at
+    least 50 ms have run: the first milliseconds of a burst run at a lower clock, e.g.
+    38.6 against 35.7 us for config 3's M = 512 GEMM) is timed with its own pair of HIP
+    events on ``stream``."""
     with torch.cuda.stream(stream):
         fn(0)
         torch.cuda.synchronize()
@@ -217,7 +219,7 @@ def _graph_time(torch, stream, fn, calls: int, reps: int = 50, warmup: int = 10)
         with torch.cuda.graph(g, stream=stream):
             for i in range(calls):
                 fn(i)
-        per = _replay_times(torch, stream, g, reps, warmup=warmup)
+        per = _replay_times(torch, stream, g, reps, warmup=warmup, min_warm_s=0.05)
     return _median(per) / calls
 
 
@@ -227,12 +229,17 @@ def _median(v: list[float]) -> float:
     return v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
 
 
-def _replay_times(torch, stream, graph, reps: int, warmup: int) -> list[float]:
-    """Seconds of each of ``reps`` replays (after ``warmup`` untimed ones), HIP events on the
-    replay stream around every replay."""
-    for _ in range(warmup):
-        graph.replay()
-    torch.cuda.synchronize()
+def _replay_times(torch, stream, graph, reps: int, warmup: int, min_warm_s: float = 0.0) -> list[float]:
+    """Seconds of each of ``reps`` replays (after ``warmup`` untimed ones, repeated until
+    ``min_warm_s`` seconds have passed), HIP events on the replay stream around every
+    replay."""
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= min_warm_s:
+            break
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
     with torch.cuda.stream(stream):
         ev[0].record(stream)
