@@ -145,6 +145,43 @@ def test_w8a8_bf16_out_bit_exact(dev, t, n):
     assert torch.equal(y.cpu(), ref)
 
 
+@pytest.mark.parametrize("ydt", ["f32", "bf16"])
+@pytest.mark.parametrize("t,n,k", [(300, 1000, 512), (300, 1004, 512), (300, 1002, 512), (1030, 8196, 256)])
+def test_gemm_epilogue_store_layouts(dev, t, n, k, ydt):
+    """The epilogue stores whole row segments through LDS when the output rows are 16-byte
+    aligned (N * bytes % 16 == 0 and an aligned y), 4-wide from registers when only
+    N % 4 == 0, element by element otherwise; ragged M and N edges store from registers.
+    Every layout, and y placed past a 16-byte boundary, gives (float(acc) * a_s) * b_s
+    in fp32 (bf16: its round to nearest even) bit for bit."""
+    from mrun_pub_amd import _native as nat
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(t + 7 * n + k)
+    qx = torch.randint(-127, 128, (t, k), dtype=torch.int8, device=dev, generator=g)
+    qw = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=g)
+    a_s = torch.rand(t, device=dev, generator=g) / 100 + 1e-3
+    b_s = torch.rand(n, device=dev, generator=g) / 100 + 1e-3
+    code = nat.QS_F32 if ydt == "f32" else nat.QS_BF16
+    dt = torch.float32 if ydt == "f32" else torch.bfloat16
+    # |acc| <= k * 127 * 127 < 2^24: the float64 product is the exact integer and float(acc)
+    # is exact, so the reference is two fp32 products (tile shapes: 256 x 128 below M * N =
+    # 1024 * 8192, 256 x 256 from there)
+    acc = qx.cpu().numpy().astype(np.float64) @ qw.cpu().numpy().astype(np.float64).T
+    ref = (torch.from_numpy(acc.astype(np.float32)) * a_s.cpu()[:, None]) * b_s.cpu()[None, :]
+    ref = ref.to(dt)
+    for shift in (0, 1):
+        buf = torch.full((t * n + 8,), float("nan"), dtype=dt, device=dev)
+        y = buf[shift : shift + t * n].view(t, n)  # shift 1: y starts 2 or 4 bytes past alignment
+        assert (y.data_ptr() % 16 == 0) == (shift == 0)
+        nat.call("qs_w8a8_gemm", nat.ptr(qx), nat.ptr(a_s), nat.ptr(qw), nat.ptr(b_s), None, None, 0, nat.ptr(y),
+                 code, t, n, k, nat.stream_of(dev))
+        torch.cuda.synchronize()
+        got = y.cpu()
+        assert torch.equal(got.view(torch.int16 if ydt == "bf16" else torch.int32),
+                           ref.view(torch.int16 if ydt == "bf16" else torch.int32)), (shift, t, n, k, ydt)
+        assert torch.isnan(buf[:shift].float()).all() and torch.isnan(buf[shift + t * n :].float()).all()
+
+
 @pytest.mark.parametrize(
     "t,n,p,ydt",
     [(300, 1000, 0, "f32"), (300, 1000, 1, "bf16"), (300, 1000, 3, "f32"), (64, 640, 8, "f32"),
