@@ -146,7 +146,8 @@ def test_w8a8_bf16_out_bit_exact(dev, t, n):
 
 
 @pytest.mark.parametrize("ydt", ["f32", "bf16"])
-@pytest.mark.parametrize("t,n,k", [(300, 1000, 512), (300, 1004, 512), (300, 1002, 512), (1030, 8196, 256)])
+@pytest.mark.parametrize("t,n,k", [(300, 1000, 512), (300, 1004, 512), (300, 1002, 512), (1030, 8196, 256),
+                                   (300, 1004, 320), (1030, 8200, 192)])
 def test_gemm_epilogue_store_layouts(dev, t, n, k, ydt):
     """The epilogue stores whole row segments through LDS when the output rows are 16-byte
     aligned (N * bytes % 16 == 0 and an aligned y), 4-wide from registers when only
@@ -165,7 +166,8 @@ def test_gemm_epilogue_store_layouts(dev, t, n, k, ydt):
     dt = torch.float32 if ydt == "f32" else torch.bfloat16
     # |acc| <= k * 127 * 127 < 2^24: the float64 product is the exact integer and float(acc)
     # is exact, so the reference is two fp32 products (tile shapes: 256 x 128 below M * N =
-    # 1024 * 8192, 256 x 256 from there)
+    # 1024 * 8192, 256 x 256 from there; K % 128 == 64 takes the 64-byte-step kernel, which
+    # shares the epilogue)
     acc = qx.cpu().numpy().astype(np.float64) @ qw.cpu().numpy().astype(np.float64).T
     ref = (torch.from_numpy(acc.astype(np.float32)) * a_s.cpu()[:, None]) * b_s.cpu()[None, :]
     ref = ref.to(dt)
