@@ -43,6 +43,9 @@ def _weights(out, inn, seed):
         (260, 130, 128),
         (1030, 8200, 64),
         (1030, 8200, 256),
+        # long K: 112 pairs of the copy ring, sums up to 14336 * 128 * 128 (below 2^31)
+        (64, 512, 14336),
+        (3, 300, 8192 + 64),
     ],
 )
 def test_int8_gemm_int32_bit_exact(dev, t, n, k):
