@@ -1706,11 +1706,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmP
   dma(0);
   dma(1);
   constexpr int NEWER = JA + JB;  // this wave's copies of the newer stage
-  static_assert(NEWER == 8 || NEWER == 6, "wait counts below");
+  static_assert(NEWER == 8 || NEWER == 6 || NEWER == 4, "wait counts below");
   if constexpr (NEWER == 8)
     asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-  else
+  else if constexpr (NEWER == 6)
     asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
   // a pair-1 copy that took the tail path issued argument loads (lgkmcnt); settle them
   // here, visibly to the compiler, so that the loop keeps its partial LDS waits
   if constexpr (PRE) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt unconstrained
@@ -1820,6 +1822,13 @@ void launch_gemm(const GemmParams& p, hipStream_t s) {
       } else {
         hipLaunchKernelGGL((k_gemm_i8_dma<256, 256, 128, 64, EPI>), dim3(G), dim3(512), 0, s, p);
       }
+    } else if (p2 && cdiv(p.M, 256) * cdiv(p.N, 128) <= 128) {
+      // few rows (M <= 256 at N <= 16384): 256 x 128 tiles would fill at most half the CUs,
+      // each with a full tile of copies; 128 x 128 tiles (8 waves of 32 x 64) double the
+      // tiles and cut each one's copies by a third
+      const int G = (int)(cdiv(p.M, 128) * cdiv(p.N, 128));
+      if (pre) hipLaunchKernelGGL((k_gemm_i8_p2<128, 128, 32, 64, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(512), 0, s, p);
+      else hipLaunchKernelGGL((k_gemm_i8_p2<128, 128, 32, 64, EPI>), dim3(G), dim3(512), 0, s, p);
     } else {
       const int G = (int)(cdiv(p.M, 256) * cdiv(p.N, 128));
       if (p2) {

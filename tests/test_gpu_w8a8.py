@@ -46,6 +46,8 @@ def _weights(out, inn, seed):
         # long K: 112 pairs of the copy ring, sums up to 14336 * 128 * 128 (below 2^31)
         (64, 512, 14336),
         (3, 300, 8192 + 64),
+        # few rows: 128 x 128 tiles (ragged M and N)
+        (200, 8200, 256),
     ],
 )
 def test_int8_gemm_int32_bit_exact(dev, t, n, k):
