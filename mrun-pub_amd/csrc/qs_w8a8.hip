@@ -1822,6 +1822,17 @@ void launch_gemm(const GemmParams& p, hipStream_t s) {
       } else {
         hipLaunchKernelGGL((k_gemm_i8_dma<256, 256, 128, 64, EPI>), dim3(G), dim3(512), 0, s, p);
       }
+    } else if (p2 && p.M <= 64) {
+      // a weight stream: 64 x 64 tiles (4 waves of 32 x 32) put twice the tiles of 128-row
+      // tiles on the CUs, with no copies for absent rows (14336 x 4096, M = 64: 24.0 ->
+      // 19.2 us; M = 128 on 128 x 64 tiles: 25.6 -> 22.4 us)
+      const int G = (int)(cdiv(p.M, 64) * cdiv(p.N, 64));
+      if (pre) hipLaunchKernelGGL((k_gemm_i8_p2<64, 64, 32, 32, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((k_gemm_i8_p2<64, 64, 32, 32, EPI>), dim3(G), dim3(256), 0, s, p);
+    } else if (p2 && p.M <= 128) {
+      const int G = (int)(cdiv(p.M, 128) * cdiv(p.N, 64));
+      if (pre) hipLaunchKernelGGL((k_gemm_i8_p2<128, 64, 32, 64, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((k_gemm_i8_p2<128, 64, 32, 64, EPI>), dim3(G), dim3(256), 0, s, p);
     } else if (p2 && cdiv(p.M, 256) * cdiv(p.N, 128) <= 128) {
       // few rows (M <= 256 at N <= 16384): 256 x 128 tiles would fill at most half the CUs,
       // each with a full tile of copies; 128 x 128 tiles (8 waves of 32 x 64) double the

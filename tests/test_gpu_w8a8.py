@@ -46,8 +46,10 @@ def _weights(out, inn, seed):
         # long K: 112 pairs of the copy ring, sums up to 14336 * 128 * 128 (below 2^31)
         (64, 512, 14336),
         (3, 300, 8192 + 64),
-        # few rows: 128 x 128 tiles (ragged M and N)
+        # few rows: 128 x 128, 128 x 64 and 64 x 64 tiles (ragged M and N)
         (200, 8200, 256),
+        (100, 1000, 384),
+        (40, 5000, 128),
     ],
 )
 def test_int8_gemm_int32_bit_exact(dev, t, n, k):
