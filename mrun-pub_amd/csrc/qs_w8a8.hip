@@ -1573,13 +1573,35 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_dma(Gemm
                                                            tid, lane, reinterpret_cast<const float*>(tail));
 }
 
-// k_gemm_i8_dma with 128-byte K steps in two LDS stages (k_gemm_i8_p2).  A copy instruction
-// then takes whole 128-byte lines (8 rows x 128 bytes) instead of half lines (16 rows x 64
-// bytes): a probe of this copy ring on 448 workgroups measured 69.8 GB/s of LDS fill per CU
-// with 64 KB in flight, against 42-43 GB/s for the half-line copies with 64 or 96 KB in
-// flight.  Stage p & 1 holds the pair of 64-k steps p; the copies of pair p + 2 go out
-// after the barrier that ends pair p, so one pair is always in flight while the other is
-// multiplied.  One barrier per 128 k.  Rows are 128 bytes; 16-byte chunk c of row r sits
+// s_waitcnt vmcnt(N) (lgkmcnt(0) too with LGK), then s_barrier; N is a compile-time count
+// of this wave's newer copies that may stay in flight.
+template <int N, bool LGK>
+__device__ __forceinline__ void vm_wait_barrier() {
+  static_assert(N == 0 || N == 4 || N == 6 || N == 8 || N == 12 || N == 18, "wait counts");
+  if constexpr (LGK) {
+    if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(18) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  } else {
+    if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+    else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+    else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    else if constexpr (N == 12) asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(18)\n\ts_barrier" ::: "memory");
+  }
+}
+
+// k_gemm_i8_dma with 128-byte K steps in S LDS stages (k_gemm_i8_p2; S = 2 for the large
+// tiles, 4 for the small ones).  A copy instruction then takes whole 128-byte lines (8 rows
+// x 128 bytes) instead of half lines (16 rows x 64 bytes): a probe of this copy ring on 448
+// workgroups measured 69.8 GB/s of LDS fill per CU with 64 KB in flight, against 42-43 GB/s
+// for the half-line copies with 64 or 96 KB in flight.  Stage p % S holds the pair of 64-k
+// steps p; the copies of pair p + S go out after the barrier that ends pair p, so S - 1
+// pairs are in flight while one is multiplied.  One barrier per 128 k.  Rows are 128 bytes; 16-byte chunk c of row r sits
 // at slot c ^ dma_swz8(r), which puts the 16 rows of each ds_read_b128 pass (see
 // dma_swz) in 16 distinct bank groups: a pass reads rows of both parities, and within a
 // parity its 8 rows have distinct (r >> 1) & 7.  Needs K % 128 == 0, 16-byte aligned rows
@@ -1588,7 +1610,12 @@ __device__ __forceinline__ int dma_swz8(int r) { return (r >> 1) & 7; }
 
 template <int BM, int BN, int WM, int WN, int EPI, int PRE = 0>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmParams p) {
-  constexpr int BK = 128, S = 2;
+  constexpr int BK = 128;
+  // stages: two for the large tiles (a third measured no faster on 256 x 128); the small
+  // tiles of few-row products, a weight stream, keep three stages of copies in flight
+  // (14336 x 4096, one box: M = 64 on 64 x 64 tiles 19.2 -> 13.1 us, M = 256 on 128 x 128
+  // tiles 25.4 -> 24.3 us)
+  constexpr int S = BM + BN <= 256 ? 4 : 2;
   constexpr int WAVES_M = BM / WM, NW = WAVES_M * (BN / WN), NT = NW * 64;
   constexpr int FM = WM / 32, FN = WN / 32;
   constexpr int TILE_A = BM * BK, TILE_B = BN * BK;  // bytes per operand per stage
@@ -1659,12 +1686,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmP
         lds_copy16(rsa, st + 1024 * c, alim, 0);  // nothing to fetch: out of range, no access
     }
   };
-  // pair kp -> stage kp & 1; pairs past K load out of the buffer's range (zero, no memory
+  // pair kp -> stage kp % S; pairs past K load out of the buffer's range (zero, no memory
   // access) into a stage that is not read again
   auto dma = [&](int kp) {
     const bool live = kp < KP;
     const int ko = live ? kp * BK : 0;
-    int8_t* st = lds + (kp & (S - 1)) * STAGE;
+    int8_t* st = lds + (kp % S) * STAGE;
     if constexpr (PRE) {
       if (kp == KP) {
         tail_copies(st);
@@ -1688,7 +1715,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmP
   const int arow = (wm * WM + (lane & 31)) * BK, brow = TILE_A + (wn * WN + (lane & 31)) * BK;
   // slice ks (0..3) of pair kp: 32 k; lanes 0-31 take chunk 2 ks, lanes 32-63 chunk 2 ks + 1
   auto frag = [&](i32x4 (&f)[FM + FN], int kp, int ks) {
-    const int8_t* st = lds + (kp & (S - 1)) * STAGE;
+    const int8_t* st = lds + (kp % S) * STAGE;
     const int co = 16 * ((2 * ks + (lane >> 5)) ^ sl);
 #pragma unroll
     for (int i = 0; i < FM; ++i) f[i] = *reinterpret_cast<const i32x4*>(st + arow + 32 * BK * i + co);
@@ -1703,24 +1730,20 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmP
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[FM + j], f[i], acc[i][j], 0, 0, 0);  // C^T tile
   };
   i32x4 fa[FM + FN], fb[FM + FN];
-  dma(0);
-  dma(1);
-  constexpr int NEWER = JA + JB;  // this wave's copies of the newer stage
-  static_assert(NEWER == 8 || NEWER == 6 || NEWER == 4, "wait counts below");
-  if constexpr (NEWER == 8)
-    asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-  else if constexpr (NEWER == 6)
-    asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
-  // a pair-1 copy that took the tail path issued argument loads (lgkmcnt); settle them
+#pragma unroll
+  for (int i = 0; i < S; ++i) dma(i);
+  constexpr int NEWER = JA + JB;  // this wave's copies of one stage
+  vm_wait_barrier<(S - 1) * NEWER, false>();  // stage 0 landed
+  // a prologue copy that took the tail path issued argument loads (lgkmcnt); settle them
   // here, visibly to the compiler, so that the loop keeps its partial LDS waits
   if constexpr (PRE) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt unconstrained
   frag(fa, 0, 0);
   // Pair kp: slices 0..3, each read one slice ahead of its MFMAs; after the last slice's
-  // reads, this wave's copies of pair kp + 1 have landed (vmcnt(0): they are the only ones
-  // out) and its reads of stage kp & 1 are done (lgkmcnt(0)), so after the barrier the
-  // stage takes the copies of pair kp + 2 while slice 3 is multiplied.
+  // reads, this wave's copies of pair kp + 1 have landed (only the S - 2 newer stages'
+  // copies may still be out) and its reads of stage kp % S are done (lgkmcnt(0)), so after
+  // the barrier the stage takes the copies of pair kp + S while slice 3 is multiplied.
+  // With S > 2 every pair issues its copies, past K too (out of range), so that the wait
+  // counts stay exact.
   auto pair = [&](int kp) {
     frag(fb, kp, 1);
     __builtin_amdgcn_sched_barrier(0);
@@ -1735,8 +1758,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmP
     mma(fa);
     __builtin_amdgcn_sched_barrier(0);
     if (kp + 1 < KP) {
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (kp + 2 <= KP) dma(kp + 2);
+      vm_wait_barrier<(S - 2) * NEWER, true>();
+      if constexpr (S == 2) {
+        if (kp + 2 <= KP) dma(kp + 2);
+      } else {
+        dma(kp + S);
+      }
       frag(fa, kp + 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1824,8 +1851,8 @@ void launch_gemm(const GemmParams& p, hipStream_t s) {
       }
     } else if (p2 && p.M <= 64) {
       // a weight stream: 64 x 64 tiles (4 waves of 32 x 32) put twice the tiles of 128-row
-      // tiles on the CUs, with no copies for absent rows (14336 x 4096, M = 64: 24.0 ->
-      // 19.2 us; M = 128 on 128 x 64 tiles: 25.6 -> 22.4 us)
+      // tiles on the CUs, with no copies for absent rows (14336 x 4096, two stages: M = 64
+      // 24.0 -> 19.2 us; M = 128 on 128 x 64 tiles 25.6 -> 22.4 us)
       const int G = (int)(cdiv(p.M, 64) * cdiv(p.N, 64));
       if (pre) hipLaunchKernelGGL((k_gemm_i8_p2<64, 64, 32, 32, EPI, EPI == EPI_I32 ? 0 : 1>), dim3(G), dim3(256), 0, s, p);
       else hipLaunchKernelGGL((k_gemm_i8_p2<64, 64, 32, 32, EPI>), dim3(G), dim3(256), 0, s, p);
