@@ -1599,13 +1599,13 @@ __device__ __forceinline__ void vm_wait_barrier() {
 // tiles, 4 for the small ones).  A copy instruction then takes whole 128-byte lines (8 rows
 // x 128 bytes) instead of half lines (16 rows x 64 bytes): a probe of this copy ring on 448
 // workgroups measured 69.8 GB/s of LDS fill per CU with 64 KB in flight, against 42-43 GB/s
-// for the half-line copies with 64 or 96 KB in flight.  Stage p % S holds the pair of 64-k
-// steps p; the copies of pair p + S go out after the barrier that ends pair p, so S - 1
-// pairs are in flight while one is multiplied.  One barrier per 128 k.  Rows are 128 bytes; 16-byte chunk c of row r sits
-// at slot c ^ dma_swz8(r), which puts the 16 rows of each ds_read_b128 pass (see
-// dma_swz) in 16 distinct bank groups: a pass reads rows of both parities, and within a
-// parity its 8 rows have distinct (r >> 1) & 7.  Needs K % 128 == 0, 16-byte aligned rows
-// and 256 * ld < 2^31.
+// for the half-line copies with 64 or 96 KB in flight.  Stage p & (S - 1) holds the pair
+// of 64-k steps p; the copies of pair p + S go out after the barrier that ends pair p, so
+// S - 1 pairs are in flight while one is multiplied.  One barrier per 128 k.  Rows are 128
+// bytes; 16-byte chunk c of row r sits at slot c ^ dma_swz8(r), which puts the 16 rows of
+// each ds_read_b128 pass (see dma_swz) in 16 distinct bank groups: a pass reads rows of
+// both parities, and within a parity its 8 rows have distinct (r >> 1) & 7.  Needs
+// K % 128 == 0, 16-byte aligned rows and 256 * ld < 2^31.
 __device__ __forceinline__ int dma_swz8(int r) { return (r >> 1) & 7; }
 
 template <int BM, int BN, int WM, int WN, int EPI, int PRE = 0>
@@ -1616,6 +1616,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmP
   // (14336 x 4096, one box: M = 64 on 64 x 64 tiles 19.2 -> 13.1 us, M = 256 on 128 x 128
   // tiles 25.4 -> 24.3 us)
   constexpr int S = BM + BN <= 256 ? 4 : 2;
+  static_assert((S & (S - 1)) == 0, "stage index by mask");
   constexpr int WAVES_M = BM / WM, NW = WAVES_M * (BN / WN), NT = NW * 64;
   constexpr int FM = WM / 32, FN = WN / 32;
   constexpr int TILE_A = BM * BK, TILE_B = BN * BK;  // bytes per operand per stage
@@ -1686,12 +1687,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmP
         lds_copy16(rsa, st + 1024 * c, alim, 0);  // nothing to fetch: out of range, no access
     }
   };
-  // pair kp -> stage kp % S; pairs past K load out of the buffer's range (zero, no memory
-  // access) into a stage that is not read again
+  // pair kp -> stage kp & (S - 1); pairs past K load out of the buffer's range (zero, no
+  // memory access) into a stage that is not read again
   auto dma = [&](int kp) {
     const bool live = kp < KP;
     const int ko = live ? kp * BK : 0;
-    int8_t* st = lds + (kp % S) * STAGE;
+    int8_t* st = lds + (kp & (S - 1)) * STAGE;
     if constexpr (PRE) {
       if (kp == KP) {
         tail_copies(st);
@@ -1715,7 +1716,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmP
   const int arow = (wm * WM + (lane & 31)) * BK, brow = TILE_A + (wn * WN + (lane & 31)) * BK;
   // slice ks (0..3) of pair kp: 32 k; lanes 0-31 take chunk 2 ks, lanes 32-63 chunk 2 ks + 1
   auto frag = [&](i32x4 (&f)[FM + FN], int kp, int ks) {
-    const int8_t* st = lds + (kp % S) * STAGE;
+    const int8_t* st = lds + (kp & (S - 1)) * STAGE;
     const int co = 16 * ((2 * ks + (lane >> 5)) ^ sl);
 #pragma unroll
     for (int i = 0; i < FM; ++i) f[i] = *reinterpret_cast<const i32x4*>(st + arow + 32 * BK * i + co);
@@ -1740,8 +1741,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void k_gemm_i8_p2(GemmP
   frag(fa, 0, 0);
   // Pair kp: slices 0..3, each read one slice ahead of its MFMAs; after the last slice's
   // reads, this wave's copies of pair kp + 1 have landed (only the S - 2 newer stages'
-  // copies may still be out) and its reads of stage kp % S are done (lgkmcnt(0)), so after
-  // the barrier the stage takes the copies of pair kp + S while slice 3 is multiplied.
+  // copies may still be out) and its reads of stage kp & (S - 1) are done (lgkmcnt(0)), so
+  // after the barrier the stage takes the copies of pair kp + S while slice 3 is multiplied.
   // With S > 2 every pair issues its copies, past K too (out of range), so that the wait
   // counts stay exact.
   auto pair = [&](int kp) {
