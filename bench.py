@@ -203,6 +203,19 @@ def cpu_baselines_per_config(seconds: float = 2.0) -> dict:
     b5 = N5 * (K5 * 3 // 8) + 2 * 2 * N5 * (K5 // 64) + 2 * K5 + 4 * N5
     both("config5_int3_m1", lambda: cpu_path.lowbit_matmul(packed, sc5, z5, x5, K5, 3, 64, 0.0), b5 / 1e9, "GB/s",
          "QStoreInt3.matmul CPU path (chunked np.unpackbits dequant + sgemm) on 2048 of the 11008 rows")
+    # offline codecs: the numpy writers restated in oracle/ (single-threaded numpy), bytes as
+    # in the device codec lines
+    from oracle import lowbit as olow
+    from oracle import qrow as oq
+
+    Wq = rng.standard_normal((1024, 4096)).astype(np.float32)
+    done, dt = _timed_loop(lambda: oq.quant_row_int8(Wq), seconds)
+    out["codec_int8"] = {"unit": "GB/s", "sample": "_quant_row_int8 on 1024 x 4096 fp32 rows (numpy)",
+                         "one_thread": round(done * (5 * 1024 * 4096 + 4 * 1024) / dt / 1e9, 3)}
+    Wl = rng.standard_normal((256, 4096)).astype(np.float32)
+    done, dt = _timed_loop(lambda: olow.quant_row_int3(Wl), seconds)
+    out["codec_int3"] = {"unit": "GB/s", "sample": "_quant_row_int3 + packing on 256 x 4096 fp32 rows (numpy)",
+                         "one_thread": round(done * (4 * 256 * 4096 + 256 * 1536 + 4 * 256 * 32) / dt / 1e9, 3)}
     return out
 
 
@@ -583,6 +596,27 @@ def secondary_measurements(torch, dev, stream) -> dict:
                     "us": round(t5 * 1e6, 2), "GB/s": round(b5 / t5 / 1e9, 1),
                     "hbm_frac": round(b5 / t5 / 1e9 / HBM_PEAK_GBS, 4)}
             del packed, sc, zp, pages
+
+    # offline codecs (the store writer's row quantizers) on the device: int8 rows of config
+    # 3's fp32 weight [14336, 4096], int3 / int2 (G 128, the writers' default) of config 5's
+    # [11008, 4096]; bytes = fp32 input + codes + fp32 scales
+    from mrun_pub_amd import codecs
+
+    Nc, Kc = 14336, 4096
+    Wc = torch.randn(Nc, Kc, device=dev, generator=gen)
+    tc = _graph_time(torch, stream, lambda i: codecs.quant_row_int8(Wc), 4)
+    bc = 4 * Nc * Kc + Nc * Kc + 4 * Nc
+    res["codec_int8_14336x4096"] = {"us": round(tc * 1e6, 2), "GB/s": round(bc / tc / 1e9, 1),
+                                    "hbm_frac": round(bc / tc / 1e9 / HBM_PEAK_GBS, 4)}
+    del Wc
+    Nc, Kc, Gc = 11008, 4096, codecs.GROUP
+    Wc = torch.randn(Nc, Kc, device=dev, generator=gen)
+    for bits, fn in ((3, codecs.quant_row_int3), (2, codecs.quant_row_int2)):
+        tc = _graph_time(torch, stream, lambda i: fn(Wc), 4)
+        bc = 4 * Nc * Kc + Nc * ((Kc * bits + 7) // 8) + 4 * Nc * ((Kc + Gc - 1) // Gc)
+        res[f"codec_int{bits}_{Nc}x{Kc}"] = {"us": round(tc * 1e6, 2), "GB/s": round(bc / tc / 1e9, 1),
+                                             "hbm_frac": round(bc / tc / 1e9 / HBM_PEAK_GBS, 4)}
+    del Wc
     return res
 
 

@@ -11,6 +11,9 @@
 //                    code = (active ? sign(blk) : 0) + 1 (_quant_row_int2, qstore_int2.py:36-63).
 //   k_pack_codes   : one thread per output byte of the LSB-first row bitstream
 //                    (np.packbits(bitorder="little"), qstore_int3.py:30-39, qstore_int2.py:24-33).
+//   k_quant_int8_v, k_quant_g128 : the same arithmetic with 16-byte loads, for rows of
+//                    whole 4-column pieces (int8) and for the writers' default G = 128
+//                    with whole groups (int3/int2, codes packed in the same launch).
 //
 // Arithmetic follows numpy's exactly:
 //   * float32 divisions by the literals 127.0 / 3.0 (numpy keeps float32 for a Python float
@@ -112,6 +115,120 @@ __global__ __launch_bounds__(256) void k_quant_int8(const float* __restrict__ W,
   }
 }
 
+// k_quant_int8 for rows of whole 4-column pieces (16-byte aligned): 16-byte loads, the
+// second pass re-reading the row from L2, four codes per 4-byte store.
+__global__ __launch_bounds__(256) void k_quant_int8_v(const float* __restrict__ W, int64_t ldw, int N, int K,
+                                                      int8_t* __restrict__ q, int64_t ldq,
+                                                      float* __restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const f32x4* w = reinterpret_cast<const f32x4*>(W + (int64_t)n * ldw);
+  const int k4 = K / 4;
+  float mx = 0.f;
+  for (int i = lane; i < k4; i += 64) {
+    const f32x4 v = w[i];
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  }
+  mx = wave_max(mx);
+  float s = mx / 127.0f;
+  if (s == 0.f) s = 1.f;
+  if (lane == 0) scales[n] = s;
+  auto code = [&](float x) -> uint32_t {
+    float r = rintf(x / s);
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    return static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(r)));
+  };
+  uint32_t* qo = reinterpret_cast<uint32_t*>(q + (int64_t)n * ldq);
+  for (int i = lane; i < k4; i += 64) {
+    const f32x4 v = w[i];
+    qo[i] = code(v[0]) | code(v[1]) << 8 | code(v[2]) << 16 | code(v[3]) << 24;
+  }
+}
+
+// k_quant_groups + k_pack_codes for G = 128 with whole groups (K % 128 == 0) and 16-byte
+// aligned rows, in one launch: half a wave per group, lane l of the half holding columns
+// 4l .. 4l + 3.  int3: the group maximum over the half, then lane pairs write their 8 codes
+// as 3 bytes.  int2: numpy's pairwise sums of 128 terms are 8 interleaved running sums
+// (terms j, j + 8, .., j + 120, in order) combined as ((r0 + r1) + (r2 + r3)) + ((r4 + r5) +
+// (r6 + r7)); the group goes through LDS so that lane j < 8 of the half forms r_j in that
+// order, and an xor butterfly over lanes 0..7 forms the combination bit for bit (IEEE
+// addition commutes).  Each lane then writes its 4 codes as one byte.
+template <int BITS>
+__global__ __launch_bounds__(256) void k_quant_g128(const float* __restrict__ W, int64_t ldw, int N, int K,
+                                                    float* __restrict__ scales, uint8_t* __restrict__ packed,
+                                                    int64_t row_bytes) {
+  __shared__ __attribute__((aligned(16))) float stage[8][128];  // one group per half wave
+  const int lane = threadIdx.x & 63, hw = threadIdx.x >> 5, l = lane & 31;
+  const int ng = K / 128;
+  const int64_t grp = (int64_t)blockIdx.x * 8 + hw;
+  const bool valid = grp < (int64_t)N * ng;
+  const int n = valid ? (int)(grp / ng) : 0;
+  const int g = valid ? (int)(grp - (int64_t)n * ng) : 0;
+  const f32x4 v = valid ? *reinterpret_cast<const f32x4*>(W + (int64_t)n * ldw + g * 128 + 4 * l)
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+  float* st = stage[hw];
+  // numpy's pairwise sum of the 128 staged values (every lane of the block takes part)
+  auto staged_sum = [&]() -> float {
+    __syncthreads();
+    float r = 0.f;
+    if (l < 8) {
+      r = st[l];
+      for (int i = 1; i < 16; ++i) r += st[l + 8 * i];
+    }
+    r += __shfl_xor(r, 1);
+    r += __shfl_xor(r, 2);
+    r += __shfl_xor(r, 4);
+    return __shfl(r, lane & 32);  // lane 0 of the half
+  };
+  uint8_t* const prow = packed + (int64_t)n * row_bytes;
+  float s;
+  if constexpr (BITS == 3) {
+    float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    for (int o = 1; o < 32; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));  // within the half
+    s = mx / 3.0f;
+    if (s == 0.f) s = 1.f;
+    uint32_t c12 = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float r = rintf(v[t] / s);
+      r = fminf(fmaxf(r, -3.f), 3.f);
+      c12 |= static_cast<uint32_t>(static_cast<int>(r) + 4) << (3 * t);
+    }
+    const uint32_t c24 = c12 | static_cast<uint32_t>(__shfl_xor(static_cast<int>(c12), 1)) << 12;
+    if (valid && (l & 1) == 0) {
+      uint8_t* const o = prow + g * 48 + 3 * (l >> 1);
+      o[0] = static_cast<uint8_t>(c24);
+      o[1] = static_cast<uint8_t>(c24 >> 8);
+      o[2] = static_cast<uint8_t>(c24 >> 16);
+    }
+  } else {
+    const f32x4 a = {fabsf(v[0]), fabsf(v[1]), fabsf(v[2]), fabsf(v[3])};
+    *reinterpret_cast<f32x4*>(st + 4 * l) = a;
+    const float sum_abs = staged_sum();
+    const float mean = static_cast<float>(static_cast<double>(sum_abs) / 128);
+    const float thr = 0.7f * mean;
+    int cnt = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) cnt += a[t] >= thr;
+    for (int o = 1; o < 32; o <<= 1) cnt += __shfl_xor(cnt, o);
+    __syncthreads();  // every half has read its first staging
+    *reinterpret_cast<f32x4*>(st + 4 * l) =
+        f32x4{a[0] >= thr ? a[0] : 0.f, a[1] >= thr ? a[1] : 0.f, a[2] >= thr ? a[2] : 0.f, a[3] >= thr ? a[3] : 0.f};
+    const float weighted = staged_sum();
+    s = cnt > 0 ? static_cast<float>(static_cast<double>(weighted) / cnt) : 1.f;
+    if (s == 0.f) s = 1.f;
+    uint32_t b = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int sg = v[t] > 0.f ? 1 : (v[t] < 0.f ? -1 : 0);
+      b |= static_cast<uint32_t>((a[t] >= thr ? sg : 0) + 1) << (2 * t);
+    }
+    if (valid) prow[g * 32 + l] = static_cast<uint8_t>(b);
+  }
+  if (valid && l == 0) scales[(int64_t)n * ng + g] = s;
+}
+
 template <int BITS>
 __global__ __launch_bounds__(256) void k_quant_groups(const float* __restrict__ W, int64_t ldw, int N, int K,
                                                       int G, float* __restrict__ scales,
@@ -185,8 +302,12 @@ extern "C" int qs_quant_rows_int8(const float* W, int64_t ldw, int64_t N, int64_
   if (N < 0 || K <= 0 || ldw < K || ldq < K) return fail(QS_ERR_INVALID, "quant_rows_int8: bad shape");
   if (N > INT_MAX || K > INT_MAX) return fail(QS_ERR_LIMIT, "quant_rows_int8: dimension exceeds int32");
   if (N == 0) return QS_OK;
-  hipLaunchKernelGGL(k_quant_int8, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     W, ldw, (int)N, (int)K, q, ldq, scales);
+  if (K % 4 == 0 && ldw % 4 == 0 && ldq % 4 == 0 && aligned(W, 16) && aligned(q, 4))
+    hipLaunchKernelGGL(k_quant_int8_v, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       W, ldw, (int)N, (int)K, q, ldq, scales);
+  else
+    hipLaunchKernelGGL(k_quant_int8, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       W, ldw, (int)N, (int)K, q, ldq, scales);
   return hip_check(hipGetLastError(), "k_quant_int8 launch");
 }
 
@@ -202,6 +323,14 @@ extern "C" int qs_quant_rows_lowbit(const float* W, int64_t ldw, int64_t N, int6
   if (N == 0) return QS_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t ng = cdiv(K, G);
+  if (G == 128 && K % 128 == 0 && ldw % 4 == 0 && aligned(W, 16)) {
+    const unsigned gg = (unsigned)cdiv(N * ng, 8);  // 8 groups per 256-thread workgroup
+    if (bits == 3)
+      hipLaunchKernelGGL(k_quant_g128<3>, dim3(gg), dim3(256), 0, s, W, ldw, (int)N, (int)K, scales, packed, row_bytes);
+    else
+      hipLaunchKernelGGL(k_quant_g128<2>, dim3(gg), dim3(256), 0, s, W, ldw, (int)N, (int)K, scales, packed, row_bytes);
+    return hip_check(hipGetLastError(), "k_quant_g128 launch");
+  }
   const unsigned gq = (unsigned)cdiv(N * ng, 256), gp = (unsigned)cdiv(N * row_bytes, 256);
   if (bits == 3) {
     hipLaunchKernelGGL(k_quant_groups<3>, dim3(gq), dim3(256), 0, s, W, ldw, (int)N, (int)K, G, scales, codes);

@@ -49,8 +49,9 @@ def _matrix(rng, n, k):
     return W
 
 
-@pytest.mark.parametrize("n,k", [(64, 1536), (7, 300), (33, 4100)])
+@pytest.mark.parametrize("n,k", [(64, 1536), (7, 300), (33, 4100), (5, 301), (9, 4099)])
 def test_int8_matches_oracle(dev, n, k):
+    # K % 4 == 0 takes the 16-byte-load kernel, the rest the scalar one
     W = _matrix(np.random.default_rng(n + k), n, k)
     q, s = _codecs().quant_row_int8(torch.from_numpy(W).to(dev))
     rq, rs = oq.quant_row_int8(W)
@@ -59,10 +60,11 @@ def test_int8_matches_oracle(dev, n, k):
 
 @pytest.mark.parametrize("bits", [3, 2])
 @pytest.mark.parametrize("G", [4, 8, 64, 128, 300, 1000, 4096])
-@pytest.mark.parametrize("k", [300, 4100])
+@pytest.mark.parametrize("k", [300, 4100, 512, 4096])
 def test_lowbit_matches_oracle(dev, bits, G, k):
     """Group sizes around numpy's pairwise-sum branches (< 8, <= 128, recursive splits),
-    ragged last groups, packed streams that end mid-byte."""
+    ragged last groups, packed streams that end mid-byte; G = 128 with K % 128 == 0 takes
+    the one-launch kernel (half a wave per group)."""
     W = _matrix(np.random.default_rng(bits * 1000 + G + k), 24, k)
     fn = _codecs().quant_row_int3 if bits == 3 else _codecs().quant_row_int2
     p, s = fn(torch.from_numpy(W).to(dev), G=G)
