@@ -433,6 +433,29 @@ def profile_lowbit(torch, dev, calls: int) -> dict:
     return out
 
 
+def profile_codecs(torch, dev, calls: int) -> dict:
+    """Eager launches of the offline codecs, ``calls`` each: int8 rows of an fp32 [14336,
+    4096] weight, int3 and int2 (G 128) of an fp32 [11008, 4096] one; prints each one's
+    algorithmic bytes (fp32 input + codes + fp32 scales)."""
+    from mrun_pub_amd import codecs
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    out: dict = {"profile": "codec", "calls": calls}
+    W = torch.randn(14336, 4096, device=dev, generator=gen)
+    for _ in range(calls):
+        codecs.quant_row_int8(W)
+    out["int8_14336x4096_bytes"] = 5 * 14336 * 4096 + 4 * 14336
+    del W
+    W = torch.randn(11008, 4096, device=dev, generator=gen)
+    for bits, fn in ((3, codecs.quant_row_int3), (2, codecs.quant_row_int2)):
+        for _ in range(calls):
+            fn(W)
+        out[f"int{bits}_11008x4096_bytes"] = 4 * 11008 * 4096 + 11008 * 4096 * bits // 8 + 4 * 11008 * 32
+    torch.cuda.synchronize()
+    return out
+
+
 def profile_mfma_kernels(torch, dev, which: str, calls: int) -> dict:
     """Eager launches of config 3's fused W8A8 GEMM or config 4's MoE layer, for counter runs
     (MFMA utilisation, HBM bytes); prints the algorithmic figures to compare against."""
@@ -663,13 +686,14 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-secondary", action="store_true", help="skip configs 1/3/4/5")
-    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "w8a8p", "moe", "moe16", "lowbit"),
+    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "w8a8p", "moe", "moe16", "lowbit", "codec"),
                     help="for rocprofv3 runs: replay exactly the timed graph of the roofline kernel (28 "
                     "paired gate/up+SwiGLU launches) or of the headline pass, --steps times after "
                     "--warmup replays; a plain 256 MiB device copy x5 (counter calibration); or config 3's "
                     "fused W8A8 GEMM (M=512 and 2048), config 3's whole w8a8_matmul with protect_k=8 (w8a8p) / "
                     "config 4's MoE layer (T=64 and 512; moe16: the weight-only flow), or config 5's low-bit "
-                    "GEMV/GEMM (both shapes, int3/int2, M=1 and 8), --steps calls each")
+                    "GEMV/GEMM (both shapes, int3/int2, M=1 and 8), or the offline codecs (int8, int3, "
+                    "int2), --steps calls each")
     ap.add_argument("--eager", action="store_true",
                     help="with --profile swiglu/stack: launch the same sequence eagerly instead of replaying "
                     "the graph (counter collection needs eager dispatches)")
@@ -706,6 +730,9 @@ def main() -> int:
         return 0
     if args.profile == "lowbit":
         print(json.dumps(profile_lowbit(torch, dev, args.steps)), flush=True)
+        return 0
+    if args.profile == "codec":
+        print(json.dumps(profile_codecs(torch, dev, args.steps)), flush=True)
         return 0
     arena, pages = build_stack(torch, dev)
     gen = torch.Generator(device=dev)

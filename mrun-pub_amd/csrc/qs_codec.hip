@@ -11,9 +11,10 @@
 //                    code = (active ? sign(blk) : 0) + 1 (_quant_row_int2, qstore_int2.py:36-63).
 //   k_pack_codes   : one thread per output byte of the LSB-first row bitstream
 //                    (np.packbits(bitorder="little"), qstore_int3.py:30-39, qstore_int2.py:24-33).
-//   k_quant_int8_v, k_quant_g128 : the same arithmetic with 16-byte loads, for rows of
-//                    whole 4-column pieces (int8) and for the writers' default G = 128
-//                    with whole groups (int3/int2, codes packed in the same launch).
+//   k_quant_int8_r/_v, k_quant_g128 : the same arithmetic with 16-byte loads, for rows of
+//                    whole 4-column pieces (int8; rows up to 4096 held in registers) and for
+//                    the writers' default G = 128 with whole groups (int3/int2, codes packed
+//                    in the same launch).
 //
 // Arithmetic follows numpy's exactly:
 //   * float32 divisions by the literals 127.0 / 3.0 (numpy keeps float32 for a Python float
@@ -143,6 +144,45 @@ __global__ __launch_bounds__(256) void k_quant_int8_v(const float* __restrict__ 
   for (int i = lane; i < k4; i += 64) {
     const f32x4 v = w[i];
     qo[i] = code(v[0]) | code(v[1]) << 8 | code(v[2]) << 16 | code(v[3]) << 24;
+  }
+}
+
+// k_quant_int8_v for K <= 4096: the row stays in registers (up to 16 four-column pieces
+// per lane), so it is read once; the two-pass form re-read it from HBM (470 MB fetched for
+// a 235 MB weight).
+__global__ __launch_bounds__(256) void k_quant_int8_r(const float* __restrict__ W, int64_t ldw, int N, int K,
+                                                      int8_t* __restrict__ q, int64_t ldq,
+                                                      float* __restrict__ scales) {
+  constexpr int V = 16;  // pieces per lane: K <= 64 * V * 4
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const f32x4* w = reinterpret_cast<const f32x4*>(W + (int64_t)n * ldw);
+  const int k4 = K / 4;
+  f32x4 v[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int i = lane + 64 * j;
+    v[j] = i < k4 ? w[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < V; ++j)
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[j][0]), fabsf(v[j][1])), fmaxf(fabsf(v[j][2]), fabsf(v[j][3]))));
+  mx = wave_max(mx);
+  float s = mx / 127.0f;
+  if (s == 0.f) s = 1.f;
+  if (lane == 0) scales[n] = s;
+  auto code = [&](float x) -> uint32_t {
+    float r = rintf(x / s);
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    return static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(r)));
+  };
+  uint32_t* qo = reinterpret_cast<uint32_t*>(q + (int64_t)n * ldq);
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int i = lane + 64 * j;
+    if (i < k4) qo[i] = code(v[j][0]) | code(v[j][1]) << 8 | code(v[j][2]) << 16 | code(v[j][3]) << 24;
   }
 }
 
@@ -302,7 +342,11 @@ extern "C" int qs_quant_rows_int8(const float* W, int64_t ldw, int64_t N, int64_
   if (N < 0 || K <= 0 || ldw < K || ldq < K) return fail(QS_ERR_INVALID, "quant_rows_int8: bad shape");
   if (N > INT_MAX || K > INT_MAX) return fail(QS_ERR_LIMIT, "quant_rows_int8: dimension exceeds int32");
   if (N == 0) return QS_OK;
-  if (K % 4 == 0 && ldw % 4 == 0 && ldq % 4 == 0 && aligned(W, 16) && aligned(q, 4))
+  const bool vec = K % 4 == 0 && ldw % 4 == 0 && ldq % 4 == 0 && aligned(W, 16) && aligned(q, 4);
+  if (vec && K <= 4096)
+    hipLaunchKernelGGL(k_quant_int8_r, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       W, ldw, (int)N, (int)K, q, ldq, scales);
+  else if (vec)
     hipLaunchKernelGGL(k_quant_int8_v, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
                        W, ldw, (int)N, (int)K, q, ldq, scales);
   else
