@@ -208,9 +208,11 @@ __global__ __launch_bounds__(256) void k_quant_g128(const float* __restrict__ W,
   const f32x4 v = valid ? *reinterpret_cast<const f32x4*>(W + (int64_t)n * ldw + g * 128 + 4 * l)
                         : f32x4{0.f, 0.f, 0.f, 0.f};
   float* st = stage[hw];
-  // numpy's pairwise sum of the 128 staged values (every lane of the block takes part)
+  // numpy's pairwise sum of the 128 staged values.  A half wave reads only what its own
+  // wave wrote, and a wave's LDS operations complete in order: waiting for this wave's
+  // writes is enough, no workgroup barrier
   auto staged_sum = [&]() -> float {
-    __syncthreads();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float r = 0.f;
     if (l < 8) {
       r = st[l];
@@ -252,7 +254,8 @@ __global__ __launch_bounds__(256) void k_quant_g128(const float* __restrict__ W,
 #pragma unroll
     for (int t = 0; t < 4; ++t) cnt += a[t] >= thr;
     for (int o = 1; o < 32; o <<= 1) cnt += __shfl_xor(cnt, o);
-    __syncthreads();  // every half has read its first staging
+    // the first staging's reads have returned (their sums were used above) before the
+    // second staging is written
     *reinterpret_cast<f32x4*>(st + 4 * l) =
         f32x4{a[0] >= thr ? a[0] : 0.f, a[1] >= thr ? a[1] : 0.f, a[2] >= thr ? a[2] : 0.f, a[3] >= thr ? a[3] : 0.f};
     const float weighted = staged_sum();
