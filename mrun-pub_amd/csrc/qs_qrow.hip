@@ -1,7 +1,7 @@
 // int8 row-scaled ("qrow") QStore linears on gfx950.
 //
 // Kernels
-//   k_dequant16 / k_dequant_any : W = float(code) * scale -> f32 / bf16 / f16.
+//   k_dequant_v / k_dequant_any : W = float(code) * scale -> f32 / bf16 / f16.
 //   k_w8a16<...>                : y = x @ W^T for bf16/f16 activations.  Weights stream
 //                                 straight from HBM into VGPRs with 128-bit loads, are
 //                                 dequantized in registers (bf16(float(code)*scale), the
@@ -67,40 +67,55 @@ struct QrowParams {
 // ----------------------------------------------------------------------------------
 // dequant
 // ----------------------------------------------------------------------------------
+// Lane-contiguous stores: a thread widens E codes (4 for fp32 output, 8 for bf16 / fp16)
+// into one 16-byte store, so a wave's store instruction writes 1 KB of consecutive output.
+// (Sixteen codes per thread wrote 64 or 32 bytes per lane as 16-byte pieces strided
+// across the wave: 79.4 against 60.7 us for a 14336 x 4096 fp32 dequant, same box.)
 template <int OUT>
-__global__ __launch_bounds__(256) void k_dequant16(const int8_t* __restrict__ codes,
+__global__ __launch_bounds__(256) void k_dequant_v(const int8_t* __restrict__ codes,
                                                    const float* __restrict__ scales,
                                                    void* __restrict__ out, int64_t N,
                                                    int64_t K, int64_t ld_out) {
-  const int64_t per_row = K / 16;
+  constexpr int E = OUT == QS_F32 ? 4 : 8;
+  const int64_t per_row = K / E;
   const int64_t total = N * per_row;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t n = i / per_row;
     const int64_t c = i - n * per_row;
-    const i32x4 w = *reinterpret_cast<const i32x4*>(codes + n * K + c * 16);
     const float s = scales[n];
-    if (OUT == QS_F32) {
-      f32x4* o = reinterpret_cast<f32x4*>(static_cast<float*>(out) + n * ld_out + c * 16);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f32x4 v;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) v[b] = byte_f32(w[j], b) * s;
-        o[j] = v;
-      }
-    } else if (OUT == QS_BF16) {
-      bf16x8 lo, hi;
-      deq16_bf16(w, s, lo, hi);
-      bf16x8* o = reinterpret_cast<bf16x8*>(static_cast<uint16_t*>(out) + n * ld_out + c * 16);
-      o[0] = lo;
-      o[1] = hi;
+    if constexpr (OUT == QS_F32) {
+      const int w = *reinterpret_cast<const int*>(codes + n * K + c * 4);
+      f32x4 v;
+      v[0] = sbyte_f32<0>(w) * s;
+      v[1] = sbyte_f32<1>(w) * s;
+      v[2] = sbyte_f32<2>(w) * s;
+      v[3] = sbyte_f32<3>(w) * s;
+      *reinterpret_cast<f32x4*>(static_cast<float*>(out) + n * ld_out + c * 4) = v;
     } else {
-      f16x8 lo, hi;
-      deq16_f16(w, s, lo, hi);
-      f16x8* o = reinterpret_cast<f16x8*>(static_cast<uint16_t*>(out) + n * ld_out + c * 16);
-      o[0] = lo;
-      o[1] = hi;
+      typedef int i32x2 __attribute__((ext_vector_type(2)));
+      const i32x2 w = *reinterpret_cast<const i32x2*>(codes + n * K + c * 8);
+      if constexpr (OUT == QS_BF16) {
+        bf16x8 o;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          o[4 * j + 0] = static_cast<__bf16>(sbyte_f32<0>(w[j]) * s);
+          o[4 * j + 1] = static_cast<__bf16>(sbyte_f32<1>(w[j]) * s);
+          o[4 * j + 2] = static_cast<__bf16>(sbyte_f32<2>(w[j]) * s);
+          o[4 * j + 3] = static_cast<__bf16>(sbyte_f32<3>(w[j]) * s);
+        }
+        *reinterpret_cast<bf16x8*>(static_cast<uint16_t*>(out) + n * ld_out + c * 8) = o;
+      } else {
+        f16x8 o;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          o[4 * j + 0] = static_cast<_Float16>(sbyte_f32<0>(w[j]) * s);
+          o[4 * j + 1] = static_cast<_Float16>(sbyte_f32<1>(w[j]) * s);
+          o[4 * j + 2] = static_cast<_Float16>(sbyte_f32<2>(w[j]) * s);
+          o[4 * j + 3] = static_cast<_Float16>(sbyte_f32<3>(w[j]) * s);
+        }
+        *reinterpret_cast<f16x8*>(static_cast<uint16_t*>(out) + n * ld_out + c * 8) = o;
+      }
     }
   }
 }
@@ -1798,14 +1813,14 @@ extern "C" int qs_qrow_dequant(const int8_t* codes, const float* scales, void* o
   const bool fast = K % 16 == 0 && aligned(codes, 16) && aligned(out, 16) &&
                     (ld_out * osz) % 16 == 0;
   if (fast) {
-    const int64_t work = N * (K / 16);
+    const int64_t work = N * (K / (out_dtype == QS_F32 ? 4 : 8));
     const unsigned blocks = (unsigned)(cdiv(work, 256) < 65536 ? cdiv(work, 256) : 65536);
     if (out_dtype == QS_F32)
-      hipLaunchKernelGGL(k_dequant16<QS_F32>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
+      hipLaunchKernelGGL(k_dequant_v<QS_F32>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
     else if (out_dtype == QS_BF16)
-      hipLaunchKernelGGL(k_dequant16<QS_BF16>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
+      hipLaunchKernelGGL(k_dequant_v<QS_BF16>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
     else
-      hipLaunchKernelGGL(k_dequant16<QS_F16>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
+      hipLaunchKernelGGL(k_dequant_v<QS_F16>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
   } else {
     const int64_t work = N * K;
     const unsigned blocks = (unsigned)(cdiv(work, 256) < 65536 ? cdiv(work, 256) : 65536);
