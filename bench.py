@@ -216,6 +216,18 @@ def cpu_baselines_per_config(seconds: float = 2.0) -> dict:
     done, dt = _timed_loop(lambda: olow.quant_row_int3(Wl), seconds)
     out["codec_int3"] = {"unit": "GB/s", "sample": "_quant_row_int3 + packing on 256 x 4096 fp32 rows (numpy)",
                          "one_thread": round(done * (4 * 256 * 4096 + 256 * 1536 + 4 * 256 * 32) / dt / 1e9, 3)}
+    # whole-weight dequant: the reference's numpy dequant restated in oracle/, fp32 out
+    qd = rng.integers(-127, 128, size=(1024, 4096), dtype=np.int8)
+    sd = (rng.uniform(0.5, 1.5, 1024) / 127).astype(np.float32)
+    done, dt = _timed_loop(lambda: oq.dequant_qrow(qd, sd), seconds)
+    out["dequant_qrow_f32"] = {"unit": "GB/s", "sample": "_dequant_qrow of 1024 x 4096 int8 rows to fp32 (numpy)",
+                               "one_thread": round(done * (5 * 1024 * 4096 + 4 * 1024) / dt / 1e9, 3)}
+    pk = rng.integers(0, 256, size=(256, 1536), dtype=np.uint8)
+    s3 = (rng.uniform(0.5, 1.5, size=(256, 64)) / 7).astype(np.float16)
+    z3 = rng.uniform(0, 7, size=(256, 64)).astype(np.float16)
+    done, dt = _timed_loop(lambda: olow.dequant(pk, s3, 4096, 3, 64, zeros=z3), seconds)
+    out["dequant_int3_f32"] = {"unit": "GB/s", "sample": "int3 G64 dequant (np.unpackbits) of 256 x 4096 to fp32 (numpy)",
+                               "one_thread": round(done * (256 * 1536 + 4 * 256 * 64 + 4 * 256 * 4096) / dt / 1e9, 3)}
     return out
 
 
@@ -456,6 +468,35 @@ def profile_codecs(torch, dev, calls: int) -> dict:
     return out
 
 
+def profile_dequant(torch, dev, calls: int) -> dict:
+    """Eager launches of the whole-weight dequants, ``calls`` each: int8 rows [14336, 4096]
+    to bf16 and fp32, int3 / int2 G64 (fp16 scale + zero) [11008, 4096] to fp32; prints
+    each one's algorithmic bytes."""
+    from mrun_pub_amd import lowbit, qrow
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    out: dict = {"profile": "dequant", "calls": calls}
+    cd = torch.randint(-127, 128, (14336, 4096), dtype=torch.int8, device=dev, generator=gen)
+    sd = (torch.rand(14336, device=dev, generator=gen) + 0.5) / 127
+    for dname, dt, es in (("bf16", torch.bfloat16, 2), ("f32", torch.float32, 4)):
+        for _ in range(calls):
+            qrow.qrow_dequant(cd, sd, dt)
+        out[f"qrow_{dname}_bytes"] = 14336 * 4096 * (1 + es) + 4 * 14336
+    del cd, sd
+    for bits in (3, 2):
+        rb = 4096 * bits // 8
+        pk = torch.randint(0, 256, (11008, rb), dtype=torch.uint8, device=dev, generator=gen)
+        sc = ((torch.rand(11008, 64, device=dev, generator=gen) + 0.5) / 7).to(torch.float16)
+        zp = (torch.rand(11008, 64, device=dev, generator=gen) * 7).to(torch.float16)
+        pg = lowbit.LowbitPage("w", bits, 64, 4096, pk, sc, zp)
+        for _ in range(calls):
+            lowbit.lowbit_dequant(pg)
+        out[f"int{bits}_bytes"] = 11008 * rb + 2 * 2 * 11008 * 64 + 4 * 11008 * 4096
+    torch.cuda.synchronize()
+    return out
+
+
 def profile_mfma_kernels(torch, dev, which: str, calls: int) -> dict:
     """Eager launches of config 3's fused W8A8 GEMM or config 4's MoE layer, for counter runs
     (MFMA utilisation, HBM bytes); prints the algorithmic figures to compare against."""
@@ -640,6 +681,31 @@ def secondary_measurements(torch, dev, stream) -> dict:
         res[f"codec_int{bits}_{Nc}x{Kc}"] = {"us": round(tc * 1e6, 2), "GB/s": round(bc / tc / 1e9, 1),
                                              "hbm_frac": round(bc / tc / 1e9 / HBM_PEAK_GBS, 4)}
     del Wc
+
+    # whole-weight dequant (QStore.weight / fp32 of the qrow and low-bit stores): int8 rows
+    # of config 3's [14336, 4096] to bf16 and fp32; int3 / int2 G64 (fp16 scale + zero) of
+    # config 5's [11008, 4096] to fp32; bytes = codes + scales (+ zeros) + output
+    for dname, dt, es in (("bf16", torch.bfloat16, 2), ("f32", torch.float32, 4)):
+        Nd, Kd = 14336, 4096
+        cd = torch.randint(-127, 128, (Nd, Kd), dtype=torch.int8, device=dev, generator=gen)
+        sd = (torch.rand(Nd, device=dev, generator=gen) + 0.5) / 127
+        td = _graph_time(torch, stream, lambda i: qrow.qrow_dequant(cd, sd, dt), 4)
+        bd = Nd * Kd + 4 * Nd + es * Nd * Kd
+        res[f"dequant_qrow_{dname}_{Nd}x{Kd}"] = {"us": round(td * 1e6, 2), "GB/s": round(bd / td / 1e9, 1),
+                                                 "hbm_frac": round(bd / td / 1e9 / HBM_PEAK_GBS, 4)}
+        del cd, sd
+    for bits in (3, 2):
+        Nd, Kd = 11008, 4096
+        rb = Kd * bits // 8
+        pk = torch.randint(0, 256, (Nd, rb), dtype=torch.uint8, device=dev, generator=gen)
+        sc = ((torch.rand(Nd, Kd // 64, device=dev, generator=gen) + 0.5) / 7).to(torch.float16)
+        zp = (torch.rand(Nd, Kd // 64, device=dev, generator=gen) * 7).to(torch.float16)
+        pg = lowbit.LowbitPage("w", bits, 64, Kd, pk, sc, zp)
+        td = _graph_time(torch, stream, lambda i: lowbit.lowbit_dequant(pg), 4)
+        bd = Nd * rb + 2 * 2 * Nd * (Kd // 64) + 4 * Nd * Kd
+        res[f"dequant_int{bits}_{Nd}x{Kd}"] = {"us": round(td * 1e6, 2), "GB/s": round(bd / td / 1e9, 1),
+                                               "hbm_frac": round(bd / td / 1e9 / HBM_PEAK_GBS, 4)}
+        del pk, sc, zp, pg
     return res
 
 
@@ -686,14 +752,15 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-secondary", action="store_true", help="skip configs 1/3/4/5")
-    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "w8a8p", "moe", "moe16", "lowbit", "codec"),
+    ap.add_argument("--profile", choices=("swiglu", "stack", "copy", "w8a8", "w8a8p", "moe", "moe16", "lowbit", "codec",
+                                          "dequant"),
                     help="for rocprofv3 runs: replay exactly the timed graph of the roofline kernel (28 "
                     "paired gate/up+SwiGLU launches) or of the headline pass, --steps times after "
                     "--warmup replays; a plain 256 MiB device copy x5 (counter calibration); or config 3's "
                     "fused W8A8 GEMM (M=512 and 2048), config 3's whole w8a8_matmul with protect_k=8 (w8a8p) / "
                     "config 4's MoE layer (T=64 and 512; moe16: the weight-only flow), or config 5's low-bit "
-                    "GEMV/GEMM (both shapes, int3/int2, M=1 and 8), or the offline codecs (int8, int3, "
-                    "int2), --steps calls each")
+                    "GEMV/GEMM (both shapes, int3/int2, M=1 and 8), the offline codecs (int8, int3, "
+                    "int2), or the whole-weight dequants (qrow bf16/fp32, int3/int2 fp32), --steps calls each")
     ap.add_argument("--eager", action="store_true",
                     help="with --profile swiglu/stack: launch the same sequence eagerly instead of replaying "
                     "the graph (counter collection needs eager dispatches)")
@@ -733,6 +800,9 @@ def main() -> int:
         return 0
     if args.profile == "codec":
         print(json.dumps(profile_codecs(torch, dev, args.steps)), flush=True)
+        return 0
+    if args.profile == "dequant":
+        print(json.dumps(profile_dequant(torch, dev, args.steps)), flush=True)
         return 0
     arena, pages = build_stack(torch, dev)
     gen = torch.Generator(device=dev)
