@@ -1013,7 +1013,14 @@ __global__ __launch_bounds__(256) void k_lowbit_dequant(LowbitParams p, int bits
 // per thread.
 __global__ __launch_bounds__(256) void k_lowbit_dequant4(LowbitParams p, int bits, int G, float* __restrict__ out) {
   const int k4 = p.K / 4;
-  const int64_t i = blockIdx.x * 256ll + threadIdx.x;
+  // Workgroup b runs on XCD b % 8.  A row's workgroups share the row's scale and zero
+  // lines, so consecutive logical indices go to one XCD and its L2 serves the repeats
+  // (with the plain order the 128-byte scale line of a 4096-column row was fetched from
+  // HBM by four XCDs): the first 8 * floor(grid / 8) workgroups are dealt out XCD-major.
+  const int64_t nb = gridDim.x, per = nb / 8;
+  const int64_t b = blockIdx.x;
+  const int64_t lb = b < 8 * per ? (b % 8) * per + b / 8 : b;
+  const int64_t i = lb * 256 + threadIdx.x;
   if (i >= (int64_t)p.N * k4) return;
   const int64_t n = i / k4;
   const int c = (int)(i - n * k4);
