@@ -1010,9 +1010,14 @@ __global__ __launch_bounds__(256) void k_lowbit_dequant(LowbitParams p, int bits
 // row (one byte at 2 bits; 12 or 16 bits from two bytes at 3 or 4) into one 16-byte store,
 // so a wave's store instruction writes 1 KB of consecutive output.  Same values; 11008 x
 // 4096 fp32 out, same box: int3 140.4 -> 43.8 us, int2 124.8 -> 38.1 us against one code
-// per thread.
+// per thread.  Each thread takes U such pieces, 256 apart, with all their loads issued
+// before the first store (a load behind a store would also wait for the store).
+constexpr int kLowbitDequantPieces = 4;
+
+template <int U>
 __global__ __launch_bounds__(256) void k_lowbit_dequant4(LowbitParams p, int bits, int G, float* __restrict__ out) {
-  const int k4 = p.K / 4;
+  const int64_t k4 = p.K / 4;
+  const int64_t total = (int64_t)p.N * k4;
   // Workgroup b runs on XCD b % 8.  A row's workgroups share the row's scale and zero
   // lines, so consecutive logical indices go to one XCD and its L2 serves the repeats
   // (with the plain order the 128-byte scale line of a 4096-column row was fetched from
@@ -1020,27 +1025,44 @@ __global__ __launch_bounds__(256) void k_lowbit_dequant4(LowbitParams p, int bit
   const int64_t nb = gridDim.x, per = nb / 8;
   const int64_t b = blockIdx.x;
   const int64_t lb = b < 8 * per ? (b % 8) * per + b / 8 : b;
-  const int64_t i = lb * 256 + threadIdx.x;
-  if (i >= (int64_t)p.N * k4) return;
-  const int64_t n = i / k4;
-  const int c = (int)(i - n * k4);
-  const int64_t bit = (int64_t)c * 4 * bits;  // 8c, 12c or 16c: the piece ends inside the row
-  const uint8_t* row = p.packed + n * p.row_bytes;
-  uint32_t v = row[bit >> 3];
-  if (bits > 2) v |= static_cast<uint32_t>(row[(bit >> 3) + 1]) << 8;
-  v >>= (bit & 7);
-  const int64_t si = n * p.ng + (4 * c) / G;
-  const float sc = p.scale_f16 ? f16_bits_to_f32(static_cast<const uint16_t*>(p.scales)[si])
-                               : static_cast<const float*>(p.scales)[si];
-  float z = p.offset;
-  if (p.zeros)
-    z = p.zero_f16 ? f16_bits_to_f32(static_cast<const uint16_t*>(p.zeros)[si])
-                   : static_cast<const float*>(p.zeros)[si];
+  const int64_t base = lb * 256 * U;
+  // the chunk's first row from one division, each piece's from a 32-bit one
+  const int64_t n0 = base / k4;
+  const uint32_t c0 = (uint32_t)(base - n0 * k4);
   const uint32_t mask = (1u << bits) - 1;
-  f32x4 o;
+  uint32_t v[U];
+  float sc[U], z[U];
+  int64_t n[U];
+  uint32_t c[U];
+  bool ok[U];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] = mul_rn(static_cast<float>((v >> (bits * e)) & mask) - z, sc);
-  *reinterpret_cast<f32x4*>(out + n * p.K + 4 * c) = o;
+  for (int u = 0; u < U; ++u) {
+    const uint32_t off = c0 + (uint32_t)(u * 256 + threadIdx.x);  // < k4 + 256 U
+    const uint32_t q = off / (uint32_t)k4;
+    ok[u] = base + u * 256 + threadIdx.x < total;
+    n[u] = ok[u] ? n0 + q : 0;
+    c[u] = ok[u] ? off - q * (uint32_t)k4 : 0u;
+    const int64_t bit = (int64_t)c[u] * 4 * bits;  // 8c, 12c or 16c: the piece ends inside the row
+    const uint8_t* row = p.packed + n[u] * p.row_bytes;
+    v[u] = row[bit >> 3];
+    if (bits > 2) v[u] |= static_cast<uint32_t>(row[(bit >> 3) + 1]) << 8;
+    v[u] >>= (bit & 7);
+    const int64_t si = n[u] * p.ng + (4 * (int64_t)c[u]) / G;
+    sc[u] = p.scale_f16 ? f16_bits_to_f32(static_cast<const uint16_t*>(p.scales)[si])
+                        : static_cast<const float*>(p.scales)[si];
+    z[u] = p.offset;
+    if (p.zeros)
+      z[u] = p.zero_f16 ? f16_bits_to_f32(static_cast<const uint16_t*>(p.zeros)[si])
+                        : static_cast<const float*>(p.zeros)[si];
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (!ok[u]) continue;
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = mul_rn(static_cast<float>((v[u] >> (bits * e)) & mask) - z[u], sc[u]);
+    *reinterpret_cast<f32x4*>(out + n[u] * p.K + 4 * (int64_t)c[u]) = o;
+  }
 }
 
 // Any layout the tiled kernels refuse (a group size other than 64 / 128, K not a multiple
@@ -1410,8 +1432,9 @@ extern "C" int qs_lowbit_dequant(const uint8_t* packed, int64_t row_bytes, const
   p.ng = (int)((K + group_size - 1) / group_size);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (K % 4 == 0 && group_size % 4 == 0 && aligned(out, 16))
-    hipLaunchKernelGGL(k_lowbit_dequant4, dim3((unsigned)cdiv(N * (K / 4), 256)), dim3(256), 0, s, p, bits, group_size,
-                       out);
+    hipLaunchKernelGGL(k_lowbit_dequant4<kLowbitDequantPieces>,
+                       dim3((unsigned)cdiv(N * (K / 4), 256 * kLowbitDequantPieces)), dim3(256), 0, s, p, bits,
+                       group_size, out);
   else
     hipLaunchKernelGGL(k_lowbit_dequant, dim3((unsigned)cdiv(N * K, 256)), dim3(256), 0, s, p, bits, group_size, out);
   return hip_check(hipGetLastError(), "k_lowbit_dequant launch");

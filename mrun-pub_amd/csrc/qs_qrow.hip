@@ -43,6 +43,7 @@
 #include "qs_common.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace qs {
 
@@ -71,50 +72,73 @@ struct QrowParams {
 // into one 16-byte store, so a wave's store instruction writes 1 KB of consecutive output.
 // (Sixteen codes per thread wrote 64 or 32 bytes per lane as 16-byte pieces strided
 // across the wave: 79.4 against 60.7 us for a 14336 x 4096 fp32 dequant, same box.)
-template <int OUT>
+// Each thread takes U such pieces, 256 apart: all U code loads are issued first and
+// waited for once, then the U stores follow, and the wave ends without waiting for them
+// (stores and loads share one completion counter, so a load issued behind a store would
+// wait for that store too).  The chunk's first row comes from one division per chunk;
+// each piece's row and column from a 32-bit division of its offset within the chunk.
+constexpr int kDequantPieces = 4;  // 16-byte pieces per thread
+
+template <int OUT, int U>
 __global__ __launch_bounds__(256) void k_dequant_v(const int8_t* __restrict__ codes,
                                                    const float* __restrict__ scales,
                                                    void* __restrict__ out, int64_t N,
                                                    int64_t K, int64_t ld_out) {
   constexpr int E = OUT == QS_F32 ? 4 : 8;
+  typedef int i32x2 __attribute__((ext_vector_type(2)));
+  using CW = typename std::conditional<E == 4, int, i32x2>::type;
   const int64_t per_row = K / E;
   const int64_t total = N * per_row;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t n = i / per_row;
-    const int64_t c = i - n * per_row;
-    const float s = scales[n];
-    if constexpr (OUT == QS_F32) {
-      const int w = *reinterpret_cast<const int*>(codes + n * K + c * 4);
-      f32x4 v;
-      v[0] = sbyte_f32<0>(w) * s;
-      v[1] = sbyte_f32<1>(w) * s;
-      v[2] = sbyte_f32<2>(w) * s;
-      v[3] = sbyte_f32<3>(w) * s;
-      *reinterpret_cast<f32x4*>(static_cast<float*>(out) + n * ld_out + c * 4) = v;
-    } else {
-      typedef int i32x2 __attribute__((ext_vector_type(2)));
-      const i32x2 w = *reinterpret_cast<const i32x2*>(codes + n * K + c * 8);
-      if constexpr (OUT == QS_BF16) {
+  for (int64_t base = (int64_t)blockIdx.x * 256 * U; base < total; base += (int64_t)gridDim.x * 256 * U) {
+    const int64_t n0 = base / per_row;
+    const uint32_t c0 = (uint32_t)(base - n0 * per_row);
+    int64_t n[U];
+    uint32_t c[U];
+    bool ok[U];
+    CW w[U];
+    float s[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t off = c0 + (uint32_t)(u * 256 + threadIdx.x);  // < per_row + 256 U
+      const uint32_t q = off / (uint32_t)per_row;
+      n[u] = n0 + q;
+      c[u] = off - q * (uint32_t)per_row;
+      ok[u] = base + u * 256 + threadIdx.x < total;
+      const int64_t nn = ok[u] ? n[u] : 0;
+      const uint32_t cc = ok[u] ? c[u] : 0u;
+      w[u] = *reinterpret_cast<const CW*>(codes + nn * K + (int64_t)cc * E);
+      s[u] = scales[nn];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!ok[u]) continue;
+      if constexpr (OUT == QS_F32) {
+        f32x4 v;
+        v[0] = sbyte_f32<0>(w[u]) * s[u];
+        v[1] = sbyte_f32<1>(w[u]) * s[u];
+        v[2] = sbyte_f32<2>(w[u]) * s[u];
+        v[3] = sbyte_f32<3>(w[u]) * s[u];
+        *reinterpret_cast<f32x4*>(static_cast<float*>(out) + n[u] * ld_out + (int64_t)c[u] * 4) = v;
+      } else if constexpr (OUT == QS_BF16) {
         bf16x8 o;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          o[4 * j + 0] = static_cast<__bf16>(sbyte_f32<0>(w[j]) * s);
-          o[4 * j + 1] = static_cast<__bf16>(sbyte_f32<1>(w[j]) * s);
-          o[4 * j + 2] = static_cast<__bf16>(sbyte_f32<2>(w[j]) * s);
-          o[4 * j + 3] = static_cast<__bf16>(sbyte_f32<3>(w[j]) * s);
+          o[4 * j + 0] = static_cast<__bf16>(sbyte_f32<0>(w[u][j]) * s[u]);
+          o[4 * j + 1] = static_cast<__bf16>(sbyte_f32<1>(w[u][j]) * s[u]);
+          o[4 * j + 2] = static_cast<__bf16>(sbyte_f32<2>(w[u][j]) * s[u]);
+          o[4 * j + 3] = static_cast<__bf16>(sbyte_f32<3>(w[u][j]) * s[u]);
         }
-        *reinterpret_cast<bf16x8*>(static_cast<uint16_t*>(out) + n * ld_out + c * 8) = o;
+        *reinterpret_cast<bf16x8*>(static_cast<uint16_t*>(out) + n[u] * ld_out + (int64_t)c[u] * 8) = o;
       } else {
         f16x8 o;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          o[4 * j + 0] = static_cast<_Float16>(sbyte_f32<0>(w[j]) * s);
-          o[4 * j + 1] = static_cast<_Float16>(sbyte_f32<1>(w[j]) * s);
-          o[4 * j + 2] = static_cast<_Float16>(sbyte_f32<2>(w[j]) * s);
-          o[4 * j + 3] = static_cast<_Float16>(sbyte_f32<3>(w[j]) * s);
+          o[4 * j + 0] = static_cast<_Float16>(sbyte_f32<0>(w[u][j]) * s[u]);
+          o[4 * j + 1] = static_cast<_Float16>(sbyte_f32<1>(w[u][j]) * s[u]);
+          o[4 * j + 2] = static_cast<_Float16>(sbyte_f32<2>(w[u][j]) * s[u]);
+          o[4 * j + 3] = static_cast<_Float16>(sbyte_f32<3>(w[u][j]) * s[u]);
         }
-        *reinterpret_cast<f16x8*>(static_cast<uint16_t*>(out) + n * ld_out + c * 8) = o;
+        *reinterpret_cast<f16x8*>(static_cast<uint16_t*>(out) + n[u] * ld_out + (int64_t)c[u] * 8) = o;
       }
     }
   }
@@ -1810,17 +1834,20 @@ extern "C" int qs_qrow_dequant(const int8_t* codes, const float* scales, void* o
   if (N == 0) return QS_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int osz = out_dtype == QS_F32 ? 4 : 2;
-  const bool fast = K % 16 == 0 && aligned(codes, 16) && aligned(out, 16) &&
-                    (ld_out * osz) % 16 == 0;
+  // per-row pieces must fit the 32-bit column arithmetic of k_dequant_v
+  const bool fast = K % 16 == 0 && aligned(codes, 16) && aligned(out, 16) && (ld_out * osz) % 16 == 0 &&
+                    K <= (int64_t(1) << 33);
   if (fast) {
+    constexpr int U = kDequantPieces;
     const int64_t work = N * (K / (out_dtype == QS_F32 ? 4 : 8));
-    const unsigned blocks = (unsigned)(cdiv(work, 256) < 65536 ? cdiv(work, 256) : 65536);
+    const int64_t chunks = cdiv(work, 256 * U);
+    const unsigned blocks = (unsigned)(chunks < 65536 ? chunks : 65536);
     if (out_dtype == QS_F32)
-      hipLaunchKernelGGL(k_dequant_v<QS_F32>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
+      hipLaunchKernelGGL((k_dequant_v<QS_F32, U>), dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
     else if (out_dtype == QS_BF16)
-      hipLaunchKernelGGL(k_dequant_v<QS_BF16>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
+      hipLaunchKernelGGL((k_dequant_v<QS_BF16, U>), dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
     else
-      hipLaunchKernelGGL(k_dequant_v<QS_F16>, dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
+      hipLaunchKernelGGL((k_dequant_v<QS_F16, U>), dim3(blocks), dim3(256), 0, s, codes, scales, out, N, K, ld_out);
   } else {
     const int64_t work = N * K;
     const unsigned blocks = (unsigned)(cdiv(work, 256) < 65536 ? cdiv(work, 256) : 65536);

@@ -52,11 +52,13 @@ def test_dequant_bit_exact(dev, bits, K, G):
 
 
 @pytest.mark.parametrize("bits", [2, 3])
-def test_dequant_asym_bit_exact(dev, bits):
-    rng = np.random.default_rng(bits)
-    packed, s, z = _asym(rng, 33, 256, bits)
-    got = _lb().lowbit_dequant(_page(dev, packed, s, 256, bits, 64, z)).cpu().numpy()
-    assert np.array_equal(got.view(np.uint32), ol.dequant(packed, s, 256, bits, 64, zeros=z).view(np.uint32))
+@pytest.mark.parametrize("N,K", [(33, 256), (1030, 4160)])
+def test_dequant_asym_bit_exact(dev, bits, N, K):
+    """(1030, 4160): many workgroups, rows of 1040 four-code pieces across their boundaries."""
+    rng = np.random.default_rng(bits + N)
+    packed, s, z = _asym(rng, N, K, bits)
+    got = _lb().lowbit_dequant(_page(dev, packed, s, K, bits, 64, z)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ol.dequant(packed, s, K, bits, 64, zeros=z).view(np.uint32))
 
 
 @pytest.mark.parametrize("bits", [2, 3])

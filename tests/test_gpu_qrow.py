@@ -32,7 +32,7 @@ def _dev(a, dev, dtype=None):
     return t if dtype is None else t.to(dtype)
 
 
-@pytest.mark.parametrize("n,k", [(64, 128), (300, 1024), (17, 48), (5, 7)])
+@pytest.mark.parametrize("n,k", [(64, 128), (300, 1024), (17, 48), (5, 7), (33, 1040), (1030, 4096)])
 @pytest.mark.parametrize("dtype", ["fp32", "bf16", "fp16"])
 def test_dequant_bit_exact(dev, n, k, dtype):
     _, codes, scales = _case(n, k, seed=n + k)
